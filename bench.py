@@ -1,0 +1,196 @@
+"""DF-J benchmark: screened density-fitted Coulomb forward + backward on one MI355X.
+
+One step = E_J = 1/2 gamma^T (V + lam I)^-1 gamma over the screened pair list plus its full
+reverse pass (J, every splat gradient and dC), with the refresh products (pair list, aux,
+Cholesky factor, pair index) built beforehand and timed separately. Inputs are the seeded
+synthetic systems of gs-dft_amd/workloads.py, resident in HBM before the timed region.
+
+Prints one JSON line. ``value`` is three-centre integrals per second through the whole step
+(N_aux x n_pairs integrals, each evaluated in the forward and again with derivatives in the
+reverse pass); ``ms_per_step`` is the fwd+bwd wall time.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP64 = 78.6e12          # MI355X FP64 (vector and matrix) FLOP/s
+PEAK_HBM = 8.0e12            # MI355X HBM3E bytes/s
+FLOPS_FWD = 379 + 40         # per three-centre integral, transcendentals counted once
+FLOPS_BWD = 740 + 40
+METRIC = "DF-J fwd+bwd wall ms; 3-centre integrals/s; % of MI355X FP64 peak"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--system", type=int, default=5, help="benchmark system 1..5")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target CPU time of the oracle baseline sample (0 disables it)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures the DF-J path on one GPU; --gpus {args.gpus} is not "
+              f"run (the multi-GPU sharding is a design in DESIGN.md, not a measured path)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import __graft_entry__ as ge
+
+    g = ge.load_package()
+    import importlib
+    wl = importlib.import_module("gs_dft_amd.workloads")
+    from gs_dft_amd import _lib
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    s = wl.make_system(args.system)
+    log(f"system {args.system} {s.name}: M={s.M} N_aux={s.n_aux} k={s.k} eps={s.eps}")
+
+    quat = torch.tensor(s.quat, device=dev)
+    ls = torch.tensor(s.log_scale, device=dev)
+    cen = torch.tensor(s.centers, device=dev)
+    C0 = torch.tensor(s.C, device=dev)
+    occ = torch.tensor(s.occ, device=dev)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam),
+                    screen=g.pairlist(s.eps, unique=s.unique, skip_pad=True))
+
+    # ------------------------------------------------------------------ refresh (timed apart)
+    _lib.profile_enable(True)
+    basis0 = g.Splat(quat=quat, log_scale=ls, centers=cen)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n0 = g.count_significant(basis0, s.eps, s.unique)
+    pad_to = g.train_pad_to(ks.screen, n0)
+    t_count = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    state = g.refresh(ks, basis0, pad_to=pad_to)
+    torch.cuda.synchronize()
+    t_refresh = time.perf_counter() - t0
+    n = state.pair_index.n_live
+    N = s.n_aux
+    screen_ms = _lib.profile_read(_lib.PROF_SCREEN, reset=True)[0]
+    metric_ms = _lib.profile_read(_lib.PROF_METRIC, reset=True)[0]
+    chol_ms = _lib.profile_read(_lib.PROF_CHOLESKY, reset=True)[0]
+    log(f"refresh: n_pairs={n} pad={pad_to} total {t_refresh * 1e3:.1f} ms "
+        f"(screen kernels {screen_ms:.1f} ms, metric {metric_ms:.1f} ms, cholesky {chol_ms:.1f} ms)")
+
+    # ------------------------------------------------------------------ step
+    def step():
+        b = g.Splat(quat=quat.clone().requires_grad_(), log_scale=ls.clone().requires_grad_(),
+                    centers=cen.clone().requires_grad_())
+        C = C0.clone().requires_grad_()
+        E = ks(g.SplatModel(basis=b, C=C, occupations=occ), state)
+        E.backward()
+        return E
+
+    for w in range(args.warmup):
+        log(f"warmup step {w + 1}/{args.warmup}")
+        step()
+    torch.cuda.synchronize()
+    for kid in (_lib.PROF_GAMMA_FWD, _lib.PROF_GAMMA_BWD, _lib.PROF_SOLVE):
+        _lib.profile_read(kid, reset=True)
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        E = step()
+        log(f"timed step {k + 1}/{args.steps}")
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    fwd_ms, fwd_n = _lib.profile_read(_lib.PROF_GAMMA_FWD, reset=True)
+    bwd_ms, bwd_n = _lib.profile_read(_lib.PROF_GAMMA_BWD, reset=True)
+    solve_ms, _ = _lib.profile_read(_lib.PROF_SOLVE, reset=True)
+    fwd_ms /= max(fwd_n, 1)
+    bwd_ms /= max(bwd_n, 1)
+    _lib.profile_enable(False)
+    integrals = float(N) * float(n)
+    fwd_tf = integrals * FLOPS_FWD / (fwd_ms * 1e-3)
+    bwd_tf = integrals * FLOPS_BWD / (bwd_ms * 1e-3)
+    log(f"E_J={E.item():.12e} step {wall * 1e3:.1f} ms; three-centre fwd {fwd_ms:.1f} ms "
+        f"({fwd_tf / 1e12:.2f} TFLOP/s), bwd {bwd_ms:.1f} ms ({bwd_tf / 1e12:.2f} TFLOP/s), "
+        f"solves {solve_ms / max(args.steps, 1):.2f} ms")
+    dom = ("reverse", bwd_ms, FLOPS_BWD, bwd_tf) if bwd_ms >= fwd_ms else ("forward", fwd_ms, FLOPS_FWD, fwd_tf)
+
+    # ------------------------------------------------------------------ CPU baseline (oracle)
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import oracle as orc
+        pi, pj, w = (t.detach().cpu().numpy() for t in state.pairs)
+        pi, pj, w = pi[:n], pj[:n], w[:n]
+        la = state.aux.log_alpha.cpu().numpy()
+        ac = state.aux.centers.cpu().numpy()
+        d = np.random.default_rng(0).normal(size=N)
+        rng = np.random.default_rng(1)
+
+        def run(m):
+            sel = np.sort(rng.choice(n, size=min(m, n), replace=False))
+            t = time.perf_counter()
+            orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sel], pj[sel], w[sel])
+            orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sel], pj[sel],
+                          w[sel], d)
+            return time.perf_counter() - t, len(sel)
+
+        probe = max(1, min(n, int(2e6 // N) + 1))
+        t_probe, m_probe = run(probe)
+        m = max(1, min(n, int(m_probe * args.cpu_seconds / max(t_probe, 1e-6))))
+        t_cpu, m_cpu = run(m) if m > m_probe else (t_probe, m_probe)
+        per_pair = t_cpu / m_cpu
+        cpu_step_ms = per_pair * n * 1e3
+        cpu = {"value": cpu_step_ms, "unit": "ms per fwd+bwd step (three-centre gamma + reverse, "
+               "extrapolated linearly in pairs)", "cores": orc.num_threads(), "kind": "port",
+               "sample": f"{m_cpu} of {n} pairs x all {N} aux functions, {t_cpu:.1f} s on "
+                         f"{orc.num_threads()} threads (C oracle, OpenMP); metric, Cholesky "
+                         f"and solves excluded",
+               "integrals_per_s": integrals / (cpu_step_ms * 1e-3)}
+        log(f"cpu baseline: {cpu_step_ms / 1e3:.1f} s per step extrapolated from {m_cpu} pairs")
+
+    out = {
+        "metric": METRIC,
+        "value": integrals / wall,
+        "unit": "three-centre integrals/s (fwd+bwd step)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"{s.name}: screened DF-J fwd+bwd, M={s.M} splats, "
+                               f"N_aux={N}, k={s.k}, eps={s.eps}, unique pairs",
+                   "system": args.system, "M": s.M, "N_aux": N, "k": s.k, "n_pairs": n,
+                   "pad_to": pad_to, "eps": s.eps, "parallelism": "single GPU"},
+        "roofline": {"bound": "fp64-valu", "kernel": f"three-centre {dom[0]}",
+                     "achieved": dom[3] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": dom[3] / PEAK_FP64, "traffic": None,
+                     "flops_per_integral": dom[2], "integrals_per_launch": integrals,
+                     "kernel_ms": dom[1]},
+        "kernels": {"three_centre_fwd_ms": fwd_ms, "three_centre_bwd_ms": bwd_ms,
+                    "fwd_frac_fp64": fwd_tf / PEAK_FP64, "bwd_frac_fp64": bwd_tf / PEAK_FP64,
+                    "fwd_integrals_per_s": integrals / (fwd_ms * 1e-3),
+                    "solves_ms": solve_ms / max(args.steps, 1)},
+        "refresh_ms": {"total": t_refresh * 1e3, "count": t_count * 1e3, "screen_kernels": screen_ms,
+                       "metric": metric_ms, "cholesky": chol_ms},
+        "cpu_baseline": cpu,
+        "E_J": E.item(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

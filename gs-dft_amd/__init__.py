@@ -1,0 +1,25 @@
+"""MI355X-native screened density-fitted Coulomb (DF-J) for floating anisotropic Gaussian splats.
+
+A drop-in for the DF-J path of gs-dft: the ``df()`` / ``pairlist()`` plugin surface, the
+``SplatState`` refresh contract and ``ScreenedProductDFCoulomb.energy``, backed by hand-written
+HIP kernels for gfx950 in ``lib/libgsdft.so`` (C ABI declared in ``include/gsdft.h``).
+"""
+from .basis import IsotropicSplat, Splat, init_product_aux
+from .energy import SplatDFJ, SplatModel, SplatState, refresh, train_pad_to
+from .ri import (aux_cholesky, aux_metric, coulomb_pairs, df_coulomb_energy_screened,
+                 df_coulomb_gamma_screened, df_coulomb_solve, shift_diag)
+from .screening import (PairIndex, build_pair_index, count_significant, live_length,
+                        neighbor_pairs, pair_weight, screened_overlap_pairs)
+from .terms import (SCREEN_PAD, CoulombTerm, DFSpec, ExactSpec, Pairlist,
+                    ScreenedProductDFCoulomb, df, exact, pairlist)
+
+__all__ = [
+    "Splat", "IsotropicSplat", "init_product_aux",
+    "SplatDFJ", "SplatModel", "SplatState", "refresh", "train_pad_to",
+    "aux_metric", "aux_cholesky", "shift_diag", "df_coulomb_gamma_screened", "df_coulomb_solve",
+    "df_coulomb_energy_screened", "coulomb_pairs",
+    "neighbor_pairs", "count_significant", "pair_weight", "screened_overlap_pairs",
+    "PairIndex", "build_pair_index", "live_length",
+    "SCREEN_PAD", "CoulombTerm", "DFSpec", "ExactSpec", "Pairlist", "ScreenedProductDFCoulomb",
+    "df", "exact", "pairlist",
+]

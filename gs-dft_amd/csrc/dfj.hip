@@ -1,0 +1,880 @@
+// Density-fitted Coulomb: product aux, metric, Cholesky, solves, and the three-centre forward
+// (gamma) and reverse (J and every splat/C gradient) passes.
+//
+// Three-centre integral (gs_dft/coulomb/ri.py:126-151,167-185) between an isotropic aux P
+// (exponent b, centre R, norm KN_P) and a pair product (precision Ah, centre Pa, KN_a):
+//   (P|a) = KN_P KN_a pref sum_t w_t (prod_k Gamma_k)^(-1/2) exp(-t^2 sum_k W_k / Gamma_k)
+// with Gamma_k = b L_k + t^2 (b + L_k) over the eigenvalues L_k of Ah. The kernels never
+// diagonalise Ah: with a = b + t^2, c = t^2 b and s = c/a,
+//   prod_k Gamma_k   = a^3 Pn(s),   Pn(s) = I3 + s (I2 + s (I1 + s)),
+//   t^2 sum W/Gamma  = s Qn(s)/Pn(s), Qn(s) = I3 q0 + s ((I1 q1 - q2) + s q1),
+// where I1, I2, I3 are the trace, principal-minor sum and determinant of Ah and q0 = |d|^2,
+// q1 = d.Ah d, q2 = |Ah d|^2 for d = R - Pa (Cayley-Hamilton). So each node is
+//   f_t = wp_t Pn^(-1/2) exp(-s Qn / Pn),   wp_t = w_t a^(-3/2),
+// all positive terms, no eigh, and differentiable at degenerate Ah.
+//
+// Work decomposition (no atomics anywhere):
+//   forward  -- one lane per aux function P; a workgroup walks a slab of pairs whose records are
+//               wave-uniform (scalar loads); per-slab partial gamma is summed in fixed order.
+//   reverse  -- one lane per pair; the wave walks the aux functions (uniform node tables); each
+//               lane accumulates its pair's 25 cotangent moments in registers; per-pair results
+//               are mapped to per-splat gradients by wave-per-splat segmented sums over the CSR
+//               pair index.
+#include <rocblas/rocblas.h>
+#include <rocsolver/rocsolver.h>
+
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+#include "internal.h"
+
+namespace gsdft {
+
+namespace {
+
+constexpr int kRec = 16;      // doubles per pair record
+constexpr int kAuxRec = 48;   // doubles per aux record of the reverse pass
+constexpr int kAcc = 25;      // cotangent moments per pair
+
+inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+// ------------------------------------------------------------------ aux
+
+struct Scales {
+    double v[16];
+    int n;
+};
+
+// gs_dft/basis/isotropic.py:269-281, diagonal_only: the self-product of each splat.
+__global__ void k_product_aux(int64_t M, const double* __restrict__ quat,
+                              const double* __restrict__ log_scale,
+                              const double* __restrict__ centers, Scales sc,
+                              double* __restrict__ log_alpha, double* __restrict__ aux_centers) {
+    const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (m >= M) return;
+    Sym3 A, Ah;
+    double N, P[3], KN;
+    splat_chart(quat + 4 * m, log_scale + 3 * m, &A, &N);
+    const double mu[3] = {centers[3 * m], centers[3 * m + 1], centers[3 * m + 2]};
+    pair_quantities(A, A, mu, mu, N, N, &Ah, P, &KN);
+    const double alpha0 = pow(det3(Ah), 1.0 / 3.0);
+    for (int s = 0; s < sc.n; ++s) {
+        const int64_t o = (int64_t)s * M + m;
+        log_alpha[o] = log(alpha0 * sc.v[s]);
+        aux_centers[3 * o] = P[0];
+        aux_centers[3 * o + 1] = P[1];
+        aux_centers[3 * o + 2] = P[2];
+    }
+}
+
+// gs_dft/basis/isotropic.py:30-39: beta = e^log_alpha, KN = (2 beta / pi)^(3/4).
+__global__ void k_aux_prep(int64_t N, const double* __restrict__ log_alpha,
+                           double* __restrict__ beta, double* __restrict__ kn) {
+    const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (p >= N) return;
+    const double b = exp(log_alpha[p]);
+    beta[p] = b;
+    kn[p] = pow(2.0 * b / kPi, 0.75);
+}
+
+__device__ __forceinline__ double boys0(double T) {
+    if (T < 1e-12) return 1.0 - T / 3.0;
+    return 0.5 * sqrt(kPi / T) * erf(sqrt(T));
+}
+
+// gs_dft/coulomb/ri.py:63-76 (omega=None) + shift_diag. One thread per element; a block covers
+// 4 rows x 64 columns so each wave writes 64 consecutive doubles of one row.
+__global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restrict__ beta,
+                                                const double* __restrict__ kn,
+                                                const double* __restrict__ R, double lam,
+                                                double* __restrict__ V) {
+    const int64_t q = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int64_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (p >= N || q >= N) return;
+    const double g1 = beta[p], g2 = beta[q];
+    const double gab = g1 * g2;
+    const double gsum = g1 + g2;
+    const double dx = R[3 * p] - R[3 * q], dy = R[3 * p + 1] - R[3 * q + 1],
+                 dz = R[3 * p + 2] - R[3 * q + 2];
+    const double PQ2 = dx * dx + dy * dy + dz * dz;
+    const double rho = gab / gsum;
+    const double T = rho * PQ2;
+    const double coul = kTwoPi25 / (gab * sqrt(gsum)) * boys0(T);
+    double v = (kn[p] * kn[q]) * coul;
+    if (p == q) v += lam;
+    V[p * N + q] = v;
+}
+
+__global__ void k_zero_upper(int64_t N, double* __restrict__ V) {
+    const int64_t q = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int64_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (p >= N || q >= N || q <= p) return;
+    V[p * N + q] = 0.0;
+}
+
+// 0.5 * a.b in one block, fixed summation order.
+__global__ __launch_bounds__(1024) void k_half_dot(int64_t N, const double* __restrict__ a,
+                                                   const double* __restrict__ b,
+                                                   double* __restrict__ out) {
+    __shared__ double part[1024];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < N; i += 1024) s += a[i] * b[i];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = 0.5 * part[0];
+}
+
+// ------------------------------------------------------------------ pair records
+
+// q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456); G lanes per pair.
+template <int G>
+__global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* __restrict__ pi,
+                                                      const int32_t* __restrict__ pj,
+                                                      const double* __restrict__ weight, int64_t k,
+                                                      const double* __restrict__ C,
+                                                      const double* __restrict__ occ,
+                                                      double* __restrict__ q) {
+    const int64_t a = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / G;
+    const int l = threadIdx.x % G;
+    const bool live = a < n;
+    const int64_t i = live ? pi[a] : 0, j = live ? pj[a] : 0;
+    double s = 0.0;
+    if (live)
+        for (int64_t o = l; o < k; o += G) s += (occ[o] * C[i * k + o]) * C[j * k + o];
+    for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (live && l == 0) q[a] = weight[a] * s;
+}
+
+// Pair record: I1 I2 I3 | Ah (6) | Pa (3) | coef = KN q pref | KN | q | pad.
+__global__ void k_pair_rec(int64_t n, const int32_t* __restrict__ pi,
+                           const int32_t* __restrict__ pj, const double* __restrict__ A6,
+                           const double* __restrict__ mu, const double* __restrict__ Nrm,
+                           const double* __restrict__ q, double* __restrict__ rec) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    const int64_t i = pi[a], j = pj[a];
+    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
+    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
+    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
+    Sym3 Ah;
+    double P[3], KN;
+    pair_quantities(Ai, Aj, mui, muj, Nrm[i], Nrm[j], &Ah, P, &KN);
+    double* r = rec + kRec * a;
+    r[0] = Ah.xx + Ah.yy + Ah.zz;
+    r[1] = Ah.xx * Ah.yy + Ah.xx * Ah.zz + Ah.yy * Ah.zz - Ah.xy * Ah.xy - Ah.xz * Ah.xz
+         - Ah.yz * Ah.yz;
+    r[2] = det3(Ah);
+    r[3] = Ah.xx; r[4] = Ah.yy; r[5] = Ah.zz; r[6] = Ah.xy; r[7] = Ah.xz; r[8] = Ah.yz;
+    r[9] = P[0]; r[10] = P[1]; r[11] = P[2];
+    r[12] = KN * kPref3c * q[a];
+    r[13] = KN;
+    r[14] = q[a];
+    r[15] = 0.0;
+}
+
+// Node constants of one aux exponent b: s_t = t^2 b / (b + t^2), wp_t = w_t (b + t^2)^(-3/2).
+__device__ __forceinline__ void node_consts(double b, double s[kNodes], double wp[kNodes]) {
+#pragma unroll
+    for (int t = 0; t < kNodes; ++t) {
+        const double t2 = quad_t(t) * quad_t(t);
+        const double a = b + t2;
+        s[t] = t2 * b / a;
+        wp[t] = quad_w(t) / (a * sqrt(a));
+    }
+}
+
+// ------------------------------------------------------------------ forward
+
+__global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const double* __restrict__ beta,
+                                                   const double* __restrict__ R,
+                                                   const double* __restrict__ kn, int64_t n,
+                                                   const double* __restrict__ rec,
+                                                   int64_t per_slab,
+                                                   double* __restrict__ partial) {
+    const int64_t P = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = P < N;
+    const double b = live ? beta[P] : 1.0;
+    const double Rx = live ? R[3 * P] : 0.0, Ry = live ? R[3 * P + 1] : 0.0,
+                 Rz = live ? R[3 * P + 2] : 0.0;
+    double s[kNodes], wp[kNodes];
+    node_consts(b, s, wp);
+    const int64_t a0 = blockIdx.y * per_slab;
+    const int64_t a1 = min(n, a0 + per_slab);
+    double acc = 0.0;
+    for (int64_t a = a0; a < a1; ++a) {
+        const double* __restrict__ r = rec + kRec * a;
+        const double I1 = r[0], I2 = r[1], I3 = r[2];
+        const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
+        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
+        const double coef = r[12];
+        const double ax = xx * dx + xy * dy + xz * dz;
+        const double ay = xy * dx + yy * dy + yz * dz;
+        const double az = xz * dx + yz * dy + zz * dz;
+        const double q0 = dx * dx + dy * dy + dz * dz;
+        const double q1 = dx * ax + dy * ay + dz * az;
+        const double q2 = ax * ax + ay * ay + az * az;
+        const double X0 = I3 * q0;
+        const double rr = I1 * q1 - q2;
+        double F = 0.0;
+#pragma unroll
+        for (int t = 0; t < kNodes; ++t) {
+            const double st = s[t];
+            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
+            const double y = rsqrt_nr(Pn);
+            const double e = exp_fast(-(st * Qn) * (y * y));
+            F = __builtin_fma(wp[t] * y, e, F);
+        }
+        acc = __builtin_fma(F, coef, acc);
+    }
+    if (live) partial[blockIdx.y * N + P] = acc * kn[P];
+}
+
+__global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ partial,
+                           double* __restrict__ out) {
+    const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (p >= N) return;
+    double s = 0.0;
+    for (int64_t k = 0; k < slabs; ++k) s += partial[k * N + p];
+    out[p] = s;
+}
+
+// ------------------------------------------------------------------ reverse
+
+// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | pad (3) | s_t (20) | wp_t (20).
+__global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
+                               const double* __restrict__ kn, const double* __restrict__ R,
+                               const double* __restrict__ dgamma,
+                               const double* __restrict__ dscale, double* __restrict__ out) {
+    const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (p >= N) return;
+    const double b = beta[p];
+    double s[kNodes], wp[kNodes];
+    node_consts(b, s, wp);
+    double* o = out + kAuxRec * p;
+    o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
+    o[3] = dgamma[p] * (dscale ? *dscale : 1.0) * kn[p];
+    o[4] = b; o[5] = 0.0; o[6] = 0.0; o[7] = 0.0;
+    for (int t = 0; t < kNodes; ++t) { o[8 + t] = s[t]; o[28 + t] = wp[t]; }
+}
+
+// One lane per pair; accumulates over a slab of aux functions
+//   jt = sum u F,  T1/T2/T3 = sum u dF/dI1,I2,I3 (through Pn and Qn),
+//   Vc = sum u dQ0 d, Va = sum u dQ1 d, Vb = sum u dQ2 d, Sa = sum u dQ1 d d^T, Sb = sum u dQ2 d d^T
+// where dQk = sum_t (df/dQn) s^k and df/dQn = -f s / Pn.
+__global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __restrict__ rec,
+                                                   int64_t N, const double* __restrict__ aux,
+                                                   int64_t per_slab,
+                                                   double* __restrict__ partial) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = a < n;
+    const double* __restrict__ r = rec + kRec * (live ? a : 0);
+    const double I1 = r[0], I2 = r[1], I3 = r[2];
+    const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
+    const double Px = r[9], Py = r[10], Pz = r[11];
+    double jt = 0, T1 = 0, T2 = 0, T3 = 0;
+    double Vc[3] = {0, 0, 0}, Va[3] = {0, 0, 0}, Vb[3] = {0, 0, 0};
+    double Sa[6] = {0, 0, 0, 0, 0, 0}, Sb[6] = {0, 0, 0, 0, 0, 0};
+    const int64_t p0 = blockIdx.y * per_slab;
+    const int64_t p1 = min(N, p0 + per_slab);
+    for (int64_t p = p0; p < p1; ++p) {
+        const double* __restrict__ x = aux + kAuxRec * p;
+        const double u = x[3];
+        const double d[3] = {x[0] - Px, x[1] - Py, x[2] - Pz};
+        const double ax = xx * d[0] + xy * d[1] + xz * d[2];
+        const double ay = xy * d[0] + yy * d[1] + yz * d[2];
+        const double az = xz * d[0] + yz * d[1] + zz * d[2];
+        const double q0 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+        const double q1 = d[0] * ax + d[1] * ay + d[2] * az;
+        const double q2 = ax * ax + ay * ay + az * az;
+        const double X0 = I3 * q0;
+        const double rr = I1 * q1 - q2;
+        double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, dQ0 = 0, dQ1 = 0, dQ2 = 0;
+#pragma unroll
+        for (int t = 0; t < kNodes; ++t) {
+            const double st = x[8 + t];
+            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
+            const double y = rsqrt_nr(Pn);
+            const double y2 = y * y;
+            const double arg = -(st * Qn) * y2;
+            const double f = x[28 + t] * y * exp_fast(arg);
+            F += f;
+            const double fy2 = f * y2;
+            const double fP = fy2 * (-arg - 0.5);       // df/dPn
+            const double fQ = -fy2 * st;                // df/dQn
+            const double fPs = fP * st, fQs = fQ * st;
+            dP0 += fP;
+            dP1 += fPs;
+            dP2 = __builtin_fma(fPs, st, dP2);
+            dQ0 += fQ;
+            dQ1 += fQs;
+            dQ2 = __builtin_fma(fQs, st, dQ2);
+        }
+        jt = __builtin_fma(u, F, jt);
+        T3 = __builtin_fma(u, __builtin_fma(q0, dQ0, dP0), T3);
+        T2 = __builtin_fma(u, dP1, T2);
+        T1 = __builtin_fma(u, __builtin_fma(q1, dQ1, dP2), T1);
+        const double c0 = u * dQ0, c1 = u * dQ1, c2 = u * dQ2;
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            Vc[m] = __builtin_fma(c0, d[m], Vc[m]);
+            const double e1 = c1 * d[m], e2 = c2 * d[m];
+            Va[m] += e1;
+            Vb[m] += e2;
+        }
+        const double e1x = c1 * d[0], e1y = c1 * d[1], e1z = c1 * d[2];
+        const double e2x = c2 * d[0], e2y = c2 * d[1], e2z = c2 * d[2];
+        Sa[0] = __builtin_fma(e1x, d[0], Sa[0]);
+        Sa[1] = __builtin_fma(e1y, d[1], Sa[1]);
+        Sa[2] = __builtin_fma(e1z, d[2], Sa[2]);
+        Sa[3] = __builtin_fma(e1x, d[1], Sa[3]);
+        Sa[4] = __builtin_fma(e1x, d[2], Sa[4]);
+        Sa[5] = __builtin_fma(e1y, d[2], Sa[5]);
+        Sb[0] = __builtin_fma(e2x, d[0], Sb[0]);
+        Sb[1] = __builtin_fma(e2y, d[1], Sb[1]);
+        Sb[2] = __builtin_fma(e2z, d[2], Sb[2]);
+        Sb[3] = __builtin_fma(e2x, d[1], Sb[3]);
+        Sb[4] = __builtin_fma(e2x, d[2], Sb[4]);
+        Sb[5] = __builtin_fma(e2y, d[2], Sb[5]);
+    }
+    if (!live) return;
+    double* o = partial + (int64_t)blockIdx.y * kAcc * n + a;
+    const double v[kAcc] = {jt, T1, T2, T3, Vc[0], Vc[1], Vc[2], Va[0], Va[1], Va[2],
+                            Vb[0], Vb[1], Vb[2], Sa[0], Sa[1], Sa[2], Sa[3], Sa[4], Sa[5],
+                            Sb[0], Sb[1], Sb[2], Sb[3], Sb[4], Sb[5]};
+#pragma unroll
+    for (int c = 0; c < kAcc; ++c) o[(int64_t)c * n] = v[c];
+}
+
+__device__ __forceinline__ void sym_mul(const double A[6], const double B[6], double M[9]) {
+    // full product of two symmetric matrices in slot form
+    const double a[9] = {A[0], A[3], A[4], A[3], A[1], A[5], A[4], A[5], A[2]};
+    const double b[9] = {B[0], B[3], B[4], B[3], B[1], B[5], B[4], B[5], B[2]};
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c)
+            M[3 * r + c] = a[3 * r] * b[c] + a[3 * r + 1] * b[3 + c] + a[3 * r + 2] * b[6 + c];
+}
+
+__device__ __forceinline__ void sym_vec(const double A[6], const double x[3], double y[3]) {
+    y[0] = A[0] * x[0] + A[3] * x[1] + A[4] * x[2];
+    y[1] = A[3] * x[0] + A[1] * x[1] + A[5] * x[2];
+    y[2] = A[4] * x[0] + A[5] * x[1] + A[2] * x[2];
+}
+
+// Per pair: sum the slab moments, map them to dE/dAh, dE/dPa, dE/dKN_a, then through
+// gs_dft/coulomb/stream.py:203-215 to the two splats. Writes J and 20 contributions (SoA):
+//   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
+__global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restrict__ pi,
+                                const int32_t* __restrict__ pj,
+                                const double* __restrict__ weight,
+                                const double* __restrict__ A6, const double* __restrict__ mu,
+                                const double* __restrict__ Nrm, const double* __restrict__ rec,
+                                const double* __restrict__ partial, double* __restrict__ J,
+                                double* __restrict__ contrib) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    if (weight[a] == 0.0) {
+        J[a] = 0.0;
+        for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
+        return;
+    }
+    double m[kAcc];
+    for (int c = 0; c < kAcc; ++c) {
+        double s = 0.0;
+        for (int64_t k = 0; k < slabs; ++k) s += partial[(k * kAcc + c) * n + a];
+        m[c] = s;
+    }
+    const double* r = rec + kRec * a;
+    const double I1 = r[0], I3 = r[2];
+    const double Ah[6] = {r[3], r[4], r[5], r[6], r[7], r[8]};
+    const double KN = r[13], q = r[14];
+    const double jt = m[0], T1 = m[1], T2 = m[2], T3 = m[3];
+    const double* Vc = m + 4;
+    const double* Va = m + 7;
+    const double* Vb = m + 10;
+    const double* Sa = m + 13;
+    const double* Sb = m + 19;
+    const double scale = q * KN * kPref3c;
+    J[a] = KN * kPref3c * jt;
+    const double gKN = q * kPref3c * jt;
+    // dE/dPa = -2 scale (I3 Vc + Ah (I1 Va + Vb) - Ah (Ah Va))
+    double w1[3] = {I1 * Va[0] + Vb[0], I1 * Va[1] + Vb[1], I1 * Va[2] + Vb[2]};
+    double t1[3], t2[3], t3[3];
+    sym_vec(Ah, w1, t1);
+    sym_vec(Ah, Va, t2);
+    sym_vec(Ah, t2, t3);
+    double gP[3];
+    for (int k = 0; k < 3; ++k) gP[k] = -2.0 * scale * (I3 * Vc[k] + t1[k] - t3[k]);
+    // dE/dAh = scale ((I1 Sa + Sb) - (Ah Sa + Sa Ah) + T1 I + T2 (I1 I - Ah) + T3 adj(Ah))
+    double AS[9];
+    sym_mul(Ah, Sa, AS);
+    const Sym3 AhS{Ah[0], Ah[1], Ah[2], Ah[3], Ah[4], Ah[5]};
+    double adj[9];
+    adj3(AhS, adj);
+    const int rr_[6] = {0, 1, 2, 0, 0, 1}, cc_[6] = {0, 1, 2, 1, 2, 2};
+    double Gh[6];
+    for (int k = 0; k < 6; ++k) {
+        const int rw = rr_[k], cl = cc_[k];
+        const double eye = (rw == cl) ? 1.0 : 0.0;
+        Gh[k] = scale * ((I1 * Sa[k] + Sb[k]) - (AS[3 * rw + cl] + AS[3 * cl + rw]) + T1 * eye
+                         + T2 * (I1 * eye - Ah[k]) + T3 * adj[3 * rw + cl]);
+    }
+    // ---- gs_dft/coulomb/stream.py:203-215 reverse
+    const int64_t i = pi[a], j = pj[a];
+    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
+    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
+    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
+    const double Ni = Nrm[i], Nj = Nrm[j];
+    Sym3 Ahp;
+    double Pc[3], KNp;
+    pair_quantities(Ai, Aj, mui, muj, Ni, Nj, &Ahp, Pc, &KNp);
+    double Gi[6] = {0, 0, 0, 0, 0, 0}, Gj[6] = {0, 0, 0, 0, 0, 0};
+    double gmi[3] = {0, 0, 0}, gmj[3] = {0, 0, 0};
+    // KN = N_i N_j K, K = exp(-e), e = d . Ai Ah^-1 Aj d
+    const double d[3] = {mui[0] - muj[0], mui[1] - muj[1], mui[2] - muj[2]};
+    double Ajd[3], Aid[3], u[3], v[3], Aiu[3], Ajv[3];
+    matvec(Aj, d, Ajd);
+    matvec(Ai, d, Aid);
+    solve3(Ahp, Ajd, u);
+    solve3(Ahp, Aid, v);
+    matvec(Ai, u, Aiu);
+    matvec(Aj, v, Ajv);
+    const double e = d[0] * Aiu[0] + d[1] * Aiu[1] + d[2] * Aiu[2];
+    const double K = exp(-e);
+    const double gNi = gKN * Nj * K, gNj = gKN * Ni * K;
+    const double ge = -gKN * KNp;
+    for (int k = 0; k < 3; ++k) {
+        const double gd = ge * (Aiu[k] + Ajv[k]);
+        gmi[k] += gd;
+        gmj[k] -= gd;
+    }
+    add_sym_outer(Gi, ge, d, u);
+    add_sym_outer(Gj, ge, v, d);
+    add_sym_outer(Gh, -ge, v, u);
+    // P = Ah^-1 (Ai mu_i + Aj mu_j)
+    double y[3];
+    solve3(Ahp, gP, y);
+    add_sym_outer(Gh, -1.0, y, Pc);
+    add_sym_outer(Gi, 1.0, y, mui);
+    add_sym_outer(Gj, 1.0, y, muj);
+    double Aiy[3], Ajy[3];
+    matvec(Ai, y, Aiy);
+    matvec(Aj, y, Ajy);
+    for (int k = 0; k < 3; ++k) { gmi[k] += Aiy[k]; gmj[k] += Ajy[k]; }
+    // Ah = Ai + Aj
+    for (int k = 0; k < 6; ++k) { Gi[k] += Gh[k]; Gj[k] += Gh[k]; }
+    double out[20];
+    for (int k = 0; k < 6; ++k) { out[k] = Gi[k]; out[10 + k] = Gj[k]; }
+    for (int k = 0; k < 3; ++k) { out[6 + k] = gmi[k]; out[16 + k] = gmj[k]; }
+    out[9] = gNi;
+    out[19] = gNj;
+    for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = out[c];
+}
+
+// One wave per splat: deterministic segmented sums of the i-side and j-side contributions, then
+// the chart reverse (gs_dft/basis/spectral.py:33-40,72-82).
+__global__ __launch_bounds__(256) void k_splat_grad(
+    int64_t M, int64_t n, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ row_perm,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ col_perm,
+    const double* __restrict__ contrib, const double* __restrict__ quat,
+    const double* __restrict__ log_scale, double* __restrict__ dquat,
+    double* __restrict__ dlog_scale, double* __restrict__ dcenters) {
+    const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (m >= M) return;
+    double acc[10];
+    for (int c = 0; c < 10; ++c) acc[c] = 0.0;
+    for (int64_t p = row_ptr[m] + lane; p < row_ptr[m + 1]; p += 64) {
+        const int64_t a = row_perm[p];
+        for (int c = 0; c < 10; ++c) acc[c] += contrib[(int64_t)c * n + a];
+    }
+    for (int64_t p = col_ptr[m] + lane; p < col_ptr[m + 1]; p += 64) {
+        const int64_t a = col_perm[p];
+        for (int c = 0; c < 10; ++c) acc[c] += contrib[(int64_t)(10 + c) * n + a];
+    }
+    for (int c = 0; c < 10; ++c) acc[c] = wave_sum(acc[c]);
+    if (lane != 0) return;
+    const double* q = quat + 4 * m;
+    const double* l = log_scale + 3 * m;
+    double R[9], qn[4], nrm;
+    quat_rotation(q, R, qn, &nrm);
+    const double av[3] = {exp(l[0]), exp(l[1]), exp(l[2])};
+    const double Nm = pow(8.0 * exp(l[0] + l[1] + l[2]) / kPi3, 0.25);
+    const double G[9] = {acc[0], acc[3], acc[4], acc[3], acc[1], acc[5], acc[4], acc[5], acc[2]};
+    double GR[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c)
+            GR[3 * r + c] = G[3 * r] * R[c] + G[3 * r + 1] * R[3 + c] + G[3 * r + 2] * R[6 + c];
+    for (int jx = 0; jx < 3; ++jx) {
+        const double ga = R[jx] * GR[jx] + R[3 + jx] * GR[3 + jx] + R[6 + jx] * GR[6 + jx];
+        dlog_scale[3 * m + jx] = av[jx] * ga + acc[9] * Nm * 0.25;
+    }
+    double gR[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) gR[3 * r + c] = 2.0 * av[c] * GR[3 * r + c];
+    const double w = qn[0], x = qn[1], yq = qn[2], z = qn[3];
+    const double gqn[4] = {
+        2 * (-z * gR[1] + yq * gR[2] + z * gR[3] - x * gR[5] - yq * gR[6] + x * gR[7]),
+        2 * (yq * gR[1] + z * gR[2] + yq * gR[3] - 2 * x * gR[4] - w * gR[5] + z * gR[6]
+             + w * gR[7] - 2 * x * gR[8]),
+        2 * (-2 * yq * gR[0] + x * gR[1] + w * gR[2] + x * gR[3] + z * gR[5] - w * gR[6]
+             + z * gR[7] - 2 * yq * gR[8]),
+        2 * (-2 * z * gR[0] - w * gR[1] + x * gR[2] + w * gR[3] - 2 * z * gR[4] + yq * gR[5]
+             + x * gR[6] + yq * gR[7])};
+    const double den = nrm + 1e-12;
+    const double dot = q[0] * gqn[0] + q[1] * gqn[1] + q[2] * gqn[2] + q[3] * gqn[3];
+    for (int t = 0; t < 4; ++t) dquat[4 * m + t] = gqn[t] / den - q[t] * dot / (nrm * den * den);
+    for (int t = 0; t < 3; ++t) dcenters[3 * m + t] = acc[6 + t];
+}
+
+// dE/dC_mo = occ_o [sum_{a: i_a=m} J_a w_a C_{j_a o} + sum_{a: j_a=m} J_a w_a C_{i_a o}]
+// (gs_dft/coulomb/ri.py:456 reverse); one wave per splat, lanes over o.
+__global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
+                                            const int32_t* __restrict__ row_ptr,
+                                            const int32_t* __restrict__ row_perm,
+                                            const int32_t* __restrict__ col_ptr,
+                                            const int32_t* __restrict__ col_perm,
+                                            const int32_t* __restrict__ pi,
+                                            const int32_t* __restrict__ pj,
+                                            const double* __restrict__ J,
+                                            const double* __restrict__ weight,
+                                            const double* __restrict__ C,
+                                            const double* __restrict__ occ,
+                                            double* __restrict__ dC) {
+    const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (m >= M) return;
+    const int64_t r0 = row_ptr[m], r1 = row_ptr[m + 1], c0 = col_ptr[m], c1 = col_ptr[m + 1];
+    for (int64_t o0 = 0; o0 < k; o0 += 64) {
+        const int64_t o = o0 + lane;
+        const bool on = o < k;
+        double acc = 0.0;
+        for (int64_t p = r0; p < r1; ++p) {
+            const int64_t a = row_perm[p];
+            const double s = J[a] * weight[a];
+            if (on) acc = __builtin_fma(s, C[(int64_t)pj[a] * k + o], acc);
+        }
+        for (int64_t p = c0; p < c1; ++p) {
+            const int64_t a = col_perm[p];
+            const double s = J[a] * weight[a];
+            if (on) acc = __builtin_fma(s, C[(int64_t)pi[a] * k + o], acc);
+        }
+        if (on) dC[m * k + o] = occ[o] * acc;
+    }
+}
+
+// ------------------------------------------------------------------ work split
+
+struct Split {
+    int64_t slabs;
+    int64_t per_slab;
+};
+
+// Forward: ceil(N/256) workgroups per slab; aim for ~16 resident rounds of 4 waves per SIMD.
+Split fwd_split(int64_t N, int64_t n) {
+    const int64_t groups = (N + 255) / 256;
+    const int64_t target = 256 * 4 * 16;                   // workgroups (of 4 waves) wanted
+    int64_t slabs = (target + groups - 1) / groups;
+    slabs = slabs < 1 ? 1 : slabs;
+    const int64_t max_slabs = (n + 7) / 8;                  // at least 8 pairs per slab
+    if (slabs > max_slabs) slabs = max_slabs < 1 ? 1 : max_slabs;
+    if (slabs > 65535) slabs = 65535;
+    const int64_t per = (n + slabs - 1) / slabs;
+    return Split{(n + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
+}
+
+Split bwd_split(int64_t N, int64_t n) {
+    const int64_t groups = (n + 255) / 256;
+    const int64_t target = 256 * 4 * 4;
+    int64_t slabs = (target + groups - 1) / groups;
+    slabs = slabs < 1 ? 1 : slabs;
+    const int64_t max_slabs = (N + 15) / 16;
+    if (slabs > max_slabs) slabs = max_slabs < 1 ? 1 : max_slabs;
+    if (slabs > 65535) slabs = 65535;
+    const int64_t per = (N + slabs - 1) / slabs;
+    return Split{(N + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
+}
+
+struct GammaWs {
+    double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
+    double *aux, *acc, *contrib;
+};
+
+int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, GammaWs* w) {
+    w->A6 = ar.take<double>(6 * M + 1);
+    w->Nrm = ar.take<double>(M + 1);
+    w->beta = ar.take<double>(N + 1);
+    w->kn = ar.take<double>(N + 1);
+    w->q = ar.take<double>(n + 1);
+    w->rec = ar.take<double>(kRec * n + kRec);
+    w->partial = w->aux = w->acc = w->contrib = nullptr;
+    if (!reverse) {
+        const Split sp = fwd_split(N, n);
+        w->partial = ar.take<double>(sp.slabs * N + 1);
+    } else {
+        const Split sp = bwd_split(N, n);
+        w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
+        w->acc = ar.take<double>(sp.slabs * kAcc * n + 1);
+        w->contrib = ar.take<double>(20 * n + 1);
+    }
+    return GSDFT_OK;
+}
+
+int launch_pair_density(int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                        int64_t k, const double* C, const double* occ, double* q, hipStream_t s) {
+    if (n <= 0) return GSDFT_OK;
+    if (k <= 8) {
+        k_pair_density<8><<<blocks_for(n * 8, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+    } else if (k <= 16) {
+        k_pair_density<16><<<blocks_for(n * 16, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+    } else if (k <= 32) {
+        k_pair_density<32><<<blocks_for(n * 32, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+    } else {
+        k_pair_density<64><<<blocks_for(n * 64, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+    }
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+// Shared prologue of forward and reverse: chart, aux quantities, pair density, pair records.
+int gamma_prologue(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                   int64_t k, const double* C, const double* occ, int64_t N,
+                   const double* log_alpha, int64_t n, const int32_t* pi, const int32_t* pj,
+                   const double* weight, GammaWs& w, hipStream_t s) {
+    GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
+    k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
+    GSDFT_HIP(hipGetLastError());
+    if (n > 0) {
+        GSDFT_TRY(launch_pair_density(n, pi, pj, weight, k, C, occ, w.q, s));
+        k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec);
+        GSDFT_HIP(hipGetLastError());
+    }
+    return GSDFT_OK;
+}
+
+// rocBLAS handle per device.
+std::mutex g_blas_mu;
+std::vector<rocblas_handle> g_blas;
+
+int blas_handle(hipStream_t s, rocblas_handle* out) {
+    int dev = 0;
+    GSDFT_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_blas_mu);
+    if ((int)g_blas.size() <= dev) g_blas.resize(dev + 1, nullptr);
+    if (!g_blas[dev]) {
+        if (rocblas_create_handle(&g_blas[dev]) != rocblas_status_success)
+            return fail(GSDFT_ERR_LIB, "rocblas_create_handle failed");
+    }
+    if (rocblas_set_stream(g_blas[dev], s) != rocblas_status_success)
+        return fail(GSDFT_ERR_LIB, "rocblas_set_stream failed");
+    *out = g_blas[dev];
+    return GSDFT_OK;
+}
+
+}  // namespace
+
+}  // namespace gsdft
+
+using namespace gsdft;
+
+extern "C" int gsdft_product_aux(int64_t M, const double* quat, const double* log_scale,
+                                 const double* centers, const double* scales, int n_scales,
+                                 double* log_alpha, double* aux_centers, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    if (M <= 0 || n_scales <= 0 || n_scales > 16 || !scales)
+        return fail(GSDFT_ERR_ARG, "gsdft_product_aux: need 1..16 scales and M > 0");
+    Scales sc{};
+    sc.n = n_scales;
+    for (int i = 0; i < n_scales; ++i) sc.v[i] = scales[i];
+    hipStream_t s = (hipStream_t)stream;
+    k_product_aux<<<blocks_for(M, 256), 256, 0, s>>>(M, quat, log_scale, centers, sc, log_alpha,
+                                                      aux_centers);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
+    if (N < 0 || !bytes) return fail(GSDFT_ERR_ARG, "metric_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    ar.take<double>(2 * N + 2);
+    ar.take<int>(4);
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double* aux_centers,
+                                double lam, double* V, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    if (N <= 0 || !log_alpha || !aux_centers || !V)
+        return fail(GSDFT_ERR_ARG, "gsdft_aux_metric: bad arguments");
+    if ((N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_aux_metric: N too large");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    double* bk = ar.take<double>(2 * N + 2);
+    if (!bk) return fail(GSDFT_ERR_WORKSPACE, "gsdft_aux_metric: workspace too small");
+    k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
+    profile_begin(kProfMetric, s);
+    k_metric<<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, V);
+    profile_end(kProfMetric, s);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+    if (N <= 0 || !V) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: bad arguments");
+    if (N > 2147483647 || (N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: N too large");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    ar.take<double>(2 * N + 2);
+    int* info = ar.take<int>(4);
+    if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_cholesky: workspace too small");
+    rocblas_handle h;
+    GSDFT_TRY(blas_handle(s, &h));
+    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle.
+    profile_begin(kProfCholesky, s);
+    rocblas_status st = rocsolver_dpotrf(h, rocblas_fill_upper, (rocblas_int)N, V, (rocblas_int)N,
+                                         info);
+    profile_end(kProfCholesky, s);
+    if (st != rocblas_status_success)
+        return fail(GSDFT_ERR_LIB, "rocsolver_dpotrf failed (status %d)", (int)st);
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
+    k_zero_upper<<<grid, 256, 0, s>>>(N, V);
+    GSDFT_HIP(hipGetLastError());
+    int h_info = 0;
+    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int), hipMemcpyDeviceToHost, s));
+    GSDFT_HIP(hipStreamSynchronize(s));
+    if (h_info != 0)
+        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %d of V + lam I is not positive "
+                    "definite", h_info);
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, double* d,
+                               double* energy, void* stream) {
+    if (N <= 0 || !L || !gamma || !d) return fail(GSDFT_ERR_ARG, "gsdft_cho_solve: bad arguments");
+    hipStream_t s = (hipStream_t)stream;
+    rocblas_handle h;
+    GSDFT_TRY(blas_handle(s, &h));
+    GSDFT_HIP(hipMemcpyAsync(d, gamma, sizeof(double) * N, hipMemcpyDeviceToDevice, s));
+    profile_begin(kProfSolve, s);
+    // column-major view of row-major L is U = L^T: L y = g is U^T y = g, then L^T d = y is U d = y
+    rocblas_status st = rocblas_dtrsv(h, rocblas_fill_upper, rocblas_operation_transpose,
+                                      rocblas_diagonal_non_unit, (rocblas_int)N, L,
+                                      (rocblas_int)N, d, 1);
+    if (st == rocblas_status_success)
+        st = rocblas_dtrsv(h, rocblas_fill_upper, rocblas_operation_none,
+                           rocblas_diagonal_non_unit, (rocblas_int)N, L, (rocblas_int)N, d, 1);
+    profile_end(kProfSolve, s);
+    if (st != rocblas_status_success)
+        return fail(GSDFT_ERR_LIB, "rocblas_dtrsv failed (status %d)", (int)st);
+    if (energy) {
+        k_half_dot<<<1, 1024, 0, s>>>(N, gamma, d, energy);
+        GSDFT_HIP(hipGetLastError());
+    }
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_gamma_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n,
+                                          size_t* bytes) {
+    (void)k;
+    if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    GammaWs w;
+    layout_gamma(ar, M, N, n, false, &w);
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n,
+                                              size_t* bytes) {
+    (void)k;
+    if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_vjp_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    GammaWs w;
+    layout_gamma(ar, M, N, n, true, &w);
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t k, const double* C, const double* occ,
+                           int64_t N, const double* log_alpha, const double* aux_centers,
+                           int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                           double* gamma, void* workspace, size_t workspace_bytes, void* stream) {
+    if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma: bad arguments");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    GammaWs w;
+    layout_gamma(ar, M, N, n, false, &w);
+    if (!w.partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_gamma: workspace too small");
+    if (n == 0) {
+        GSDFT_HIP(hipMemsetAsync(gamma, 0, sizeof(double) * N, s));
+        return GSDFT_OK;
+    }
+    GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
+                             weight, w, s));
+    const Split sp = fwd_split(N, n);
+    dim3 grid((unsigned)((N + 255) / 256), (unsigned)sp.slabs);
+    profile_begin(kProfGammaFwd, s);
+    k_gamma_fwd<<<grid, 256, 0, s>>>(N, w.beta, aux_centers, w.kn, n, w.rec, sp.per_slab,
+                                     w.partial);
+    profile_end(kProfGammaFwd, s);
+    GSDFT_HIP(hipGetLastError());
+    k_slab_sum<<<blocks_for(N, 256), 256, 0, s>>>(N, sp.slabs, w.partial, gamma);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,
+                               const double* centers, int64_t k, const double* C,
+                               const double* occ, int64_t N, const double* log_alpha,
+                               const double* aux_centers, int64_t n, const int32_t* pi,
+                               const int32_t* pj, const double* weight, const int32_t* row_ptr,
+                               const int32_t* row_perm, const int32_t* col_ptr,
+                               const int32_t* col_perm, const double* dgamma,
+                               const double* dgamma_scale, double* J, double* dquat,
+                               double* dlog_scale, double* dcenters, double* dC, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !dgamma || !dquat || !dlog_scale || !dcenters ||
+        !dC || !row_ptr || !col_ptr || (n > 0 && (!J || !row_perm || !col_perm)))
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma_vjp: bad arguments");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    GammaWs w;
+    layout_gamma(ar, M, N, n, true, &w);
+    if (!w.contrib) return fail(GSDFT_ERR_WORKSPACE, "gsdft_gamma_vjp: workspace too small");
+    GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
+                             weight, w, s));
+    if (n > 0) {
+        k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, w.beta, w.kn, aux_centers, dgamma,
+                                                          dgamma_scale, w.aux);
+        const Split sp = bwd_split(N, n);
+        dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+        profile_begin(kProfGammaBwd, s);
+        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec, N, w.aux, sp.per_slab, w.acc);
+        profile_end(kProfGammaBwd, s);
+        GSDFT_HIP(hipGetLastError());
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, pi, pj, weight, w.A6,
+                                                           centers, w.Nrm, w.rec, w.acc, J,
+                                                           w.contrib);
+        GSDFT_HIP(hipGetLastError());
+    }
+    k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
+                                                         col_perm, w.contrib, quat, log_scale,
+                                                         dquat, dlog_scale, dcenters);
+    k_dC<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi,
+                                                 pj, J, weight, C, occ, dC);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}

@@ -1,0 +1,52 @@
+// Host-side launchers shared between the translation units of libgsdft.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/gsdft.h"
+
+namespace gsdft {
+
+// Error reporting: a thread-local message behind gsdft_last_error().
+int fail(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+
+#define GSDFT_HIP(call)                                                   \
+    do {                                                                  \
+        hipError_t e_ = (call);                                           \
+        if (e_ != hipSuccess) return ::gsdft::hip_fail(e_, #call);        \
+    } while (0)
+
+#define GSDFT_TRY(call)                                                   \
+    do {                                                                  \
+        int rc_ = (call);                                                 \
+        if (rc_ != GSDFT_OK) return rc_;                                  \
+    } while (0)
+
+// Bump allocator over a caller-provided workspace (256-byte aligned slices).
+struct Arena {
+    char* base;
+    size_t cap;
+    size_t used;
+    template <class T>
+    T* take(size_t count) {
+        size_t off = (used + 255) & ~size_t(255);
+        used = off + count * sizeof(T);
+        return (base && used <= cap) ? reinterpret_cast<T*>(base + off) : nullptr;
+    }
+    size_t need() const { return (used + 255) & ~size_t(255); }
+};
+
+// Optional per-kernel timing with HIP events on the launch stream.
+void profile_begin(int id, hipStream_t s);
+void profile_end(int id, hipStream_t s);
+enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMetric = 3,
+                 kProfCholesky = 4, kProfSolve = 5, kProfCount = 6 };
+
+// chart_screen.hip
+int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,
+                 hipStream_t s);
+
+}  // namespace gsdft

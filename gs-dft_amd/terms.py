@@ -1,0 +1,132 @@
+"""The Coulomb plugin surface of the screened DF-J path, mirroring gs_dft/ks/terms.py.
+
+``df()`` and ``pairlist()`` build the same frozen spec values as the reference
+(terms.py:58-139) and ``_make_coulomb`` resolves ``df()`` + ``screen=pairlist(...)`` to
+``ScreenedProductDFCoulomb``, whose ``energy`` has the reference signature
+``energy(basis, C_orth, P, occ, state) -> (E_J, E_K)`` (terms.py:146-169,236-256).
+"""
+from __future__ import annotations
+
+import abc
+from dataclasses import dataclass
+
+import torch
+
+from . import ri as _cdf
+
+
+@dataclass(frozen=True)
+class ExactSpec:
+    """Exact streamed-ERI Coulomb backend (gs_dft/ks/terms.py:48-55). Accepted as a spec value;
+    the exact path is not part of this library, so resolving it raises."""
+
+    chunk: int | None = None
+
+
+@dataclass(frozen=True)
+class DFSpec:
+    """Frozen pair-product density-fitting backend (gs_dft/ks/terms.py:58-65)."""
+
+    scales: tuple = (1.0,)
+    diagonal: bool = True
+    lam: float = 1e-8
+    chunk: int = 2048
+
+
+SCREEN_PAD = 2.0
+"""Default pair-list pad multiplier (gs_dft/ks/terms.py:68)."""
+
+
+@dataclass(frozen=True)
+class Pairlist:
+    """Significant-overlap pair screening spec (gs_dft/ks/terms.py:73-89)."""
+
+    eps: float = 1e-7
+    pad: float = SCREEN_PAD
+    unique: bool = False
+    skip_pad: bool = False
+
+
+def exact(*, chunk: int | None = None) -> ExactSpec:
+    return ExactSpec(chunk=chunk)
+
+
+def df(*, scales: tuple = (1.0,), diagonal: bool = True, lam: float = 1e-8,
+       chunk: int = 2048) -> DFSpec:
+    """Density-fitted Coulomb on the frozen self-product aux (gs_dft/ks/terms.py:108-124)."""
+    if not scales:
+        raise ValueError("df(scales=...) needs at least one exponent scale.")
+    return DFSpec(scales=tuple(float(s) for s in scales), diagonal=bool(diagonal),
+                  lam=float(lam), chunk=int(chunk))
+
+
+def pairlist(eps: float = 1e-7, *, pad: float = SCREEN_PAD, unique: bool = False,
+             skip_pad: bool = False) -> Pairlist:
+    """Screen to the pairs with |S_ij| > eps (gs_dft/ks/terms.py:127-139)."""
+    return Pairlist(eps=float(eps), pad=float(pad), unique=bool(unique), skip_pad=bool(skip_pad))
+
+
+class CoulombTerm(abc.ABC):
+    """``(E_J, E_K)`` of a splat density (gs_dft/ks/terms.py:146-177)."""
+
+    hf_coeff: float = 0.0
+    hf_coeff_lr: float = 0.0
+    omega: float = 0.0
+
+    @abc.abstractmethod
+    def energy(self, basis, C_orth, P, occ, state) -> tuple[torch.Tensor, torch.Tensor]:
+        raise NotImplementedError
+
+    def energy_lr(self, basis, C_orth, P, occ, state) -> torch.Tensor:
+        return torch.zeros((), dtype=torch.float64, device=C_orth.device)
+
+
+@dataclass(frozen=True)
+class ScreenedProductDFCoulomb(CoulombTerm):
+    """Frozen pair-product RI-J over the significant pairs (gs_dft/ks/terms.py:236-256)."""
+
+    hf_coeff: float = 0.0
+    hf_coeff_lr: float = 0.0
+    omega: float = 0.0
+    lam: float = 1e-8
+    chunk: int = 2048
+    scales: tuple = (1.0,)
+    diagonal: bool = True
+    skip_pad: bool = False
+
+    def energy(self, basis, C_orth, P, occ, state):
+        pi, pj, valid = state.pairs
+        e_j = _cdf.df_coulomb_energy_screened(basis, C_orth, occ, state.aux, pi, pj,
+                                              lam=self.lam, chunk=self.chunk, valid=valid,
+                                              cholV=state.cholV, skip_pad=self.skip_pad,
+                                              index=getattr(state, "pair_index", None))
+        if self.hf_coeff != 0.0:
+            raise NotImplementedError("screened RI-K (hybrid exchange) is not part of this "
+                                      "library; use a pure functional (hf_coeff = 0)")
+        return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
+
+
+def hf_coeff(xc) -> float:
+    """Exact-exchange fraction a_x of a functional (gs_dft/ks/terms.py:267-270)."""
+    a = getattr(xc, "exact_exchange_fraction", None)
+    return float(a) if a is not None else float(getattr(xc, "hf_coeff", 0.0))
+
+
+def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
+                  omega: float = 0.0, skip_pad: bool = False) -> CoulombTerm:
+    """Resolve a spec into its term (gs_dft/ks/terms.py:273-301). Only the screened DF-J
+    strategy is implemented here; the others raise with the reason."""
+    if isinstance(spec, DFSpec):
+        if not screened:
+            raise NotImplementedError("dense (unscreened) DF is not part of this library; pass "
+                                      "screen=pairlist(eps=-1.0) for the full pair list")
+        if a_x != 0.0 or a_x_lr != 0.0:
+            raise NotImplementedError("screened RI-K (hybrid exchange) is not part of this "
+                                      "library; use a pure functional")
+        return ScreenedProductDFCoulomb(hf_coeff=a_x, hf_coeff_lr=a_x_lr, omega=omega,
+                                        lam=spec.lam, chunk=spec.chunk, scales=spec.scales,
+                                        diagonal=spec.diagonal, skip_pad=bool(skip_pad))
+    if isinstance(spec, ExactSpec):
+        raise NotImplementedError("coulomb=exact() (the exact streamed ERI) is not part of this "
+                                  "library; use coulomb=df()")
+    raise TypeError(f"coulomb must come from exact() or df(), got {spec!r}")

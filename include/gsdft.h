@@ -1,0 +1,141 @@
+/* gsdft.h -- C ABI of the MI355X (gfx950) screened density-fitted Coulomb (DF-J) library.
+ *
+ * Every entry point takes device pointers, a caller-owned device workspace (size from the matching
+ * *_workspace_size query) and a hipStream_t passed as void*. Kernels are enqueued on that stream;
+ * an entry point returns before they finish unless its comment says it synchronises. Returns a
+ * GSDFT_* status; gsdft_last_error() gives the message of the last failure on the calling thread.
+ *
+ * Layouts (all row-major, FP64 unless noted):
+ *   quat (M,4) as (w,x,y,z), unnormalised; log_scale (M,3); centers (M,3);
+ *   A6 (M,6) symmetric precision as xx,yy,zz,xy,xz,yz; norm (M);
+ *   C (M,k); occ (k); pair list pi, pj (int32) and weight (n);
+ *   aux log_alpha (N), aux_centers (N,3); metric V and its factor L (N,N) with L lower.
+ *
+ * Each declaration names the reference function it replaces (file:line in andresguzco/gs-dft).
+ */
+#ifndef GSDFT_H
+#define GSDFT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSDFT_OK 0
+#define GSDFT_ERR_ARG 1          /* invalid argument (sizes, null pointers)                     */
+#define GSDFT_ERR_OVERFLOW 2     /* significant pairs exceed twice the pad (pairs.py:157-161)   */
+#define GSDFT_ERR_NOT_PD 3       /* Cholesky met a non-positive pivot                           */
+#define GSDFT_ERR_HIP 4          /* HIP runtime error                                           */
+#define GSDFT_ERR_LIB 5          /* rocBLAS / rocSOLVER / hipCUB error                          */
+#define GSDFT_ERR_WORKSPACE 6    /* workspace too small; the query names the size               */
+
+int gsdft_abi_version(void);
+const char* gsdft_last_error(void);
+
+/* Splat chart. Replaces Splat.A / Splat.norm, gs_dft/basis/spectral.py:33-40,72-82. */
+int gsdft_splat_chart(int64_t M, const double* quat, const double* log_scale, double* A6,
+                      double* norm, void* stream);
+
+/* S_ij on a listed set of pairs. Replaces screened_overlap_pairs / _full_overlap_pairs,
+ * gs_dft/screening/pairs.py:342-345,373-375. Workspace: gsdft_screen_workspace_size(M,0,0). */
+int gsdft_overlap_pairs(int64_t M, const double* quat, const double* log_scale,
+                        const double* centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                        double* S, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace for the screening calls. keep_cap = 0 for counting and for lists that fit their
+ * pad; keep_cap >= n_sig for the keep-largest overflow path. */
+int gsdft_screen_workspace_size(int64_t M, int unique, int64_t keep_cap, size_t* bytes);
+
+/* Number of pairs with |S_ij| > eps (j >= i when unique). Replaces _count_significant,
+ * gs_dft/screening/pairs.py:103-118. Synchronises the stream (one host read, as the reference's
+ * int() at pairs.py:279). eps < 0 counts every pair without evaluating S. */
+int gsdft_screen_count(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, void* workspace,
+                       size_t workspace_bytes, int64_t* n_sig, void* stream);
+
+/* The padded pair list: lexsorted (ascending i*M+j), padding (0,0) with weight 0 at the tail,
+ * weight 2 - delta_ij in unique mode and 1 otherwise. When n_sig > pad_to the pad_to largest |S|
+ * are kept (ties by lower flat index) and re-sorted by flat index; beyond 2*pad_to the call fails
+ * with GSDFT_ERR_OVERFLOW. If the overflow path needs a bigger workspace the call returns
+ * GSDFT_ERR_WORKSPACE with *n_sig set. Synchronises the stream. Replaces neighbor_pairs,
+ * _scan_flat_indices, _decode_flat, _keep_largest and _pair_weights,
+ * gs_dft/screening/pairs.py:50-100,121-164,225-322. */
+int gsdft_screen_build(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, int64_t pad_to,
+                       int32_t* pi, int32_t* pj, double* weight, void* workspace,
+                       size_t workspace_bytes, int64_t* n_sig, void* stream);
+
+/* CSR views of the first n list entries for the atomics-free per-splat reductions of the
+ * backward pass: row_ptr/row_perm group entries by pi, col_ptr/col_perm by pj, each group in list
+ * order. row_ptr and col_ptr hold M+1 entries, the perms n. No reference counterpart: the
+ * reference scatters with segment_sum inside JAX autodiff (gs_dft/coulomb/ri.py:436-469). */
+int gsdft_pair_index_workspace_size(int64_t M, int64_t n, size_t* bytes);
+int gsdft_pair_index(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                     int32_t* row_ptr, int32_t* row_perm, int32_t* col_ptr, int32_t* col_perm,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Frozen diagonal product aux: log_alpha (n_scales*M) and centres, scale-major. scales is a
+ * HOST array. Replaces init_product_aux(diagonal_only=True), gs_dft/basis/isotropic.py:81-116.
+ * Workspace: gsdft_screen_workspace_size(M,0,0). */
+int gsdft_product_aux(int64_t M, const double* quat, const double* log_scale,
+                      const double* centers, const double* scales, int n_scales,
+                      double* log_alpha, double* aux_centers, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Workspace for gsdft_aux_metric and gsdft_cholesky. */
+int gsdft_metric_workspace_size(int64_t N, size_t* bytes);
+
+/* V_PQ = (P|Q) with lam added to the diagonal. Replaces aux_metric / coulomb_block /
+ * _coulomb_rows (+ shift_diag), gs_dft/coulomb/ri.py:63-123,243-250,267-275. */
+int gsdft_aux_metric(int64_t N, const double* log_alpha, const double* aux_centers, double lam,
+                     double* V, void* workspace, size_t workspace_bytes, void* stream);
+
+/* In-place lower Cholesky of V (row-major), strict upper triangle zeroed. Synchronises the stream
+ * to read the factorisation status. Replaces _chol_donated / aux_cholesky,
+ * gs_dft/coulomb/ri.py:253-264. */
+int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t workspace_bytes, void* stream);
+
+/* d = (L L^T)^-1 gamma and, when energy is non-null, *energy = 0.5 gamma.d (device scalar).
+ * Replaces df_coulomb_solve's cho_solve branch, gs_dft/coulomb/ri.py:472-479. */
+int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, double* d, double* energy,
+                    void* stream);
+
+/* gamma_P = sum_a (P|a) q_a over the first n list entries, q_a = w_a sum_o occ_o C_io C_jo.
+ * Replaces df_coulomb_gamma_screened, gs_dft/coulomb/ri.py:436-469 (with full_isobra_block
+ * :126-151 and the node kernel :167-185). */
+int gsdft_gamma_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, size_t* bytes);
+int gsdft_gamma(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                int64_t k, const double* C, const double* occ, int64_t N,
+                const double* log_alpha, const double* aux_centers, int64_t n,
+                const int32_t* pi, const int32_t* pj, const double* weight, double* gamma,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Reverse mode of gsdft_gamma for the cotangent dgamma (N), scaled by the device scalar
+ * *dgamma_scale when non-null: J (n) = sum_P dgamma_P (P|a) (0 on zero-weight entries), and the
+ * gradients w.r.t. quat, log_scale, centers (M,4/3/3) and C (M,k), aux held constant. Needs the
+ * pair index of the same n entries. Replaces JAX's reverse pass through
+ * gs_dft/coulomb/ri.py:436-469, :190-222, gs_dft/coulomb/stream.py:203-215 and
+ * gs_dft/basis/spectral.py:33-40,72-82 (gs_dft/ks/train.py:367-373 holds the aux constant). */
+int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, size_t* bytes);
+int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,
+                    const double* centers, int64_t k, const double* C, const double* occ,
+                    int64_t N, const double* log_alpha, const double* aux_centers, int64_t n,
+                    const int32_t* pi, const int32_t* pj, const double* weight,
+                    const int32_t* row_ptr, const int32_t* row_perm, const int32_t* col_ptr,
+                    const int32_t* col_perm, const double* dgamma, const double* dgamma_scale,
+                    double* J, double* dquat, double* dlog_scale, double* dcenters, double* dC,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
+ * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve.
+ * gsdft_profile_read synchronises the recorded events and returns the summed milliseconds and
+ * the launch count since the last reset. */
+int gsdft_profile_enable(int on);
+int gsdft_profile_read(int id, double* total_ms, int64_t* launches, int reset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

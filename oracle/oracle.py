@@ -1,0 +1,241 @@
+"""numpy bindings of the C oracle (``oracle/c/oracle.c``).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the benchmark's CPU baseline.
+The shipped package never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "build" / "liboracle.so"
+
+_lib = None
+
+_D = ctypes.POINTER(ctypes.c_double)
+_I32 = ctypes.POINTER(ctypes.c_int32)
+_I64 = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+
+
+def build() -> pathlib.Path:
+    """Compile the oracle with its Makefile (gcc + OpenMP)."""
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.orc_count_significant.restype = ctypes.c_int64
+        L.orc_boys0.restype = ctypes.c_double
+        L.orc_boys0.argtypes = [ctypes.c_double]
+        L.orc_neighbor_pairs.restype = ctypes.c_int
+        L.orc_cholesky.restype = ctypes.c_int
+        L.orc_num_threads.restype = ctypes.c_int
+        # the reference's own table (gs_dft/integrals/dense.py:46-53, numpy leggauss)
+        t, w = reference_quad_table(20)
+        L.orc_set_quad_table(_d(t), _d(w))
+        _lib = L
+    return _lib
+
+
+def _d(a):
+    return a.ctypes.data_as(_D)
+
+
+def _f64(a):
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def reference_quad_table(n: int = 20):
+    """gs_dft/integrals/dense.py:46-53: numpy leggauss mapped to [0, inf) by t = s/(1-s)."""
+    x, wl = np.polynomial.legendre.leggauss(n)
+    s = (x + 1.0) / 2.0
+    t = np.ascontiguousarray(s / (1.0 - s), dtype=np.float64)
+    w = np.ascontiguousarray((wl / 2.0) * (1.0 / (1.0 - s) ** 2), dtype=np.float64)
+    return t, w
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+def quad_table(n: int = 20):
+    t = np.empty(n)
+    w = np.empty(n)
+    lib().orc_quad_table(ctypes.c_int(n), _d(t), _d(w))
+    return t, w
+
+
+def chart(quat, log_scale):
+    quat, log_scale = _f64(quat), _f64(log_scale)
+    M = quat.shape[0]
+    A = np.empty((M, 3, 3))
+    N = np.empty(M)
+    lib().orc_chart(_i64(M), _d(quat), _d(log_scale), _d(A), _d(N))
+    return A, N
+
+
+def pair_quantities(A, mu, norm, pi, pj):
+    A, mu, norm, pi, pj = _f64(A), _f64(mu), _f64(norm), _i32(pi), _i32(pj)
+    n = pi.shape[0]
+    Ah = np.empty((n, 3, 3))
+    P = np.empty((n, 3))
+    KN = np.empty(n)
+    lib().orc_pair_quantities(_i64(A.shape[0]), _d(A), _d(mu), _d(norm), _i64(n),
+                              pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32),
+                              _d(Ah), _d(P), _d(KN))
+    return Ah, P, KN
+
+
+def overlap_pairs(quat, log_scale, centers, pi, pj):
+    quat, log_scale, centers, pi, pj = _f64(quat), _f64(log_scale), _f64(centers), _i32(pi), _i32(pj)
+    S = np.empty(pi.shape[0])
+    lib().orc_overlap_pairs(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                            _i64(pi.shape[0]), pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32),
+                            _d(S))
+    return S
+
+
+def count_significant(quat, log_scale, centers, eps, unique):
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    return int(lib().orc_count_significant(_i64(quat.shape[0]), _d(quat), _d(log_scale),
+                                           _d(centers), ctypes.c_double(eps), ctypes.c_int(int(unique))))
+
+
+def neighbor_pairs(quat, log_scale, centers, eps, pad_to=None, unique=False):
+    """(pi, pj, weight, n_sig). Raises ValueError where the reference raises (n_sig > 2 pad)."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    M = quat.shape[0]
+    n_all = M * (M + 1) // 2 if unique else M * M
+    if pad_to is None:
+        length = n_all if eps < 0 else count_significant(quat, log_scale, centers, eps, unique)
+    else:
+        length = int(pad_to)
+    pi = np.zeros(max(length, 1), np.int32)
+    pj = np.zeros(max(length, 1), np.int32)
+    w = np.zeros(max(length, 1))
+    n_out = ctypes.c_int64()
+    n_sig = ctypes.c_int64()
+    rc = lib().orc_neighbor_pairs(_i64(M), _d(quat), _d(log_scale), _d(centers),
+                                  ctypes.c_double(eps), _i64(-1 if pad_to is None else int(pad_to)),
+                                  ctypes.c_int(int(unique)), pi.ctypes.data_as(_I32),
+                                  pj.ctypes.data_as(_I32), _d(w), ctypes.byref(n_out),
+                                  ctypes.byref(n_sig))
+    if rc == 2:
+        raise ValueError(f"neighbor_pairs: {n_sig.value} significant pairs exceed 2x the pad "
+                         f"({2 * int(pad_to)})")
+    m = int(n_out.value)
+    return pi[:m], pj[:m], w[:m], int(n_sig.value)
+
+
+def product_aux(quat, log_scale, centers, scales):
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    sc = _f64(np.asarray(scales, float))
+    M = quat.shape[0]
+    la = np.empty(len(sc) * M)
+    cen = np.empty((len(sc) * M, 3))
+    lib().orc_product_aux(_i64(M), _d(quat), _d(log_scale), _d(centers), _d(sc),
+                          ctypes.c_int(len(sc)), _d(la), _d(cen))
+    return la, cen
+
+
+def boys0(T: float) -> float:
+    return float(lib().orc_boys0(float(T)))
+
+
+def aux_metric(log_alpha, centers, lam=0.0):
+    la, cen = _f64(log_alpha), _f64(centers)
+    N = la.shape[0]
+    V = np.empty((N, N))
+    lib().orc_aux_metric(_i64(N), _d(la), _d(cen), ctypes.c_double(lam), _d(V))
+    return V
+
+
+def cholesky(V):
+    L = np.array(V, dtype=np.float64, copy=True, order="C")
+    rc = lib().orc_cholesky(_i64(L.shape[0]), _d(L))
+    if rc:
+        raise np.linalg.LinAlgError("oracle Cholesky: matrix not positive definite")
+    return L
+
+
+def cho_solve(L, gamma):
+    L, g = _f64(L), _f64(gamma)
+    d = np.empty_like(g)
+    lib().orc_cho_solve(_i64(L.shape[0]), _d(L), _d(g), _d(d))
+    return d
+
+
+def three_center_block(quat, log_scale, centers, log_alpha, aux_centers, pi, pj):
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    la, ac, pi, pj = _f64(log_alpha), _f64(aux_centers), _i32(pi), _i32(pj)
+    N, n = la.shape[0], pi.shape[0]
+    B = np.empty((N, n))
+    lib().orc_three_center_block(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                                 _i64(N), _d(la), _d(ac), _i64(n), pi.ctypes.data_as(_I32),
+                                 pj.ctypes.data_as(_I32), _d(B))
+    return B
+
+
+def gamma(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, weight):
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    C, occ, la, ac = _f64(C), _f64(occ), _f64(log_alpha), _f64(aux_centers)
+    pi, pj, w = _i32(pi), _i32(pj), _f64(weight)
+    N = la.shape[0]
+    g = np.empty(N)
+    lib().orc_gamma(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers), _i64(C.shape[1]),
+                    _d(C), _d(occ), _i64(N), _d(la), _d(ac), _i64(pi.shape[0]),
+                    pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32), _d(w), _d(g))
+    return g
+
+
+def gamma_vjp(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, weight, dgamma):
+    """(J, dquat, dlog_scale, dcenters, dC) for the upstream cotangent ``dgamma``."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    C, occ, la, ac = _f64(C), _f64(occ), _f64(log_alpha), _f64(aux_centers)
+    pi, pj, w, dg = _i32(pi), _i32(pj), _f64(weight), _f64(dgamma)
+    M, k, n = quat.shape[0], C.shape[1], pi.shape[0]
+    J = np.empty(n)
+    dq = np.empty((M, 4))
+    dl = np.empty((M, 3))
+    dc = np.empty((M, 3))
+    dC = np.empty((M, k))
+    lib().orc_gamma_vjp(_i64(M), _d(quat), _d(log_scale), _d(centers), _i64(k), _d(C), _d(occ),
+                        _i64(la.shape[0]), _d(la), _d(ac), _i64(n), pi.ctypes.data_as(_I32),
+                        pj.ctypes.data_as(_I32), _d(w), _d(dg), _d(J), _d(dq), _d(dl), _d(dc),
+                        _d(dC))
+    return J, dq, dl, dc, dC
+
+
+def dfj_energy(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, weight, lam):
+    """(E_J, gamma, d, L) following gs_dft/coulomb/ri.py:485-494 with the refresh factor."""
+    g = gamma(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, weight)
+    L = cholesky(aux_metric(log_alpha, aux_centers, lam))
+    d = cho_solve(L, g)
+    return 0.5 * float(np.dot(g, d)), g, d, L
+
+
+def dfj_grad(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, weight, lam):
+    """(E_J, J, dquat, dlog_scale, dcenters, dC) of E_J = 1/2 gamma^T (V + lam I)^-1 gamma."""
+    E, g, d, _L = dfj_energy(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj,
+                             weight, lam)
+    return (E,) + gamma_vjp(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj,
+                            weight, d)
+
+
+def set_threads(n: int) -> None:
+    os.environ["OMP_NUM_THREADS"] = str(int(n))

@@ -1,0 +1,200 @@
+"""Literal float64 restatement of the reference DF-J kernels in PyTorch (CPU), differentiable by
+autograd.
+
+TEST INFRASTRUCTURE ONLY. Where the C oracle rewrites the (iso aux | full pair) node sum in
+rotation invariants, this module follows the reference line by line: an ``eigh`` of the pair
+precision, the rotated displacement squared, and the per-axis node loop. Autograd through it
+plays the role of JAX reverse mode, so it pins both the C oracle's forward and its hand-written
+reverse pass. Use it on small systems only (it materialises the (N_aux, n_pair) block).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+PI = math.pi
+
+
+def quad_table(n: int = 20):
+    """gs_dft/integrals/dense.py:46-53 -- numpy leggauss mapped to [0, inf) by t = s/(1-s)."""
+    nodes_01, weights_01 = np.polynomial.legendre.leggauss(n)
+    s = (nodes_01 + 1.0) / 2.0
+    w_s = weights_01 / 2.0
+    t = s / (1.0 - s)
+    jacobian = 1.0 / (1.0 - s) ** 2
+    return np.asarray(t, dtype=np.float64), np.asarray(w_s * jacobian, dtype=np.float64)
+
+
+_QT, _QW = quad_table(20)
+QUAD_T_LIST = [float(t) for t in _QT]
+QUAD_W_LIST = [float(w) for w in _QW]
+
+
+def quat_to_rotation(q):
+    """gs_dft/basis/spectral.py:33-40"""
+    q = q / (torch.linalg.norm(q, dim=-1, keepdim=True) + 1e-12)
+    w, x, y, z = q[..., 0], q[..., 1], q[..., 2], q[..., 3]
+    r0 = torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)], dim=-1)
+    r1 = torch.stack([2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)], dim=-1)
+    r2 = torch.stack([2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)], dim=-1)
+    return torch.stack([r0, r1, r2], dim=-2)
+
+
+def splat_A(quat, log_scale):
+    """gs_dft/basis/spectral.py:72-76"""
+    R = quat_to_rotation(quat)
+    a = torch.exp(log_scale)
+    return torch.einsum("mij,mj,mkj->mik", R, a, R)
+
+
+def splat_norm(log_scale):
+    """gs_dft/basis/spectral.py:79-82"""
+    detA = torch.exp(torch.sum(log_scale, dim=-1))
+    return (8.0 * detA / PI ** 3) ** 0.25
+
+
+def det3(A):
+    """gs_dft/integrals/linalg3.py:17-22"""
+    return (A[..., 0, 0] * (A[..., 1, 1] * A[..., 2, 2] - A[..., 1, 2] * A[..., 2, 1])
+            - A[..., 0, 1] * (A[..., 1, 0] * A[..., 2, 2] - A[..., 1, 2] * A[..., 2, 0])
+            + A[..., 0, 2] * (A[..., 1, 0] * A[..., 2, 1] - A[..., 1, 1] * A[..., 2, 0]))
+
+
+def adj3(A):
+    """gs_dft/integrals/linalg3.py:26-41"""
+    c00 = A[..., 1, 1] * A[..., 2, 2] - A[..., 1, 2] * A[..., 2, 1]
+    c01 = A[..., 0, 2] * A[..., 2, 1] - A[..., 0, 1] * A[..., 2, 2]
+    c02 = A[..., 0, 1] * A[..., 1, 2] - A[..., 0, 2] * A[..., 1, 1]
+    c10 = A[..., 1, 2] * A[..., 2, 0] - A[..., 1, 0] * A[..., 2, 2]
+    c11 = A[..., 0, 0] * A[..., 2, 2] - A[..., 0, 2] * A[..., 2, 0]
+    c12 = A[..., 0, 2] * A[..., 1, 0] - A[..., 0, 0] * A[..., 1, 2]
+    c20 = A[..., 1, 0] * A[..., 2, 1] - A[..., 1, 1] * A[..., 2, 0]
+    c21 = A[..., 0, 1] * A[..., 2, 0] - A[..., 0, 0] * A[..., 2, 1]
+    c22 = A[..., 0, 0] * A[..., 1, 1] - A[..., 0, 1] * A[..., 1, 0]
+    return torch.stack([torch.stack([c00, c01, c02], dim=-1),
+                        torch.stack([c10, c11, c12], dim=-1),
+                        torch.stack([c20, c21, c22], dim=-1)], dim=-2)
+
+
+def solve3(A, b):
+    """gs_dft/integrals/linalg3.py:49-51"""
+    return torch.einsum("...kl,...l->...k", adj3(A), b) / det3(A)[..., None]
+
+
+def full_pair_quantities(A, mu, N, pi, pj):
+    """gs_dft/coulomb/stream.py:203-215"""
+    Ai, Aj = A[pi], A[pj]
+    mui, muj = mu[pi], mu[pj]
+    Aij = Ai + Aj
+    rhs = torch.einsum("pkl,pl->pk", Ai, mui) + torch.einsum("pkl,pl->pk", Aj, muj)
+    Pa = solve3(Aij, rhs)
+    d = mui - muj
+    Ajd = torch.einsum("pkl,pl->pk", Aj, d)
+    AiAinvAjd = torch.einsum("pkl,pl->pk", Ai, solve3(Aij, Ajd))
+    K = torch.exp(-torch.sum(d * AiAinvAjd, dim=-1))
+    return Aij, Pa, N[pi] * N[pj] * K
+
+
+def full_overlap_pairs(quat, log_scale, centers, pi, pj):
+    """gs_dft/screening/pairs.py:342-345"""
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    Aij, _, NK = full_pair_quantities(A, centers, N, pi, pj)
+    return NK * PI ** 1.5 / torch.sqrt(det3(Aij))
+
+
+def init_product_aux(quat, log_scale, centers, scales=(1.0,)):
+    """gs_dft/basis/isotropic.py:269-281 (diagonal_only=True) -> (log_alpha, centers)."""
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    idx = torch.arange(A.shape[0])
+    Aij, Pa, _ = full_pair_quantities(A, centers, N, idx, idx)
+    alpha0 = det3(Aij) ** (1.0 / 3.0)
+    log_alpha = torch.cat([torch.log(alpha0 * float(s)) for s in scales])
+    return log_alpha, torch.cat([Pa for _ in scales], dim=0)
+
+
+def boys0(T):
+    """F0(T) = 0.5 sqrt(pi/T) erf(sqrt(T)) with the series 1 - T/3 below 1e-12."""
+    Ts = torch.where(T < 1e-12, torch.ones_like(T), T)
+    big = 0.5 * torch.sqrt(PI / Ts) * torch.special.erf(torch.sqrt(Ts))
+    return torch.where(T < 1e-12, 1.0 - T / 3.0, big)
+
+
+def coulomb_block(g1, P1, KN1, g2, P2, KN2):
+    """gs_dft/coulomb/ri.py:63-76 (omega=None)"""
+    gab = g1[:, None] * g2[None, :]
+    gsum = g1[:, None] + g2[None, :]
+    PQ2 = torch.sum((P1[:, None, :] - P2[None, :, :]) ** 2, dim=-1)
+    rho = gab / gsum
+    T = rho * PQ2
+    F0 = boys0(T)
+    coulomb = 2.0 * PI ** 2.5 / (gab * torch.sqrt(gsum)) * F0
+    return (KN1[:, None] * KN2[None, :]) * coulomb
+
+
+def aux_quantities(log_alpha, centers):
+    """gs_dft/basis/isotropic.py:30-39 and gs_dft/coulomb/ri.py:238-240"""
+    beta = torch.exp(log_alpha)
+    return beta, centers, (2.0 * beta / PI) ** 0.75
+
+
+def aux_metric(log_alpha, centers):
+    b, R, n = aux_quantities(log_alpha, centers)
+    return coulomb_block(b, R, n, b, R, n)
+
+
+def isobra_nodes(beta, dp2, Lam, table=None):
+    """gs_dft/coulomb/ri.py:167-185, the static node unroll (``table`` = (t list, w list) to
+    integrate with another rule; the reference's 20 nodes by default)."""
+    t_list, w_list = (QUAD_T_LIST, QUAD_W_LIST) if table is None else table
+    b = beta[:, None]
+    L0, L1, L2 = Lam[None, :, 0], Lam[None, :, 1], Lam[None, :, 2]
+    coul = torch.zeros((beta.shape[0], Lam.shape[0]), dtype=beta.dtype)
+    for t, w in zip(t_list, w_list):
+        t2 = t * t
+        G0 = b * L0 + t2 * (b + L0)
+        G1 = b * L1 + t2 * (b + L1)
+        G2 = b * L2 + t2 * (b + L2)
+        invp = 1.0 / (G0 * G1 * G2)
+        num = b * (L0 * dp2[..., 0] * G1 * G2
+                   + L1 * dp2[..., 1] * G0 * G2
+                   + L2 * dp2[..., 2] * G0 * G1)
+        coul = coul + w * torch.sqrt(invp) * torch.exp(-t2 * num * invp)
+    return coul
+
+
+def full_isobra_block(beta, R_aux, KN_aux, A_pair, P_pair, KN_pair, table=None):
+    """gs_dft/coulomb/ri.py:126-151"""
+    Lam, U = torch.linalg.eigh(A_pair)
+    d = R_aux[:, None, :] - P_pair[None, :, :]
+    dp2 = torch.einsum("bki,abk->abi", U, d) ** 2
+    coul = isobra_nodes(beta, dp2, Lam, table)
+    pref = 2.0 * PI ** 3 / math.sqrt(PI)
+    return (KN_aux[:, None] * KN_pair[None, :]) * pref * coul
+
+
+def gamma_screened(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, valid,
+                   chunk=2048):
+    """gs_dft/coulomb/ri.py:436-469 (chunked, no remat needed for the values)."""
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    aux_q = aux_quantities(log_alpha, aux_centers)
+    n = pi.shape[0]
+    gamma = torch.zeros(log_alpha.shape[0], dtype=torch.float64)
+    for s in range(0, n, chunk):
+        ci, cj, cv = pi[s:s + chunk], pj[s:s + chunk], valid[s:s + chunk]
+        q = cv.to(torch.float64) * torch.sum(occ[None, :] * C[ci] * C[cj], dim=1)
+        block = full_isobra_block(*aux_q, *full_pair_quantities(A, centers, N, ci, cj))
+        gamma = gamma + block @ q
+    return gamma
+
+
+def coulomb_solve(gamma, L):
+    """gs_dft/coulomb/ri.py:479 -- 0.5 gamma^T cho_solve((L, lower), gamma)."""
+    d = torch.cholesky_solve(gamma[:, None], L, upper=False)[:, 0]
+    return 0.5 * torch.dot(gamma, d)
+
+
+def as_t(x, requires_grad=False, dtype=torch.float64):
+    t = torch.as_tensor(np.asarray(x), dtype=dtype).clone()
+    return t.requires_grad_(requires_grad) if requires_grad else t

@@ -1,0 +1,305 @@
+"""Parity of the HIP path against the CPU oracle on the same seeded inputs.
+
+Bars: the pair list bit-exact (indices, order, weights); S within a few ulps; aux, metric,
+gamma, E_J and J within 1e-10 relative (gamma ~1e-12 in practice); gradients within 1e-9
+relative to the largest entry.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_max
+
+pytestmark = pytest.mark.gpu
+
+REL_E = 1e-10
+REL_G = 1e-9
+
+
+def _splat(g, s, grad=False):
+    mk = lambda a: torch.tensor(a, device="cuda", dtype=torch.float64).requires_grad_(grad)
+    return g.Splat(quat=mk(s.quat), log_scale=mk(s.log_scale), centers=mk(s.centers))
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+SMALL = [dict(M=24, k=5, n_atoms=3, seed=1), dict(M=60, k=7, n_atoms=5, seed=2, spread=4.0),
+         dict(M=200, k=9, n_atoms=8, seed=3, spread=6.0)]
+
+
+def _small(wl, spec):
+    spec = dict(spec)
+    return wl.make_small(spec.pop("M"), spec.pop("k"), **spec)
+
+
+# ----------------------------------------------------------------------------- chart / overlap
+
+def test_chart_matches_oracle(g, wl, orc, cuda):
+    s = _small(wl, SMALL[2])
+    A, N = _splat(g, s).chart()
+    Ao, No = orc.chart(s.quat, s.log_scale)
+    assert rel_max(_np(A), Ao) < 4e-16 * 8 and rel_max(_np(N), No) < 4e-16 * 8
+
+
+def test_overlap_matches_oracle_to_ulps(g, wl, orc, cuda):
+    s = _small(wl, SMALL[2])
+    M = s.M
+    pi = np.repeat(np.arange(M), M).astype(np.int32)
+    pj = np.tile(np.arange(M), M).astype(np.int32)
+    S = _np(g.screened_overlap_pairs(_splat(g, s), torch.tensor(pi, device="cuda"),
+                                     torch.tensor(pj, device="cuda")))
+    So = orc.overlap_pairs(s.quat, s.log_scale, s.centers, pi, pj)
+    ulps = np.abs(S - So) / np.spacing(np.abs(So))
+    print(f"[overlap] max ulp difference {ulps.max():.1f}")
+    assert ulps.max() <= 8
+
+
+# ----------------------------------------------------------------------------- pair list
+
+def _check_list(g, s, orc, eps, unique, pad_to=None):
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=eps, pad_to=pad_to, unique=unique)
+    ri, rj, rw, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, pad_to, unique)
+    assert np.array_equal(_np(pi), ri) and np.array_equal(_np(pj), rj)
+    w = _np(v)
+    if unique:
+        assert v.dtype == torch.float64 and np.array_equal(w, rw)
+    else:
+        assert v.dtype == torch.bool and np.array_equal(w, rw != 0)
+    return len(ri), n_sig
+
+
+@pytest.mark.parametrize("unique", [False, True])
+@pytest.mark.parametrize("eps", [1e-5, 1e-7, 1e-9])
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_pair_list_bit_exact_small(g, wl, orc, cuda, which, eps, unique):
+    s = _small(wl, SMALL[which])
+    n, n_sig = _check_list(g, s, orc, eps, unique)
+    assert n == n_sig == g.count_significant(_splat(g, s), eps, unique)
+
+
+@pytest.mark.parametrize("system", [1, 2, 3])
+@pytest.mark.parametrize("eps", [1e-5, 1e-7, 1e-9])
+def test_pair_list_bit_exact_benchmark_systems(g, wl, orc, cuda, system, eps):
+    s = wl.make_system(system)
+    print(f"[pairs] system {system} M={s.M} eps={eps}", flush=True)
+    n, _ = _check_list(g, s, orc, eps, True)
+    if system < 3:
+        _check_list(g, s, orc, eps, False)
+    print(f"[pairs] system {system}: {n} unique pairs bit-exact", flush=True)
+
+
+def test_pair_list_padding_full_and_overflow(g, wl, orc, cuda):
+    """gs-dft tests/unit/test_device_pairs.py:62,76,91,146 and test_pair_tricks.py:57,260."""
+    s = _small(wl, SMALL[1])
+    M = s.M
+    for unique in (False, True):
+        n, _ = _check_list(g, s, orc, 1e-7, unique)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=n + 37)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=M * M + 500)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=n // 2 + 1)          # keep-largest
+        with pytest.raises(ValueError, match="exceed"):
+            g.neighbor_pairs(_splat(g, s), eps=1e-7, pad_to=n // 3, unique=unique)
+    for pad in (None, M * M, M * M + 313):
+        _check_list(g, s, orc, -1.0, False, pad_to=pad)
+    _check_list(g, s, orc, -1.0, True)
+    _check_list(g, s, orc, -1.0, False, pad_to=M * M // 2)                # eps<0, pad < M^2
+
+
+def test_empty_list(g, wl, cuda):
+    s = wl.make_small(8, 2, n_atoms=8, spread=200.0, seed=4, width=(0.3, 0.31))
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=0.5, unique=False)
+    assert pi.shape[0] == 8 and bool(v.all())              # only the diagonal (S_ii = 1)
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=2.0)
+    assert pi.shape[0] == 0
+
+
+# ----------------------------------------------------------------------------- aux / metric
+
+def test_product_aux_and_metric_match_oracle(g, wl, orc, cuda):
+    s = wl.make_system(2)
+    aux = g.init_product_aux(_splat(g, s), scales=s.scales)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    assert rel_max(_np(aux.log_alpha), la) < 1e-15 and rel_max(_np(aux.centers), ac) < 1e-14
+    V = _np(g.aux_metric(aux))
+    Vo = orc.aux_metric(la, ac)
+    assert np.max(np.abs(V - Vo) / np.abs(Vo)) < 1e-13
+    assert np.array_equal(V, V.T)
+
+
+def test_cholesky_and_solve(g, wl, orc, cuda):
+    s = wl.make_system(1)
+    aux = g.init_product_aux(_splat(g, s), scales=s.scales)
+    L = g.aux_cholesky(aux, 1e-8)
+    Ln = _np(L)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    V = orc.aux_metric(la, ac, 1e-8)
+    assert np.all(np.triu(Ln, 1) == 0)
+    assert rel_max(Ln @ Ln.T, V) < 1e-14
+    gam = torch.randn(V.shape[0], device="cuda", dtype=torch.float64)
+    E = g.df_coulomb_solve(gam, aux, cholV=L).item()
+    En = 0.5 * _np(gam) @ np.linalg.solve(V, _np(gam))
+    print(f"[solve] cond(V+lam I) = {np.linalg.cond(V):.3e}")
+    assert abs(E - En) < 1e-10 * abs(En)
+
+
+# ----------------------------------------------------------------------------- gamma / E_J / grads
+
+def _problem(wl, orc, s, eps=None, unique=True):
+    eps = s.eps if eps is None else eps
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, None, unique)
+    return la, ac, pi, pj, w
+
+
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_gamma_matches_oracle_small(g, wl, orc, cuda, which):
+    s = _small(wl, SMALL[which])
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    gam = _np(g.df_coulomb_gamma_screened(_splat(g, s), torch.tensor(s.C, device="cuda"),
+                                          s.occ, aux, pi, pj, valid=w))
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w)
+    print(f"[gamma] M={s.M} n={len(pi)} N={len(la)} rel {rel_max(gam, go):.2e}")
+    assert rel_max(gam, go) < 1e-12
+
+
+def _energy_grads(g, s, la, ac, pi, pj, w, lam, pad_to=None):
+    basis = _splat(g, s, grad=True)
+    C = torch.tensor(s.C, device="cuda", dtype=torch.float64, requires_grad=True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    L = g.aux_cholesky(aux, lam)
+    if pad_to is not None:
+        extra = pad_to - len(pi)
+        pi = np.concatenate([pi, np.zeros(extra, np.int32)])
+        pj = np.concatenate([pj, np.zeros(extra, np.int32)])
+        w = np.concatenate([w, np.zeros(extra)])
+    E = g.df_coulomb_energy_screened(basis, C, s.occ, aux, pi, pj, lam=lam, valid=w, cholV=L)
+    E.backward()
+    return (E.item(), _np(basis.quat.grad), _np(basis.log_scale.grad), _np(basis.centers.grad),
+            _np(C.grad))
+
+
+@pytest.mark.parametrize("case", ["small0", "small1", "system1", "system2"])
+def test_energy_and_gradients_match_oracle(g, wl, orc, cuda, case):
+    s = _small(wl, SMALL[int(case[-1])]) if case.startswith("small") else wl.make_system(int(case[-1]))
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    print(f"[dfj] {case}: M={s.M} n={len(pi)} N={len(la)} k={s.k}", flush=True)
+    got = _energy_grads(g, s, la, ac, pi, pj, w, s.lam)
+    ref = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w, s.lam)
+    rel = abs(got[0] - ref[0]) / abs(ref[0])
+    print(f"[dfj] {case}: E_J gpu {got[0]:.15e} oracle {ref[0]:.15e} rel {rel:.2e}")
+    assert rel < REL_E
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"), got[1:], ref[2:]):
+        err = rel_max(a, b)
+        print(f"[dfj] {case}: d{name} rel-to-max {err:.2e}")
+        assert err < REL_G
+
+
+def test_J_on_the_pair_list_matches_oracle(g, wl, orc, cuda):
+    s = _small(wl, SMALL[1])
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    J = _np(g.coulomb_pairs(_splat(g, s), torch.tensor(s.C, device="cuda"), s.occ, aux, pi, pj,
+                            lam=s.lam, valid=w))
+    ref = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w, s.lam)
+    assert rel_max(J, ref[1]) < REL_E
+
+
+def test_general_cotangent_of_gamma(g, wl, orc, cuda):
+    """Reverse of gamma alone for d(sum gamma^2) (gs-dft tests/unit/test_pair_tricks.py:81)."""
+    s = _small(wl, SMALL[0])
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    basis = _splat(g, s, grad=True)
+    C = torch.tensor(s.C, device="cuda", dtype=torch.float64, requires_grad=True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    gam = g.df_coulomb_gamma_screened(basis, C, s.occ, aux, pi, pj, valid=w)
+    (gam ** 2).sum().backward()
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w)
+    ref = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w, 2 * go)
+    for a, b in zip((basis.quat.grad, basis.log_scale.grad, basis.centers.grad, C.grad), ref[1:]):
+        assert rel_max(_np(a), b) < REL_G
+
+
+def test_unique_equals_ordered_and_padding_is_exact(g, wl, orc, cuda):
+    """gs-dft tests/unit/test_pair_tricks.py:81,107 on the GPU path: the unique list reproduces
+    the ordered one, and appended padding (weight 0) changes nothing."""
+    s = _small(wl, SMALL[1])
+    la, ac, ui, uj, uw = _problem(wl, orc, s, unique=True)
+    _, _, oi, oj, ow = _problem(wl, orc, s, unique=False)
+    eu = _energy_grads(g, s, la, ac, ui, uj, uw, s.lam)
+    eo = _energy_grads(g, s, la, ac, oi, oj, ow, s.lam)
+    ep = _energy_grads(g, s, la, ac, ui, uj, uw, s.lam, pad_to=2 * len(ui) + 100)
+    assert abs(eu[0] - eo[0]) < 1e-10 * abs(eo[0])
+    assert eu[0] == ep[0]
+    for a, b, c in zip(eu[1:], eo[1:], ep[1:]):
+        assert rel_max(a, b) < 1e-9 and np.array_equal(a, c)
+
+
+def test_results_are_deterministic(g, wl, orc, cuda):
+    s = _small(wl, SMALL[2])
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    a = _energy_grads(g, s, la, ac, pi, pj, w, s.lam)
+    b = _energy_grads(g, s, la, ac, pi, pj, w, s.lam)
+    assert a[0] == b[0] and all(np.array_equal(x, y) for x, y in zip(a[1:], b[1:]))
+
+
+def test_plugin_surface_end_to_end(g, wl, orc, cuda):
+    """df() + pairlist() + refresh() + ScreenedProductDFCoulomb.energy, as a trainer calls them
+    (gs_dft/ks/train.py:355-382), against the oracle."""
+    s = wl.make_system(1)
+    basis = _splat(g, s, grad=True)
+    C = torch.tensor(s.C, device="cuda", dtype=torch.float64, requires_grad=True)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam),
+                    screen=g.pairlist(s.eps, unique=True, skip_pad=True))
+    n0 = g.neighbor_pairs(basis, eps=s.eps, unique=True)[0].shape[0]
+    state = g.refresh(ks, basis, pad_to=g.train_pad_to(ks.screen, n0))
+    assert state.pairs[0].shape[0] == 2 * n0 and state.cholV is not None
+    state2 = g.refresh(ks, basis, like=state)
+    assert state2.pairs[0].shape[0] == 2 * n0
+    E_J, E_K = ks.coulomb.energy(basis, C, None, torch.tensor(s.occ, device="cuda"), state)
+    assert E_K.item() == 0.0
+    E_J.backward()
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    ref = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w, s.lam)
+    assert abs(E_J.item() - ref[0]) < REL_E * abs(ref[0])
+    for a, b in zip((basis.quat, basis.log_scale, basis.centers, C), ref[2:]):
+        assert rel_max(_np(a.grad), b) < REL_G
+
+
+def test_system3_sampled_gamma_and_directional_derivative(g, wl, orc, cuda):
+    """Alkane (M=2000, N_aux=8000): gamma on a sample of aux functions against the oracle, and
+    the gradient's directional derivative against central differences of the GPU energy."""
+    s = wl.make_system(3)
+    basis = _splat(g, s)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(s.eps, unique=True))
+    state = g.refresh(ks, basis)
+    pi, pj, w = (_np(t) for t in state.pairs)
+    C = torch.tensor(s.C, device="cuda")
+    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, state.aux, state.pairs[0],
+                                          state.pairs[1], valid=state.pairs[2],
+                                          index=state.pair_index))
+    rng = np.random.default_rng(0)
+    sel = np.sort(rng.choice(len(gam), 48, replace=False))
+    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pi, pj, w)
+    print(f"[system3] n={len(pi)} sampled gamma rel {rel_max(gam[sel], go):.2e}", flush=True)
+    assert rel_max(gam[sel], go) < 1e-12
+    b2 = _splat(g, s, grad=True)
+    Cg = C.clone().requires_grad_()
+    E = ks(g.SplatModel(basis=b2, C=Cg, occupations=torch.tensor(s.occ, device="cuda")), state)
+    E.backward()
+    dirs = [torch.randn_like(t) for t in (b2.quat, b2.log_scale, b2.centers, Cg)]
+    dd = sum((t.grad * d).sum().item() for t, d in zip((b2.quat, b2.log_scale, b2.centers, Cg), dirs))
+    h = 1e-5
+
+    def e_at(sign):
+        with torch.no_grad():
+            b = g.Splat(quat=b2.quat + sign * h * dirs[0], log_scale=b2.log_scale + sign * h * dirs[1],
+                        centers=b2.centers + sign * h * dirs[2])
+            return ks(g.SplatModel(basis=b, C=Cg + sign * h * dirs[3],
+                                   occupations=torch.tensor(s.occ, device="cuda")), state).item()
+    fd = (e_at(1) - e_at(-1)) / (2 * h)
+    print(f"[system3] directional derivative {dd:.10e} vs central difference {fd:.10e}")
+    assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))

@@ -1,0 +1,61 @@
+"""Host-side plugin surface (no GPU): spec values, validation and errors mirror
+gs_dft/ks/terms.py and gs_dft/ks/train.py."""
+import pytest
+
+
+def test_df_spec_defaults_and_validation(g):
+    d = g.df()
+    assert d == g.DFSpec(scales=(1.0,), diagonal=True, lam=1e-8, chunk=2048)
+    assert g.df(scales=(0.5, 1, 2)).scales == (0.5, 1.0, 2.0)
+    with pytest.raises(ValueError, match="at least one"):
+        g.df(scales=())
+
+
+def test_pairlist_defaults(g):
+    p = g.pairlist()
+    assert (p.eps, p.pad, p.unique, p.skip_pad) == (1e-7, g.SCREEN_PAD, False, False)
+    assert g.SCREEN_PAD == 2.0
+    assert g.pairlist(1e-5, unique=True).unique is True
+
+
+def test_make_coulomb_resolves_only_the_screened_df_strategy(g):
+    from gs_dft_amd.terms import _make_coulomb
+    t = _make_coulomb(g.df(lam=1e-6), screened=True, skip_pad=True)
+    assert isinstance(t, g.ScreenedProductDFCoulomb) and t.lam == 1e-6 and t.skip_pad
+    with pytest.raises(NotImplementedError):
+        _make_coulomb(g.df(), screened=False)
+    with pytest.raises(NotImplementedError):
+        _make_coulomb(g.exact(), screened=True)
+    with pytest.raises(NotImplementedError):
+        _make_coulomb(g.df(), screened=True, a_x=0.25)
+    with pytest.raises(TypeError):
+        _make_coulomb("df", screened=True)
+
+
+def test_train_pad_rule(g):
+    """pad_to = ceil(pad * n0 / G) * G (gs_dft/ks/train.py:359)."""
+    assert g.train_pad_to(g.pairlist(), 1001) == 2002
+    assert g.train_pad_to(g.pairlist(pad=1.5), 1001, 4) == 1504
+    assert g.train_pad_to(g.pairlist(pad=1.25), 7) == 8
+
+
+def test_state_checks(g):
+    ks = g.SplatDFJ(coulomb=g.df(), screen=g.pairlist())
+    with pytest.raises(ValueError, match="state.pairs"):
+        ks._check_state(g.SplatState())
+    with pytest.raises(ValueError, match="product aux"):
+        ks._check_state(g.SplatState(pairs=(1, 2, 3)))
+    with pytest.raises(NotImplementedError):
+        g.SplatDFJ(coulomb=g.df(), screen=None)
+    with pytest.raises(NotImplementedError):
+        g.SplatDFJ(coulomb=g.df(), screen=g.pairlist(), mesh=object())
+
+
+def test_workloads_are_deterministic_and_sized(wl):
+    a, b = wl.make_system(1), wl.make_system(1)
+    assert (a.quat == b.quat).all() and (a.C == b.C).all()
+    assert (a.M, a.k, a.n_aux) == (126, 11, 504)
+    s3 = wl.make_system(3)
+    assert (s3.M, s3.k, s3.n_aux) == (2000, 81, 8000) and s3.atoms.shape == (62, 3)
+    import numpy as np
+    assert abs(np.linalg.norm(s3.C, axis=0).mean() - np.sqrt(2000 / 81)) < 0.5

@@ -1,0 +1,415 @@
+"""Pins the CPU oracle (oracle/c/oracle.c) before it is trusted as the parity checker.
+
+Every check below is independent of the oracle's own formulas: closed forms (isotropic overlap,
+Gaussian Coulomb integrals, point-charge limits), invariants (normalisation, symmetry, rotation
+equivariance), LAPACK, brute force, a literal eigh-based restatement of the reference kernel in
+torch (oracle/torch_ref.py) with autograd for gradients, and finite differences. The reference
+holds no golden vectors for this path (every DF-J test in gs-dft is relational), so these are
+the pins.
+"""
+import math
+import re
+
+import numpy as np
+import pytest
+import torch
+from scipy.special import erf
+
+from conftest import ROOT, rel_max
+
+
+def _t(x, grad=False):
+    t = torch.as_tensor(np.asarray(x), dtype=torch.float64).clone()
+    return t.requires_grad_(grad) if grad else t
+
+
+def _idx(a):
+    return torch.as_tensor(np.asarray(a, dtype=np.int64))
+
+
+# ----------------------------------------------------------------------------- node table
+
+def test_quad_table_newton_matches_numpy_leggauss(orc):
+    t, w = orc.quad_table(20)
+    tn, wn = orc.reference_quad_table(20)
+    # the half-line map amplifies node round-off by 1/(1-s) ~ 300 at the last node
+    assert rel_max(t, tn) < 1e-13 and np.max(np.abs(w - wn) / wn) < 1e-12
+
+
+def test_library_table_is_numpy_leggauss_bit_exact(orc):
+    src = (ROOT / "gs-dft_amd" / "csrc" / "common.h").read_text()
+    blocks = re.findall(r"constexpr double [tw]\[kNodes\] = \{(.*?)\};", src, re.S)
+    assert len(blocks) == 2
+    vals = [np.array([float.fromhex(v.strip()) for v in b.split(",")]) for b in blocks]
+    tn, wn = orc.reference_quad_table(20)
+    assert np.array_equal(vals[0], tn) and np.array_equal(vals[1], wn)
+
+
+def test_quad_table_integrates_the_coulomb_kernel(orc):
+    """sum_t w_t exp(-t^2 r^2) ~ sqrt(pi)/(2 r): the half-line rule behind 1/r (the 20 nodes are
+    accurate to ~1e-3 relative at r ~ 0.1-10, which is why parity is against the same rule)."""
+    t, w = orc.reference_quad_table(20)
+    for r in (0.3, 1.0, 3.0):
+        approx = np.sum(w * np.exp(-(t * r) ** 2))
+        assert abs(approx - math.sqrt(math.pi) / (2 * r)) < 2e-3 * math.sqrt(math.pi) / (2 * r)
+
+
+# ----------------------------------------------------------------------------- chart
+
+def test_chart_matches_literal_restatement_and_closed_forms(orc, tr, wl):
+    s = wl.make_small(40, 3, seed=3)
+    A, N = orc.chart(s.quat, s.log_scale)
+    At = tr.splat_A(_t(s.quat), _t(s.log_scale)).numpy()
+    assert np.max(np.abs(A - At)) < 1e-14 * np.max(np.abs(At))
+    # det A = exp(sum l), N = (8 det A / pi^3)^(1/4): eigen-structure closed forms. The chart
+    # divides q by |q| + 1e-12 (spectral.py:35), so R is orthogonal only to ~2e-12 and these hold
+    # to ~1e-11.
+    assert np.max(np.abs(np.linalg.det(A) / np.exp(s.log_scale.sum(1)) - 1)) < 1e-10
+    assert np.max(np.abs(N - (8 * np.exp(s.log_scale.sum(1)) / math.pi ** 3) ** 0.25) / N) < 1e-15
+    ev = np.sort(np.linalg.eigvalsh(A), axis=1)
+    assert np.max(np.abs(ev / np.sort(np.exp(s.log_scale), axis=1) - 1)) < 1e-10
+
+
+def test_chart_rotation_equivariance(orc, tr, wl):
+    """q -> q_Q (x) q gives A -> Q A Q^T (gs-dft tests/unit/test_splat_chart.py:35)."""
+    s = wl.make_small(12, 3, seed=4)
+    qQ = np.array([0.3, -0.5, 0.7, 0.2]); qQ /= np.linalg.norm(qQ)
+    Q = tr.quat_to_rotation(_t(qQ)).numpy()
+    aw, ax, ay, az = qQ
+    b = s.quat
+    qrot = np.stack([aw * b[:, 0] - ax * b[:, 1] - ay * b[:, 2] - az * b[:, 3],
+                     aw * b[:, 1] + ax * b[:, 0] + ay * b[:, 3] - az * b[:, 2],
+                     aw * b[:, 2] - ax * b[:, 3] + ay * b[:, 0] + az * b[:, 1],
+                     aw * b[:, 3] + ax * b[:, 2] - ay * b[:, 1] + az * b[:, 0]], axis=1)
+    A, _ = orc.chart(s.quat, s.log_scale)
+    Ar, _ = orc.chart(qrot, s.log_scale)
+    # equivariance holds to the chart's own orthogonality (~1e-11, see the |q| + 1e-12 above)
+    assert np.max(np.abs(Ar - np.einsum("ij,mjk,lk->mil", Q, A, Q))) < 1e-10 * np.max(np.abs(A))
+
+
+# ----------------------------------------------------------------------------- overlap
+
+def test_overlap_isotropic_closed_form(orc):
+    rng = np.random.default_rng(5)
+    M = 30
+    alpha = np.exp(rng.uniform(-2, 2, M))
+    quat = np.tile([1.0, 0, 0, 0], (M, 1))
+    ls = np.repeat(np.log(alpha)[:, None], 3, 1)
+    mu = rng.normal(0, 1.5, (M, 3))
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    S = orc.overlap_pairs(quat, ls, mu, pi, pj)
+    ai, aj = alpha[pi], alpha[pj]
+    d2 = np.sum((mu[pi] - mu[pj]) ** 2, 1)
+    ref = (2 * np.sqrt(ai * aj) / (ai + aj)) ** 1.5 * np.exp(-ai * aj / (ai + aj) * d2)
+    assert np.max(np.abs(S - ref) / ref) < 1e-13
+
+
+def test_overlap_normalised_symmetric_and_literal(orc, tr, wl):
+    s = wl.make_small(25, 3, seed=6)
+    M = s.M
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    S = orc.overlap_pairs(s.quat, s.log_scale, s.centers, pi, pj).reshape(M, M)
+    # unit-normalised splats (to the chart's ~1e-11 orthogonality, spectral.py:35), symmetric,
+    # and bounded by Cauchy-Schwarz
+    assert np.max(np.abs(np.diag(S) - 1.0)) < 1e-10
+    assert np.max(np.abs(S - S.T)) < 1e-14 * np.max(S)
+    assert np.all(S <= 1.0 + 1e-10)
+    St = tr.full_overlap_pairs(_t(s.quat), _t(s.log_scale), _t(s.centers), _idx(pi), _idx(pj))
+    assert np.max(np.abs(S.reshape(-1) - St.numpy()) / St.numpy()) < 1e-13
+
+
+# ----------------------------------------------------------------------------- pair list
+
+def _dense_S(tr, s):
+    M = s.M
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    return np.abs(tr.full_overlap_pairs(_t(s.quat), _t(s.log_scale), _t(s.centers), _idx(pi),
+                                        _idx(pj)).numpy()).reshape(M, M)
+
+
+@pytest.mark.parametrize("unique", [False, True])
+@pytest.mark.parametrize("eps", [1e-2, 1e-5, 1e-9])
+def test_pairs_are_the_thresholded_set_lexsorted(orc, tr, wl, unique, eps):
+    """gs-dft tests/unit/test_device_pairs.py:50 and test_pair_tricks.py:229."""
+    s = wl.make_small(60, 3, n_atoms=5, spread=4.0, seed=8)
+    S = _dense_S(tr, s)
+    M = s.M
+    want = [(i, j) for i in range(M) for j in range(M) if S[i, j] > eps and (j >= i or not unique)]
+    # knife-edge audit: no pair within 1e-10 relative of eps, so the literal/oracle ulp-level
+    # differences cannot flip membership
+    assert not np.any(np.abs(S - eps) < 1e-10 * eps)
+    pi, pj, w, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, None, unique)
+    assert n_sig == len(want) == len(pi)
+    assert list(zip(pi.tolist(), pj.tolist())) == want
+    exp_w = [(1.0 if i == j else 2.0) if unique else 1.0 for i, j in want]
+    assert np.array_equal(w, exp_w)
+    assert orc.count_significant(s.quat, s.log_scale, s.centers, eps, unique) == len(want)
+
+
+def test_unique_covers_ordered_with_weights(orc, wl):
+    """gs-dft tests/unit/test_pair_tricks.py:44."""
+    s = wl.make_small(48, 3, n_atoms=6, spread=3.0, seed=9)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-6, None, False)
+    ui, uj, uw, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-6, None, True)
+    assert np.all(uj >= ui) and set(np.unique(uw)) <= {1.0, 2.0}
+    assert int(uw.sum()) == len(pi)
+    ordered = set(zip(pi.tolist(), pj.tolist()))
+    assert all((i, j) in ordered for i, j in zip(ui.tolist(), uj.tolist()))
+
+
+def test_padding_tail_and_full_lists(orc, wl):
+    """gs-dft tests/unit/test_device_pairs.py:62,91,146 and test_pair_tricks.py:57."""
+    s = wl.make_small(24, 3, seed=10)
+    M = s.M
+    pi, pj, w, n = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    pad = len(pi) + 37
+    qi, qj, qw, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, pad, False)
+    assert len(qi) == pad and np.array_equal(qi[:len(pi)], pi) and np.all(qw[len(pi):] == 0)
+    assert np.all(qi[len(pi):] == 0) and np.all(qj[len(pi):] == 0)
+    big = M * M + 500
+    bi, _, bw, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, big, False)
+    assert len(bi) == big
+    for pad_to in (None, M * M, M * M + 313):
+        fi, fj, fw, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, -1.0, pad_to, False)
+        assert np.array_equal(fi[:M * M], np.repeat(np.arange(M), M))
+        assert np.array_equal(fj[:M * M], np.tile(np.arange(M), M))
+        assert np.all(fw[:M * M] == 1) and np.all(fw[M * M:] == 0)
+    ui, uj, uw, _ = orc.neighbor_pairs(s.quat[:7], s.log_scale[:7], s.centers[:7], -1.0, None, True)
+    assert len(ui) == 28 and uw.sum() == 49.0
+
+
+def test_overflow_keeps_the_largest_exactly(orc, tr, wl):
+    """gs-dft tests/unit/test_pair_tricks.py:260: the pad_to largest |S|, re-lexsorted, and
+    ValueError beyond twice the pad (pairs.py:157-161)."""
+    s = wl.make_small(40, 3, n_atoms=4, spread=3.0, seed=11)
+    S = _dense_S(tr, s)
+    M = s.M
+    for unique in (False, True):
+        mask = S > 1e-6
+        if unique:
+            mask &= np.triu(np.ones((M, M), bool))
+        flat = np.nonzero(mask.reshape(-1))[0]
+        vals = S.reshape(-1)[flat]
+        pad = len(flat) // 2 + 1
+        want = np.sort(flat[np.argsort(-vals, kind="stable")[:pad]])
+        pi, pj, w, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-6, pad, unique)
+        got = pi.astype(np.int64) * M + pj
+        assert n_sig == len(flat) and np.array_equal(got, want) and np.all(w > 0)
+        with pytest.raises(ValueError):
+            orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-6, len(flat) // 3, unique)
+
+
+# ----------------------------------------------------------------------------- aux + metric
+
+def test_product_aux_closed_form_and_literal(orc, tr, wl):
+    s = wl.make_small(30, 3, seed=12)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (0.5, 1.0, 2.0))
+    lat, act = tr.init_product_aux(_t(s.quat), _t(s.log_scale), _t(s.centers), (0.5, 1.0, 2.0))
+    assert np.max(np.abs(la - lat.numpy())) < 1e-14 and np.max(np.abs(ac - act.numpy())) < 1e-13
+    # self-product exponent det(2A)^(1/3) = 2 exp(mean l) (to the chart's ~1e-11 orthogonality),
+    # centre = the splat centre
+    base = np.log(2.0) + s.log_scale.mean(1)
+    M = s.M
+    for k, sc in enumerate((0.5, 1.0, 2.0)):
+        assert np.max(np.abs(la[k * M:(k + 1) * M] - (base + np.log(sc)))) < 1e-10
+        assert np.max(np.abs(ac[k * M:(k + 1) * M] - s.centers)) < 1e-12
+    assert len(la) == 3 * M                       # N_aux = mult * M (test_aux_mult.py:29)
+
+
+def _gauss_coulomb(a, A, b, B):
+    """(s_a|1/r|s_b) of unit-L2-normalised s-Gaussians, textbook erf form."""
+    NA, NB = (2 * a / math.pi) ** 0.75, (2 * b / math.pi) ** 0.75
+    p = a * b / (a + b)
+    R = np.linalg.norm(np.asarray(A) - np.asarray(B))
+    pref = NA * NB * (math.pi / a) ** 1.5 * (math.pi / b) ** 1.5
+    return pref * (erf(math.sqrt(p) * R) / R if R > 0 else 2 * math.sqrt(p / math.pi))
+
+
+def test_metric_textbook_closed_form_and_limits(orc):
+    rng = np.random.default_rng(13)
+    N = 40
+    la = rng.uniform(-2.5, 2.0, N)
+    cen = rng.normal(0, 2.0, (N, 3))
+    cen[5] = cen[4]                                        # a coincident pair (T = 0)
+    V = orc.aux_metric(la, cen)
+    beta = np.exp(la)
+    ref = np.array([[_gauss_coulomb(beta[p], cen[p], beta[q], cen[q]) for q in range(N)]
+                    for p in range(N)])
+    assert np.max(np.abs(V - ref) / np.abs(ref)) < 1e-13
+    assert np.max(np.abs(np.diag(V) - 4 * math.pi / beta) * beta) < 1e-13
+    assert np.array_equal(V, V.T)
+    # point-charge limit: charges (2 pi / beta)^(3/4) at large separation
+    far = orc.aux_metric(np.log([0.8, 1.3]), np.array([[0, 0, 0], [0, 0, 60.0]]))
+    q = (2 * math.pi / np.array([0.8, 1.3])) ** 0.75
+    assert abs(far[0, 1] - q[0] * q[1] / 60.0) < 1e-12 * far[0, 1]
+    assert abs(orc.boys0(0.0) - 1.0) < 1e-16 and abs(orc.boys0(1e-13) - (1 - 1e-13 / 3)) < 1e-16
+
+
+def test_cholesky_and_solve_match_lapack(orc, wl):
+    s = wl.make_small(40, 3, seed=14)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (0.5, 1.0, 2.0, 4.0))
+    V = orc.aux_metric(la, ac, 1e-8)
+    L = orc.cholesky(V)
+    Ln = np.linalg.cholesky(V)
+    assert np.max(np.abs(L - Ln)) < 1e-9 * np.max(np.abs(Ln))
+    assert np.all(np.triu(L, 1) == 0)
+    g = np.random.default_rng(0).normal(size=V.shape[0])
+    d = orc.cho_solve(L, g)
+    dn = np.linalg.solve(V, g)
+    # relational bound of gs-dft tests/unit/test_refresh_cholv.py:24 (cho_solve == dense solve)
+    assert abs(0.5 * g @ d - 0.5 * g @ dn) < 1e-10 * max(1.0, abs(0.5 * g @ dn))
+
+
+# ----------------------------------------------------------------------------- three-centre
+
+def test_three_centre_matches_literal_eigh_kernel(orc, tr, wl):
+    s = wl.make_small(20, 3, seed=15)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (0.5, 2.0))
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-9, None, True)
+    B = orc.three_center_block(s.quat, s.log_scale, s.centers, la, ac, pi, pj)
+    A, N = tr.splat_A(_t(s.quat), _t(s.log_scale)), tr.splat_norm(_t(s.log_scale))
+    Bt = tr.full_isobra_block(*tr.aux_quantities(_t(la), _t(ac)),
+                              *tr.full_pair_quantities(A, _t(s.centers), N, _idx(pi), _idx(pj))).numpy()
+    assert np.max(np.abs(B - Bt) / np.abs(Bt)) < 1e-12
+
+
+def test_three_centre_structure_converges_to_boys(orc, tr):
+    """Isotropic pair products: the (iso aux | pair) integral is the textbook s-s Coulomb
+    integral. The reference's integrand (literal eigh form) under a 400-node rule reproduces the
+    closed form to 1e-9, and the 20-node oracle agrees with the 20-node literal kernel; so the
+    prefactor and node algebra are pinned independently of the 20-node table."""
+    rng = np.random.default_rng(16)
+    M = 6
+    alpha = np.exp(rng.uniform(-1.5, 1.0, M))
+    quat = np.tile([1.0, 0, 0, 0], (M, 1))
+    ls = np.repeat(np.log(alpha)[:, None], 3, 1)
+    mu = rng.normal(0, 1.2, (M, 3))
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    la = rng.uniform(-1.0, 1.5, 5)
+    ac = rng.normal(0, 1.5, (5, 3))
+    x, wl_ = np.polynomial.legendre.leggauss(400)
+    sgl = (x + 1) / 2
+    table = ([float(v) for v in sgl / (1 - sgl)], [float(v) for v in (wl_ / 2) / (1 - sgl) ** 2])
+    A, N = tr.splat_A(_t(quat), _t(ls)), tr.splat_norm(_t(ls))
+    Ah, P, KN = tr.full_pair_quantities(A, _t(mu), N, _idx(pi), _idx(pj))
+    Bconv = tr.full_isobra_block(*tr.aux_quantities(_t(la), _t(ac)), Ah, P, KN, table).numpy()
+    beta = np.exp(la)
+    p = alpha[pi] + alpha[pj]
+    for a_ in range(len(pi)):
+        for P_ in range(len(la)):
+            # pair product = KN_a * exp(-p |r - P|^2); aux = KN_P exp(-beta |r - R|^2)
+            R = np.linalg.norm(ac[P_] - P.numpy()[a_])
+            red = beta[P_] * p[a_] / (beta[P_] + p[a_])
+            F0 = erf(math.sqrt(red) * R) / (R * math.sqrt(red)) * math.sqrt(math.pi) / 2 if R > 0 else 1.0
+            ref = ((2 * beta[P_] / math.pi) ** 0.75 * KN.numpy()[a_] * 2 * math.pi ** 2.5
+                   / (beta[P_] * p[a_] * math.sqrt(beta[P_] + p[a_])) * F0)
+            assert abs(Bconv[P_, a_] - ref) < 1e-9 * abs(ref)
+    B20 = orc.three_center_block(quat, ls, mu, la, ac, pi, pj)
+    B20t = tr.full_isobra_block(*tr.aux_quantities(_t(la), _t(ac)), Ah, P, KN).numpy()
+    assert np.max(np.abs(B20 - B20t) / np.abs(B20t)) < 1e-12
+
+
+# ----------------------------------------------------------------------------- gamma / E_J / grads
+
+def _system(wl, orc, M=24, k=5, seed=1, n_scales=2, eps=1e-7, unique=True):
+    s = wl.make_small(M, k, n_atoms=3, seed=seed, n_scales=n_scales)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, None, unique)
+    return s, la, ac, pi, pj, w
+
+
+def test_gamma_matches_literal(orc, tr, wl):
+    s, la, ac, pi, pj, w = _system(wl, orc)
+    g = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w)
+    gt = tr.gamma_screened(_t(s.quat), _t(s.log_scale), _t(s.centers), _t(s.C), _t(s.occ),
+                           _t(la), _t(ac), _idx(pi), _idx(pj), _t(w), chunk=50)
+    assert rel_max(g, gt.numpy()) < 1e-13
+
+
+def test_unique_equals_ordered_values_and_gradients(orc, wl):
+    """gs-dft tests/unit/test_pair_tricks.py:81 (relational: the unique list with weights 2 - d_ij
+    must reproduce the ordered list)."""
+    s, la, ac, ui, uj, uw = _system(wl, orc, unique=True)
+    _, _, _, oi, oj, ow = _system(wl, orc, unique=False)
+    gu = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, ui, uj, uw)
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, oi, oj, ow)
+    assert rel_max(gu, go) < 1e-12
+    gu_ = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, ui, uj, uw, gu)
+    go_ = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, oi, oj, ow, go)
+    for a, b in zip(gu_[1:], go_[1:]):
+        assert rel_max(a, b) < 1e-11
+
+
+def test_energy_and_gradients_match_autograd_of_literal(orc, tr, wl):
+    s, la, ac, pi, pj, w = _system(wl, orc, M=20, k=4, seed=2)
+    lam = 1e-8
+    E, J, dq, dl, dc, dC = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac,
+                                        pi, pj, w, lam)
+    q, l, c, C = (_t(a, True) for a in (s.quat, s.log_scale, s.centers, s.C))
+    g = tr.gamma_screened(q, l, c, C, _t(s.occ), _t(la), _t(ac), _idx(pi), _idx(pj), _t(w))
+    V = tr.aux_metric(_t(la), _t(ac)) + lam * torch.eye(len(la), dtype=torch.float64)
+    Et = tr.coulomb_solve(g, torch.linalg.cholesky(V))
+    Et.backward()
+    assert abs(E - Et.item()) < 1e-11 * abs(E) and E > 0
+    for a, b in ((dq, q.grad), (dl, l.grad), (dc, c.grad), (dC, C.grad)):
+        assert rel_max(a, b.numpy()) < 1e-9
+    # J_a = dE/dq_a: the derivative of the literal E w.r.t. the pair densities
+    gq = torch.zeros(len(pi), dtype=torch.float64, requires_grad=True)
+    qa = _t(w) * torch.sum(_t(s.occ)[None] * _t(s.C)[_idx(pi)] * _t(s.C)[_idx(pj)], 1)
+    A, N = tr.splat_A(_t(s.quat), _t(s.log_scale)), tr.splat_norm(_t(s.log_scale))
+    B = tr.full_isobra_block(*tr.aux_quantities(_t(la), _t(ac)),
+                             *tr.full_pair_quantities(A, _t(s.centers), N, _idx(pi), _idx(pj)))
+    Eq = tr.coulomb_solve(B @ (qa + gq), torch.linalg.cholesky(V))
+    Eq.backward()
+    assert rel_max(J, gq.grad.numpy()) < 1e-10
+
+
+def test_gradients_finite_differences(orc, wl):
+    """Central differences of the oracle's own E_J (coarse: 1e-6) on a few coordinates."""
+    s, la, ac, pi, pj, w = _system(wl, orc, M=16, k=3, seed=3)
+    lam = 1e-8
+
+    def energy(quat, ls, cen, C):
+        return orc.dfj_energy(quat, ls, cen, C, s.occ, la, ac, pi, pj, w, lam)[0]
+
+    E, J, dq, dl, dc, dC = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac,
+                                        pi, pj, w, lam)
+    h = 1e-5
+    for which, grad in ((0, dq), (1, dl), (2, dc), (3, dC)):
+        base = [s.quat.copy(), s.log_scale.copy(), s.centers.copy(), s.C.copy()]
+        for (r, col) in ((0, 0), (3, 1), (7, grad.shape[1] - 1)):
+            up = [b.copy() for b in base]; dn = [b.copy() for b in base]
+            up[which][r, col] += h; dn[which][r, col] -= h
+            fd = (energy(*up) - energy(*dn)) / (2 * h)
+            assert abs(fd - grad[r, col]) < 1e-6 * max(1.0, np.max(np.abs(grad)))
+
+
+def test_gradients_finite_at_isotropic_splats(orc, wl):
+    """The reference's eigh VJP is NaN at exactly degenerate Ah (gs_dft/coulomb/ri.py:139-143);
+    the invariant form is smooth there, and its gradient matches finite differences."""
+    s = wl.make_small(10, 3, seed=4)
+    ls = np.repeat(s.log_scale[:, :1], 3, 1)                   # isotropic splats
+    la, ac = orc.product_aux(s.quat, ls, s.centers, (1.0,))
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, ls, s.centers, 1e-7, None, True)
+    E, J, dq, dl, dc, dC = orc.dfj_grad(s.quat, ls, s.centers, s.C, s.occ, la, ac, pi, pj, w, 1e-8)
+    for a in (dq, dl, dc, dC):
+        assert np.all(np.isfinite(a))
+    assert np.max(np.abs(dq)) < 1e-8 * max(1.0, np.max(np.abs(dc)))   # dA/dq = 0 at isotropy
+    h = 1e-5
+    c2 = s.centers.copy(); c2[2, 1] += h
+    c3 = s.centers.copy(); c3[2, 1] -= h
+    fd = (orc.dfj_energy(s.quat, ls, c2, s.C, s.occ, la, ac, pi, pj, w, 1e-8)[0]
+          - orc.dfj_energy(s.quat, ls, c3, s.C, s.occ, la, ac, pi, pj, w, 1e-8)[0]) / (2 * h)
+    assert abs(fd - dc[2, 1]) < 1e-6 * max(1.0, abs(dc[2, 1]))
+
+
+def test_full_list_equals_dense_sum(orc, wl):
+    """Screened gamma over the full ordered list == the dense contraction over all M^2 pairs
+    with P = C C^T (gs-dft tests/unit/test_coulomb_df.py:107)."""
+    s = wl.make_small(12, 3, seed=5)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (1.0,))
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, -1.0, None, False)
+    g = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w)
+    B = orc.three_center_block(s.quat, s.log_scale, s.centers, la, ac, pi, pj)
+    P = s.C @ np.diag(s.occ) @ s.C.T
+    assert rel_max(g, B @ P.reshape(-1)) < 1e-13
