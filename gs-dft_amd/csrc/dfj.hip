@@ -34,7 +34,7 @@ namespace gsdft {
 namespace {
 
 constexpr int kRec = 16;      // doubles per pair record
-constexpr int kAuxRec = 48;   // doubles per aux record of the reverse pass
+constexpr int kAuxRec = 88;   // doubles per aux record of the reverse pass
 constexpr int kAcc = 25;      // cotangent moments per pair
 
 inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
@@ -196,6 +196,9 @@ __global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const double* __re
                                                    const double* __restrict__ rec,
                                                    int64_t per_slab,
                                                    double* __restrict__ partial) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
     const int64_t P = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = P < N;
     const double b = live ? beta[P] : 1.0;
@@ -226,10 +229,11 @@ __global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const double* __re
             const double st = s[t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const double y = rsqrt_nr(Pn);
-            const double e = exp_fast(-(st * Qn) * (y * y));
+            const double y = rsqrt1(Pn);
+            const double e = exp_neg_tab((st * Qn) * (y * y), tab);
             F = __builtin_fma(wp[t] * y, e, F);
         }
+        F = (q0 == q0) ? F : q0;                 // a NaN centre propagates, as in the reference
         acc = __builtin_fma(F, coef, acc);
     }
     if (live) partial[blockIdx.y * N + P] = acc * kn[P];
@@ -246,7 +250,7 @@ __global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ 
 
 // ------------------------------------------------------------------ reverse
 
-// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | pad (3) | s_t (20) | wp_t (20).
+// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | pad (3) | s_t | wp_t | s_t^2 | s_t^3.
 __global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
                                const double* __restrict__ dgamma,
@@ -260,17 +264,26 @@ __global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
     o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
     o[3] = dgamma[p] * (dscale ? *dscale : 1.0) * kn[p];
     o[4] = b; o[5] = 0.0; o[6] = 0.0; o[7] = 0.0;
-    for (int t = 0; t < kNodes; ++t) { o[8 + t] = s[t]; o[28 + t] = wp[t]; }
+    for (int t = 0; t < kNodes; ++t) {
+        o[8 + t] = s[t];
+        o[8 + kNodes + t] = wp[t];
+        o[8 + 2 * kNodes + t] = s[t] * s[t];
+        o[8 + 3 * kNodes + t] = s[t] * s[t] * s[t];
+    }
 }
 
-// One lane per pair; accumulates over a slab of aux functions
+// One lane per pair; accumulates over a slab of aux functions (u = dgamma_P KN_P)
 //   jt = sum u F,  T1/T2/T3 = sum u dF/dI1,I2,I3 (through Pn and Qn),
 //   Vc = sum u dQ0 d, Va = sum u dQ1 d, Vb = sum u dQ2 d, Sa = sum u dQ1 d d^T, Sb = sum u dQ2 d d^T
-// where dQk = sum_t (df/dQn) s^k and df/dQn = -f s / Pn.
+// where dQk = sum_t (df/dQn) s^k = -sum_t g_t s^(k+1), dPk = sum_t (df/dPn) s^k, with
+// f_t = wp_t y e^-z, y = Pn^(-1/2), z = s Qn / Pn, g_t = f_t / Pn and df/dPn = g_t (z - 1/2).
 __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __restrict__ rec,
                                                    int64_t N, const double* __restrict__ aux,
                                                    int64_t per_slab,
                                                    double* __restrict__ partial) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = a < n;
     const double* __restrict__ r = rec + kRec * (live ? a : 0);
@@ -294,42 +307,40 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
         const double q2 = ax * ax + ay * ay + az * az;
         const double X0 = I3 * q0;
         const double rr = I1 * q1 - q2;
-        double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, dQ0 = 0, dQ1 = 0, dQ2 = 0;
+        double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
 #pragma unroll
         for (int t = 0; t < kNodes; ++t) {
             const double st = x[8 + t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const double y = rsqrt_nr(Pn);
+            const double y = rsqrt1(Pn);
             const double y2 = y * y;
-            const double arg = -(st * Qn) * y2;
-            const double f = x[28 + t] * y * exp_fast(arg);
+            const double z = (st * Qn) * y2;
+            const double f = (x[8 + kNodes + t] * y) * exp_neg_tab(z, tab);
             F += f;
-            const double fy2 = f * y2;
-            const double fP = fy2 * (-arg - 0.5);       // df/dPn
-            const double fQ = -fy2 * st;                // df/dQn
-            const double fPs = fP * st, fQs = fQ * st;
-            dP0 += fP;
-            dP1 += fPs;
-            dP2 = __builtin_fma(fPs, st, dP2);
-            dQ0 += fQ;
-            dQ1 += fQs;
-            dQ2 = __builtin_fma(fQs, st, dQ2);
+            const double g = f * y2;
+            const double gh = g * (z - 0.5);            // df/dPn
+            dP0 += gh;
+            dP1 = __builtin_fma(gh, st, dP1);
+            dP2 = __builtin_fma(gh, x[8 + 2 * kNodes + t], dP2);
+            gs1 = __builtin_fma(g, st, gs1);
+            gs2 = __builtin_fma(g, x[8 + 2 * kNodes + t], gs2);
+            gs3 = __builtin_fma(g, x[8 + 3 * kNodes + t], gs3);
         }
+        F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
+        const double dQ0 = -gs1, dQ1 = -gs2, dQ2 = -gs3;
         jt = __builtin_fma(u, F, jt);
         T3 = __builtin_fma(u, __builtin_fma(q0, dQ0, dP0), T3);
         T2 = __builtin_fma(u, dP1, T2);
         T1 = __builtin_fma(u, __builtin_fma(q1, dQ1, dP2), T1);
         const double c0 = u * dQ0, c1 = u * dQ1, c2 = u * dQ2;
-#pragma unroll
-        for (int m = 0; m < 3; ++m) {
-            Vc[m] = __builtin_fma(c0, d[m], Vc[m]);
-            const double e1 = c1 * d[m], e2 = c2 * d[m];
-            Va[m] += e1;
-            Vb[m] += e2;
-        }
         const double e1x = c1 * d[0], e1y = c1 * d[1], e1z = c1 * d[2];
         const double e2x = c2 * d[0], e2y = c2 * d[1], e2z = c2 * d[2];
+        Vc[0] = __builtin_fma(c0, d[0], Vc[0]);
+        Vc[1] = __builtin_fma(c0, d[1], Vc[1]);
+        Vc[2] = __builtin_fma(c0, d[2], Vc[2]);
+        Va[0] += e1x; Va[1] += e1y; Va[2] += e1z;
+        Vb[0] += e2x; Vb[1] += e2y; Vb[2] += e2z;
         Sa[0] = __builtin_fma(e1x, d[0], Sa[0]);
         Sa[1] = __builtin_fma(e1y, d[1], Sa[1]);
         Sa[2] = __builtin_fma(e1z, d[2], Sa[2]);
