@@ -774,20 +774,10 @@ extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, 
                                double* energy, void* stream) {
     if (N <= 0 || !L || !gamma || !d) return fail(GSDFT_ERR_ARG, "gsdft_cho_solve: bad arguments");
     hipStream_t s = (hipStream_t)stream;
-    rocblas_handle h;
-    GSDFT_TRY(blas_handle(s, &h));
     GSDFT_HIP(hipMemcpyAsync(d, gamma, sizeof(double) * N, hipMemcpyDeviceToDevice, s));
     profile_begin(kProfSolve, s);
-    // column-major view of row-major L is U = L^T: L y = g is U^T y = g, then L^T d = y is U d = y
-    // (ILP64 entry points: N * N exceeds int32 from N = 46341)
-    rocblas_status st = rocblas_dtrsv_64(h, rocblas_fill_upper, rocblas_operation_transpose,
-                                         rocblas_diagonal_non_unit, N, L, N, d, 1);
-    if (st == rocblas_status_success)
-        st = rocblas_dtrsv_64(h, rocblas_fill_upper, rocblas_operation_none,
-                              rocblas_diagonal_non_unit, N, L, N, d, 1);
+    GSDFT_TRY(launch_trsv_pair(N, L, d, s));
     profile_end(kProfSolve, s);
-    if (st != rocblas_status_success)
-        return fail(GSDFT_ERR_LIB, "rocblas_dtrsv failed (status %d)", (int)st);
     if (energy) {
         k_half_dot<<<1, 1024, 0, s>>>(N, gamma, d, energy);
         GSDFT_HIP(hipGetLastError());

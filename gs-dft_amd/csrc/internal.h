@@ -45,7 +45,10 @@ void profile_end(int id, hipStream_t s);
 enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMetric = 3,
                  kProfCholesky = 4, kProfSolve = 5, kProfCount = 6 };
 
-// chart_screen.hip
+// solve.hip: forward then backward substitution with the row-major lower factor, in place.
+int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
+
+// screen.hip
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,
                  hipStream_t s);
 
