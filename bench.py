@@ -23,8 +23,13 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_FP64 = 78.6e12          # MI355X FP64 (vector and matrix) FLOP/s
 PEAK_HBM = 8.0e12            # MI355X HBM3E bytes/s
-FLOPS_FWD = 379 + 40         # per three-centre integral, transcendentals counted once
-FLOPS_BWD = 740 + 40
+# Algorithmic FP64 work per three-centre integral (P,a) at 20 nodes, transcendentals (rsqrt, exp)
+# counted as one flop each: a per-integral prologue/epilogue plus a per-node part.
+NODES = 20
+FWD_PER_INTEGRAL, FWD_PER_NODE = 39, 17 + 2
+BWD_PER_INTEGRAL, BWD_PER_NODE = 40, 35 + 2
+FLOPS_FWD = FWD_PER_INTEGRAL + NODES * FWD_PER_NODE     # 419
+FLOPS_BWD = BWD_PER_INTEGRAL + NODES * BWD_PER_NODE     # 780
 METRIC = "DF-J fwd+bwd wall ms; 3-centre integrals/s; % of MI355X FP64 peak"
 
 
@@ -42,9 +47,8 @@ def main() -> int:
                     help="target CPU time of the oracle baseline sample (0 disables it)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures the DF-J path on one GPU; --gpus {args.gpus} is not "
-              f"run (the multi-GPU sharding is a design in DESIGN.md, not a measured path)",
-              file=sys.stderr)
+        print(f"bench.py: the DF-J path is measured on one GPU only; --gpus {args.gpus} is not "
+              f"run (sharding over several GPUs is designed, not built)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -104,6 +108,7 @@ def main() -> int:
     torch.cuda.synchronize()
     for kid in (_lib.PROF_GAMMA_FWD, _lib.PROF_GAMMA_BWD, _lib.PROF_SOLVE):
         _lib.profile_read(kid, reset=True)
+        _lib.profile_read_work(kid, reset=True)
     t0 = time.perf_counter()
     for k in range(args.steps):
         E = step()
@@ -113,16 +118,34 @@ def main() -> int:
     fwd_ms, fwd_n = _lib.profile_read(_lib.PROF_GAMMA_FWD, reset=True)
     bwd_ms, bwd_n = _lib.profile_read(_lib.PROF_GAMMA_BWD, reset=True)
     solve_ms, _ = _lib.profile_read(_lib.PROF_SOLVE, reset=True)
+    fwd_nodes = _lib.profile_read_work(_lib.PROF_GAMMA_FWD, reset=True) / max(fwd_n, 1)
+    bwd_nodes = _lib.profile_read_work(_lib.PROF_GAMMA_BWD, reset=True) / max(bwd_n, 1)
     fwd_ms /= max(fwd_n, 1)
     bwd_ms /= max(bwd_n, 1)
     _lib.profile_enable(False)
     integrals = float(N) * float(n)
     fwd_tf = integrals * FLOPS_FWD / (fwd_ms * 1e-3)
     bwd_tf = integrals * FLOPS_BWD / (bwd_ms * 1e-3)
+    # What the kernels executed: the node screen leaves out nodes whose terms are below e^-46.
+    fwd_exec_tf = (integrals * FWD_PER_INTEGRAL + fwd_nodes * FWD_PER_NODE) / (fwd_ms * 1e-3)
+    bwd_exec_tf = (integrals * BWD_PER_INTEGRAL + bwd_nodes * BWD_PER_NODE) / (bwd_ms * 1e-3)
+    fwd_node_frac = fwd_nodes / (NODES * integrals)
+    bwd_node_frac = bwd_nodes / (NODES * integrals)
     log(f"E_J={E.item():.12e} step {wall * 1e3:.1f} ms; three-centre fwd {fwd_ms:.1f} ms "
-        f"({fwd_tf / 1e12:.2f} TFLOP/s), bwd {bwd_ms:.1f} ms ({bwd_tf / 1e12:.2f} TFLOP/s), "
+        f"({fwd_tf / 1e12:.2f} TFLOP/s per integral, {fwd_exec_tf / 1e12:.2f} executed, "
+        f"{100 * fwd_node_frac:.1f}% of nodes), bwd {bwd_ms:.1f} ms ({bwd_tf / 1e12:.2f} / "
+        f"{bwd_exec_tf / 1e12:.2f} TFLOP/s, {100 * bwd_node_frac:.1f}% of nodes), "
         f"solves {solve_ms / max(args.steps, 1):.2f} ms")
-    dom = ("reverse", bwd_ms, FLOPS_BWD, bwd_tf) if bwd_ms >= fwd_ms else ("forward", fwd_ms, FLOPS_FWD, fwd_tf)
+    if bwd_ms >= fwd_ms:
+        dom = ("reverse", "k_gamma_bwd", bwd_ms, FLOPS_BWD, bwd_tf, bwd_exec_tf, bwd_node_frac)
+    else:
+        dom = ("forward", "k_gamma_fwd", fwd_ms, FLOPS_FWD, fwd_tf, fwd_exec_tf, fwd_node_frac)
+    traffic = None
+    tfile = ROOT / "profiles" / "three_centre_traffic.json"
+    if tfile.exists():
+        rec = json.loads(tfile.read_text()).get(s.name, {}).get(dom[1])
+        if rec:
+            traffic = rec["fetch_bytes"] + rec["write_bytes"]
 
     # ------------------------------------------------------------------ CPU baseline (oracle)
     cpu = None
@@ -174,13 +197,22 @@ def main() -> int:
                                f"N_aux={N}, k={s.k}, eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "N_aux": N, "k": s.k, "n_pairs": n,
                    "pad_to": pad_to, "eps": s.eps, "parallelism": "single GPU"},
-        "roofline": {"bound": "fp64-valu", "kernel": f"three-centre {dom[0]}",
-                     "achieved": dom[3] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
-                     "frac": dom[3] / PEAK_FP64, "traffic": None,
-                     "flops_per_integral": dom[2], "integrals_per_launch": integrals,
-                     "kernel_ms": dom[1]},
+        "roofline": {"bound": "mfma", "kernel": f"three-centre {dom[0]} ({dom[1]})",
+                     "achieved": dom[4] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": dom[4] / PEAK_FP64, "traffic": traffic,
+                     "flops_per_integral": dom[3], "integrals_per_launch": integrals,
+                     "kernel_ms": dom[2],
+                     "executed_achieved": dom[5] / 1e12, "executed_frac": dom[5] / PEAK_FP64,
+                     "nodes_evaluated_frac": dom[6],
+                     "note": "FP64 compute bound on the vector ALUs (MI355X FP64 vector peak = "
+                             "FP64 matrix peak = 78.6 TFLOP/s); achieved counts the fixed "
+                             "per-integral work, executed_* only the nodes the screen kept"},
         "kernels": {"three_centre_fwd_ms": fwd_ms, "three_centre_bwd_ms": bwd_ms,
                     "fwd_frac_fp64": fwd_tf / PEAK_FP64, "bwd_frac_fp64": bwd_tf / PEAK_FP64,
+                    "fwd_executed_frac_fp64": fwd_exec_tf / PEAK_FP64,
+                    "bwd_executed_frac_fp64": bwd_exec_tf / PEAK_FP64,
+                    "fwd_nodes_evaluated_frac": fwd_node_frac,
+                    "bwd_nodes_evaluated_frac": bwd_node_frac,
                     "fwd_integrals_per_s": integrals / (fwd_ms * 1e-3),
                     "solves_ms": solve_ms / max(args.steps, 1)},
         "refresh_ms": {"total": t_refresh * 1e3, "count": t_count * 1e3, "screen_kernels": screen_ms,

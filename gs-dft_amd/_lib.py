@@ -54,6 +54,7 @@ SIGNATURES = {
                         _vp],
     "gsdft_profile_enable": [_int],
     "gsdft_profile_read": [_int, _pd, _pi64, _int],
+    "gsdft_profile_read_work": [_int, ctypes.POINTER(ctypes.c_uint64), _int],
 }
 
 _lib = None
@@ -141,3 +142,12 @@ def profile_read(kernel_id: int, reset: bool = False) -> tuple[float, int]:
     check(lib().gsdft_profile_read(int(kernel_id), ctypes.byref(ms), ctypes.byref(n),
                                    int(bool(reset))), "gsdft_profile_read")
     return float(ms.value), int(n.value)
+
+
+def profile_read_work(kernel_id: int, reset: bool = False) -> int:
+    """Work units executed by ``kernel_id`` while profiling was on (three-centre kernels:
+    quadrature nodes evaluated over live lanes)."""
+    units = ctypes.c_uint64(0)
+    check(lib().gsdft_profile_read_work(int(kernel_id), ctypes.byref(units), int(bool(reset))),
+          "gsdft_profile_read_work")
+    return int(units.value)

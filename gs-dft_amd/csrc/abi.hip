@@ -22,6 +22,8 @@ std::vector<EventPair> g_open[kProfCount];     // recorded, not yet read
 std::vector<hipEvent_t> g_pending_start[kProfCount];
 double g_total_ms[kProfCount] = {0};
 int64_t g_launches[kProfCount] = {0};
+unsigned long long* g_work_dev = nullptr;   // kProfCount work counters on g_work_device
+int g_work_device = -1;
 }  // namespace
 
 int fail(int code, const char* fmt, ...) {
@@ -55,6 +57,14 @@ void profile_end(int id, hipStream_t s) {
     g_pending_start[id].pop_back();
 }
 
+unsigned long long* profile_work_counter(int id) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (!g_prof_on || !g_work_dev || id < 0 || id >= kProfCount) return nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != g_work_device) return nullptr;
+    return g_work_dev + id;
+}
+
 }  // namespace gsdft
 
 using namespace gsdft;
@@ -66,6 +76,30 @@ extern "C" const char* gsdft_last_error(void) { return g_err; }
 extern "C" int gsdft_profile_enable(int on) {
     std::lock_guard<std::mutex> lk(g_prof_mu);
     g_prof_on = on != 0;
+    if (g_prof_on && !g_work_dev) {
+        GSDFT_HIP(hipGetDevice(&g_work_device));
+        GSDFT_HIP(hipMalloc((void**)&g_work_dev, sizeof(unsigned long long) * kProfCount));
+        GSDFT_HIP(hipMemset(g_work_dev, 0, sizeof(unsigned long long) * kProfCount));
+    }
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_profile_read_work(int id, uint64_t* units, int reset) {
+    if (id < 0 || id >= kProfCount || !units)
+        return fail(GSDFT_ERR_ARG, "gsdft_profile_read_work: bad id");
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    *units = 0;
+    if (!g_work_dev) return GSDFT_OK;
+    int dev = -1;
+    GSDFT_HIP(hipGetDevice(&dev));
+    GSDFT_HIP(hipSetDevice(g_work_device));
+    unsigned long long v = 0;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(&v, g_work_dev + id, sizeof v, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && reset) e = hipMemset(g_work_dev + id, 0, sizeof v);
+    (void)hipSetDevice(dev);
+    if (e != hipSuccess) return hip_fail(e, "gsdft_profile_read_work");
+    *units = (uint64_t)v;
     return GSDFT_OK;
 }
 

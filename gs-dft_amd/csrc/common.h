@@ -73,10 +73,15 @@ __device__ __forceinline__ double exp_fast(double x) {
 // 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308 stands in for the
 // smaller values, whose contribution to any node sum is far below round-off). A NaN z is lost
 // here; callers check their inputs for NaN once per integral instead of once per node.
+// The integer 256 m + j = round(-z 256/ln2) is formed by adding 1.5 * 2^52 in the same fma: the
+// sum's unit in the last place is 1, so it is rounded to an integer, which then sits in the low
+// 32 bits of the mantissa as a two's-complement int (|256 m + j| <= 261581 < 2^51).
 __device__ __forceinline__ double exp_neg_tab(double z, const double* __restrict__ tab) {
+    constexpr double kShift = 0x1.8p52;
     z = __builtin_fmin(z, 708.3);
-    const double kf = __builtin_rint(z * -0x1.71547652b82fep+8);        // -z * 256/ln2
-    const int k = (int)kf;
+    const double sh = __builtin_fma(z, -0x1.71547652b82fep+8, kShift);  // -z * 256/ln2 + shift
+    const double kf = sh - kShift;
+    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
     double r = __builtin_fma(-kf, 0x1.62e42fee00000p-9, -z);            // ln2_hi / 256
     r = __builtin_fma(-kf, 0x1.a39ef35793c76p-41, r);                   // ln2_lo / 256
     double p = __builtin_fma(r, 4.16666666666666666667e-02, 1.66666666666666666667e-01);
@@ -84,6 +89,30 @@ __device__ __forceinline__ double exp_neg_tab(double z, const double* __restrict
     p = __builtin_fma(p, r, 1.0);
     p = __builtin_fma(p, r, 1.0);
     return __builtin_ldexp(tab[k & 255] * p, k >> 8);
+}
+
+// One node of the three-centre quadrature: with P = Pn(s) > 0 and sQ = s Qn(s), returns
+// y0 e^(-sQ/P + eps/2) (= P^(-1/2) e^(-sQ/P)) and sets z = sQ/P and ip = 1/P, from the hardware
+// 1/sqrt estimate y0 (relative error ~5e-8) without a separate Newton step. With h = y0^2 and
+// eps = 1 - P h: 1/P = h (1 + eps + eps^2) + O(eps^3) and P^(-1/2) = y0 e^(eps/2 + eps^2/4 + ...),
+// so the result carries a relative error ~eps^2/4 < 3e-15 whatever z is (one Newton step on y0
+// would leave 3 eps^2/8 on y and 3 eps^2/4 z on the exponential).
+struct NodeVal {
+    double y0;   // hardware estimate of P^(-1/2)
+    double z;    // s Qn / Pn
+    double ip;   // 1 / Pn
+    double arg;  // z - eps/2: y0 e^-arg = P^(-1/2) e^-z
+};
+
+__device__ __forceinline__ NodeVal node_val(double P, double sQ) {
+    NodeVal v;
+    v.y0 = __builtin_amdgcn_rsq(P);
+    const double h = v.y0 * v.y0;
+    const double eps = __builtin_fma(-P, h, 1.0);
+    v.ip = __builtin_fma(h, __builtin_fma(eps, eps, eps), h);
+    v.z = sQ * v.ip;
+    v.arg = __builtin_fma(eps, -0.5, v.z);
+    return v;
 }
 
 // 2^(j/256), j = 0..255, correctly rounded (the table of exp_neg_tab).

@@ -24,6 +24,7 @@
 #include <rocsolver/rocsolver.h>
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -104,6 +105,11 @@ __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restr
     double v = (kn[p] * kn[q]) * coul;
     if (p == q) v += lam;
     V[p * N + q] = v;
+}
+
+__global__ void k_fill(int64_t n, double v, double* __restrict__ out) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i < n) out[i] = v;
 }
 
 __global__ void k_zero_upper(int64_t N, double* __restrict__ V) {
@@ -188,27 +194,80 @@ __device__ __forceinline__ void node_consts(double b, double s[kNodes], double w
     }
 }
 
+// ------------------------------------------------------------------ node screen
+// The nodes run in increasing t, and the exponent of node t is
+//   z_t = s_t Qn/Pn = sum_k dp_k^2 / (1/s_t + 1/L_k),   1/s_t = 1/t^2 + 1/b,
+// (dp = d in the eigenbasis of Ah, L_k its eigenvalues), which grows with t. Once z_t > kSkipZ on
+// every live lane of a wave, each remaining node is below e^-46 ~ 1.1e-20 of its own prefactor
+// wp_t Pn^(-1/2) (<= that of the first node, which carries e^-z_0 ~ 1 unless the whole
+// integral is itself that small), so the wave leaves the node loop: the integral changes by less
+// than 1e-18 relative, far below the round-off of the node sum. The reverse pass screens the same
+// way; its node terms carry e^-z times z^m s^k (m <= 1, k <= 3), and z e^-z <= 46 e^-46 ~ 5e-19
+// beyond the cut, so each skipped moment term is as negligible against the kept terms of the
+// same sums over aux functions. Checks start at node kFirstSkip, before which z_t <= t^2 |d|^2
+// stays small for any pair within ~40 Bohr.
+constexpr double kSkipZ = 46.0;
+constexpr int kFirstSkip = 5;
+constexpr int kSkipStride = 2;   // nodes between checks: each check closes a basic block, and two
+                                 // nodes per block leave the scheduler room to hide LDS latency
+
+__host__ __device__ constexpr bool screen_after(int t) {
+    return t >= kFirstSkip && (t - kFirstSkip) % kSkipStride == kSkipStride - 1 && t + 1 < kNodes;
+}
+
+// Lanes past the end of the work hold a centre kFarAway Bohr off (z ~ 1e40 at every node from
+// kFirstSkip on), so they never keep a wave in the loop and need no mask of their own.
+constexpr double kFarAway = 1e20;
+
+__device__ __forceinline__ bool wave_all_beyond(double z) {
+    return __builtin_amdgcn_ballot_w64(!(z > kSkipZ)) == 0;
+}
+
+// body(std::integral_constant<int, t>) for t = 0, 1, ..., kNodes - 1 until it returns true: a
+// fully unrolled node loop with early exits (node tables stay in registers). Returns the number
+// of nodes evaluated (wave-uniform).
+template <int T, class Body>
+__device__ __forceinline__ uint32_t node_loop(Body& body) {
+    if constexpr (T < kNodes) {
+        if (body(std::integral_constant<int, T>{})) return T + 1;
+        return node_loop<T + 1>(body);
+    } else {
+        return kNodes;
+    }
+}
+
+// Profiling only: adds this wave's node evaluations over its live lanes to *work.
+__device__ __forceinline__ void count_work(unsigned long long* work, bool live, uint32_t nodes) {
+    if (!work) return;
+    const uint64_t lanes = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live));
+    if ((threadIdx.x & 63) == 0) atomicAdd(work, (unsigned long long)(lanes * nodes));
+}
+
 // ------------------------------------------------------------------ forward
 
-__global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const double* __restrict__ beta,
+__global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const int32_t* __restrict__ order,
+                                                   const double* __restrict__ beta,
                                                    const double* __restrict__ R,
                                                    const double* __restrict__ kn, int64_t n,
                                                    const double* __restrict__ rec,
                                                    int64_t per_slab,
-                                                   double* __restrict__ partial) {
+                                                   double* __restrict__ partial,
+                                                   unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
-    const int64_t P = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = P < N;
+    const int64_t lane_id = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = lane_id < N;
+    const int64_t P = live ? order[lane_id] : 0;
     const double b = live ? beta[P] : 1.0;
-    const double Rx = live ? R[3 * P] : 0.0, Ry = live ? R[3 * P + 1] : 0.0,
-                 Rz = live ? R[3 * P + 2] : 0.0;
+    const double Rx = live ? R[3 * P] : kFarAway, Ry = live ? R[3 * P + 1] : kFarAway,
+                 Rz = live ? R[3 * P + 2] : kFarAway;
     double s[kNodes], wp[kNodes];
     node_consts(b, s, wp);
     const int64_t a0 = blockIdx.y * per_slab;
     const int64_t a1 = min(n, a0 + per_slab);
     double acc = 0.0;
+    uint32_t nodes = 0;
     for (int64_t a = a0; a < a1; ++a) {
         const double* __restrict__ r = rec + kRec * a;
         const double I1 = r[0], I2 = r[1], I3 = r[2];
@@ -224,19 +283,21 @@ __global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const double* __re
         const double X0 = I3 * q0;
         const double rr = I1 * q1 - q2;
         double F = 0.0;
-#pragma unroll
-        for (int t = 0; t < kNodes; ++t) {
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
             const double st = s[t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const double y = rsqrt1(Pn);
-            const double e = exp_neg_tab((st * Qn) * (y * y), tab);
-            F = __builtin_fma(wp[t] * y, e, F);
-        }
+            const NodeVal v = node_val(Pn, st * Qn);
+            F = __builtin_fma(wp[t] * v.y0, exp_neg_tab(v.arg, tab), F);
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates, as in the reference
         acc = __builtin_fma(F, coef, acc);
     }
     if (live) partial[blockIdx.y * N + P] = acc * kn[P];
+    count_work(work, live, nodes);
 }
 
 __global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ partial,
@@ -280,7 +341,8 @@ __global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
 __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __restrict__ rec,
                                                    int64_t N, const double* __restrict__ aux,
                                                    int64_t per_slab,
-                                                   double* __restrict__ partial) {
+                                                   double* __restrict__ partial,
+                                                   unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
@@ -289,12 +351,14 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
     const double* __restrict__ r = rec + kRec * (live ? a : 0);
     const double I1 = r[0], I2 = r[1], I3 = r[2];
     const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
-    const double Px = r[9], Py = r[10], Pz = r[11];
+    const double Px = live ? r[9] : kFarAway, Py = live ? r[10] : kFarAway,
+                 Pz = live ? r[11] : kFarAway;
     double jt = 0, T1 = 0, T2 = 0, T3 = 0;
     double Vc[3] = {0, 0, 0}, Va[3] = {0, 0, 0}, Vb[3] = {0, 0, 0};
     double Sa[6] = {0, 0, 0, 0, 0, 0}, Sb[6] = {0, 0, 0, 0, 0, 0};
     const int64_t p0 = blockIdx.y * per_slab;
     const int64_t p1 = min(N, p0 + per_slab);
+    uint32_t nodes = 0;
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
         const double u = x[3];
@@ -308,25 +372,25 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
         const double X0 = I3 * q0;
         const double rr = I1 * q1 - q2;
         double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
-#pragma unroll
-        for (int t = 0; t < kNodes; ++t) {
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
             const double st = x[8 + t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const double y = rsqrt1(Pn);
-            const double y2 = y * y;
-            const double z = (st * Qn) * y2;
-            const double f = (x[8 + kNodes + t] * y) * exp_neg_tab(z, tab);
+            const NodeVal v = node_val(Pn, st * Qn);
+            const double f = (x[8 + kNodes + t] * v.y0) * exp_neg_tab(v.arg, tab);
             F += f;
-            const double g = f * y2;
-            const double gh = g * (z - 0.5);            // df/dPn
+            const double g = f * v.ip;
+            const double gh = g * (v.z - 0.5);          // df/dPn
             dP0 += gh;
             dP1 = __builtin_fma(gh, st, dP1);
             dP2 = __builtin_fma(gh, x[8 + 2 * kNodes + t], dP2);
             gs1 = __builtin_fma(g, st, gs1);
             gs2 = __builtin_fma(g, x[8 + 2 * kNodes + t], gs2);
             gs3 = __builtin_fma(g, x[8 + 3 * kNodes + t], gs3);
-        }
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
         const double dQ0 = -gs1, dQ1 = -gs2, dQ2 = -gs3;
         jt = __builtin_fma(u, F, jt);
@@ -354,6 +418,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
         Sb[4] = __builtin_fma(e2x, d[2], Sb[4]);
         Sb[5] = __builtin_fma(e2y, d[2], Sb[5]);
     }
+    count_work(work, live, nodes);
     if (!live) return;
     double* o = partial + (int64_t)blockIdx.y * kAcc * n + a;
     const double v[kAcc] = {jt, T1, T2, T3, Vc[0], Vc[1], Vc[2], Va[0], Va[1], Va[2],
@@ -545,7 +610,11 @@ __global__ __launch_bounds__(256) void k_splat_grad(
 }
 
 // dE/dC_mo = occ_o [sum_{a: i_a=m} J_a w_a C_{j_a o} + sum_{a: j_a=m} J_a w_a C_{i_a o}]
-// (gs_dft/coulomb/ri.py:456 reverse); one wave per splat, lanes over o.
+// (gs_dft/coulomb/ri.py:456 reverse). One workgroup per splat; thread t owns orbitals
+// o = t + 256 c for c < CH, so each pair's scale and partner index are read once per workgroup
+// and the partner's C row is streamed coalesced. Orbitals beyond 256 CH are covered by further
+// passes over the splat's pairs.
+template <int CH>
 __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
                                             const int32_t* __restrict__ row_ptr,
                                             const int32_t* __restrict__ row_perm,
@@ -558,25 +627,37 @@ __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
                                             const double* __restrict__ C,
                                             const double* __restrict__ occ,
                                             double* __restrict__ dC) {
-    const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    if (m >= M) return;
+    const int64_t m = blockIdx.x;
     const int64_t r0 = row_ptr[m], r1 = row_ptr[m + 1], c0 = col_ptr[m], c1 = col_ptr[m + 1];
-    for (int64_t o0 = 0; o0 < k; o0 += 64) {
-        const int64_t o = o0 + lane;
-        const bool on = o < k;
-        double acc = 0.0;
+    for (int64_t base = 0; base < k; base += 256 * CH) {
+        double acc[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) acc[c] = 0.0;
         for (int64_t p = r0; p < r1; ++p) {
             const int64_t a = row_perm[p];
-            const double s = J[a] * weight[a];
-            if (on) acc = __builtin_fma(s, C[(int64_t)pj[a] * k + o], acc);
+            const double sc = J[a] * weight[a];
+            const double* __restrict__ row = C + (int64_t)pj[a] * k;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int64_t o = base + threadIdx.x + 256 * c;
+                if (o < k) acc[c] = __builtin_fma(sc, row[o], acc[c]);
+            }
         }
         for (int64_t p = c0; p < c1; ++p) {
             const int64_t a = col_perm[p];
-            const double s = J[a] * weight[a];
-            if (on) acc = __builtin_fma(s, C[(int64_t)pi[a] * k + o], acc);
+            const double sc = J[a] * weight[a];
+            const double* __restrict__ row = C + (int64_t)pi[a] * k;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int64_t o = base + threadIdx.x + 256 * c;
+                if (o < k) acc[c] = __builtin_fma(sc, row[o], acc[c]);
+            }
         }
-        if (on) dC[m * k + o] = occ[o] * acc;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t o = base + threadIdx.x + 256 * c;
+            if (o < k) dC[m * k + o] = occ[o] * acc[c];
+        }
     }
 }
 
@@ -615,6 +696,7 @@ Split bwd_split(int64_t N, int64_t n) {
 struct GammaWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
     double *aux, *acc, *contrib;
+    AuxOrderWs order;
 };
 
 int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, GammaWs* w) {
@@ -626,6 +708,7 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
     w->rec = ar.take<double>(kRec * n + kRec);
     w->partial = w->aux = w->acc = w->contrib = nullptr;
     if (!reverse) {
+        GSDFT_TRY(aux_order_layout(ar, N, &w->order));
         const Split sp = fwd_split(N, n);
         w->partial = ar.take<double>(sp.slabs * N + 1);
     } else {
@@ -791,7 +874,7 @@ extern "C" int gsdft_gamma_workspace_size(int64_t M, int64_t k, int64_t N, int64
     if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_workspace_size: bad arguments");
     Arena ar{nullptr, 0, 0};
     GammaWs w;
-    layout_gamma(ar, M, N, n, false, &w);
+    GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
     *bytes = ar.need();
     return GSDFT_OK;
 }
@@ -802,7 +885,7 @@ extern "C" int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, i
     if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_vjp_workspace_size: bad arguments");
     Arena ar{nullptr, 0, 0};
     GammaWs w;
-    layout_gamma(ar, M, N, n, true, &w);
+    GSDFT_TRY(layout_gamma(ar, M, N, n, true, &w));
     *bytes = ar.need();
     return GSDFT_OK;
 }
@@ -817,19 +900,21 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GammaWs w;
-    layout_gamma(ar, M, N, n, false, &w);
+    GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
     if (!w.partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_gamma: workspace too small");
     if (n == 0) {
-        GSDFT_HIP(hipMemsetAsync(gamma, 0, sizeof(double) * N, s));
+        k_fill<<<blocks_for(N, 256), 256, 0, s>>>(N, 0.0, gamma);
+        GSDFT_HIP(hipGetLastError());
         return GSDFT_OK;
     }
     GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
                              weight, w, s));
+    GSDFT_TRY(launch_aux_order(N, log_alpha, aux_centers, w.order, s));
     const Split sp = fwd_split(N, n);
     dim3 grid((unsigned)((N + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfGammaFwd, s);
-    k_gamma_fwd<<<grid, 256, 0, s>>>(N, w.beta, aux_centers, w.kn, n, w.rec, sp.per_slab,
-                                     w.partial);
+    k_gamma_fwd<<<grid, 256, 0, s>>>(N, w.order.order, w.beta, aux_centers, w.kn, n, w.rec,
+                                     sp.per_slab, w.partial, profile_work_counter(kProfGammaFwd));
     profile_end(kProfGammaFwd, s);
     GSDFT_HIP(hipGetLastError());
     k_slab_sum<<<blocks_for(N, 256), 256, 0, s>>>(N, sp.slabs, w.partial, gamma);
@@ -853,7 +938,7 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GammaWs w;
-    layout_gamma(ar, M, N, n, true, &w);
+    GSDFT_TRY(layout_gamma(ar, M, N, n, true, &w));
     if (!w.contrib) return fail(GSDFT_ERR_WORKSPACE, "gsdft_gamma_vjp: workspace too small");
     GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
                              weight, w, s));
@@ -863,7 +948,8 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         const Split sp = bwd_split(N, n);
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
-        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec, N, w.aux, sp.per_slab, w.acc);
+        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec, N, w.aux, sp.per_slab, w.acc,
+                                         profile_work_counter(kProfGammaBwd));
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
         k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, pi, pj, weight, w.A6,
@@ -874,8 +960,15 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
                                                          col_perm, w.contrib, quat, log_scale,
                                                          dquat, dlog_scale, dcenters);
-    k_dC<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi,
-                                                 pj, J, weight, C, occ, dC);
+    if (k <= 256)
+        k_dC<1><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
+    else if (k <= 1024)
+        k_dC<4><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
+    else
+        k_dC<8><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }

@@ -42,11 +42,25 @@ struct Arena {
 // Optional per-kernel timing with HIP events on the launch stream.
 void profile_begin(int id, hipStream_t s);
 void profile_end(int id, hipStream_t s);
+// Device counter of work units for kernel id while profiling is on (current device only), else
+// nullptr; kernels given a counter add their executed units to it.
+unsigned long long* profile_work_counter(int id);
 enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMetric = 3,
                  kProfCholesky = 4, kProfSolve = 5, kProfCount = 6 };
 
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
+
+// order.hip: lane order of the forward three-centre pass (order[lane] = aux index).
+struct AuxOrderWs {
+    uint32_t *key_in, *key_out;
+    int32_t *idx_in, *order;
+    char* sort_tmp;
+    size_t sort_bytes;
+};
+int aux_order_layout(Arena& ar, int64_t N, AuxOrderWs* w);
+int launch_aux_order(int64_t N, const double* log_alpha, const double* aux_centers,
+                     const AuxOrderWs& w, hipStream_t s);
 
 // screen.hip
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,

@@ -212,6 +212,42 @@ def test_energy_and_gradients_match_oracle(g, wl, orc, cuda, case):
         assert err < REL_G
 
 
+def test_node_screen_far_apart_matches_oracle(g, wl, orc, cuda):
+    """Atoms spread over 50 Bohr: most waves leave the 20-node loop early (node terms below
+    e^-46 of their prefactor), yet gamma, E_J and every gradient match the oracle's full
+    20-node sums."""
+    from gs_dft_amd import _lib
+    s = wl.make_small(320, 6, n_atoms=10, seed=7, spread=25.0)
+    la, ac, pi, pj, w = _problem(wl, orc, s)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    _lib.profile_enable(True)
+    try:
+        for kid in (_lib.PROF_GAMMA_FWD, _lib.PROF_GAMMA_BWD):
+            _lib.profile_read_work(kid, reset=True)
+        gam = _np(g.df_coulomb_gamma_screened(_splat(g, s), torch.tensor(s.C, device="cuda"),
+                                              s.occ, aux, pi, pj, valid=w))
+        fwd_nodes = _lib.profile_read_work(_lib.PROF_GAMMA_FWD, reset=True)
+        got = _energy_grads(g, s, la, ac, pi, pj, w, s.lam)
+        bwd_nodes = _lib.profile_read_work(_lib.PROF_GAMMA_BWD, reset=True)
+    finally:
+        _lib.profile_enable(False)
+    full = 20 * len(la) * len(pi)
+    print(f"[screen] M={s.M} n={len(pi)} N={len(la)}: nodes evaluated fwd {fwd_nodes / full:.3f} "
+          f"bwd {bwd_nodes / full:.3f} of all")
+    assert 0 < fwd_nodes < 0.9 * full and 0 < bwd_nodes < 0.9 * full
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w)
+    print(f"[screen] gamma rel {rel_max(gam, go):.2e}")
+    assert rel_max(gam, go) < 1e-12
+    ref = orc.dfj_grad(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi, pj, w, s.lam)
+    rel = abs(got[0] - ref[0]) / abs(ref[0])
+    print(f"[screen] E_J rel {rel:.2e}")
+    assert rel < REL_E
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"), got[1:], ref[2:]):
+        err = rel_max(a, b)
+        print(f"[screen] d{name} rel-to-max {err:.2e}")
+        assert err < REL_G
+
+
 def test_J_on_the_pair_list_matches_oracle(g, wl, orc, cuda):
     s = _small(wl, SMALL[1])
     la, ac, pi, pj, w = _problem(wl, orc, s)
