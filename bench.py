@@ -45,7 +45,19 @@ def main() -> int:
     ap.add_argument("--system", type=int, default=5, help="benchmark system 1..5")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 2 GiB device-to-device once (scales the HBM byte counters "
+                         "FETCH_SIZE / WRITE_SIZE of a profiler run) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        x = torch.ones(1 << 28, dtype=torch.float64, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": x.numel() * 8}), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py: the DF-J path is measured on one GPU only; --gpus {args.gpus} is not "
               f"run (sharding over several GPUs is designed, not built)", file=sys.stderr)
