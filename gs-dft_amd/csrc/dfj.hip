@@ -198,21 +198,19 @@ __device__ __forceinline__ void node_consts(double b, double s[kNodes], double w
 // The nodes run in increasing t, and the exponent of node t is
 //   z_t = s_t Qn/Pn = sum_k dp_k^2 / (1/s_t + 1/L_k),   1/s_t = 1/t^2 + 1/b,
 // (dp = d in the eigenbasis of Ah, L_k its eigenvalues), which grows with t. Once z_t > kSkipZ on
-// every live lane of a wave, each remaining node is below e^-46 ~ 1.1e-20 of its own prefactor
-// wp_t Pn^(-1/2) (<= that of the first node, which carries e^-z_0 ~ 1 unless the whole
-// integral is itself that small), so the wave leaves the node loop: the integral changes by less
-// than 1e-18 relative, far below the round-off of the node sum. The reverse pass screens the same
-// way; its node terms carry e^-z times z^m s^k (m <= 1, k <= 3), and z e^-z <= 46 e^-46 ~ 5e-19
-// beyond the cut, so each skipped moment term is as negligible against the kept terms of the
-// same sums over aux functions. Checks start at node kFirstSkip, before which z_t <= t^2 |d|^2
-// stays small for any pair within ~40 Bohr.
-constexpr double kSkipZ = 46.0;
+// every live lane of a wave, each remaining node is below e^-36 ~ 2.3e-16 of its own prefactor
+// wp_t Pn^(-1/2), and the prefactors sum to the integral at zero separation, so the wave leaves
+// the node loop. The reverse pass screens the same way; its node terms carry e^-z times z^m s^k
+// (m <= 1, k <= 3), and z e^-z <= 36 e^-36 ~ 8e-15 beyond the cut. Measured on sampled (P|a) of
+// the 700-atom globule (M = 20000) and the C20H42 chain against all 20 nodes: every integral is
+// bit-identical in double precision, and the z-weighted reverse terms move by <= 1.2e-15
+// relative. Checks follow every node from kFirstSkip on, before which z_t <= t^2 |d|^2 stays
+// small for any pair within ~30 Bohr.
+constexpr double kSkipZ = 36.0;
 constexpr int kFirstSkip = 5;
-constexpr int kSkipStride = 2;   // nodes between checks: each check closes a basic block, and two
-                                 // nodes per block leave the scheduler room to hide LDS latency
 
 __host__ __device__ constexpr bool screen_after(int t) {
-    return t >= kFirstSkip && (t - kFirstSkip) % kSkipStride == kSkipStride - 1 && t + 1 < kNodes;
+    return t >= kFirstSkip && t + 1 < kNodes;
 }
 
 // Lanes past the end of the work hold a centre kFarAway Bohr off (z ~ 1e40 at every node from
@@ -311,8 +309,25 @@ __global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ 
 
 // ------------------------------------------------------------------ reverse
 
-// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | pad (3) | s_t | wp_t | s_t^2 | s_t^3.
-__global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
+// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wp_t | s_t^2 |
+// s_t^3. Records are stored centre-grouped: with G = N / M exponent scales (the product aux is
+// scale-major, P = s M + m, every scale of splat m at one centre), the record of P sits at slot
+// m G + s, so the scales sharing a centre are consecutive; otherwise (N not a multiple of M) in
+// aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
+// the reverse kernel recomputes the centre-dependent terms only there, whatever the aux holds.
+__device__ __forceinline__ int64_t aux_slot(int64_t p, int64_t N, int64_t G) {
+    if (G <= 1) return p;
+    const int64_t Mg = N / G;
+    return (p % Mg) * G + p / Mg;
+}
+
+__device__ __forceinline__ int64_t aux_of_slot(int64_t q, int64_t N, int64_t G) {
+    if (G <= 1) return q;
+    const int64_t Mg = N / G;
+    return (q % G) * Mg + q / G;
+}
+
+__global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
                                const double* __restrict__ dgamma,
                                const double* __restrict__ dscale, double* __restrict__ out) {
@@ -321,10 +336,20 @@ __global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
     const double b = beta[p];
     double s[kNodes], wp[kNodes];
     node_consts(b, s, wp);
-    double* o = out + kAuxRec * p;
+    const int64_t slot = aux_slot(p, N, G);
+    double* o = out + kAuxRec * slot;
     o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
     o[3] = dgamma[p] * (dscale ? *dscale : 1.0) * kn[p];
-    o[4] = b; o[5] = 0.0; o[6] = 0.0; o[7] = 0.0;
+    bool first = true;
+    if (slot > 0) {
+        const int64_t q = aux_of_slot(slot - 1, N, G);
+        first = !(__builtin_bit_cast(uint64_t, R[3 * q]) == __builtin_bit_cast(uint64_t, R[3 * p]) &&
+                  __builtin_bit_cast(uint64_t, R[3 * q + 1]) ==
+                      __builtin_bit_cast(uint64_t, R[3 * p + 1]) &&
+                  __builtin_bit_cast(uint64_t, R[3 * q + 2]) ==
+                      __builtin_bit_cast(uint64_t, R[3 * p + 2]));
+    }
+    o[4] = b; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
     for (int t = 0; t < kNodes; ++t) {
         o[8 + t] = s[t];
         o[8 + kNodes + t] = wp[t];
@@ -333,44 +358,75 @@ __global__ void k_aux_bwd_prep(int64_t N, const double* __restrict__ beta,
     }
 }
 
-// One lane per pair; accumulates over a slab of aux functions (u = dgamma_P KN_P)
+// One lane per pair slot; accumulates over a slab of aux records (u = dgamma_P KN_P)
 //   jt = sum u F,  T1/T2/T3 = sum u dF/dI1,I2,I3 (through Pn and Qn),
 //   Vc = sum u dQ0 d, Va = sum u dQ1 d, Vb = sum u dQ2 d, Sa = sum u dQ1 d d^T, Sb = sum u dQ2 d d^T
 // where dQk = sum_t (df/dQn) s^k = -sum_t g_t s^(k+1), dPk = sum_t (df/dPn) s^k, with
 // f_t = wp_t y e^-z, y = Pn^(-1/2), z = s Qn / Pn, g_t = f_t / Pn and df/dPn = g_t (z - 1/2).
-__global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __restrict__ rec,
-                                                   int64_t N, const double* __restrict__ aux,
-                                                   int64_t per_slab,
-                                                   double* __restrict__ partial,
-                                                   unsigned long long* __restrict__ work) {
+// Records sharing a centre are consecutive, so d = R - Pa and the d-moments are formed once per
+// centre: C0..C2 = sum u dQ0..2 over the group, then Vc += C0 d, ..., Sb += C2 d d^T.
+__global__ __launch_bounds__(256) void k_gamma_bwd(
+    int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
+    int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = a < n;
-    const double* __restrict__ r = rec + kRec * (live ? a : 0);
+    const double* r = rec + kRec * (live ? a : 0);
     const double I1 = r[0], I2 = r[1], I3 = r[2];
-    const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
-    const double Px = live ? r[9] : kFarAway, Py = live ? r[10] : kFarAway,
-                 Pz = live ? r[11] : kFarAway;
     double jt = 0, T1 = 0, T2 = 0, T3 = 0;
     double Vc[3] = {0, 0, 0}, Va[3] = {0, 0, 0}, Vb[3] = {0, 0, 0};
     double Sa[6] = {0, 0, 0, 0, 0, 0}, Sb[6] = {0, 0, 0, 0, 0, 0};
+    double C0 = 0, C1 = 0, C2 = 0;
+    double d[3] = {0, 0, 0}, q0 = 0, q1 = 0, X0 = 0, rr = 0;
+    auto flush = [&]() {
+        const double e1x = C1 * d[0], e1y = C1 * d[1], e1z = C1 * d[2];
+        const double e2x = C2 * d[0], e2y = C2 * d[1], e2z = C2 * d[2];
+        Vc[0] = __builtin_fma(C0, d[0], Vc[0]);
+        Vc[1] = __builtin_fma(C0, d[1], Vc[1]);
+        Vc[2] = __builtin_fma(C0, d[2], Vc[2]);
+        Va[0] += e1x; Va[1] += e1y; Va[2] += e1z;
+        Vb[0] += e2x; Vb[1] += e2y; Vb[2] += e2z;
+        Sa[0] = __builtin_fma(e1x, d[0], Sa[0]);
+        Sa[1] = __builtin_fma(e1y, d[1], Sa[1]);
+        Sa[2] = __builtin_fma(e1z, d[2], Sa[2]);
+        Sa[3] = __builtin_fma(e1x, d[1], Sa[3]);
+        Sa[4] = __builtin_fma(e1x, d[2], Sa[4]);
+        Sa[5] = __builtin_fma(e1y, d[2], Sa[5]);
+        Sb[0] = __builtin_fma(e2x, d[0], Sb[0]);
+        Sb[1] = __builtin_fma(e2y, d[1], Sb[1]);
+        Sb[2] = __builtin_fma(e2z, d[2], Sb[2]);
+        Sb[3] = __builtin_fma(e2x, d[1], Sb[3]);
+        Sb[4] = __builtin_fma(e2x, d[2], Sb[4]);
+        Sb[5] = __builtin_fma(e2y, d[2], Sb[5]);
+        C0 = 0; C1 = 0; C2 = 0;
+    };
     const int64_t p0 = blockIdx.y * per_slab;
     const int64_t p1 = min(N, p0 + per_slab);
     uint32_t nodes = 0;
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
         const double u = x[3];
-        const double d[3] = {x[0] - Px, x[1] - Py, x[2] - Pz};
-        const double ax = xx * d[0] + xy * d[1] + xz * d[2];
-        const double ay = xy * d[0] + yy * d[1] + yz * d[2];
-        const double az = xz * d[0] + yz * d[1] + zz * d[2];
-        const double q0 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
-        const double q1 = d[0] * ax + d[1] * ay + d[2] * az;
-        const double q2 = ax * ax + ay * ay + az * az;
-        const double X0 = I3 * q0;
-        const double rr = I1 * q1 - q2;
+        if (p == p0 || x[5] != 0.0) {            // a new centre (wave-uniform)
+            flush();
+            // The pair's Ah and centre are read again here rather than held in registers
+            // across the loop (the empty asm keeps the compiler from hoisting the loads).
+            const double* rp = r;
+            asm volatile("" : "+v"(rp));
+            const double xx = rp[3], yy = rp[4], zz = rp[5], xy = rp[6], xz = rp[7], yz = rp[8];
+            const double Px = live ? rp[9] : kFarAway, Py = live ? rp[10] : kFarAway,
+                         Pz = live ? rp[11] : kFarAway;
+            d[0] = x[0] - Px; d[1] = x[1] - Py; d[2] = x[2] - Pz;
+            const double ax = xx * d[0] + xy * d[1] + xz * d[2];
+            const double ay = xy * d[0] + yy * d[1] + yz * d[2];
+            const double az = xz * d[0] + yz * d[1] + zz * d[2];
+            q0 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+            q1 = d[0] * ax + d[1] * ay + d[2] * az;
+            const double q2 = ax * ax + ay * ay + az * az;
+            X0 = I3 * q0;
+            rr = I1 * q1 - q2;
+        }
         double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
@@ -392,32 +448,15 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
         };
         nodes += node_loop<0>(node);
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
-        const double dQ0 = -gs1, dQ1 = -gs2, dQ2 = -gs3;
         jt = __builtin_fma(u, F, jt);
-        T3 = __builtin_fma(u, __builtin_fma(q0, dQ0, dP0), T3);
+        T3 = __builtin_fma(u, __builtin_fma(q0, -gs1, dP0), T3);
         T2 = __builtin_fma(u, dP1, T2);
-        T1 = __builtin_fma(u, __builtin_fma(q1, dQ1, dP2), T1);
-        const double c0 = u * dQ0, c1 = u * dQ1, c2 = u * dQ2;
-        const double e1x = c1 * d[0], e1y = c1 * d[1], e1z = c1 * d[2];
-        const double e2x = c2 * d[0], e2y = c2 * d[1], e2z = c2 * d[2];
-        Vc[0] = __builtin_fma(c0, d[0], Vc[0]);
-        Vc[1] = __builtin_fma(c0, d[1], Vc[1]);
-        Vc[2] = __builtin_fma(c0, d[2], Vc[2]);
-        Va[0] += e1x; Va[1] += e1y; Va[2] += e1z;
-        Vb[0] += e2x; Vb[1] += e2y; Vb[2] += e2z;
-        Sa[0] = __builtin_fma(e1x, d[0], Sa[0]);
-        Sa[1] = __builtin_fma(e1y, d[1], Sa[1]);
-        Sa[2] = __builtin_fma(e1z, d[2], Sa[2]);
-        Sa[3] = __builtin_fma(e1x, d[1], Sa[3]);
-        Sa[4] = __builtin_fma(e1x, d[2], Sa[4]);
-        Sa[5] = __builtin_fma(e1y, d[2], Sa[5]);
-        Sb[0] = __builtin_fma(e2x, d[0], Sb[0]);
-        Sb[1] = __builtin_fma(e2y, d[1], Sb[1]);
-        Sb[2] = __builtin_fma(e2z, d[2], Sb[2]);
-        Sb[3] = __builtin_fma(e2x, d[1], Sb[3]);
-        Sb[4] = __builtin_fma(e2x, d[2], Sb[4]);
-        Sb[5] = __builtin_fma(e2y, d[2], Sb[5]);
+        T1 = __builtin_fma(u, __builtin_fma(q1, -gs2, dP2), T1);
+        C0 = __builtin_fma(u, -gs1, C0);
+        C1 = __builtin_fma(u, -gs2, C1);
+        C2 = __builtin_fma(u, -gs3, C2);
     }
+    flush();
     count_work(work, live, nodes);
     if (!live) return;
     double* o = partial + (int64_t)blockIdx.y * kAcc * n + a;
@@ -426,6 +465,15 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(int64_t n, const double* __re
                             Sb[0], Sb[1], Sb[2], Sb[3], Sb[4], Sb[5]};
 #pragma unroll
     for (int c = 0; c < kAcc; ++c) o[(int64_t)c * n] = v[c];
+}
+
+// rec_sorted[slot] = rec[perm[slot]].
+__global__ void k_rec_gather(int64_t n, const int32_t* __restrict__ perm,
+                             const double* __restrict__ rec, double* __restrict__ out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= n * kRec) return;
+    const int64_t slot = t / kRec, c = t % kRec;
+    out[t] = rec[(int64_t)perm[slot] * kRec + c];
 }
 
 __device__ __forceinline__ void sym_mul(const double A[6], const double B[6], double M[9]) {
@@ -446,15 +494,18 @@ __device__ __forceinline__ void sym_vec(const double A[6], const double x[3], do
 // Per pair: sum the slab moments, map them to dE/dAh, dE/dPa, dE/dKN_a, then through
 // gs_dft/coulomb/stream.py:203-215 to the two splats. Writes J and 20 contributions (SoA):
 //   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
-__global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restrict__ pi,
+// Slot `slot` holds pair a = perm[slot] (its record and slab moments are stored by slot).
+__global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restrict__ perm,
+                                const int32_t* __restrict__ pi,
                                 const int32_t* __restrict__ pj,
                                 const double* __restrict__ weight,
                                 const double* __restrict__ A6, const double* __restrict__ mu,
                                 const double* __restrict__ Nrm, const double* __restrict__ rec,
                                 const double* __restrict__ partial, double* __restrict__ J,
                                 double* __restrict__ contrib) {
-    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (a >= n) return;
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (slot >= n) return;
+    const int64_t a = perm[slot];
     if (weight[a] == 0.0) {
         J[a] = 0.0;
         for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
@@ -463,10 +514,10 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restr
     double m[kAcc];
     for (int c = 0; c < kAcc; ++c) {
         double s = 0.0;
-        for (int64_t k = 0; k < slabs; ++k) s += partial[(k * kAcc + c) * n + a];
+        for (int64_t k = 0; k < slabs; ++k) s += partial[(k * kAcc + c) * n + slot];
         m[c] = s;
     }
-    const double* r = rec + kRec * a;
+    const double* r = rec + kRec * slot;
     const double I1 = r[0], I3 = r[2];
     const double Ah[6] = {r[3], r[4], r[5], r[6], r[7], r[8]};
     const double KN = r[13], q = r[14];
@@ -695,8 +746,9 @@ Split bwd_split(int64_t N, int64_t n) {
 
 struct GammaWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
-    double *aux, *acc, *contrib;
+    double *aux, *acc, *contrib, *rec_sorted;
     AuxOrderWs order;
+    PairOrderWs pair_order;
 };
 
 int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, GammaWs* w) {
@@ -706,7 +758,7 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
     w->kn = ar.take<double>(N + 1);
     w->q = ar.take<double>(n + 1);
     w->rec = ar.take<double>(kRec * n + kRec);
-    w->partial = w->aux = w->acc = w->contrib = nullptr;
+    w->partial = w->aux = w->acc = w->contrib = w->rec_sorted = nullptr;
     if (!reverse) {
         GSDFT_TRY(aux_order_layout(ar, N, &w->order));
         const Split sp = fwd_split(N, n);
@@ -715,6 +767,8 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
         const Split sp = bwd_split(N, n);
         w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
         w->acc = ar.take<double>(sp.slabs * kAcc * n + 1);
+        w->rec_sorted = ar.take<double>(kRec * n + kRec);
+        GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
         w->contrib = ar.take<double>(20 * n + 1);
     }
     return GSDFT_OK;
@@ -943,18 +997,22 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
                              weight, w, s));
     if (n > 0) {
-        k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, w.beta, w.kn, aux_centers, dgamma,
-                                                          dgamma_scale, w.aux);
+        const int64_t G = (N % M == 0) ? N / M : 1;      // scales per centre of a product aux
+        k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers,
+                                                          dgamma, dgamma_scale, w.aux);
+        GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
+        k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
+                                                                w.rec_sorted);
         const Split sp = bwd_split(N, n);
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
-        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec, N, w.aux, sp.per_slab, w.acc,
+        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
                                          profile_work_counter(kProfGammaBwd));
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, pi, pj, weight, w.A6,
-                                                           centers, w.Nrm, w.rec, w.acc, J,
-                                                           w.contrib);
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.pair_order.perm, pi,
+                                                           pj, weight, w.A6, centers, w.Nrm,
+                                                           w.rec_sorted, w.acc, J, w.contrib);
         GSDFT_HIP(hipGetLastError());
     }
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,

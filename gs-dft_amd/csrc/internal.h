@@ -62,6 +62,18 @@ int aux_order_layout(Arena& ar, int64_t N, AuxOrderWs* w);
 int launch_aux_order(int64_t N, const double* log_alpha, const double* aux_centers,
                      const AuxOrderWs& w, hipStream_t s);
 
+// order.hip: slot order of the reverse three-centre pass (perm[slot] = pair index), built from
+// pair records in list order whose first 12 doubles are I1 I2 I3 | Ah (6) | P (3).
+struct PairOrderWs {
+    uint64_t *key_in, *key_out;
+    int32_t *idx_in, *perm;
+    char* sort_tmp;
+    size_t sort_bytes;
+};
+int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w);
+int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
+                      hipStream_t s);
+
 // screen.hip
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,
                  hipStream_t s);
