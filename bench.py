@@ -138,7 +138,7 @@ def main() -> int:
     integrals = float(N) * float(n)
     fwd_tf = integrals * FLOPS_FWD / (fwd_ms * 1e-3)
     bwd_tf = integrals * FLOPS_BWD / (bwd_ms * 1e-3)
-    # What the kernels executed: the node screen leaves out nodes whose terms are below e^-46.
+    # What the kernels executed: the node screen leaves out nodes whose terms are below e^-36.
     fwd_exec_tf = (integrals * FWD_PER_INTEGRAL + fwd_nodes * FWD_PER_NODE) / (fwd_ms * 1e-3)
     bwd_exec_tf = (integrals * BWD_PER_INTEGRAL + bwd_nodes * BWD_PER_NODE) / (bwd_ms * 1e-3)
     fwd_node_frac = fwd_nodes / (NODES * integrals)
