@@ -52,6 +52,13 @@ SIGNATURES = {
     "gsdft_gamma_vjp": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp,
                         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                         _vp],
+    "gsdft_density_pairs": [_i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp],
+    "gsdft_external_workspace_size": [_i64, _i64, _i64, _i64, _psz],
+    "gsdft_nuclear_pairs": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz,
+                            _vp],
+    "gsdft_external_energy": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                              _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _sz, _vp],
     "gsdft_profile_enable": [_int],
     "gsdft_profile_read": [_int, _pd, _pi64, _int],
     "gsdft_profile_read_work": [_int, ctypes.POINTER(ctypes.c_uint64), _int],

@@ -119,10 +119,10 @@ __global__ void k_zero_upper(int64_t N, double* __restrict__ V) {
     V[p * N + q] = 0.0;
 }
 
-// 0.5 * a.b in one block, fixed summation order.
-__global__ __launch_bounds__(1024) void k_half_dot(int64_t N, const double* __restrict__ a,
-                                                   const double* __restrict__ b,
-                                                   double* __restrict__ out) {
+// scale * a.b in one block, fixed summation order.
+__global__ __launch_bounds__(1024) void k_scaled_dot(int64_t N, const double* __restrict__ a,
+                                                     const double* __restrict__ b, double scale,
+                                                     double* __restrict__ out) {
     __shared__ double part[1024];
     double s = 0.0;
     for (int64_t i = threadIdx.x; i < N; i += 1024) s += a[i] * b[i];
@@ -132,12 +132,13 @@ __global__ __launch_bounds__(1024) void k_half_dot(int64_t N, const double* __re
         if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) *out = 0.5 * part[0];
+    if (threadIdx.x == 0) *out = scale * part[0];
 }
 
 // ------------------------------------------------------------------ pair records
 
-// q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456); G lanes per pair.
+// q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456; w_a = 1 for a null weight); G lanes
+// per pair.
 template <int G>
 __global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* __restrict__ pi,
                                                       const int32_t* __restrict__ pj,
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* 
     if (live)
         for (int64_t o = l; o < k; o += G) s += (occ[o] * C[i * k + o]) * C[j * k + o];
     for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (live && l == 0) q[a] = weight[a] * s;
+    if (live && l == 0) q[a] = (weight ? weight[a] : 1.0) * s;
 }
 
 // Pair record: I1 I2 I3 | Ah (6) | Pa (3) | coef = KN q pref | KN | q | pad.
@@ -494,8 +495,11 @@ __device__ __forceinline__ void sym_vec(const double A[6], const double x[3], do
 // Per pair: sum the slab moments, map them to dE/dAh, dE/dPa, dE/dKN_a, then through
 // gs_dft/coulomb/stream.py:203-215 to the two splats. Writes J and 20 contributions (SoA):
 //   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
-// Slot `slot` holds pair a = perm[slot] (its record and slab moments are stored by slot).
-__global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restrict__ perm,
+// Slot `slot` holds pair a = perm[slot] (its record and slab moments are stored by slot). pref is
+// the integral's prefactor (2 pi^3/sqrt(pi) for (P|a), 2 pi for the nuclear attraction); a null
+// weight treats every entry as live.
+__global__ void k_pair_finalize(int64_t n, int64_t slabs, double pref,
+                                const int32_t* __restrict__ perm,
                                 const int32_t* __restrict__ pi,
                                 const int32_t* __restrict__ pj,
                                 const double* __restrict__ weight,
@@ -506,7 +510,7 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restr
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (slot >= n) return;
     const int64_t a = perm[slot];
-    if (weight[a] == 0.0) {
+    if (weight && weight[a] == 0.0) {
         J[a] = 0.0;
         for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
         return;
@@ -527,9 +531,9 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, const int32_t* __restr
     const double* Vb = m + 10;
     const double* Sa = m + 13;
     const double* Sb = m + 19;
-    const double scale = q * KN * kPref3c;
-    J[a] = KN * kPref3c * jt;
-    const double gKN = q * kPref3c * jt;
+    const double scale = q * KN * pref;
+    J[a] = KN * pref * jt;
+    const double gKN = q * pref * jt;
     // dE/dPa = -2 scale (I3 Vc + Ah (I1 Va + Vb) - Ah (Ah Va))
     double w1[3] = {I1 * Va[0] + Vb[0], I1 * Va[1] + Vb[1], I1 * Va[2] + Vb[2]};
     double t1[3], t2[3], t3[3];
@@ -712,6 +716,118 @@ __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
     }
 }
 
+// ------------------------------------------------------------------ nuclear attraction
+// gs_dft/screening/pairs.py:348-370: V_a = -N_i N_j K sum_A Z_A (2/sqrt(pi)) sum_t w_t pi^1.5
+// det(B_t)^(-1/2) exp(-(t^2 |d|^2 - t^4 d.adj(B_t) d / det B_t)), B_t = Ah + t^2 I, d = Pa - R_A.
+// With s = t^2: det B_t = Pn(s) and the exponent is s d.Ah (Ah + s I)^-1 d = s Qn(s)/Pn(s), the
+// three-centre node of an aux function whose exponent b grows without bound (s_t = t^2 b/(b + t^2)
+// -> t^2, w_t (b + t^2)^(-3/2) -> w_t once the aux norm is divided out). So the nuclei enter the
+// reverse kernel as aux records with s_t = t^2, wp_t = w_t and u = -Z_A, and the prefactor is
+// (2/sqrt(pi)) pi^1.5 = 2 pi.
+constexpr double kPrefNuc = 2.0 * kPi;
+
+__global__ void k_atom_rec(int64_t n_atoms, const double* __restrict__ coords,
+                           const double* __restrict__ charges, double* __restrict__ out) {
+    const int64_t A = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (A >= n_atoms) return;
+    double* o = out + kAuxRec * A;
+    o[0] = coords[3 * A]; o[1] = coords[3 * A + 1]; o[2] = coords[3 * A + 2];
+    o[3] = -charges[A];
+    bool first = true;
+    if (A > 0)
+        first = !(__builtin_bit_cast(uint64_t, coords[3 * A - 3]) ==
+                      __builtin_bit_cast(uint64_t, coords[3 * A]) &&
+                  __builtin_bit_cast(uint64_t, coords[3 * A - 2]) ==
+                      __builtin_bit_cast(uint64_t, coords[3 * A + 1]) &&
+                  __builtin_bit_cast(uint64_t, coords[3 * A - 1]) ==
+                      __builtin_bit_cast(uint64_t, coords[3 * A + 2]));
+    o[4] = 0.0; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
+    for (int t = 0; t < kNodes; ++t) {
+        const double t2 = quad_t(t) * quad_t(t);
+        o[8 + t] = t2;
+        o[8 + kNodes + t] = quad_w(t);
+        o[8 + 2 * kNodes + t] = t2 * t2;
+        o[8 + 3 * kNodes + t] = t2 * t2 * t2;
+    }
+}
+
+// dE/dR_A of E = sum_a q_a V_a: one lane per atom, the pairs of a slab wave-uniform (scalar loads
+// of the list-order records); per-slab partial sums (slabs, n_atoms, 3), summed in fixed order.
+// With F = sum_t w_t Pn^(-1/2) e^(-s Qn/Pn) and g_t = f_t / Pn: dF/dq0 = -I3 sum g s,
+// dF/dq1 = -(I1 sum g s^2 + sum g s^3), dF/dq2 = sum g s^2, and dF/dR = 2 (dF/dq0 d + dF/dq1 Ah d
+// + dF/dq2 Ah^2 d) for d = R - Pa.
+__global__ __launch_bounds__(256) void k_vne_atom_grad(int64_t n_atoms,
+                                                       const double* __restrict__ coords,
+                                                       const double* __restrict__ charges,
+                                                       int64_t n, const double* __restrict__ rec,
+                                                       int64_t per_slab,
+                                                       double* __restrict__ partial) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
+    const int64_t A = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = A < n_atoms;
+    const double Rx = live ? coords[3 * A] : kFarAway, Ry = live ? coords[3 * A + 1] : kFarAway,
+                 Rz = live ? coords[3 * A + 2] : kFarAway;
+    const int64_t a0 = blockIdx.y * per_slab;
+    const int64_t a1 = min(n, a0 + per_slab);
+    double gx = 0.0, gy = 0.0, gz = 0.0;
+    for (int64_t a = a0; a < a1; ++a) {
+        const double* __restrict__ r = rec + kRec * a;
+        const double c = r[13] * r[14];          // KN_a q_a, wave-uniform
+        if (c == 0.0) continue;                  // zero weight or zero density: adds exactly 0
+        const double I1 = r[0], I2 = r[1], I3 = r[2];
+        const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
+        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
+        const double ax = xx * dx + xy * dy + xz * dz;
+        const double ay = xy * dx + yy * dy + yz * dz;
+        const double az = xz * dx + yz * dy + zz * dz;
+        const double bx = xx * ax + xy * ay + xz * az;
+        const double by = xy * ax + yy * ay + yz * az;
+        const double bz = xz * ax + yz * ay + zz * az;
+        const double q0 = dx * dx + dy * dy + dz * dz;
+        const double q1 = dx * ax + dy * ay + dz * az;
+        const double q2 = ax * ax + ay * ay + az * az;
+        const double X0 = I3 * q0;
+        const double rr = I1 * q1 - q2;
+        double gs1 = 0.0, gs2 = 0.0, gs3 = 0.0;
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr double st = quad_t(t) * quad_t(t);
+            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
+            const NodeVal v = node_val(Pn, st * Qn);
+            const double g = ((quad_w(t) * v.y0) * exp_neg_tab(v.arg, tab)) * v.ip;
+            gs1 = __builtin_fma(g, st, gs1);
+            gs2 = __builtin_fma(g, st * st, gs2);
+            gs3 = __builtin_fma(g, st * st * st, gs3);
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        node_loop<0>(node);
+        const double f0 = -I3 * gs1, f1 = -(I1 * gs2 + gs3), f2 = gs2;
+        const double s2 = 2.0 * c;
+        gx = __builtin_fma(s2, f0 * dx + f1 * ax + f2 * bx, gx);
+        gy = __builtin_fma(s2, f0 * dy + f1 * ay + f2 * by, gy);
+        gz = __builtin_fma(s2, f0 * dz + f1 * az + f2 * bz, gz);
+    }
+    if (!live) return;
+    const double u = -charges[A] * kPrefNuc;
+    double* o = partial + ((int64_t)blockIdx.y * n_atoms + A) * 3;
+    o[0] = u * gx;
+    o[1] = u * gy;
+    o[2] = u * gz;
+}
+
+// out[i] (i < count) = sum over slabs of partial[slab * count + i], fixed order.
+__global__ void k_slab_sum_flat(int64_t count, int64_t slabs, const double* __restrict__ partial,
+                                double* __restrict__ out) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    double s = 0.0;
+    for (int64_t k = 0; k < slabs; ++k) s += partial[k * count + i];
+    out[i] = s;
+}
+
 // ------------------------------------------------------------------ work split
 
 struct Split {
@@ -721,7 +837,7 @@ struct Split {
 
 // Forward: ceil(N/256) workgroups per slab; aim for ~16 resident rounds of 4 waves per SIMD.
 Split fwd_split(int64_t N, int64_t n) {
-    const int64_t groups = (N + 255) / 256;
+    const int64_t groups = N > 0 ? (N + 255) / 256 : 1;
     const int64_t target = 256 * 4 * 16;                   // workgroups (of 4 waves) wanted
     int64_t slabs = (target + groups - 1) / groups;
     slabs = slabs < 1 ? 1 : slabs;
@@ -733,7 +849,7 @@ Split fwd_split(int64_t N, int64_t n) {
 }
 
 Split bwd_split(int64_t N, int64_t n) {
-    const int64_t groups = (n + 255) / 256;
+    const int64_t groups = n > 0 ? (n + 255) / 256 : 1;
     const int64_t target = 256 * 4 * 4;
     int64_t slabs = (target + groups - 1) / groups;
     slabs = slabs < 1 ? 1 : slabs;
@@ -742,6 +858,19 @@ Split bwd_split(int64_t N, int64_t n) {
     if (slabs > 65535) slabs = 65535;
     const int64_t per = (N + slabs - 1) / slabs;
     return Split{(N + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
+}
+
+// Atom-gradient pass of the nuclear attraction: ceil(n_atoms/256) workgroups per slab of pairs.
+Split atom_split(int64_t n_atoms, int64_t n) {
+    const int64_t groups = n_atoms > 0 ? (n_atoms + 255) / 256 : 1;
+    const int64_t target = 256 * 4 * 4;
+    int64_t slabs = (target + groups - 1) / groups;
+    const int64_t max_slabs = (n + 63) / 64;                // at least 64 pairs per slab
+    if (slabs > max_slabs) slabs = max_slabs;
+    if (slabs < 1) slabs = 1;
+    if (slabs > 65535) slabs = 65535;
+    const int64_t per = n > 0 ? (n + slabs - 1) / slabs : 1;
+    return Split{n > 0 ? (n + per - 1) / per : 1, per};
 }
 
 struct GammaWs {
@@ -790,16 +919,41 @@ int launch_pair_density(int64_t n, const int32_t* pi, const int32_t* pj, const d
     return GSDFT_OK;
 }
 
-// Shared prologue of forward and reverse: chart, aux quantities, pair density, pair records.
+int launch_dC(int64_t M, int64_t k, const int32_t* row_ptr, const int32_t* row_perm,
+              const int32_t* col_ptr, const int32_t* col_perm, const int32_t* pi,
+              const int32_t* pj, const double* J, const double* weight, const double* C,
+              const double* occ, double* dC, hipStream_t s) {
+    if (k <= 256)
+        k_dC<1><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
+    else if (k <= 1024)
+        k_dC<4><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
+    else
+        k_dC<8><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                            weight, C, occ, dC);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+// Shared prologue of forward and reverse: chart, aux quantities (skipped for a null log_alpha),
+// pair density (zero for a null C), pair records.
 int gamma_prologue(int64_t M, const double* quat, const double* log_scale, const double* centers,
                    int64_t k, const double* C, const double* occ, int64_t N,
                    const double* log_alpha, int64_t n, const int32_t* pi, const int32_t* pj,
                    const double* weight, GammaWs& w, hipStream_t s) {
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
-    k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
-    GSDFT_HIP(hipGetLastError());
+    if (log_alpha) {
+        k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
+        GSDFT_HIP(hipGetLastError());
+    }
     if (n > 0) {
-        GSDFT_TRY(launch_pair_density(n, pi, pj, weight, k, C, occ, w.q, s));
+        if (C) {
+            GSDFT_TRY(launch_pair_density(n, pi, pj, weight, k, C, occ, w.q, s));
+        } else {                                 // values only: q = 0 zeroes every gradient term
+            k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 0.0, w.q);
+            GSDFT_HIP(hipGetLastError());
+        }
         k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec);
         GSDFT_HIP(hipGetLastError());
     }
@@ -916,7 +1070,7 @@ extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, 
     GSDFT_TRY(launch_trsv_pair(N, L, d, s));
     profile_end(kProfSolve, s);
     if (energy) {
-        k_half_dot<<<1, 1024, 0, s>>>(N, gamma, d, energy);
+        k_scaled_dot<<<1, 1024, 0, s>>>(N, gamma, d, 0.5, energy);
         GSDFT_HIP(hipGetLastError());
     }
     return GSDFT_OK;
@@ -1010,7 +1164,7 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
                                          profile_work_counter(kProfGammaBwd));
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.pair_order.perm, pi,
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPref3c, w.pair_order.perm, pi,
                                                            pj, weight, w.A6, centers, w.Nrm,
                                                            w.rec_sorted, w.acc, J, w.contrib);
         GSDFT_HIP(hipGetLastError());
@@ -1018,15 +1172,160 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
                                                          col_perm, w.contrib, quat, log_scale,
                                                          dquat, dlog_scale, dcenters);
-    if (k <= 256)
-        k_dC<1><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
-                                            weight, C, occ, dC);
-    else if (k <= 1024)
-        k_dC<4><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
-                                            weight, C, occ, dC);
-    else
-        k_dC<8><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
-                                            weight, C, occ, dC);
+    GSDFT_TRY(launch_dC(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J, weight, C, occ, dC,
+                        s));
+    return GSDFT_OK;
+}
+
+// ------------------------------------------------------------------ nuclear attraction (C ABI)
+
+namespace gsdft {
+namespace {
+
+struct ExternalWs {
+    GammaWs g;
+    double* atom_partial;
+};
+
+int layout_external(Arena& ar, int64_t M, int64_t n, int64_t n_atoms, ExternalWs* w) {
+    GSDFT_TRY(layout_gamma(ar, M, n_atoms, n, true, &w->g));
+    const Split sa = atom_split(n_atoms, n);
+    w->atom_partial = ar.take<double>(sa.slabs * n_atoms * 3 + 3);
+    return GSDFT_OK;
+}
+
+// V (n) = the nuclear attraction of every listed pair (J of the reverse kernel with the nuclei as
+// point-charge records) and, for a non-null C, the slot moments behind its gradient.
+int external_pass(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                  int64_t k, const double* C, const double* occ, int64_t n, const int32_t* pi,
+                  const int32_t* pj, const double* weight, int64_t n_atoms,
+                  const double* atom_coords, const double* atom_charges, double* V,
+                  ExternalWs& w, hipStream_t s) {
+    GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, n_atoms, nullptr, n, pi, pj,
+                             weight, w.g, s));
+    k_atom_rec<<<blocks_for(n_atoms, 256), 256, 0, s>>>(n_atoms, atom_coords, atom_charges,
+                                                        w.g.aux);
+    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_pair_order(n, w.g.rec, kRec, w.g.pair_order, s));
+    k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.g.pair_order.perm, w.g.rec,
+                                                            w.g.rec_sorted);
+    const Split sp = bwd_split(n_atoms, n);
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+    k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab, w.g.acc,
+                                     nullptr);
+    GSDFT_HIP(hipGetLastError());
+    k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPrefNuc,
+                                                       w.g.pair_order.perm, pi, pj, weight,
+                                                       w.g.A6, centers, w.g.Nrm, w.g.rec_sorted,
+                                                       w.g.acc, V, w.g.contrib);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }
+
+int check_atoms(int64_t n_atoms, const double* coords, const double* charges) {
+    if (n_atoms <= 0 || !coords || !charges)
+        return fail(GSDFT_ERR_ARG, "nuclear attraction: need n_atoms > 0, coordinates and charges");
+    return GSDFT_OK;
+}
+
+}  // namespace
+}  // namespace gsdft
+
+extern "C" int gsdft_external_workspace_size(int64_t M, int64_t k, int64_t n, int64_t n_atoms,
+                                             size_t* bytes) {
+    (void)k;
+    if (M < 0 || n < 0 || n_atoms < 0 || !bytes)
+        return fail(GSDFT_ERR_ARG, "external_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    ExternalWs w;
+    GSDFT_TRY(layout_external(ar, M, n, n_atoms, &w));
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_nuclear_pairs(int64_t M, const double* quat, const double* log_scale,
+                                   const double* centers, int64_t n, const int32_t* pi,
+                                   const int32_t* pj, int64_t n_atoms, const double* atom_coords,
+                                   const double* atom_charges, double* V, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    if (M <= 0 || n < 0 || (n > 0 && (!pi || !pj || !V)))
+        return fail(GSDFT_ERR_ARG, "gsdft_nuclear_pairs: bad arguments");
+    GSDFT_TRY(check_atoms(n_atoms, atom_coords, atom_charges));
+    if (n == 0) return GSDFT_OK;
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    ExternalWs w;
+    GSDFT_TRY(layout_external(ar, M, n, n_atoms, &w));
+    if (!w.atom_partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_nuclear_pairs: workspace too small");
+    return external_pass(M, quat, log_scale, centers, 0, nullptr, nullptr, n, pi, pj, nullptr,
+                         n_atoms, atom_coords, atom_charges, V, w, s);
+}
+
+extern "C" int gsdft_external_energy(
+    int64_t M, const double* quat, const double* log_scale, const double* centers, int64_t k,
+    const double* C, const double* occ, int64_t n, const int32_t* pi, const int32_t* pj,
+    const double* weight, const int32_t* row_ptr, const int32_t* row_perm,
+    const int32_t* col_ptr, const int32_t* col_perm, int64_t n_atoms, const double* atom_coords,
+    const double* atom_charges, double* energy, double* V, double* dquat, double* dlog_scale,
+    double* dcenters, double* dC, double* datoms, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    const bool splat_grad = dquat || dlog_scale || dcenters || dC;
+    if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy || (n > 0 && (!pi || !pj || !weight || !V)))
+        return fail(GSDFT_ERR_ARG, "gsdft_external_energy: bad arguments");
+    if (splat_grad && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
+                       (n > 0 && (!row_perm || !col_perm))))
+        return fail(GSDFT_ERR_ARG, "gsdft_external_energy: the splat gradients come together "
+                    "(dquat, dlog_scale, dcenters, dC) and need the pair index");
+    GSDFT_TRY(check_atoms(n_atoms, atom_coords, atom_charges));
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    ExternalWs w;
+    GSDFT_TRY(layout_external(ar, M, n, n_atoms, &w));
+    if (!w.atom_partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_external_energy: workspace too small");
+    if (n == 0) {
+        k_fill<<<1, 256, 0, s>>>(1, 0.0, energy);
+        if (splat_grad) {
+            k_fill<<<blocks_for(4 * M, 256), 256, 0, s>>>(4 * M, 0.0, dquat);
+            k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dlog_scale);
+            k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dcenters);
+            k_fill<<<blocks_for(M * k, 256), 256, 0, s>>>(M * k, 0.0, dC);
+        }
+        if (datoms) k_fill<<<blocks_for(3 * n_atoms, 256), 256, 0, s>>>(3 * n_atoms, 0.0, datoms);
+        GSDFT_HIP(hipGetLastError());
+        return GSDFT_OK;
+    }
+    GSDFT_TRY(external_pass(M, quat, log_scale, centers, k, C, occ, n, pi, pj, weight, n_atoms,
+                            atom_coords, atom_charges, V, w, s));
+    // E = sum_a q_a V_a (gs_dft/screening/pairs.py:429-432), fixed summation order
+    k_scaled_dot<<<1, 1024, 0, s>>>(n, w.g.q, V, 1.0, energy);
+    GSDFT_HIP(hipGetLastError());
+    if (splat_grad) {
+        k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
+                                                             col_perm, w.g.contrib, quat,
+                                                             log_scale, dquat, dlog_scale,
+                                                             dcenters);
+        GSDFT_HIP(hipGetLastError());
+        GSDFT_TRY(launch_dC(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, V, weight, C, occ,
+                            dC, s));
+    }
+    if (datoms) {
+        const Split sa = atom_split(n_atoms, n);
+        dim3 grid((unsigned)((n_atoms + 255) / 256), (unsigned)sa.slabs);
+        k_vne_atom_grad<<<grid, 256, 0, s>>>(n_atoms, atom_coords, atom_charges, n, w.g.rec,
+                                             sa.per_slab, w.atom_partial);
+        GSDFT_HIP(hipGetLastError());
+        k_slab_sum_flat<<<blocks_for(3 * n_atoms, 256), 256, 0, s>>>(3 * n_atoms, sa.slabs,
+                                                                     w.atom_partial, datoms);
+        GSDFT_HIP(hipGetLastError());
+    }
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_density_pairs(int64_t n, const int32_t* pi, const int32_t* pj, int64_t k,
+                                   const double* C, const double* occ, double* out,
+                                   void* stream) {
+    if (n < 0 || k <= 0 || (n > 0 && (!pi || !pj || !C || !occ || !out)))
+        return fail(GSDFT_ERR_ARG, "gsdft_density_pairs: bad arguments");
+    return launch_pair_density(n, pi, pj, nullptr, k, C, occ, out, (hipStream_t)stream);
+}
+

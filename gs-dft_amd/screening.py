@@ -139,3 +139,133 @@ def build_pair_index(M: int, pi, pj, valid) -> PairIndex:
                                   _lib.ptr(ws), ws.numel(), _lib.stream()), "gsdft_pair_index")
     return PairIndex(n_live=n, row_ptr=row_ptr, row_perm=row_perm, col_ptr=col_ptr,
                      col_perm=col_perm)
+
+
+# ------------------------------------------------------------------------ nuclear attraction
+
+def _atoms(atom_coords, atom_charges, dev):
+    R = _lib.f64(atom_coords, dev).reshape(-1, 3).contiguous()
+    Z = _lib.f64(atom_charges, dev).reshape(-1).contiguous()
+    if R.shape[0] != Z.shape[0] or R.shape[0] == 0:
+        raise ValueError(f"atom_coords (n_atoms, 3) and atom_charges (n_atoms,) must agree and be "
+                         f"non-empty, got {tuple(R.shape)} and {tuple(Z.shape)}")
+    return R, Z
+
+
+def density_pairs(C_orth, occ, pi, pj) -> torch.Tensor:
+    """P_ij = sum_o occ_o C_io C_jo on the listed pairs (gs_dft/screening/pairs.py:383-386), without
+    forming the dense M x M density; values only."""
+    dev = _lib.device()
+    C = _lib.f64(C_orth.detach() if isinstance(C_orth, torch.Tensor) else C_orth, dev)
+    o = _lib.f64(occ.detach() if isinstance(occ, torch.Tensor) else occ, dev).reshape(-1)
+    pi, pj = _lib.i32(pi, dev), _lib.i32(pj, dev)
+    if C.dim() != 2 or o.shape[0] != C.shape[1]:
+        raise ValueError("density_pairs: C_orth must be (M, k) with one occupation per column")
+    out = torch.empty(pi.shape[0], dtype=torch.float64, device=dev)
+    _lib.check(_lib.lib().gsdft_density_pairs(pi.shape[0], _lib.ptr(pi), _lib.ptr(pj), C.shape[1],
+                                              _lib.ptr(C), _lib.ptr(o), _lib.ptr(out),
+                                              _lib.stream()), "density_pairs")
+    return out
+
+
+def screened_nuclear_pairs(splats, pi, pj, atom_coords, atom_charges) -> torch.Tensor:
+    """V_ij of the listed pairs (gs_dft/screening/pairs.py:348-370,378-380): the nuclear attraction
+    -N_i N_j K sum_A Z_A v_A by the reference's 20-node Laplace rule; values only."""
+    if not _has_splat_interface(splats):
+        raise NotImplementedError(f"screened_nuclear_pairs: {type(splats).__name__} is not a Splat")
+    M = splats.n_basis
+    q, l, c = _splat_args(splats)
+    dev = q.device
+    pi, pj = _lib.i32(pi, dev), _lib.i32(pj, dev)
+    R, Z = _atoms(atom_coords, atom_charges, dev)
+    n = pi.shape[0]
+    V = torch.empty(n, dtype=torch.float64, device=dev)
+    L = _lib.lib()
+    ws = _lib.workspace(_lib.size_query(L.gsdft_external_workspace_size, M, 1, n, R.shape[0]), dev)
+    _lib.check(L.gsdft_nuclear_pairs(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), n, _lib.ptr(pi),
+                                     _lib.ptr(pj), R.shape[0], _lib.ptr(R), _lib.ptr(Z),
+                                     _lib.ptr(V), _lib.ptr(ws), ws.numel(), _lib.stream()),
+               "screened_nuclear_pairs")
+    return V
+
+
+class _ExternalFn(torch.autograd.Function):
+    """E_ext = sum_a w_a P_a V_a in one library pass; with gradients requested, the same pass also
+    writes dE/d(quat, log_scale, centers, C_orth, atom_coords), which the backward scales by the
+    incoming cotangent."""
+
+    @staticmethod
+    def forward(ctx, quat, log_scale, centers, C, R, x):
+        M, k, n, dev = x["M"], x["k"], x["n"], x["dev"]
+        grads = any(ctx.needs_input_grad[:5])
+        E = torch.empty((), dtype=torch.float64, device=dev)
+        V = torch.empty(max(n, 1), dtype=torch.float64, device=dev)
+        outs = [None] * 5
+        if grads:
+            outs = [torch.empty((M, 4), dtype=torch.float64, device=dev),
+                    torch.empty((M, 3), dtype=torch.float64, device=dev),
+                    torch.empty((M, 3), dtype=torch.float64, device=dev),
+                    torch.empty((M, k), dtype=torch.float64, device=dev),
+                    torch.empty_like(x["R"])]
+            idx = build_pair_index(M, x["pi"][:n], x["pj"][:n], x["w"][:n])
+            csr = (idx.row_ptr, idx.row_perm, idx.col_ptr, idx.col_perm)
+        else:
+            csr = (None, None, None, None)
+        L = _lib.lib()
+        ws = _lib.workspace(_lib.size_query(L.gsdft_external_workspace_size, M, k, n,
+                                            x["R"].shape[0]), dev)
+        q, l, c, Cd = (t.detach().contiguous() for t in (quat, log_scale, centers, C))
+        _lib.check(L.gsdft_external_energy(
+            M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), k, _lib.ptr(Cd), _lib.ptr(x["occ"]), n,
+            _lib.ptr(x["pi"]), _lib.ptr(x["pj"]), _lib.ptr(x["w"]), *(_lib.ptr(t) for t in csr),
+            x["R"].shape[0], _lib.ptr(x["R"]), _lib.ptr(x["Z"]), _lib.ptr(E), _lib.ptr(V),
+            *(_lib.ptr(t) for t in outs), _lib.ptr(ws), ws.numel(), _lib.stream()),
+            "screened_external_energy")
+        ctx.grads = outs if grads else None
+        return E
+
+    @staticmethod
+    def backward(ctx, gE):
+        if ctx.grads is None:
+            return None, None, None, None, None, None
+        return tuple(g * gE for g in ctx.grads) + (None,)
+
+
+def screened_external_energy(splats, C_orth, occ, pi, pj, atom_coords, atom_charges, valid=None,
+                             chunk: int = 8192, skip_pad: bool = False) -> torch.Tensor:
+    """E_external = sum_a w_a P_a V_a over the listed pairs (gs_dft/screening/pairs.py:409-440),
+    differentiable w.r.t. the splat leaves, ``C_orth`` and ``atom_coords`` (the nuclear charges are
+    held constant). ``valid`` weights the entries (bool or the unique-list weights 2 - delta_ij;
+    padding carries 0). ``chunk`` and ``skip_pad`` shaped the reference's XLA stream and do not
+    change its value; the library always skips the appended padding."""
+    del chunk, skip_pad
+    if not _has_splat_interface(splats):
+        raise NotImplementedError(f"screened_external_energy: {type(splats).__name__} is not a "
+                                  f"Splat")
+    dev = _lib.device()
+    M = splats.n_basis
+    C = C_orth if isinstance(C_orth, torch.Tensor) else _lib.f64(C_orth, dev)
+    if C.device != dev or C.dtype != torch.float64:
+        C = C.to(device=dev, dtype=torch.float64)
+    if C.dim() != 2 or C.shape[0] != M:
+        raise ValueError(f"C_orth must be (M, k) with M = {M}, got {tuple(C.shape)}")
+    occ_t = _lib.f64(occ.detach() if isinstance(occ, torch.Tensor) else occ, dev).reshape(-1)
+    if occ_t.shape[0] != C.shape[1]:
+        raise ValueError("occ must have one entry per column of C_orth")
+    pi_t, pj_t = _lib.i32(pi, dev), _lib.i32(pj, dev)
+    w = (torch.ones(pi_t.shape[0], dtype=torch.float64, device=dev) if valid is None
+         else _lib.f64(pair_weight(torch.as_tensor(valid)), dev).reshape(-1))
+    if pj_t.shape[0] != pi_t.shape[0] or w.shape[0] != pi_t.shape[0]:
+        raise ValueError("pi, pj and valid must have the same length")
+    n = live_length(w)
+    if n > 0:
+        lo = int(torch.minimum(pi_t[:n].min(), pj_t[:n].min()))
+        hi = int(torch.maximum(pi_t[:n].max(), pj_t[:n].max()))
+        if lo < 0 or hi >= M:
+            raise ValueError(f"pair indices must lie in [0, {M}), got [{lo}, {hi}]")
+    R_in = atom_coords if isinstance(atom_coords, torch.Tensor) else _lib.f64(atom_coords, dev)
+    R, Z = _atoms(R_in.detach(), atom_charges, dev)
+    Rg = R_in if (isinstance(R_in, torch.Tensor) and R_in.requires_grad) else R
+    x = {"M": M, "k": int(C.shape[1]), "n": n, "dev": dev, "occ": occ_t, "pi": pi_t, "pj": pj_t,
+         "w": w, "R": R, "Z": Z}
+    return _ExternalFn.apply(splats.quat, splats.log_scale, splats.centers, C, Rg, x)

@@ -14,7 +14,8 @@ Conventions fixed by this module (the benchmark descriptions leave them open):
   precision eigenvalue is 1/(2 sigma^2) and the anisotropy ratio of widths is at most 10;
 * the product auxiliary basis uses 4 exponent scales (0.5, 1, 2, 4), so N_aux = 4 M;
 * C ~ N(0,1), divided by sqrt(k) for the alkane and the two globules; occupations are 1;
-* eps = 1e-7, lam = 1e-8, unique pair mode with weights 2 - delta_ij.
+* eps = 1e-7, lam = 1e-8, unique pair mode with weights 2 - delta_ij;
+* nuclear charges H = 1, C = 6, O = 8 (small random systems cycle 6, 1, 8 over their atoms).
 
 Geometries (Bohr): CO2 with C at the origin and O at z = +-2.196; eight waters with O on a
 2x2x2 cubic lattice of spacing 3.0 jittered by U(-0.3, 0.3), H at 1.81 Bohr and 104.5 degrees in
@@ -50,6 +51,7 @@ class System:
     lam: float = 1e-8
     scales: tuple = AUX_SCALES
     unique: bool = True
+    charges: np.ndarray | None = None   # (n_atoms,) nuclear charges, in the order of ``atoms``
 
     @property
     def M(self) -> int:
@@ -158,6 +160,16 @@ _SPECS = {
 
 NAMES = {v[0]: k for k, v in _SPECS.items()}
 
+# Nuclear charges in the order each geometry lists its atoms (globules place the elements of
+# their count table in order).
+_CHARGES = {
+    1: lambda: np.array([6.0, 8.0, 8.0]),
+    2: lambda: np.tile([8.0, 1.0, 1.0], 8),
+    3: lambda: np.array([6.0] * 20 + [1.0] * 42),
+    4: lambda: np.array([6.0] * 100 + [1.0] * 200),
+    5: lambda: np.array([6.0] * 200 + [1.0] * 400 + [8.0] * 100),
+}
+
 
 def make_system(index: int, *, eps: float = 1e-7) -> System:
     """Benchmark system ``index`` in 1..5 (seed ``index - 1``)."""
@@ -180,7 +192,7 @@ def make_system(index: int, *, eps: float = 1e-7) -> System:
     if scale_c:
         C /= math.sqrt(k)
     return System(name=name, atoms=atoms, quat=quat, log_scale=log_scale, centers=centers,
-                  C=C, occ=np.ones(k), eps=eps)
+                  C=C, occ=np.ones(k), eps=eps, charges=_CHARGES[index]())
 
 
 def make_small(M: int, k: int, n_atoms: int = 4, seed: int = 0, spread: float = 2.5,
@@ -200,4 +212,5 @@ def make_small(M: int, k: int, n_atoms: int = 4, seed: int = 0, spread: float = 
     C = rng.normal(size=(M, k)) / math.sqrt(k)
     scales = AUX_SCALES[1:1 + n_scales] if n_scales < len(AUX_SCALES) else AUX_SCALES
     return System(name=f"small{M}", atoms=atoms, quat=q, log_scale=log_scale, centers=centers,
-                  C=C, occ=np.ones(k), scales=tuple(scales))
+                  C=C, occ=np.ones(k), scales=tuple(scales),
+                  charges=np.resize(np.array([6.0, 1.0, 8.0]), n_atoms))

@@ -128,6 +128,40 @@ int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,
                     double* J, double* dquat, double* dlog_scale, double* dcenters, double* dC,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* out (n) = P_ij = sum_o occ_o C_io C_jo on the listed pairs. Replaces density_pairs,
+ * gs_dft/screening/pairs.py:383-386. */
+int gsdft_density_pairs(int64_t n, const int32_t* pi, const int32_t* pj, int64_t k,
+                        const double* C, const double* occ, double* out, void* stream);
+
+/* Nuclear attraction over the pair list. Workspace for both calls below. */
+int gsdft_external_workspace_size(int64_t M, int64_t k, int64_t n, int64_t n_atoms,
+                                  size_t* bytes);
+
+/* V (n) = V_ij of every listed pair, -N_i N_j K sum_A Z_A (2/sqrt(pi)) sum_t w_t pi^1.5
+ * det(B_t)^(-1/2) exp(...) with B_t = A_ij + t^2 I; atom_coords (n_atoms,3), atom_charges
+ * (n_atoms). Replaces screened_nuclear_pairs / _full_nuclear_pairs,
+ * gs_dft/screening/pairs.py:348-370,378-380. */
+int gsdft_nuclear_pairs(int64_t M, const double* quat, const double* log_scale,
+                        const double* centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                        int64_t n_atoms, const double* atom_coords, const double* atom_charges,
+                        double* V, void* workspace, size_t workspace_bytes, void* stream);
+
+/* *energy (device scalar) = sum_a w_a P_a V_a over the first n list entries, P_a = sum_o occ_o
+ * C_io C_jo, and V (n) as gsdft_nuclear_pairs (0 on zero-weight entries). Optional outputs (null
+ * to skip): the gradients w.r.t. quat, log_scale, centers and C (all four together, with the pair
+ * index of the same n entries) and w.r.t. atom_coords (n_atoms,3). Replaces
+ * screened_external_energy, gs_dft/screening/pairs.py:409-440, with
+ * JAX's reverse pass through it (the only term gs_dft/ks/forces.py:53-77 differentiates in R). */
+int gsdft_external_energy(int64_t M, const double* quat, const double* log_scale,
+                          const double* centers, int64_t k, const double* C, const double* occ,
+                          int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                          const int32_t* row_ptr, const int32_t* row_perm,
+                          const int32_t* col_ptr, const int32_t* col_perm, int64_t n_atoms,
+                          const double* atom_coords, const double* atom_charges, double* energy,
+                          double* V, double* dquat, double* dlog_scale, double* dcenters,
+                          double* dC, double* datoms, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve.
  * gsdft_profile_read synchronises the recorded events and returns the summed milliseconds and

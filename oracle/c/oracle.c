@@ -759,3 +759,69 @@ void orc_gamma_vjp(int64_t M, const double* quat, const double* log_scale, const
     aux_free(&aq);
     chart_free(&c);
 }
+
+/* ---------------------------------------------------------------- nuclear attraction */
+
+/* gs_dft/screening/pairs.py:348-370 in its own (literal) form: per node B = A_ij + t^2 I,
+ * invdet = 1/det(B), qf = d.adj(B).d, expo = t^2 |d|^2 - t^4 qf invdet, and
+ * vA = (2/sqrt(pi)) sum_t w_t pi^1.5 sqrt(invdet) exp(-expo); V = -sum_A Z_A vA N_i N_j K. */
+static double nuclear_one(const double* tq, const double* wq, const double* A, const double* P,
+                          double NK, int64_t n_atoms, const double* coords,
+                          const double* charges) {
+    double V = 0.0;
+    for (int64_t at = 0; at < n_atoms; ++at) {
+        const double* R = coords + 3 * at;
+        double d[3] = {P[0] - R[0], P[1] - R[1], P[2] - R[2]};
+        double d2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+        double vA = 0.0;
+        for (int t = 0; t < NQ; ++t) {
+            double t2 = tq[t] * tq[t];
+            double B[9];
+            memcpy(B, A, sizeof B);
+            B[0] += t2; B[4] += t2; B[8] += t2;
+            double invdet = 1.0 / det3(B);
+            double adj[9], ad[3];
+            adj3(B, adj);
+            matvec3(adj, d, ad);
+            double qf = d[0] * ad[0] + d[1] * ad[1] + d[2] * ad[2];
+            double expo = t2 * d2 - (t2 * t2) * qf * invdet;
+            vA += (wq[t] * PI15) * sqrt(invdet) * exp(-expo);
+        }
+        vA *= 2.0 / sqrt(M_PI);
+        V += charges[at] * vA;
+    }
+    return -V * NK;
+}
+
+void orc_nuclear_pairs(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                       int64_t n_atoms, const double* coords, const double* charges, double* V) {
+    double tq[NQ], wq[NQ];
+    node_table(tq, wq);
+    Chart c = chart_alloc(M, quat, log_scale);
+#pragma omp parallel for schedule(static)
+    for (int64_t a = 0; a < n; ++a) {
+        double Ah[9], P[3], KN;
+        pair_q(c.A9 + 9 * pi[a], c.A9 + 9 * pj[a], centers + 3 * pi[a], centers + 3 * pj[a],
+               c.norm[pi[a]], c.norm[pj[a]], Ah, P, &KN, NULL);
+        V[a] = nuclear_one(tq, wq, Ah, P, KN, n_atoms, coords, charges);
+    }
+    chart_free(&c);
+}
+
+/* gs_dft/screening/pairs.py:409-440: E = sum_a w_a P_a V_a, P_a = sum_o occ_o C_io C_jo. */
+double orc_external_energy(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t k, const double* C, const double* occ,
+                           int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                           int64_t n_atoms, const double* coords, const double* charges) {
+    double* V = (double*)malloc(sizeof(double) * (n > 0 ? n : 1));
+    orc_nuclear_pairs(M, quat, log_scale, centers, n, pi, pj, n_atoms, coords, charges, V);
+    double E = 0.0;
+    for (int64_t a = 0; a < n; ++a) {
+        if (weight[a] == 0.0) continue;
+        E += weight[a] * pair_density(k, C, occ, pi[a], pj[a]) * V[a];
+    }
+    free(V);
+    return E;
+}
+

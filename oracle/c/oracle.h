@@ -94,6 +94,18 @@ void orc_gamma_vjp(int64_t M, const double* quat, const double* log_scale, const
                    double* dcenters, double* dC);
 
 /* The worker count the OpenMP loops above use (1 when built without OpenMP). */
+/* V (n) of gs_dft/screening/pairs.py:348-370 for the listed pairs and nuclei (coords (n_atoms,3),
+ * charges (n_atoms)), in the reference's B = A + t^2 I form. */
+void orc_nuclear_pairs(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                       int64_t n_atoms, const double* coords, const double* charges, double* V);
+
+/* E_ext = sum_a w_a P_a V_a (gs_dft/screening/pairs.py:409-440). */
+double orc_external_energy(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t k, const double* C, const double* occ,
+                           int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                           int64_t n_atoms, const double* coords, const double* charges);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

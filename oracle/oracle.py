@@ -41,6 +41,7 @@ def lib():
         L.orc_neighbor_pairs.restype = ctypes.c_int
         L.orc_cholesky.restype = ctypes.c_int
         L.orc_num_threads.restype = ctypes.c_int
+        L.orc_external_energy.restype = ctypes.c_double
         # the reference's own table (gs_dft/integrals/dense.py:46-53, numpy leggauss)
         t, w = reference_quad_table(20)
         L.orc_set_quad_table(_d(t), _d(w))
@@ -235,6 +236,29 @@ def dfj_grad(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj, w
                              weight, lam)
     return (E,) + gamma_vjp(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi, pj,
                             weight, d)
+
+
+def nuclear_pairs(quat, log_scale, centers, pi, pj, atom_coords, atom_charges):
+    """V (n) of gs_dft/screening/pairs.py:348-370 for the listed pairs."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    pi, pj = _i32(pi), _i32(pj)
+    R, Z = _f64(atom_coords).reshape(-1, 3), _f64(atom_charges).reshape(-1)
+    V = np.empty(pi.shape[0])
+    lib().orc_nuclear_pairs(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                            _i64(pi.shape[0]), pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32),
+                            _i64(R.shape[0]), _d(R), _d(Z), _d(V))
+    return V
+
+
+def external_energy(quat, log_scale, centers, C, occ, pi, pj, weight, atom_coords, atom_charges):
+    """E_ext = sum_a w_a P_a V_a (gs_dft/screening/pairs.py:409-440)."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    C, occ, pi, pj, w = _f64(C), _f64(occ), _i32(pi), _i32(pj), _f64(weight)
+    R, Z = _f64(atom_coords).reshape(-1, 3), _f64(atom_charges).reshape(-1)
+    return float(lib().orc_external_energy(
+        _i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers), _i64(C.shape[1]), _d(C),
+        _d(occ), _i64(pi.shape[0]), pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32), _d(w),
+        _i64(R.shape[0]), _d(R), _d(Z)))
 
 
 def set_threads(n: int) -> None:

@@ -198,3 +198,33 @@ def coulomb_solve(gamma, L):
 def as_t(x, requires_grad=False, dtype=torch.float64):
     t = torch.as_tensor(np.asarray(x), dtype=dtype).clone()
     return t.requires_grad_(requires_grad) if requires_grad else t
+
+
+def full_nuclear_pairs(quat, log_scale, centers, pi, pj, atom_coords, atom_charges, table=None):
+    """gs_dft/screening/pairs.py:348-370, node by node: B = A_ij + t^2 I, one reciprocal of det B
+    per pair, the adjugate form of the exponent (``table`` = (t list, w list) for another rule)."""
+    t_list, w_list = (QUAD_T_LIST, QUAD_W_LIST) if table is None else table
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    Aij, mup, NK = full_pair_quantities(A, centers, N, pi, pj)
+    d = mup[:, None, :] - atom_coords[None, :, :]
+    d2 = torch.sum(d * d, dim=-1)
+    eye = torch.eye(3, dtype=torch.float64)
+    vA = torch.zeros(d2.shape, dtype=torch.float64)
+    for t, w in zip(t_list, w_list):
+        t2 = t * t
+        B = Aij + t2 * eye
+        invdet = 1.0 / det3(B)
+        qf = torch.einsum("pak,pkl,pal->pa", d, adj3(B), d)
+        expo = t2 * d2 - (t2 * t2) * qf * invdet[:, None]
+        vA = vA + (w * PI ** 1.5) * torch.sqrt(invdet)[:, None] * torch.exp(-expo)
+    vA = (2.0 / math.sqrt(PI)) * vA
+    return -torch.sum(atom_charges[None, :] * vA, dim=1) * NK
+
+
+def screened_external_energy(quat, log_scale, centers, C, occ, pi, pj, valid, atom_coords,
+                             atom_charges):
+    """gs_dft/screening/pairs.py:409-440 (one chunk: the sum does not depend on chunking)."""
+    Pp = valid.to(torch.float64) * torch.sum(occ[None, :] * C[pi] * C[pj], dim=1)
+    V = full_nuclear_pairs(quat, log_scale, centers, pi, pj, atom_coords, atom_charges)
+    return torch.sum(Pp * V)
+

@@ -56,3 +56,17 @@ def test_no_cpu_fallback(g):
     from gs_dft_amd import _lib
     with pytest.raises(_lib.GsdftError):
         g.Splat(quat=[[1.0, 0, 0, 0]], log_scale=[[0.0, 0, 0]], centers=[[0.0, 0, 0]])
+
+
+def test_workspace_queries_accept_empty_inputs(built):
+    """Size queries are host arithmetic (plus library size queries that may report an error
+    without a GPU): an empty pair list or atom set must give a status, never a crash."""
+    lib = built.lib()
+    out = ctypes.c_size_t(0)
+    for fn, args in ((lib.gsdft_gamma_workspace_size, (4, 1, 4, 0)),
+                     (lib.gsdft_gamma_vjp_workspace_size, (4, 1, 4, 0)),
+                     (lib.gsdft_gamma_vjp_workspace_size, (4, 1, 0, 0)),
+                     (lib.gsdft_external_workspace_size, (4, 1, 0, 0)),
+                     (lib.gsdft_external_workspace_size, (4, 1, 10, 0))):
+        rc = fn(*args, ctypes.byref(out))
+        assert rc in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)

@@ -413,3 +413,143 @@ def test_full_list_equals_dense_sum(orc, wl):
     B = orc.three_center_block(s.quat, s.log_scale, s.centers, la, ac, pi, pj)
     P = s.C @ np.diag(s.occ) @ s.C.T
     assert rel_max(g, B @ P.reshape(-1)) < 1e-13
+
+
+# ----------------------------------------------------------------------------- nuclear attraction
+
+def _nuc_system(wl, orc, M=24, k=5, seed=3, unique=True):
+    s = wl.make_small(M, k, n_atoms=3, seed=seed)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, unique)
+    return s, pi, pj, w
+
+
+def test_nuclear_pairs_match_literal_restatement(orc, tr, wl):
+    """gs_dft/screening/pairs.py:348-370: the C oracle against the torch line-by-line form."""
+    for seed in (3, 4):
+        s, pi, pj, w = _nuc_system(wl, orc, seed=seed)
+        V = orc.nuclear_pairs(s.quat, s.log_scale, s.centers, pi, pj, s.atoms, s.charges)
+        Vt = tr.full_nuclear_pairs(_t(s.quat), _t(s.log_scale), _t(s.centers), _idx(pi),
+                                   _idx(pj), _t(s.atoms), _t(s.charges)).numpy()
+        assert np.all(V < 0) and np.max(np.abs(V - Vt) / np.abs(Vt)) < 1e-13
+        E = orc.external_energy(s.quat, s.log_scale, s.centers, s.C, s.occ, pi, pj, w, s.atoms,
+                                s.charges)
+        Et = tr.screened_external_energy(_t(s.quat), _t(s.log_scale), _t(s.centers), _t(s.C),
+                                         _t(s.occ), _idx(pi), _idx(pj), _t(w), _t(s.atoms),
+                                         _t(s.charges)).item()
+        assert abs(E - Et) < 1e-13 * abs(Et)
+
+
+def test_nuclear_invariant_form_equals_literal_node():
+    """The library evaluates det(A + sI) and the exponent through the invariants I1, I2, I3 and
+    q0 = |d|^2, q1 = d.A d, q2 = |A d|^2: det = Pn(s) = I3 + s (I2 + s (I1 + s)) and
+    t^2 |d|^2 - t^4 d.adj(B) d / det B = s Qn(s) / Pn(s), Qn = I3 q0 + s (I1 q1 - q2) + s^2 q1,
+    with s = t^2 (Cayley-Hamilton)."""
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        X = rng.normal(size=(3, 3))
+        A = X @ X.T + rng.uniform(0.05, 3.0) * np.eye(3)
+        d = rng.normal(0, 3.0, 3)
+        t = rng.uniform(0.01, 30.0)
+        s = t * t
+        B = A + s * np.eye(3)
+        adjB = np.linalg.inv(B) * np.linalg.det(B)
+        expo = s * (d @ d) - s * s * (d @ adjB @ d) / np.linalg.det(B)
+        I1, I3 = np.trace(A), np.linalg.det(A)
+        I2 = 0.5 * (I1 * I1 - np.trace(A @ A))
+        Pn = I3 + s * (I2 + s * (I1 + s))
+        q0, q1, q2 = d @ d, d @ A @ d, (A @ d) @ (A @ d)
+        Qn = I3 * q0 + s * ((I1 * q1 - q2) + s * q1)
+        assert abs(Pn - np.linalg.det(B)) < 1e-11 * abs(Pn)
+        assert abs(s * Qn / Pn - expo) < 1e-10 * max(abs(expo), 1.0)
+
+
+def test_nuclear_converges_to_point_charge_closed_form(orc, tr):
+    """Isotropic pair products p = a_i + a_j: the electron-nucleus integral of
+    exp(-p |r - P|^2) with a charge Z at R is -Z (2 pi / p) F0(p |P - R|^2). The reference's node
+    formula under a 400-node rule reproduces it to 1e-10, and the 20-node oracle agrees with the
+    20-node literal form, so prefactor and node algebra are pinned apart from the table."""
+    rng = np.random.default_rng(21)
+    M = 5
+    alpha = np.exp(rng.uniform(-1.5, 1.0, M))
+    quat = rng.normal(size=(M, 4))
+    ls = np.repeat(np.log(alpha)[:, None], 3, 1)
+    mu = rng.normal(0, 1.2, (M, 3))
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    atoms = rng.normal(0, 2.0, (4, 3)); Z = np.array([1.0, 6.0, 8.0, 7.0])
+    x, wl_ = np.polynomial.legendre.leggauss(400)
+    sgl = (x + 1) / 2
+    table = ([float(v) for v in sgl / (1 - sgl)], [float(v) for v in (wl_ / 2) / (1 - sgl) ** 2])
+    Vc = tr.full_nuclear_pairs(_t(quat), _t(ls), _t(mu), _idx(pi), _idx(pj), _t(atoms), _t(Z),
+                               table).numpy()
+    A, N = tr.splat_A(_t(quat), _t(ls)), tr.splat_norm(_t(ls))
+    _, P, KN = tr.full_pair_quantities(A, _t(mu), N, _idx(pi), _idx(pj))
+    P, KN = P.numpy(), KN.numpy()
+    p = alpha[pi] + alpha[pj]
+    for a_ in range(len(pi)):
+        ref = 0.0
+        for at in range(len(Z)):
+            T = p[a_] * np.sum((P[a_] - atoms[at]) ** 2)
+            F0 = 0.5 * math.sqrt(math.pi / T) * erf(math.sqrt(T)) if T > 1e-12 else 1.0 - T / 3
+            ref -= Z[at] * 2 * math.pi / p[a_] * F0
+        assert abs(Vc[a_] - KN[a_] * ref) < 1e-10 * abs(KN[a_] * ref)
+    V20 = orc.nuclear_pairs(quat, ls, mu, pi, pj, atoms, Z)
+    V20t = tr.full_nuclear_pairs(_t(quat), _t(ls), _t(mu), _idx(pi), _idx(pj), _t(atoms),
+                                 _t(Z)).numpy()
+    assert np.max(np.abs(V20 - V20t) / np.abs(V20t)) < 1e-13
+
+
+def test_external_energy_invariances(orc, wl):
+    """Moving splats and nuclei together (translation, rotation) leaves E_ext unchanged, the
+    unique list with weights 2 - delta_ij equals the ordered list, and padding adds nothing."""
+    s, pi, pj, w = _nuc_system(wl, orc)
+    E = orc.external_energy(s.quat, s.log_scale, s.centers, s.C, s.occ, pi, pj, w, s.atoms,
+                            s.charges)
+    shift = np.array([1.3, -0.7, 2.1])
+    Es = orc.external_energy(s.quat, s.log_scale, s.centers + shift, s.C, s.occ, pi, pj, w,
+                             s.atoms + shift, s.charges)
+    assert abs(Es - E) < 1e-12 * abs(E)
+    th = 0.7
+    Rz = np.array([[math.cos(th), -math.sin(th), 0], [math.sin(th), math.cos(th), 0], [0, 0, 1]])
+    qz = np.array([math.cos(th / 2), 0, 0, math.sin(th / 2)])     # rotation about z by th
+    w0, x0, y0, z0 = qz
+    qr = np.array([[w0 * a - x0 * b - y0 * c - z0 * d, w0 * b + x0 * a + y0 * d - z0 * c,
+                    w0 * c - x0 * d + y0 * a + z0 * b, w0 * d + x0 * c - y0 * b + z0 * a]
+                   for a, b, c, d in s.quat])
+    Er = orc.external_energy(qr, s.log_scale, s.centers @ Rz.T, s.C, s.occ, pi, pj, w,
+                             s.atoms @ Rz.T, s.charges)
+    assert abs(Er - E) < 1e-11 * abs(E)
+    po, qo, wo, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    Eo = orc.external_energy(s.quat, s.log_scale, s.centers, s.C, s.occ, po, qo, wo, s.atoms,
+                             s.charges)
+    assert abs(Eo - E) < 1e-12 * abs(E)
+    pad = len(pi) + 17
+    pp, qp, wp, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, pad, True)
+    Ep = orc.external_energy(s.quat, s.log_scale, s.centers, s.C, s.occ, pp, qp, wp, s.atoms,
+                             s.charges)
+    assert Ep == E
+
+
+def test_external_energy_autograd_matches_finite_differences(orc, tr, wl):
+    """Autograd of the literal restatement (the gradient reference for the GPU) against central
+    differences of the C oracle, for nuclear coordinates and splat leaves."""
+    s, pi, pj, w = _nuc_system(wl, orc, M=16, seed=7)
+    args = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    R = _t(s.atoms, True)
+    E = tr.screened_external_energy(*args, _t(s.occ), _idx(pi), _idx(pj), _t(w), R,
+                                    _t(s.charges))
+    E.backward()
+    h = 1e-5
+
+    def f(**kw):
+        v = dict(quat=s.quat, log_scale=s.log_scale, centers=s.centers, C=s.C, atoms=s.atoms)
+        v.update(kw)
+        return orc.external_energy(v["quat"], v["log_scale"], v["centers"], v["C"], s.occ, pi, pj,
+                                   w, v["atoms"], s.charges)
+
+    for name, arr, g in (("atoms", s.atoms, R.grad), ("centers", s.centers, args[2].grad),
+                         ("log_scale", s.log_scale, args[1].grad), ("quat", s.quat, args[0].grad)):
+        for idx in [(0, 0), (1, 2), (arr.shape[0] - 1, 1)]:
+            up, dn = arr.copy(), arr.copy()
+            up[idx] += h; dn[idx] -= h
+            fd = (f(**{name: up}) - f(**{name: dn})) / (2 * h)
+            assert abs(fd - g[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
