@@ -21,7 +21,8 @@ GSDFT_ERR_HIP = 4
 GSDFT_ERR_LIB = 5
 GSDFT_ERR_WORKSPACE = 6
 
-PROF_GAMMA_FWD, PROF_GAMMA_BWD, PROF_SCREEN, PROF_METRIC, PROF_CHOLESKY, PROF_SOLVE = range(6)
+(PROF_GAMMA_FWD, PROF_GAMMA_BWD, PROF_SCREEN, PROF_METRIC, PROF_CHOLESKY, PROF_SOLVE,
+ PROF_NUC_PAIRS, PROF_NUC_ATOMS) = range(8)
 
 _i64, _i32, _int, _dbl, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
 _vp = ctypes.c_void_p

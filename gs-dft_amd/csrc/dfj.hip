@@ -761,7 +761,8 @@ __global__ __launch_bounds__(256) void k_vne_atom_grad(int64_t n_atoms,
                                                        const double* __restrict__ charges,
                                                        int64_t n, const double* __restrict__ rec,
                                                        int64_t per_slab,
-                                                       double* __restrict__ partial) {
+                                                       double* __restrict__ partial,
+                                                       unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
@@ -772,6 +773,7 @@ __global__ __launch_bounds__(256) void k_vne_atom_grad(int64_t n_atoms,
     const int64_t a0 = blockIdx.y * per_slab;
     const int64_t a1 = min(n, a0 + per_slab);
     double gx = 0.0, gy = 0.0, gz = 0.0;
+    uint32_t nodes = 0;
     for (int64_t a = a0; a < a1; ++a) {
         const double* __restrict__ r = rec + kRec * a;
         const double c = r[13] * r[14];          // KN_a q_a, wave-uniform
@@ -803,13 +805,14 @@ __global__ __launch_bounds__(256) void k_vne_atom_grad(int64_t n_atoms,
             gs3 = __builtin_fma(g, st * st * st, gs3);
             return screen_after(t) && wave_all_beyond(v.z);
         };
-        node_loop<0>(node);
+        nodes += node_loop<0>(node);
         const double f0 = -I3 * gs1, f1 = -(I1 * gs2 + gs3), f2 = gs2;
         const double s2 = 2.0 * c;
         gx = __builtin_fma(s2, f0 * dx + f1 * ax + f2 * bx, gx);
         gy = __builtin_fma(s2, f0 * dy + f1 * ay + f2 * by, gy);
         gz = __builtin_fma(s2, f0 * dz + f1 * az + f2 * bz, gz);
     }
+    count_work(work, live, nodes);
     if (!live) return;
     const double u = -charges[A] * kPrefNuc;
     double* o = partial + ((int64_t)blockIdx.y * n_atoms + A) * 3;
@@ -1211,8 +1214,10 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
                                                             w.g.rec_sorted);
     const Split sp = bwd_split(n_atoms, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+    profile_begin(kProfNucPairs, s);
     k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab, w.g.acc,
-                                     nullptr);
+                                     profile_work_counter(kProfNucPairs));
+    profile_end(kProfNucPairs, s);
     GSDFT_HIP(hipGetLastError());
     k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPrefNuc,
                                                        w.g.pair_order.perm, pi, pj, weight,
@@ -1311,8 +1316,11 @@ extern "C" int gsdft_external_energy(
     if (datoms) {
         const Split sa = atom_split(n_atoms, n);
         dim3 grid((unsigned)((n_atoms + 255) / 256), (unsigned)sa.slabs);
+        profile_begin(kProfNucAtoms, s);
         k_vne_atom_grad<<<grid, 256, 0, s>>>(n_atoms, atom_coords, atom_charges, n, w.g.rec,
-                                             sa.per_slab, w.atom_partial);
+                                             sa.per_slab, w.atom_partial,
+                                             profile_work_counter(kProfNucAtoms));
+        profile_end(kProfNucAtoms, s);
         GSDFT_HIP(hipGetLastError());
         k_slab_sum_flat<<<blocks_for(3 * n_atoms, 256), 256, 0, s>>>(3 * n_atoms, sa.slabs,
                                                                      w.atom_partial, datoms);

@@ -163,11 +163,13 @@ int gsdft_external_energy(int64_t M, const double* quat, const double* log_scale
                           void* stream);
 
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
- * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve.
- * gsdft_profile_read synchronises the recorded events and returns the summed milliseconds and
- * the launch count since the last reset. gsdft_profile_read_work returns the work units the
- * kernels executed while profiling was on (ids 0 and 1: quadrature nodes evaluated, summed over
- * live lanes, so at most 20 N n per launch; other ids: 0). Profiling allocates a few bytes of
+ * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
+ * 6 nuclear attraction per pair (values and splat moments), 7 nuclear attraction per nucleus
+ * (nuclear gradient). gsdft_profile_read synchronises the recorded events and returns the summed
+ * milliseconds and the launch count since the last reset. gsdft_profile_read_work returns the
+ * work units the kernels executed while profiling was on (ids 0, 1, 6, 7: quadrature nodes
+ * evaluated, summed over live lanes, so at most 20 x (aux functions or nuclei) x pairs per
+ * launch; other ids: 0). Profiling allocates a few bytes of
  * device memory on the device current when it is first enabled. */
 int gsdft_profile_enable(int on);
 int gsdft_profile_read(int id, double* total_ms, int64_t* launches, int reset);
