@@ -6,12 +6,13 @@ HIP kernels for gfx950 in ``lib/libgsdft.so`` (C ABI declared in ``include/gsdft
 """
 from .basis import IsotropicSplat, Splat, init_product_aux
 from .energy import SplatDFJ, SplatModel, SplatState, refresh, train_pad_to
+from .exact import screened_coulomb_J, screened_coulomb_energy
 from .ri import (aux_cholesky, aux_metric, coulomb_pairs, df_coulomb_energy_screened,
                  df_coulomb_gamma_screened, df_coulomb_solve, shift_diag)
 from .screening import (PairIndex, build_pair_index, count_significant, density_pairs,
                         live_length, neighbor_pairs, pair_weight, screened_external_energy,
                         screened_nuclear_pairs, screened_overlap_pairs)
-from .terms import (SCREEN_PAD, CoulombTerm, DFSpec, ExactSpec, Pairlist,
+from .terms import (SCREEN_PAD, CoulombTerm, DFSpec, ExactSpec, Pairlist, ScreenedExactCoulomb,
                     ScreenedProductDFCoulomb, df, exact, pairlist)
 
 __all__ = [
@@ -19,9 +20,11 @@ __all__ = [
     "SplatDFJ", "SplatModel", "SplatState", "refresh", "train_pad_to",
     "aux_metric", "aux_cholesky", "shift_diag", "df_coulomb_gamma_screened", "df_coulomb_solve",
     "df_coulomb_energy_screened", "coulomb_pairs",
+    "screened_coulomb_energy", "screened_coulomb_J",
     "neighbor_pairs", "count_significant", "pair_weight", "screened_overlap_pairs",
     "density_pairs", "screened_nuclear_pairs", "screened_external_energy",
     "PairIndex", "build_pair_index", "live_length",
     "SCREEN_PAD", "CoulombTerm", "DFSpec", "ExactSpec", "Pairlist", "ScreenedProductDFCoulomb",
+    "ScreenedExactCoulomb",
     "df", "exact", "pairlist",
 ]

@@ -22,7 +22,7 @@ GSDFT_ERR_LIB = 5
 GSDFT_ERR_WORKSPACE = 6
 
 (PROF_GAMMA_FWD, PROF_GAMMA_BWD, PROF_SCREEN, PROF_METRIC, PROF_CHOLESKY, PROF_SOLVE,
- PROF_NUC_PAIRS, PROF_NUC_ATOMS) = range(8)
+ PROF_NUC_PAIRS, PROF_NUC_ATOMS, PROF_ERI_FWD, PROF_ERI_BWD) = range(10)
 
 _i64, _i32, _int, _dbl, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
 _vp = ctypes.c_void_p
@@ -60,6 +60,9 @@ SIGNATURES = {
     "gsdft_external_energy": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
                               _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                               _vp, _sz, _vp],
+    "gsdft_exact_coulomb_workspace_size": [_i64, _i64, _i64, _int, _psz],
+    "gsdft_exact_coulomb": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                            _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_profile_enable": [_int],
     "gsdft_profile_read": [_int, _pd, _pi64, _int],
     "gsdft_profile_read_work": [_int, ctypes.POINTER(ctypes.c_uint64), _int],

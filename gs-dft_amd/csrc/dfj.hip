@@ -492,6 +492,63 @@ __device__ __forceinline__ void sym_vec(const double A[6], const double x[3], do
     y[2] = A[4] * x[0] + A[5] * x[1] + A[2] * x[2];
 }
 
+// Reverse of gs_dft/coulomb/stream.py:203-215 for pair a = (i, j): from dE/dAh (Gh, six slots,
+// updated in place), dE/dPa (gP) and dE/dKN_a (gKN) to the 20 per-pair splat contributions (SoA):
+//   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
+__device__ void pair_reverse(int64_t n, int64_t a, int64_t i, int64_t j,
+                             const double* __restrict__ A6, const double* __restrict__ mu,
+                             const double* __restrict__ Nrm, double Gh[6], const double gP[3],
+                             double gKN, double* __restrict__ contrib) {
+    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
+    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
+    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
+    const double Ni = Nrm[i], Nj = Nrm[j];
+    Sym3 Ahp;
+    double Pc[3], KNp;
+    pair_quantities(Ai, Aj, mui, muj, Ni, Nj, &Ahp, Pc, &KNp);
+    double Gi[6] = {0, 0, 0, 0, 0, 0}, Gj[6] = {0, 0, 0, 0, 0, 0};
+    double gmi[3] = {0, 0, 0}, gmj[3] = {0, 0, 0};
+    // KN = N_i N_j K, K = exp(-e), e = d . Ai Ah^-1 Aj d
+    const double d[3] = {mui[0] - muj[0], mui[1] - muj[1], mui[2] - muj[2]};
+    double Ajd[3], Aid[3], u[3], v[3], Aiu[3], Ajv[3];
+    matvec(Aj, d, Ajd);
+    matvec(Ai, d, Aid);
+    solve3(Ahp, Ajd, u);
+    solve3(Ahp, Aid, v);
+    matvec(Ai, u, Aiu);
+    matvec(Aj, v, Ajv);
+    const double e = d[0] * Aiu[0] + d[1] * Aiu[1] + d[2] * Aiu[2];
+    const double K = exp(-e);
+    const double gNi = gKN * Nj * K, gNj = gKN * Ni * K;
+    const double ge = -gKN * KNp;
+    for (int k = 0; k < 3; ++k) {
+        const double gd = ge * (Aiu[k] + Ajv[k]);
+        gmi[k] += gd;
+        gmj[k] -= gd;
+    }
+    add_sym_outer(Gi, ge, d, u);
+    add_sym_outer(Gj, ge, v, d);
+    add_sym_outer(Gh, -ge, v, u);
+    // P = Ah^-1 (Ai mu_i + Aj mu_j)
+    double y[3];
+    solve3(Ahp, gP, y);
+    add_sym_outer(Gh, -1.0, y, Pc);
+    add_sym_outer(Gi, 1.0, y, mui);
+    add_sym_outer(Gj, 1.0, y, muj);
+    double Aiy[3], Ajy[3];
+    matvec(Ai, y, Aiy);
+    matvec(Aj, y, Ajy);
+    for (int k = 0; k < 3; ++k) { gmi[k] += Aiy[k]; gmj[k] += Ajy[k]; }
+    // Ah = Ai + Aj
+    for (int k = 0; k < 6; ++k) { Gi[k] += Gh[k]; Gj[k] += Gh[k]; }
+    double out[20];
+    for (int k = 0; k < 6; ++k) { out[k] = Gi[k]; out[10 + k] = Gj[k]; }
+    for (int k = 0; k < 3; ++k) { out[6 + k] = gmi[k]; out[16 + k] = gmj[k]; }
+    out[9] = gNi;
+    out[19] = gNj;
+    for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = out[c];
+}
+
 // Per pair: sum the slab moments, map them to dE/dAh, dE/dPa, dE/dKN_a, then through
 // gs_dft/coulomb/stream.py:203-215 to the two splats. Writes J and 20 contributions (SoA):
 //   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
@@ -556,56 +613,7 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, double pref,
         Gh[k] = scale * ((I1 * Sa[k] + Sb[k]) - (AS[3 * rw + cl] + AS[3 * cl + rw]) + T1 * eye
                          + T2 * (I1 * eye - Ah[k]) + T3 * adj[3 * rw + cl]);
     }
-    // ---- gs_dft/coulomb/stream.py:203-215 reverse
-    const int64_t i = pi[a], j = pj[a];
-    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
-    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
-    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
-    const double Ni = Nrm[i], Nj = Nrm[j];
-    Sym3 Ahp;
-    double Pc[3], KNp;
-    pair_quantities(Ai, Aj, mui, muj, Ni, Nj, &Ahp, Pc, &KNp);
-    double Gi[6] = {0, 0, 0, 0, 0, 0}, Gj[6] = {0, 0, 0, 0, 0, 0};
-    double gmi[3] = {0, 0, 0}, gmj[3] = {0, 0, 0};
-    // KN = N_i N_j K, K = exp(-e), e = d . Ai Ah^-1 Aj d
-    const double d[3] = {mui[0] - muj[0], mui[1] - muj[1], mui[2] - muj[2]};
-    double Ajd[3], Aid[3], u[3], v[3], Aiu[3], Ajv[3];
-    matvec(Aj, d, Ajd);
-    matvec(Ai, d, Aid);
-    solve3(Ahp, Ajd, u);
-    solve3(Ahp, Aid, v);
-    matvec(Ai, u, Aiu);
-    matvec(Aj, v, Ajv);
-    const double e = d[0] * Aiu[0] + d[1] * Aiu[1] + d[2] * Aiu[2];
-    const double K = exp(-e);
-    const double gNi = gKN * Nj * K, gNj = gKN * Ni * K;
-    const double ge = -gKN * KNp;
-    for (int k = 0; k < 3; ++k) {
-        const double gd = ge * (Aiu[k] + Ajv[k]);
-        gmi[k] += gd;
-        gmj[k] -= gd;
-    }
-    add_sym_outer(Gi, ge, d, u);
-    add_sym_outer(Gj, ge, v, d);
-    add_sym_outer(Gh, -ge, v, u);
-    // P = Ah^-1 (Ai mu_i + Aj mu_j)
-    double y[3];
-    solve3(Ahp, gP, y);
-    add_sym_outer(Gh, -1.0, y, Pc);
-    add_sym_outer(Gi, 1.0, y, mui);
-    add_sym_outer(Gj, 1.0, y, muj);
-    double Aiy[3], Ajy[3];
-    matvec(Ai, y, Aiy);
-    matvec(Aj, y, Ajy);
-    for (int k = 0; k < 3; ++k) { gmi[k] += Aiy[k]; gmj[k] += Ajy[k]; }
-    // Ah = Ai + Aj
-    for (int k = 0; k < 6; ++k) { Gi[k] += Gh[k]; Gj[k] += Gh[k]; }
-    double out[20];
-    for (int k = 0; k < 6; ++k) { out[k] = Gi[k]; out[10 + k] = Gj[k]; }
-    for (int k = 0; k < 3; ++k) { out[6 + k] = gmi[k]; out[16 + k] = gmj[k]; }
-    out[9] = gNi;
-    out[19] = gNj;
-    for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = out[c];
+    pair_reverse(n, a, pi[a], pj[a], A6, mu, Nrm, Gh, gP, gKN, contrib);
 }
 
 // One wave per splat: deterministic segmented sums of the i-side and j-side contributions, then
@@ -829,6 +837,285 @@ __global__ void k_slab_sum_flat(int64_t count, int64_t slabs, const double* __re
     double s = 0.0;
     for (int64_t k = 0; k < slabs; ++k) s += partial[k * count + i];
     out[i] = s;
+}
+
+// ------------------------------------------------------------------ exact pair-pair Coulomb
+// gs_dft/coulomb/stream.py:249-281,296-320: (a|b) = KN_a KN_b (2/sqrt(pi)) sum_t w_t pi^3
+// det(G_t)^(-1/2) exp(-quad_t), G_t the 6x6 block precision [[A_a + sI, -sI], [-sI, A_b + sI]]
+// at s = t^2 (the reference reduces it by a Schur complement). With T = A_a^-1 + A_b^-1 and
+// d = P_a - P_b, det G_t = det A_a det A_b det(I + sT) and quad_t = s d.(I + sT)^-1 d, and
+// Cayley-Hamilton gives, division-free,
+//   E(s) = det(I + sT) = 1 + s (J1 + s (J2 + s J3)),  J1 = tr T, J2 = tr adj T, J3 = det T,
+//   s d.adj(I + sT).d = s (p0 + s (p1 + s p2)),     p0 = |d|^2, p1 = J1 p0 - d.T d, p2 = d.adj T.d,
+// so (a|b) = h_a h_b 2 pi^2.5 sum_t w_t E^(-1/2) e^(-z), z = s (p0 + s p1 + s^2 p2) / E, with
+// h = KN det(A)^(-1/2) per pair -- the node of the three-centre kernels with s_t = t^2.
+// Pair record (slot order): A^-1 (6) | P (3) | h | Pw = w sum_o occ_o C_io C_jo | pad.
+constexpr int kEriRec = 12;
+constexpr double kPrefEri = kTwoPi25;                 // (2/sqrt(pi)) pi^3 = 2 pi^2.5
+
+__global__ void k_eri_rec(int64_t n, const int32_t* __restrict__ perm,
+                          const int32_t* __restrict__ pi, const int32_t* __restrict__ pj,
+                          const double* __restrict__ A6, const double* __restrict__ mu,
+                          const double* __restrict__ Nrm, const double* __restrict__ q,
+                          double* __restrict__ rec) {
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (slot >= n) return;
+    const int64_t a = perm[slot];
+    const int64_t i = pi[a], j = pj[a];
+    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
+    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
+    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
+    Sym3 Ah;
+    double P[3], KN;
+    pair_quantities(Ai, Aj, mui, muj, Nrm[i], Nrm[j], &Ah, P, &KN);
+    double c[9];
+    adj3(Ah, c);
+    const double det = det3(Ah);
+    double* r = rec + kEriRec * slot;
+    r[0] = c[0] / det; r[1] = c[4] / det; r[2] = c[8] / det;
+    r[3] = c[1] / det; r[4] = c[2] / det; r[5] = c[5] / det;
+    r[6] = P[0]; r[7] = P[1]; r[8] = P[2];
+    r[9] = KN / sqrt(det);
+    r[10] = q[a];
+    r[11] = 0.0;
+}
+
+// The centre-dependent scalars of one pair-pair from T (six slots) and d.
+struct EriGeom {
+    double J1, J2, J3, p0, p1, p2;
+};
+
+__device__ __forceinline__ EriGeom eri_geom(const double T[6], const double d[3], double adjT[6],
+                                           double Td[3]) {
+    const double xx = T[0], yy = T[1], zz = T[2], xy = T[3], xz = T[4], yz = T[5];
+    adjT[0] = __builtin_fma(yy, zz, -yz * yz);
+    adjT[1] = __builtin_fma(xx, zz, -xz * xz);
+    adjT[2] = __builtin_fma(xx, yy, -xy * xy);
+    adjT[3] = __builtin_fma(xz, yz, -xy * zz);
+    adjT[4] = __builtin_fma(xy, yz, -xz * yy);
+    adjT[5] = __builtin_fma(xy, xz, -xx * yz);
+    EriGeom g;
+    g.J1 = xx + yy + zz;
+    g.J2 = adjT[0] + adjT[1] + adjT[2];
+    g.J3 = __builtin_fma(xx, adjT[0], __builtin_fma(xy, adjT[3], xz * adjT[4]));
+    Td[0] = __builtin_fma(xx, d[0], __builtin_fma(xy, d[1], xz * d[2]));
+    Td[1] = __builtin_fma(xy, d[0], __builtin_fma(yy, d[1], yz * d[2]));
+    Td[2] = __builtin_fma(xz, d[0], __builtin_fma(yz, d[1], zz * d[2]));
+    g.p0 = __builtin_fma(d[0], d[0], __builtin_fma(d[1], d[1], d[2] * d[2]));
+    const double dTd = __builtin_fma(d[0], Td[0], __builtin_fma(d[1], Td[1], d[2] * Td[2]));
+    g.p1 = __builtin_fma(g.J1, g.p0, -dTd);
+    const double ax = __builtin_fma(adjT[0], d[0], __builtin_fma(adjT[3], d[1], adjT[4] * d[2]));
+    const double ay = __builtin_fma(adjT[3], d[0], __builtin_fma(adjT[1], d[1], adjT[5] * d[2]));
+    const double az = __builtin_fma(adjT[4], d[0], __builtin_fma(adjT[5], d[1], adjT[2] * d[2]));
+    g.p2 = __builtin_fma(d[0], ax, __builtin_fma(d[1], ay, d[2] * az));
+    return g;
+}
+
+// Jpart[slab][slot] = sum_{b in slab} Pw_b h_b F_ab (times h_a 2 pi^2.5 in k_eri_finish): one lane
+// per bra slot, the ket records of a slab wave-uniform.
+__global__ __launch_bounds__(256) void k_eri_fwd(int64_t n, const double* __restrict__ rec,
+                                                 int64_t per_slab, double* __restrict__ partial,
+                                                 unsigned long long* __restrict__ work) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = a < n;
+    const double* __restrict__ ra = rec + kEriRec * (live ? a : 0);
+    const double Ta[6] = {ra[0], ra[1], ra[2], ra[3], ra[4], ra[5]};
+    const double Px = live ? ra[6] : kFarAway, Py = live ? ra[7] : kFarAway,
+                 Pz = live ? ra[8] : kFarAway;
+    const int64_t b0 = blockIdx.y * per_slab;
+    const int64_t b1 = min(n, b0 + per_slab);
+    double acc = 0.0;
+    uint32_t nodes = 0;
+    for (int64_t b = b0; b < b1; ++b) {
+        const double* __restrict__ rb = rec + kEriRec * b;
+        const double cb = rb[9] * rb[10];              // h_b Pw_b, wave-uniform
+        if (cb == 0.0) continue;                       // padding adds exactly 0
+        const double T[6] = {Ta[0] + rb[0], Ta[1] + rb[1], Ta[2] + rb[2],
+                             Ta[3] + rb[3], Ta[4] + rb[4], Ta[5] + rb[5]};
+        const double d[3] = {Px - rb[6], Py - rb[7], Pz - rb[8]};
+        double adjT[6], Td[3];
+        const EriGeom G = eri_geom(T, d, adjT, Td);
+        double F = 0.0;
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr double st = quad_t(t) * quad_t(t);
+            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
+                                                              G.J1), 1.0);
+            const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
+            const NodeVal v = node_val(Es, st * num);
+            F = __builtin_fma(quad_w(t) * v.y0, exp_neg_tab(v.arg, tab), F);
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
+        F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
+        acc = __builtin_fma(F, cb, acc);
+    }
+    count_work(work, live, nodes);
+    if (live) partial[blockIdx.y * n + a] = acc;
+}
+
+// Reverse: per bra slot the moments MJ = sum_b c_b F, MT = sum_b c_b dF/dT (six slots) and
+// Md = sum_b c_b dF/dd, c_b = h_b Pw_b, stored (slabs, 10, n).
+//   node sums: F, A_k = sum g (z - 1/2) s^k, B_k = sum g s^k (k = 1..3), g = f / E;
+//   dF/dJ_k = A_k, dF/dp_k = -B_(k+1); with p1 = J1 p0 - d.T d and p2 = |T d|^2 - J1 d.T d + J2 p0:
+//   dF/dT = gJ1 I + gJ2 (J1 I - T) + gJ3 adj T - gp1' d d^T
+//           + gp2 ((T d d^T + d d^T T) - (d.T d) I - J1 d d^T + p0 (J1 I - T)),
+//   dF/dd = 2 (gp0' d + gp1'' T d + gp2 adj(T) d), primes folding the p1 chain.
+constexpr int kEriAcc = 10;
+
+__global__ __launch_bounds__(256) void k_eri_bwd(int64_t n, const double* __restrict__ rec,
+                                                 int64_t per_slab, double* __restrict__ partial,
+                                                 unsigned long long* __restrict__ work) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = a < n;
+    const double* __restrict__ ra = rec + kEriRec * (live ? a : 0);
+    const double Ta[6] = {ra[0], ra[1], ra[2], ra[3], ra[4], ra[5]};
+    const double Px = live ? ra[6] : kFarAway, Py = live ? ra[7] : kFarAway,
+                 Pz = live ? ra[8] : kFarAway;
+    const int64_t b0 = blockIdx.y * per_slab;
+    const int64_t b1 = min(n, b0 + per_slab);
+    double MJ = 0.0, MT[6] = {0, 0, 0, 0, 0, 0}, Md[3] = {0, 0, 0};
+    uint32_t nodes = 0;
+    for (int64_t b = b0; b < b1; ++b) {
+        const double* __restrict__ rb = rec + kEriRec * b;
+        const double cb = rb[9] * rb[10];
+        if (cb == 0.0) continue;
+        const double T[6] = {Ta[0] + rb[0], Ta[1] + rb[1], Ta[2] + rb[2],
+                             Ta[3] + rb[3], Ta[4] + rb[4], Ta[5] + rb[5]};
+        const double d[3] = {Px - rb[6], Py - rb[7], Pz - rb[8]};
+        double adjT[6], Td[3];
+        const EriGeom G = eri_geom(T, d, adjT, Td);
+        double F = 0, A1 = 0, A2 = 0, A3 = 0, B1 = 0, B2 = 0, B3 = 0;
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr double st = quad_t(t) * quad_t(t);
+            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
+                                                              G.J1), 1.0);
+            const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
+            const NodeVal v = node_val(Es, st * num);
+            const double f = (quad_w(t) * v.y0) * exp_neg_tab(v.arg, tab);
+            F += f;
+            const double g = f * v.ip;
+            const double gh = g * (v.z - 0.5);
+            A1 = __builtin_fma(gh, st, A1);
+            A2 = __builtin_fma(gh, st * st, A2);
+            A3 = __builtin_fma(gh, st * st * st, A3);
+            B1 = __builtin_fma(g, st, B1);
+            B2 = __builtin_fma(g, st * st, B2);
+            B3 = __builtin_fma(g, st * st * st, B3);
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
+        F = (G.p0 == G.p0) ? F : G.p0;
+        // chain to T and d
+        const double gp1 = -B2, gp2 = -B3;
+        const double gJ1 = __builtin_fma(gp1, G.p0, A1);             // p1 = J1 p0 - d.T d
+        const double gp0 = __builtin_fma(gp1, G.J1, -B1);
+        const double gJ2 = A2, gJ3 = A3;
+        const double dTd = __builtin_fma(d[0], Td[0], __builtin_fma(d[1], Td[1], d[2] * Td[2]));
+        // diagonal part: (gJ1 + gJ2 J1 - gp2 dTd + gp2 p0 J1) I
+        const double diag = gJ1 + G.J1 * __builtin_fma(gp2, G.p0, gJ2) - gp2 * dTd;
+        const double cT = -__builtin_fma(gp2, G.p0, gJ2);           // coefficient of T
+        const double cdd = -__builtin_fma(gp2, G.J1, gp1);          // coefficient of d d^T
+        const int rr_[6] = {0, 1, 2, 0, 0, 1}, cc_[6] = {0, 1, 2, 1, 2, 2};
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const int r = rr_[k], c = cc_[k];
+            double gt = __builtin_fma(cT, T[k], gJ3 * adjT[k]);
+            gt = __builtin_fma(cdd, d[r] * d[c], gt);
+            gt = __builtin_fma(gp2, __builtin_fma(Td[r], d[c], d[r] * Td[c]), gt);
+            if (r == c) gt += diag;
+            MT[k] = __builtin_fma(cb, gt, MT[k]);
+        }
+        const double ax = __builtin_fma(adjT[0], d[0], __builtin_fma(adjT[3], d[1], adjT[4] * d[2]));
+        const double ay = __builtin_fma(adjT[3], d[0], __builtin_fma(adjT[1], d[1], adjT[5] * d[2]));
+        const double az = __builtin_fma(adjT[4], d[0], __builtin_fma(adjT[5], d[1], adjT[2] * d[2]));
+        const double c2 = 2.0 * cb;
+        Md[0] = __builtin_fma(c2, __builtin_fma(gp0, d[0], __builtin_fma(-gp1, Td[0], gp2 * ax)), Md[0]);
+        Md[1] = __builtin_fma(c2, __builtin_fma(gp0, d[1], __builtin_fma(-gp1, Td[1], gp2 * ay)), Md[1]);
+        Md[2] = __builtin_fma(c2, __builtin_fma(gp0, d[2], __builtin_fma(-gp1, Td[2], gp2 * az)), Md[2]);
+        MJ = __builtin_fma(F, cb, MJ);
+    }
+    count_work(work, live, nodes);
+    if (!live) return;
+    double* o = partial + (int64_t)blockIdx.y * kEriAcc * n + a;
+    const double v[kEriAcc] = {MJ, MT[0], MT[1], MT[2], MT[3], MT[4], MT[5], Md[0], Md[1], Md[2]};
+#pragma unroll
+    for (int c = 0; c < kEriAcc; ++c) o[(int64_t)c * n] = v[c];
+}
+
+// J[perm[slot]] = h_a 2 pi^2.5 sum_slabs Jpart (0 on zero-weight entries).
+__global__ void k_eri_finish(int64_t n, int64_t slabs, const int32_t* __restrict__ perm,
+                             const double* __restrict__ rec, const double* __restrict__ partial,
+                             double* __restrict__ J) {
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (slot >= n) return;
+    const double* r = rec + kEriRec * slot;
+    double acc = 0.0;
+    for (int64_t k = 0; k < slabs; ++k) acc += partial[k * n + slot];
+    J[perm[slot]] = (r[10] == 0.0) ? 0.0 : r[9] * kPrefEri * acc;
+}
+
+// Per slot: J and the pair's gradient from the reverse moments. E = 1/2 sum_ab Pw_a Pw_b (a|b), so
+// dE/dh_a = Pw_a pref MJ, dE/dT_a = Pw_a h_a pref MT (T = A_a^-1 + A_b^-1, so dE/dA_a =
+// -A^-1 (dE/dT_a) A^-1), dE/dP_a = Pw_a h_a pref Md; h = KN det(A)^(-1/2) adds
+// dE/dKN = gh det(A)^(-1/2) and dE/dA = -gh h A^-1 / 2. Then the pair reverse to the two splats.
+__global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restrict__ perm,
+                               const int32_t* __restrict__ pi, const int32_t* __restrict__ pj,
+                               const double* __restrict__ A6, const double* __restrict__ mu,
+                               const double* __restrict__ Nrm, const double* __restrict__ rec,
+                               const double* __restrict__ partial, double* __restrict__ J,
+                               double* __restrict__ contrib) {
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (slot >= n) return;
+    const int64_t a = perm[slot];
+    const double* r = rec + kEriRec * slot;
+    const double h = r[9], Pw = r[10];
+    if (Pw == 0.0) {
+        J[a] = 0.0;
+        for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
+        return;
+    }
+    double m[kEriAcc];
+    for (int c = 0; c < kEriAcc; ++c) {
+        double s = 0.0;
+        for (int64_t k = 0; k < slabs; ++k) s += partial[(k * kEriAcc + c) * n + slot];
+        m[c] = s;
+    }
+    J[a] = h * kPrefEri * m[0];
+    const double gh = Pw * kPrefEri * m[0];
+    const double sc = Pw * h * kPrefEri;
+    const double Ai[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
+    const double GT[6] = {sc * m[1], sc * m[2], sc * m[3], sc * m[4], sc * m[5], sc * m[6]};
+    double gP[3] = {sc * m[7], sc * m[8], sc * m[9]};
+    // dE/dA = -A^-1 GT A^-1 - gh h A^-1 / 2
+    double X[9];
+    sym_mul(Ai, GT, X);
+    const double ai[9] = {Ai[0], Ai[3], Ai[4], Ai[3], Ai[1], Ai[5], Ai[4], Ai[5], Ai[2]};
+    const int rr_[6] = {0, 1, 2, 0, 0, 1}, cc_[6] = {0, 1, 2, 1, 2, 2};
+    double Gh[6];
+    for (int k = 0; k < 6; ++k) {
+        const int rw = rr_[k], cl = cc_[k];
+        const double xa = X[3 * rw] * ai[cl] + X[3 * rw + 1] * ai[3 + cl] + X[3 * rw + 2] * ai[6 + cl];
+        Gh[k] = -xa - 0.5 * gh * h * Ai[k];
+    }
+    const int64_t i = pi[a], j = pj[a];
+    // h = KN det(A)^(-1/2): dE/dKN = gh det(A)^(-1/2) = gh h / KN (KN > 0 for every listed pair)
+    const double Ni = Nrm[i], Nj = Nrm[j];
+    const Sym3 Asi = load_sym(A6 + 6 * i), Asj = load_sym(A6 + 6 * j);
+    const double mui[3] = {mu[3 * i], mu[3 * i + 1], mu[3 * i + 2]};
+    const double muj[3] = {mu[3 * j], mu[3 * j + 1], mu[3 * j + 2]};
+    Sym3 Ahp;
+    double Pc[3], KN;
+    pair_quantities(Asi, Asj, mui, muj, Ni, Nj, &Ahp, Pc, &KN);
+    const double gKN = gh * sqrt(1.0 / det3(Ahp));
+    pair_reverse(n, a, i, j, A6, mu, Nrm, Gh, gP, gKN, contrib);
 }
 
 // ------------------------------------------------------------------ work split
@@ -1335,5 +1622,122 @@ extern "C" int gsdft_density_pairs(int64_t n, const int32_t* pi, const int32_t* 
     if (n < 0 || k <= 0 || (n > 0 && (!pi || !pj || !C || !occ || !out)))
         return fail(GSDFT_ERR_ARG, "gsdft_density_pairs: bad arguments");
     return launch_pair_density(n, pi, pj, nullptr, k, C, occ, out, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ exact Coulomb (C ABI)
+
+namespace gsdft {
+namespace {
+
+struct EriWs {
+    double *A6, *Nrm, *q, *rec3, *rec, *partial, *contrib;
+    PairOrderWs order;
+};
+
+int layout_eri(Arena& ar, int64_t M, int64_t n, bool grads, EriWs* w) {
+    w->A6 = ar.take<double>(6 * M + 1);
+    w->Nrm = ar.take<double>(M + 1);
+    w->q = ar.take<double>(n + 1);
+    w->rec3 = ar.take<double>(kRec * n + kRec);
+    w->rec = ar.take<double>(kEriRec * n + kEriRec);
+    GSDFT_TRY(pair_order_layout(ar, n, &w->order));
+    const Split sp = bwd_split(n, n);
+    w->partial = ar.take<double>(sp.slabs * (grads ? kEriAcc : 1) * n + 1);
+    w->contrib = grads ? ar.take<double>(20 * n + 1) : nullptr;
+    return GSDFT_OK;
+}
+
+}  // namespace
+}  // namespace gsdft
+
+extern "C" int gsdft_exact_coulomb_workspace_size(int64_t M, int64_t k, int64_t n, int grads,
+                                                  size_t* bytes) {
+    (void)k;
+    if (M < 0 || n < 0 || !bytes)
+        return fail(GSDFT_ERR_ARG, "exact_coulomb_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    EriWs w;
+    GSDFT_TRY(layout_eri(ar, M, n, grads != 0, &w));
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
+                                   const double* centers, int64_t k, const double* C,
+                                   const double* occ, int64_t n, const int32_t* pi,
+                                   const int32_t* pj, const double* weight,
+                                   const int32_t* row_ptr, const int32_t* row_perm,
+                                   const int32_t* col_ptr, const int32_t* col_perm,
+                                   double* energy, double* J, double* dquat, double* dlog_scale,
+                                   double* dcenters, double* dC, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    const bool grads = dquat || dlog_scale || dcenters || dC;
+    if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy ||
+        (n > 0 && (!pi || !pj || !weight || !J)))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: bad arguments");
+    if (grads && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
+                  (n > 0 && (!row_perm || !col_perm))))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: the gradients come together (dquat, "
+                    "dlog_scale, dcenters, dC) and need the pair index");
+    if (n > INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the int32 range");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    EriWs w;
+    GSDFT_TRY(layout_eri(ar, M, n, grads, &w));
+    if (!w.partial || (grads && !w.contrib))
+        return fail(GSDFT_ERR_WORKSPACE, "gsdft_exact_coulomb: workspace too small");
+    if (n == 0) {
+        k_fill<<<1, 256, 0, s>>>(1, 0.0, energy);
+        if (grads) {
+            k_fill<<<blocks_for(4 * M, 256), 256, 0, s>>>(4 * M, 0.0, dquat);
+            k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dlog_scale);
+            k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dcenters);
+            k_fill<<<blocks_for(M * k, 256), 256, 0, s>>>(M * k, 0.0, dC);
+        }
+        GSDFT_HIP(hipGetLastError());
+        return GSDFT_OK;
+    }
+    GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
+    GSDFT_TRY(launch_pair_density(n, pi, pj, weight, k, C, occ, w.q, s));
+    k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec3);
+    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_pair_order(n, w.rec3, kRec, w.order, s));
+    k_eri_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, w.order.perm, pi, pj, w.A6, centers, w.Nrm,
+                                                 w.q, w.rec);
+    GSDFT_HIP(hipGetLastError());
+    const Split sp = bwd_split(n, n);
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+    if (!grads) {
+        profile_begin(kProfEriFwd, s);
+        k_eri_fwd<<<grid, 256, 0, s>>>(n, w.rec, sp.per_slab, w.partial,
+                                       profile_work_counter(kProfEriFwd));
+        profile_end(kProfEriFwd, s);
+        GSDFT_HIP(hipGetLastError());
+        k_eri_finish<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.order.perm, w.rec,
+                                                        w.partial, J);
+    } else {
+        profile_begin(kProfEriBwd, s);
+        k_eri_bwd<<<grid, 256, 0, s>>>(n, w.rec, sp.per_slab, w.partial,
+                                       profile_work_counter(kProfEriBwd));
+        profile_end(kProfEriBwd, s);
+        GSDFT_HIP(hipGetLastError());
+        k_eri_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.order.perm, pi, pj,
+                                                          w.A6, centers, w.Nrm, w.rec,
+                                                          w.partial, J, w.contrib);
+    }
+    GSDFT_HIP(hipGetLastError());
+    // E_J = 1/2 sum_a Pw_a J_a (gs_dft/coulomb/stream.py:319-320), fixed summation order
+    k_scaled_dot<<<1, 1024, 0, s>>>(n, w.q, J, 0.5, energy);
+    GSDFT_HIP(hipGetLastError());
+    if (grads) {
+        k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
+                                                             col_perm, w.contrib, quat,
+                                                             log_scale, dquat, dlog_scale,
+                                                             dcenters);
+        GSDFT_HIP(hipGetLastError());
+        GSDFT_TRY(launch_dC(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J, weight, C, occ,
+                            dC, s));
+    }
+    return GSDFT_OK;
 }
 

@@ -47,7 +47,7 @@ void profile_end(int id, hipStream_t s);
 unsigned long long* profile_work_counter(int id);
 enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMetric = 3,
                  kProfCholesky = 4, kProfSolve = 5, kProfNucPairs = 6, kProfNucAtoms = 7,
-                 kProfCount = 8 };
+                 kProfEriFwd = 8, kProfEriBwd = 9, kProfCount = 10 };
 
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);

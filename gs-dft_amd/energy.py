@@ -16,7 +16,7 @@ import torch
 from . import ri as _cdf
 from . import screening as _scr
 from .basis import Splat, init_product_aux
-from .terms import DFSpec, Pairlist, ScreenedProductDFCoulomb, _make_coulomb
+from .terms import DFSpec, ExactSpec, Pairlist, ScreenedProductDFCoulomb, _make_coulomb
 
 
 @dataclasses.dataclass
@@ -54,10 +54,11 @@ def train_pad_to(screen: Pairlist, n0: int, n_devices: int = 1) -> int:
 
 
 class SplatDFJ:
-    """E_J of a splat model through ``coulomb=df()`` and ``screen=pairlist(...)``."""
+    """E_J of a splat model through ``coulomb=df()`` (or ``exact()``) and
+    ``screen=pairlist(...)``."""
 
-    def __init__(self, *, coulomb: DFSpec | None = None, screen: Pairlist | None = None,
-                 xc=None, mesh=None):
+    def __init__(self, *, coulomb: DFSpec | ExactSpec | None = None,
+                 screen: Pairlist | None = None, xc=None, mesh=None):
         if mesh is not None:
             raise NotImplementedError("mesh= shards the step across GPUs; this library runs the "
                                       "DF-J path on one GPU")

@@ -1,9 +1,10 @@
-"""The Coulomb plugin surface of the screened DF-J path, mirroring gs_dft/ks/terms.py.
+"""The Coulomb plugin surface of the screened paths, mirroring gs_dft/ks/terms.py.
 
-``df()`` and ``pairlist()`` build the same frozen spec values as the reference
+``df()``, ``exact()`` and ``pairlist()`` build the same frozen spec values as the reference
 (terms.py:58-139) and ``_make_coulomb`` resolves ``df()`` + ``screen=pairlist(...)`` to
-``ScreenedProductDFCoulomb``, whose ``energy`` has the reference signature
-``energy(basis, C_orth, P, occ, state) -> (E_J, E_K)`` (terms.py:146-169,236-256).
+``ScreenedProductDFCoulomb`` and ``exact()`` + ``screen=pairlist(...)`` to
+``ScreenedExactCoulomb``, whose ``energy`` has the reference signature
+``energy(basis, C_orth, P, occ, state) -> (E_J, E_K)`` (terms.py:146-169,193-205,236-256).
 """
 from __future__ import annotations
 
@@ -12,13 +13,15 @@ from dataclasses import dataclass
 
 import torch
 
+from . import exact as _cs
 from . import ri as _cdf
 
 
 @dataclass(frozen=True)
 class ExactSpec:
-    """Exact streamed-ERI Coulomb backend (gs_dft/ks/terms.py:48-55). Accepted as a spec value;
-    the exact path is not part of this library, so resolving it raises."""
+    """Exact streamed-ERI Coulomb backend (gs_dft/ks/terms.py:48-55). With a pair screen it
+    resolves to ``ScreenedExactCoulomb``; the dense (unscreened) exact strategy is not part of
+    this library. ``chunk=None`` is the strategy default (128 screened)."""
 
     chunk: int | None = None
 
@@ -106,6 +109,22 @@ class ScreenedProductDFCoulomb(CoulombTerm):
         return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
 
 
+@dataclass(frozen=True)
+class ScreenedExactCoulomb(CoulombTerm):
+    """Exact streamed ERI over the significant pairs, density-fitting free
+    (gs_dft/ks/terms.py:193-205); pure functionals only (no screened exact exchange)."""
+
+    hf_coeff: float = 0.0
+    chunk: int = 128
+
+    def energy(self, basis, C_orth, P, occ, state):
+        pi, pj, valid = state.pairs
+        e_j = _cs.screened_coulomb_energy(basis, C_orth, occ, pi, pj, valid=valid,
+                                          bra_chunk=self.chunk,
+                                          index=getattr(state, "pair_index", None))
+        return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
+
+
 def hf_coeff(xc) -> float:
     """Exact-exchange fraction a_x of a functional (gs_dft/ks/terms.py:267-270)."""
     a = getattr(xc, "exact_exchange_fraction", None)
@@ -114,8 +133,8 @@ def hf_coeff(xc) -> float:
 
 def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
                   omega: float = 0.0, skip_pad: bool = False) -> CoulombTerm:
-    """Resolve a spec into its term (gs_dft/ks/terms.py:273-301). Only the screened DF-J
-    strategy is implemented here; the others raise with the reason."""
+    """Resolve a spec into its term (gs_dft/ks/terms.py:273-301). The screened strategies
+    (DF-J and exact) are implemented here; the others raise with the reason."""
     if isinstance(spec, DFSpec):
         if not screened:
             raise NotImplementedError("dense (unscreened) DF is not part of this library; pass "
@@ -127,6 +146,15 @@ def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
                                         lam=spec.lam, chunk=spec.chunk, scales=spec.scales,
                                         diagonal=spec.diagonal, skip_pad=bool(skip_pad))
     if isinstance(spec, ExactSpec):
-        raise NotImplementedError("coulomb=exact() (the exact streamed ERI) is not part of this "
-                                  "library; use coulomb=df()")
+        if a_x_lr != 0.0:
+            raise ValueError("coulomb=exact() has no range-separated exchange path; a functional "
+                             f"with hf_coeff_lr={a_x_lr} needs coulomb=df()")
+        if not screened:
+            raise NotImplementedError("the dense exact Coulomb (StreamedExactCoulomb) is not part "
+                                      "of this library; pass screen=pairlist(eps=-1.0) for the "
+                                      "full pair list")
+        if a_x != 0.0:
+            raise ValueError("screened exact Coulomb has no exact-exchange path; use a pure "
+                             "functional or coulomb=df() (screened RI-K) for hybrids.")
+        return ScreenedExactCoulomb(hf_coeff=0.0, chunk=128 if spec.chunk is None else spec.chunk)
     raise TypeError(f"coulomb must come from exact() or df(), got {spec!r}")

@@ -162,14 +162,33 @@ int gsdft_external_energy(int64_t M, const double* quat, const double* log_scale
                           double* dC, double* datoms, void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* Exact Hartree energy over the pair list (density-fitting free): *energy (device scalar) =
+ * 1/2 sum_{a,b} (a|b) Pw_a Pw_b over the first n entries, Pw_a = w_a sum_o occ_o C_io C_jo, with
+ * (a|b) the pair-pair Coulomb integral at the reference's 20-node rule, and J (n) = sum_b (a|b)
+ * Pw_b (0 on zero-weight entries). Optional: the gradients w.r.t. quat, log_scale, centers and
+ * C (all four, with the pair index of the same n entries; grads = 1 in the workspace query).
+ * O(n^2) work. Replaces screened_coulomb_energy / full_eri_block_schur and JAX's reverse pass
+ * through them, gs_dft/coulomb/stream.py:249-281,296-320 (ScreenedExactCoulomb,
+ * gs_dft/ks/terms.py:193-205). */
+int gsdft_exact_coulomb_workspace_size(int64_t M, int64_t k, int64_t n, int grads,
+                                       size_t* bytes);
+int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
+                        const double* centers, int64_t k, const double* C, const double* occ,
+                        int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                        const int32_t* row_ptr, const int32_t* row_perm, const int32_t* col_ptr,
+                        const int32_t* col_perm, double* energy, double* J, double* dquat,
+                        double* dlog_scale, double* dcenters, double* dC, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
  * 6 nuclear attraction per pair (values and splat moments), 7 nuclear attraction per nucleus
- * (nuclear gradient). gsdft_profile_read synchronises the recorded events and returns the summed
+ * (nuclear gradient), 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and
+ * gradient moments). gsdft_profile_read synchronises the recorded events and returns the summed
  * milliseconds and the launch count since the last reset. gsdft_profile_read_work returns the
- * work units the kernels executed while profiling was on (ids 0, 1, 6, 7: quadrature nodes
- * evaluated, summed over live lanes, so at most 20 x (aux functions or nuclei) x pairs per
- * launch; other ids: 0). Profiling allocates a few bytes of
+ * work units the kernels executed while profiling was on (ids 0, 1, 6-9: quadrature nodes
+ * evaluated, summed over live lanes, so at most 20 x (aux functions, nuclei or pairs) x pairs
+ * per launch; other ids: 0). Profiling allocates a few bytes of
  * device memory on the device current when it is first enabled. */
 int gsdft_profile_enable(int on);
 int gsdft_profile_read(int id, double* total_ms, int64_t* launches, int reset);

@@ -825,3 +825,94 @@ double orc_external_energy(int64_t M, const double* quat, const double* log_scal
     return E;
 }
 
+/* ---------------------------------------------------------------- exact pair-pair Coulomb */
+
+static void inv3m(const double* A, double* Ai) {
+    double c[9];
+    adj3(A, c);
+    double det = det3(A);
+    for (int m = 0; m < 9; ++m) Ai[m] = c[m] / det;
+}
+
+/* (a|b) of gs_dft/coulomb/stream.py:249-281 (full_eri_block_schur) for one pair-pair, node by
+ * node in the Schur-complement form: X = A_a + t^2 I, u = X^-1 v_a, S = Y - t^4 X^-1 with
+ * Y = A_b + t^2 I, w = t^2 u + v_b, quad = c.v - (v_a.u + w.S^-1 w), det G = det X det S. */
+static double eri_schur_one(const double* tq, const double* wq, const PairRec* a,
+                            const PairRec* b) {
+    double va[3], vb[3];
+    matvec3(a->A, a->P, va);
+    matvec3(b->A, b->P, vb);
+    double cv = (a->P[0] * va[0] + a->P[1] * va[1] + a->P[2] * va[2])
+              + (b->P[0] * vb[0] + b->P[1] * vb[1] + b->P[2] * vb[2]);
+    double coul = 0.0;
+    for (int t = 0; t < NQ; ++t) {
+        double t2 = tq[t] * tq[t];
+        double X[9], Xi[9], u[3], Y[9], S[9], w[3], z[3];
+        memcpy(X, a->A, sizeof X);
+        X[0] += t2; X[4] += t2; X[8] += t2;
+        inv3m(X, Xi);
+        matvec3(Xi, va, u);
+        double vau = va[0] * u[0] + va[1] * u[1] + va[2] * u[2];
+        memcpy(Y, b->A, sizeof Y);
+        Y[0] += t2; Y[4] += t2; Y[8] += t2;
+        for (int m = 0; m < 9; ++m) S[m] = Y[m] - t2 * t2 * Xi[m];
+        for (int m = 0; m < 3; ++m) w[m] = t2 * u[m] + vb[m];
+        solve3(S, w, z);
+        double quad = cv - (vau + (w[0] * z[0] + w[1] * z[1] + w[2] * z[2]));
+        double detG = det3(X) * det3(S);
+        double It = (M_PI * M_PI * M_PI) / sqrt(detG) * exp(-quad);
+        coul += wq[t] * (2.0 / sqrt(M_PI)) * It;
+    }
+    return a->KN * b->KN * coul;
+}
+
+void orc_eri_block(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                   int64_t na, const int32_t* ai, const int32_t* aj, int64_t nb,
+                   const int32_t* bi, const int32_t* bj, double* out) {
+    double tq[NQ], wq[NQ];
+    node_table(tq, wq);
+    Chart c = chart_alloc(M, quat, log_scale);
+    PairRec* ra = (PairRec*)malloc(sizeof(PairRec) * (na > 0 ? na : 1));
+    PairRec* rb = (PairRec*)malloc(sizeof(PairRec) * (nb > 0 ? nb : 1));
+    for (int64_t x = 0; x < na; ++x) pair_rec(c.A9, centers, c.norm, ai[x], aj[x], ra + x);
+    for (int64_t x = 0; x < nb; ++x) pair_rec(c.A9, centers, c.norm, bi[x], bj[x], rb + x);
+#pragma omp parallel for schedule(static)
+    for (int64_t x = 0; x < na; ++x)
+        for (int64_t y = 0; y < nb; ++y) out[x * nb + y] = eri_schur_one(tq, wq, ra + x, rb + y);
+    free(ra);
+    free(rb);
+    chart_free(&c);
+}
+
+/* Jvec_a = sum_b (a|b) Pw_b with Pw_b = w_b sum_o occ_o C_io C_jo (stream.py:296-320), and the
+ * energy 1/2 sum_a Pw_a Jvec_a as the return value. */
+double orc_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
+                         const double* centers, int64_t k, const double* C, const double* occ,
+                         int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                         double* J) {
+    double tq[NQ], wq[NQ];
+    node_table(tq, wq);
+    Chart c = chart_alloc(M, quat, log_scale);
+    PairRec* r = (PairRec*)malloc(sizeof(PairRec) * (n > 0 ? n : 1));
+    double* Pw = (double*)malloc(sizeof(double) * (n > 0 ? n : 1));
+    for (int64_t a = 0; a < n; ++a) {
+        pair_rec(c.A9, centers, c.norm, pi[a], pj[a], r + a);
+        Pw[a] = weight[a] * pair_density(k, C, occ, pi[a], pj[a]);
+    }
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t a = 0; a < n; ++a) {
+        double acc = 0.0;
+        for (int64_t b = 0; b < n; ++b) {
+            if (Pw[b] == 0.0) continue;
+            acc += eri_schur_one(tq, wq, r + a, r + b) * Pw[b];
+        }
+        J[a] = acc;
+    }
+    double E = 0.0;
+    for (int64_t a = 0; a < n; ++a) E += Pw[a] * J[a];
+    free(Pw);
+    free(r);
+    chart_free(&c);
+    return 0.5 * E;
+}
+

@@ -106,6 +106,19 @@ double orc_external_energy(int64_t M, const double* quat, const double* log_scal
                            int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
                            int64_t n_atoms, const double* coords, const double* charges);
 
+/* (a|b) of gs_dft/coulomb/stream.py:249-281 for bra pairs (ai, aj) x ket pairs (bi, bj), row-major
+ * (na, nb), in the reference's Schur-complement node form. */
+void orc_eri_block(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                   int64_t na, const int32_t* ai, const int32_t* aj, int64_t nb,
+                   const int32_t* bi, const int32_t* bj, double* out);
+
+/* J (n) = sum_b (a|b) Pw_b over the list; returns E_J = 1/2 sum_a Pw_a J_a
+ * (gs_dft/coulomb/stream.py:296-320). */
+double orc_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
+                         const double* centers, int64_t k, const double* C, const double* occ,
+                         int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                         double* J);
+
 int orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -42,6 +42,7 @@ def lib():
         L.orc_cholesky.restype = ctypes.c_int
         L.orc_num_threads.restype = ctypes.c_int
         L.orc_external_energy.restype = ctypes.c_double
+        L.orc_exact_coulomb.restype = ctypes.c_double
         # the reference's own table (gs_dft/integrals/dense.py:46-53, numpy leggauss)
         t, w = reference_quad_table(20)
         L.orc_set_quad_table(_d(t), _d(w))
@@ -259,6 +260,29 @@ def external_energy(quat, log_scale, centers, C, occ, pi, pj, weight, atom_coord
         _i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers), _i64(C.shape[1]), _d(C),
         _d(occ), _i64(pi.shape[0]), pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32), _d(w),
         _i64(R.shape[0]), _d(R), _d(Z)))
+
+
+def eri_block(quat, log_scale, centers, ai, aj, bi, bj):
+    """(a|b) (na, nb) of gs_dft/coulomb/stream.py:249-281."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    ai, aj, bi, bj = _i32(ai), _i32(aj), _i32(bi), _i32(bj)
+    out = np.empty((ai.shape[0], bi.shape[0]))
+    lib().orc_eri_block(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                        _i64(ai.shape[0]), ai.ctypes.data_as(_I32), aj.ctypes.data_as(_I32),
+                        _i64(bi.shape[0]), bi.ctypes.data_as(_I32), bj.ctypes.data_as(_I32),
+                        _d(out))
+    return out
+
+
+def exact_coulomb(quat, log_scale, centers, C, occ, pi, pj, weight):
+    """(E_J, Jvec) of gs_dft/coulomb/stream.py:296-320 over the listed pairs."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    C, occ, pi, pj, w = _f64(C), _f64(occ), _i32(pi), _i32(pj), _f64(weight)
+    J = np.empty(pi.shape[0])
+    E = lib().orc_exact_coulomb(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                                _i64(C.shape[1]), _d(C), _d(occ), _i64(pi.shape[0]),
+                                pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32), _d(w), _d(J))
+    return float(E), J
 
 
 def set_threads(n: int) -> None:

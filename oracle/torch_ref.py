@@ -228,3 +228,44 @@ def screened_external_energy(quat, log_scale, centers, C, occ, pi, pj, valid, at
     V = full_nuclear_pairs(quat, log_scale, centers, pi, pj, atom_coords, atom_charges)
     return torch.sum(Pp * V)
 
+
+def inv3(A):
+    """gs_dft/integrals/linalg3.py:44-46"""
+    return adj3(A) / det3(A)[..., None, None]
+
+
+def full_eri_block_schur(quat, log_scale, centers, bra_i, bra_j, ket_i, ket_j, table=None):
+    """gs_dft/coulomb/stream.py:249-281, node by node (``table`` = (t list, w list) for another
+    rule)."""
+    t_list, w_list = (QUAD_T_LIST, QUAD_W_LIST) if table is None else table
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    Aa, Pa, KNa = full_pair_quantities(A, centers, N, bra_i, bra_j)
+    Ab, Pb, KNb = full_pair_quantities(A, centers, N, ket_i, ket_j)
+    va = torch.einsum("akl,al->ak", Aa, Pa)
+    vb = torch.einsum("bkl,bl->bk", Ab, Pb)
+    cv = torch.sum(Pa * va, -1)[:, None] + torch.sum(Pb * vb, -1)[None, :]
+    eye = torch.eye(3, dtype=torch.float64)
+    coul = torch.zeros((Aa.shape[0], Ab.shape[0]), dtype=torch.float64)
+    for t, w_q in zip(t_list, w_list):
+        t2 = t * t
+        X = Aa + t2 * eye
+        Xinv = inv3(X)
+        u = torch.einsum("akl,al->ak", Xinv, va)
+        vau = torch.sum(va * u, -1)
+        Y = Ab + t2 * eye
+        S = Y[None, :] - t2 * t2 * Xinv[:, None]
+        w = t2 * u[:, None, :] + vb[None, :, :]
+        z = solve3(S, w)
+        quad = cv - (vau[:, None] + torch.sum(w * z, -1))
+        detG = det3(X)[:, None] * det3(S)
+        I_t = PI ** 3 / torch.sqrt(detG) * torch.exp(-quad)
+        coul = coul + w_q * (2.0 / math.sqrt(PI)) * I_t
+    return (KNa[:, None] * KNb[None, :]) * coul
+
+
+def screened_coulomb_energy(quat, log_scale, centers, C, occ, pi, pj, valid):
+    """gs_dft/coulomb/stream.py:296-320 (one bra chunk: the sum does not depend on chunking)."""
+    Pw = valid.to(torch.float64) * torch.sum(occ[None, :] * C[pi] * C[pj], dim=1)
+    block = full_eri_block_schur(quat, log_scale, centers, pi, pj, pi, pj)
+    return 0.5 * torch.sum((block @ Pw) * Pw)
+

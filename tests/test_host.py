@@ -18,14 +18,24 @@ def test_pairlist_defaults(g):
     assert g.pairlist(1e-5, unique=True).unique is True
 
 
-def test_make_coulomb_resolves_only_the_screened_df_strategy(g):
+def test_make_coulomb_resolves_the_screened_strategies(g):
+    """gs_dft/ks/terms.py:273-301: df() and exact() with a screen resolve to their screened terms
+    (exact() with the reference's default chunk 128); the dense strategies, hybrids on the
+    screened paths and range-separated exchange with exact() raise."""
     from gs_dft_amd.terms import _make_coulomb
     t = _make_coulomb(g.df(lam=1e-6), screened=True, skip_pad=True)
     assert isinstance(t, g.ScreenedProductDFCoulomb) and t.lam == 1e-6 and t.skip_pad
+    e = _make_coulomb(g.exact(), screened=True)
+    assert isinstance(e, g.ScreenedExactCoulomb) and e.chunk == 128 and e.hf_coeff == 0.0
+    assert _make_coulomb(g.exact(chunk=32), screened=True).chunk == 32
     with pytest.raises(NotImplementedError):
         _make_coulomb(g.df(), screened=False)
     with pytest.raises(NotImplementedError):
-        _make_coulomb(g.exact(), screened=True)
+        _make_coulomb(g.exact(), screened=False)
+    with pytest.raises(ValueError):
+        _make_coulomb(g.exact(), screened=True, a_x=0.25)
+    with pytest.raises(ValueError):
+        _make_coulomb(g.exact(), screened=True, a_x_lr=0.5)
     with pytest.raises(NotImplementedError):
         _make_coulomb(g.df(), screened=True, a_x=0.25)
     with pytest.raises(TypeError):

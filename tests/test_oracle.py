@@ -553,3 +553,110 @@ def test_external_energy_autograd_matches_finite_differences(orc, tr, wl):
             up[idx] += h; dn[idx] -= h
             fd = (f(**{name: up}) - f(**{name: dn})) / (2 * h)
             assert abs(fd - g[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
+
+
+# ----------------------------------------------------------------------------- exact pair-pair Coulomb
+
+def test_eri_matches_literal_schur_and_is_symmetric(orc, tr, wl):
+    """gs_dft/coulomb/stream.py:249-281: the C oracle against the torch line-by-line Schur form,
+    and (a|b) = (b|a)."""
+    s, pi, pj, w = _nuc_system(wl, orc, seed=3)
+    B = orc.eri_block(s.quat, s.log_scale, s.centers, pi, pj, pi, pj)
+    Bt = tr.full_eri_block_schur(_t(s.quat), _t(s.log_scale), _t(s.centers), _idx(pi), _idx(pj),
+                                 _idx(pi), _idx(pj)).numpy()
+    assert np.max(np.abs(B - Bt) / np.abs(Bt)) < 1e-12
+    assert np.max(np.abs(B - B.T)) < 1e-13 * np.max(np.abs(B))
+    E, J = orc.exact_coulomb(s.quat, s.log_scale, s.centers, s.C, s.occ, pi, pj, w)
+    Et = tr.screened_coulomb_energy(_t(s.quat), _t(s.log_scale), _t(s.centers), _t(s.C),
+                                    _t(s.occ), _idx(pi), _idx(pj), _t(w)).item()
+    assert abs(E - Et) < 1e-13 * abs(Et)
+
+
+def test_eri_division_free_form_equals_schur_form(orc, wl):
+    """The library evaluates each node as det(I + sT)^(-1/2) exp(-s d.(I + sT)^-1 d) with
+    T = A_a^-1 + A_b^-1 and d = P_a - P_b, through J1..J3 = invariants of T and
+    p0 = |d|^2, p1 = J1 p0 - d.T d, p2 = d.adj(T) d (Cayley-Hamilton); the prefactor
+    2 pi^2.5 KN_a KN_b (det A_a det A_b)^(-1/2). Checked against the reference's Schur form."""
+    s, pi, pj, w = _nuc_system(wl, orc, seed=4)
+    B = orc.eri_block(s.quat, s.log_scale, s.centers, pi, pj, pi, pj)
+    A9, N = orc.chart(s.quat, s.log_scale)
+    Ah, P, KN = orc.pair_quantities(A9, s.centers, N, pi, pj)
+    tq, wq = orc.reference_quad_table(20)
+    rng = np.random.default_rng(0)
+    for a, b in rng.integers(0, len(pi), (300, 2)):
+        T = np.linalg.inv(Ah[a]) + np.linalg.inv(Ah[b])
+        d = P[a] - P[b]
+        J1, J3 = np.trace(T), np.linalg.det(T)
+        J2 = 0.5 * (J1 * J1 - np.trace(T @ T))
+        p0 = d @ d
+        p1 = J1 * p0 - d @ T @ d
+        p2 = d @ (np.linalg.inv(T) * J3) @ d
+        sv = tq * tq
+        E = 1 + sv * (J1 + sv * (J2 + sv * J3))
+        F = np.sum(wq * E ** -0.5 * np.exp(-sv * (p0 + sv * (p1 + sv * p2)) / E))
+        val = (KN[a] * KN[b] * 2 * math.pi ** 2.5
+               * (np.linalg.det(Ah[a]) * np.linalg.det(Ah[b])) ** -0.5 * F)
+        assert abs(val - B[a, b]) < 1e-12 * abs(B[a, b])
+
+
+def test_eri_converges_to_isotropic_closed_form(tr):
+    """Isotropic pair products p, q: (a|b) = KN_a KN_b 2 pi^2.5 / (p q sqrt(p + q)) F0(rho R^2),
+    rho = p q / (p + q) -- the reference's node formula under a 400-node rule reproduces it."""
+    rng = np.random.default_rng(31)
+    M = 5
+    alpha = np.exp(rng.uniform(-1.0, 1.0, M))
+    quat = rng.normal(size=(M, 4))
+    ls = np.repeat(np.log(alpha)[:, None], 3, 1)
+    mu = rng.normal(0, 1.5, (M, 3))
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    x, wl_ = np.polynomial.legendre.leggauss(400)
+    sgl = (x + 1) / 2
+    table = ([float(v) for v in sgl / (1 - sgl)], [float(v) for v in (wl_ / 2) / (1 - sgl) ** 2])
+    Bc = tr.full_eri_block_schur(_t(quat), _t(ls), _t(mu), _idx(pi), _idx(pj), _idx(pi),
+                                 _idx(pj), table).numpy()
+    A, N = tr.splat_A(_t(quat), _t(ls)), tr.splat_norm(_t(ls))
+    _, P, KN = tr.full_pair_quantities(A, _t(mu), N, _idx(pi), _idx(pj))
+    P, KN = P.numpy(), KN.numpy()
+    pp = alpha[pi] + alpha[pj]
+    for a in range(len(pi)):
+        for b in range(len(pi)):
+            rho = pp[a] * pp[b] / (pp[a] + pp[b])
+            T = rho * np.sum((P[a] - P[b]) ** 2)
+            F0 = 0.5 * math.sqrt(math.pi / T) * erf(math.sqrt(T)) if T > 1e-12 else 1.0 - T / 3
+            ref = KN[a] * KN[b] * 2 * math.pi ** 2.5 / (pp[a] * pp[b] * math.sqrt(pp[a] + pp[b])) * F0
+            assert abs(Bc[a, b] - ref) < 1e-10 * abs(ref)
+
+
+def test_exact_coulomb_invariances_and_autograd(orc, tr, wl):
+    """Unique list (weights 2 - delta_ij) equals the ordered list; padding adds nothing; the full
+    list exceeds the DF energy (E_J^DF <= E_J, gs-dft tests/unit/test_coulomb_df.py:54); autograd
+    of the literal form agrees with central differences of the oracle."""
+    s, pi, pj, w = _nuc_system(wl, orc, M=16, seed=7)
+    E, _ = orc.exact_coulomb(s.quat, s.log_scale, s.centers, s.C, s.occ, pi, pj, w)
+    po, qo, wo, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    Eo, _ = orc.exact_coulomb(s.quat, s.log_scale, s.centers, s.C, s.occ, po, qo, wo)
+    assert abs(Eo - E) < 1e-12 * abs(E)
+    pp, qp, wp, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, len(pi) + 9, True)
+    Ep, _ = orc.exact_coulomb(s.quat, s.log_scale, s.centers, s.C, s.occ, pp, qp, wp)
+    assert Ep == E
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (0.5, 1.0, 2.0, 4.0))
+    fi, fj, fw, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, -1.0, None, True)
+    Efull, _ = orc.exact_coulomb(s.quat, s.log_scale, s.centers, s.C, s.occ, fi, fj, fw)
+    Edf = orc.dfj_energy(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, fi, fj, fw, 1e-8)[0]
+    assert Edf <= Efull * (1 + 1e-9)
+    args = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_coulomb_energy(*args, _t(s.occ), _idx(pi), _idx(pj), _t(w))
+    Et.backward()
+    h = 1e-5
+    for k, (name, arr) in enumerate((("quat", s.quat), ("log_scale", s.log_scale),
+                                     ("centers", s.centers), ("C", s.C))):
+        for idx in [(0, 0), (arr.shape[0] - 1, 1)]:
+            up, dn = arr.copy(), arr.copy()
+            up[idx] += h; dn[idx] -= h
+            v = dict(quat=s.quat, log_scale=s.log_scale, centers=s.centers, C=s.C)
+            v[name] = up
+            eu, _ = orc.exact_coulomb(v["quat"], v["log_scale"], v["centers"], v["C"], s.occ, pi, pj, w)
+            v[name] = dn
+            ed, _ = orc.exact_coulomb(v["quat"], v["log_scale"], v["centers"], v["C"], s.occ, pi, pj, w)
+            fd = (eu - ed) / (2 * h)
+            assert abs(fd - args[k].grad[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
