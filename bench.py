@@ -42,12 +42,15 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--system", type=int, default=5, help="benchmark system 1..5")
+    ap.add_argument("--system", type=int, default=None,
+                    help="benchmark system 1..5 (default 5; 3 for --term exact)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
-    ap.add_argument("--term", choices=("dfj", "nuclear"), default="dfj",
+    ap.add_argument("--term", choices=("dfj", "nuclear", "exact"), default="dfj",
                     help="dfj: the screened DF-J step (the headline); nuclear: the screened "
-                         "nuclear attraction E_ext with every gradient on the same pair list")
+                         "nuclear attraction E_ext with every gradient on the same pair list; "
+                         "exact: the exact screened Coulomb E_J with every gradient (O(n^2), "
+                         "system 3 unless --system is given)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 2 GiB device-to-device once (scales the HBM byte counters "
                          "FETCH_SIZE / WRITE_SIZE of a profiler run) and exit")
@@ -66,8 +69,12 @@ def main() -> int:
               f"run (sharding over several GPUs is designed, not built)", file=sys.stderr)
         return 2
 
+    if args.system is None:
+        args.system = 3 if args.term == "exact" else 5
     if args.term == "nuclear":
         return run_nuclear(args)
+    if args.term == "exact":
+        return run_exact(args)
 
     import numpy as np
     import torch
@@ -361,6 +368,134 @@ def run_nuclear(args) -> int:
                     "nuclear_nodes_evaluated_frac": atom_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
         "E_ext": E.item(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+# Exact pair-pair Coulomb, per (a, b) integral at 20 nodes: a prologue of T = A_a^-1 + A_b^-1,
+# d, adj T, the invariants J1..J3 and p0..p2 (~100 flops), then per node the three-centre node
+# (17 + 2); the reverse adds the node moments (16 + 2 per node) and the chain to dF/dT, dF/dd
+# (~120 flops).
+ERI_FWD_PER_INTEGRAL, ERI_FWD_PER_NODE = 100, 19
+ERI_BWD_PER_INTEGRAL, ERI_BWD_PER_NODE = 220, 37
+FLOPS_ERI_FWD = ERI_FWD_PER_INTEGRAL + NODES * ERI_FWD_PER_NODE     # 480
+FLOPS_ERI_BWD = ERI_BWD_PER_INTEGRAL + NODES * ERI_BWD_PER_NODE     # 960
+
+
+def run_exact(args) -> int:
+    """Exact E_J = 1/2 sum_{a,b} (a|b) Pw_a Pw_b over the screened pair list: one step = the energy
+    with every gradient (one reverse-kernel pass over all n^2 pair-pairs plus the per-splat
+    reductions); the energy-only evaluation is timed beside it."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as ge
+
+    g = ge.load_package()
+    import importlib
+    wl = importlib.import_module("gs_dft_amd.workloads")
+    from gs_dft_amd import _lib
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    s = wl.make_system(args.system)
+    log(f"system {args.system} {s.name}: M={s.M} k={s.k} eps={s.eps}")
+    mk = lambda a: torch.tensor(a, device=dev, dtype=torch.float64)
+    quat, ls, cen, C0, occ = mk(s.quat), mk(s.log_scale), mk(s.centers), mk(s.C), mk(s.occ)
+    basis0 = g.Splat(quat=quat, log_scale=ls, centers=cen)
+    pi, pj, w = g.neighbor_pairs(basis0, s.eps, unique=True)
+    index = g.build_pair_index(s.M, pi, pj, w)
+    n = int(pi.shape[0])
+    integrals = float(n) * n
+    log(f"pairs n={n}: {integrals:.4e} pair-pair integrals per pass")
+
+    def step():
+        b = g.Splat(quat=quat.clone().requires_grad_(), log_scale=ls.clone().requires_grad_(),
+                    centers=cen.clone().requires_grad_())
+        C = C0.clone().requires_grad_()
+        E = g.screened_coulomb_energy(b, C, occ, pi, pj, valid=w, index=index)
+        E.backward()
+        return E
+
+    _lib.profile_enable(True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for kid in (_lib.PROF_ERI_FWD, _lib.PROF_ERI_BWD):
+        _lib.profile_read(kid, reset=True)
+        _lib.profile_read_work(kid, reset=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        E = step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    with torch.no_grad():
+        t1 = time.perf_counter()
+        E0 = g.screened_coulomb_energy(basis0, C0, occ, pi, pj, valid=w, index=index)
+        torch.cuda.synchronize()
+        wall_e = time.perf_counter() - t1
+    bwd_ms, bwd_k = _lib.profile_read(_lib.PROF_ERI_BWD, reset=True)
+    fwd_ms, fwd_k = _lib.profile_read(_lib.PROF_ERI_FWD, reset=True)
+    bwd_nodes = _lib.profile_read_work(_lib.PROF_ERI_BWD, reset=True) / max(bwd_k, 1)
+    fwd_nodes = _lib.profile_read_work(_lib.PROF_ERI_FWD, reset=True) / max(fwd_k, 1)
+    _lib.profile_enable(False)
+    bwd_ms /= max(bwd_k, 1)
+    fwd_ms /= max(fwd_k, 1)
+    bwd_tf = integrals * FLOPS_ERI_BWD / (bwd_ms * 1e-3)
+    fwd_tf = integrals * FLOPS_ERI_FWD / (fwd_ms * 1e-3)
+    log(f"E_J={E.item():.12e} (energy only {E0.item():.12e}) step {wall * 1e3:.1f} ms, energy "
+        f"only {wall_e * 1e3:.1f} ms; reverse kernel {bwd_ms:.1f} ms ({bwd_tf / 1e12:.2f} "
+        f"TFLOP/s, {bwd_nodes / (NODES * integrals):.3f} of nodes), forward kernel "
+        f"{fwd_ms:.1f} ms ({fwd_tf / 1e12:.2f} TFLOP/s, {fwd_nodes / (NODES * integrals):.3f})")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import oracle as orc
+        pin, pjn, wn = (t.cpu().numpy() for t in (pi, pj, w))
+        rng = np.random.default_rng(1)
+
+        def run(m):
+            sel = np.sort(rng.choice(n, size=min(m, n), replace=False))
+            t = time.perf_counter()
+            orc.eri_block(s.quat, s.log_scale, s.centers, pin[sel], pjn[sel], pin, pjn)
+            return time.perf_counter() - t, len(sel)
+
+        t_probe, m_probe = run(max(1, min(n, int(2e6 // n) + 1)))
+        m = max(1, min(n, int(m_probe * args.cpu_seconds / max(t_probe, 1e-6))))
+        t_cpu, m_cpu = run(m) if m > m_probe else (t_probe, m_probe)
+        cpu_ms = t_cpu / m_cpu * n * 1e3
+        cpu = {"value": cpu_ms, "unit": "ms per energy evaluation (all (a|b), extrapolated "
+               "linearly in bra pairs)", "cores": orc.num_threads(), "kind": "port",
+               "sample": f"{m_cpu} of {n} bra pairs x all {n} ket pairs, {t_cpu:.1f} s on "
+                         f"{orc.num_threads()} threads (C oracle, OpenMP, the reference's Schur "
+                         f"node form); energy only",
+               "integrals_per_s": integrals / (cpu_ms * 1e-3)}
+        log(f"cpu baseline: {cpu_ms / 1e3:.1f} s per energy extrapolated from {m_cpu} bra pairs")
+
+    out = {
+        "metric": "exact screened E_J fwd+bwd wall ms; pair-pair integrals/s",
+        "value": integrals / wall,
+        "unit": "pair-pair integrals/s (energy + all gradients)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"{s.name}: exact screened Coulomb, M={s.M} splats, k={s.k}, "
+                               f"eps={s.eps}, unique pairs",
+                   "system": args.system, "M": s.M, "k": s.k, "n_pairs": n, "eps": s.eps,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "exact pair-pair reverse (k_eri_bwd)",
+                     "achieved": bwd_tf / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": bwd_tf / PEAK_FP64, "traffic": None,
+                     "flops_per_integral": FLOPS_ERI_BWD, "integrals_per_launch": integrals,
+                     "kernel_ms": bwd_ms,
+                     "note": "FP64 vector bound; fixed per-integral work at 20 nodes"},
+        "kernels": {"reverse_ms": bwd_ms, "forward_ms": fwd_ms,
+                    "energy_only_ms": wall_e * 1e3,
+                    "forward_frac_fp64": fwd_tf / PEAK_FP64,
+                    "reverse_nodes_evaluated_frac": bwd_nodes / (NODES * integrals),
+                    "forward_nodes_evaluated_frac": fwd_nodes / (NODES * integrals)},
+        "cpu_baseline": cpu,
+        "E_J": E.item(),
     }
     print(json.dumps(out), flush=True)
     return 0
