@@ -370,12 +370,20 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
+    // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
+    // slot per lane, structure of arrays) rather than in registers across the loop.
+    __shared__ double geo[9][256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
-    __syncthreads();
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = a < n;
     const double* r = rec + kRec * (live ? a : 0);
     const double I1 = r[0], I2 = r[1], I3 = r[2];
+#pragma unroll
+    for (int c = 0; c < 6; ++c) geo[c][threadIdx.x] = r[3 + c];
+    geo[6][threadIdx.x] = live ? r[9] : kFarAway;
+    geo[7][threadIdx.x] = live ? r[10] : kFarAway;
+    geo[8][threadIdx.x] = live ? r[11] : kFarAway;
+    __syncthreads();
     double jt = 0, T1 = 0, T2 = 0, T3 = 0;
     double Vc[3] = {0, 0, 0}, Va[3] = {0, 0, 0}, Vb[3] = {0, 0, 0};
     double Sa[6] = {0, 0, 0, 0, 0, 0}, Sb[6] = {0, 0, 0, 0, 0, 0};
@@ -411,14 +419,10 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         const double u = x[3];
         if (p == p0 || x[5] != 0.0) {            // a new centre (wave-uniform)
             flush();
-            // The pair's Ah and centre are read again here rather than held in registers
-            // across the loop (the empty asm keeps the compiler from hoisting the loads).
-            const double* rp = r;
-            asm volatile("" : "+v"(rp));
-            const double xx = rp[3], yy = rp[4], zz = rp[5], xy = rp[6], xz = rp[7], yz = rp[8];
-            const double Px = live ? rp[9] : kFarAway, Py = live ? rp[10] : kFarAway,
-                         Pz = live ? rp[11] : kFarAway;
-            d[0] = x[0] - Px; d[1] = x[1] - Py; d[2] = x[2] - Pz;
+            const int l = threadIdx.x;
+            const double xx = geo[0][l], yy = geo[1][l], zz = geo[2][l], xy = geo[3][l],
+                         xz = geo[4][l], yz = geo[5][l];
+            d[0] = x[0] - geo[6][l]; d[1] = x[1] - geo[7][l]; d[2] = x[2] - geo[8][l];
             const double ax = xx * d[0] + xy * d[1] + xz * d[2];
             const double ay = xy * d[0] + yy * d[1] + yz * d[2];
             const double az = xz * d[0] + yz * d[1] + zz * d[2];
