@@ -354,3 +354,35 @@ def test_system3_sampled_gamma_and_directional_derivative(g, wl, orc, cuda):
     fd = (e_at(1) - e_at(-1)) / (2 * h)
     print(f"[system3] directional derivative {dd:.10e} vs central difference {fd:.10e}")
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
+
+
+def test_globule700_sampled_gamma_and_J(g, wl, orc, cuda):
+    """The headline shape (globule700: M = 20000, N_aux = 80000, ~1.1e7 unique pairs, every slab
+    and screen path of the full-size launch): gamma on sampled aux functions and J = sum_P
+    dgamma_P (P|a) on sampled pairs, for a random dgamma, against the oracle over all pairs and
+    all aux functions respectively."""
+    from gs_dft_amd import ri as _ri
+    s = wl.make_system(5)
+    basis = _splat(g, s)
+    pi, pj, w = g.neighbor_pairs(basis, s.eps, unique=True)
+    aux = g.init_product_aux(basis, scales=s.scales)
+    C = torch.tensor(s.C, device="cuda")
+    print(f"[globule700] n={pi.shape[0]} N={aux.n_basis}", flush=True)
+    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, aux, pi, pj, valid=w))
+    pin, pjn, wn = _np(pi), _np(pj), _np(w)
+    la, ac = _np(aux.log_alpha), _np(aux.centers)
+    rng = np.random.default_rng(5)
+    sel = np.sort(rng.choice(len(la), 6, replace=False))
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
+    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
+    print(f"[globule700] sampled gamma max elementwise rel {err:.2e}", flush=True)
+    assert err < 1e-12
+    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
+    x = _ri._Inputs(basis, C, s.occ, aux, pi, pj, w, None)
+    J = _np(_ri._gamma_vjp(x, dg, None)[0])
+    psel = np.sort(rng.choice(len(pin), 64, replace=False))
+    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
+                       wn[psel], _np(dg))[0]
+    errJ = rel_max(J[psel], Jo)
+    print(f"[globule700] sampled J rel-to-max {errJ:.2e}", flush=True)
+    assert errJ < 1e-11
