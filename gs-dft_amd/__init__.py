@@ -7,6 +7,7 @@ HIP kernels for gfx950 in ``lib/libgsdft.so`` (C ABI declared in ``include/gsdft
 from .basis import IsotropicSplat, Splat, init_product_aux
 from .energy import SplatDFJ, SplatModel, SplatState, refresh, train_pad_to
 from .exact import screened_coulomb_J, screened_coulomb_energy
+from .grid import chunked_density, chunked_density_and_grad, chunked_density_grad_tau
 from .ri import (aux_cholesky, aux_metric, coulomb_pairs, df_coulomb_energy_screened,
                  df_coulomb_gamma_screened, df_coulomb_solve, shift_diag)
 from .screening import (PairIndex, build_pair_index, count_significant, density_pairs,
@@ -21,6 +22,7 @@ __all__ = [
     "aux_metric", "aux_cholesky", "shift_diag", "df_coulomb_gamma_screened", "df_coulomb_solve",
     "df_coulomb_energy_screened", "coulomb_pairs",
     "screened_coulomb_energy", "screened_coulomb_J",
+    "chunked_density", "chunked_density_and_grad", "chunked_density_grad_tau",
     "neighbor_pairs", "count_significant", "pair_weight", "screened_overlap_pairs",
     "density_pairs", "screened_nuclear_pairs", "screened_external_energy",
     "PairIndex", "build_pair_index", "live_length",

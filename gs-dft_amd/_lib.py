@@ -63,6 +63,11 @@ SIGNATURES = {
     "gsdft_exact_coulomb_workspace_size": [_i64, _i64, _i64, _int, _psz],
     "gsdft_exact_coulomb": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "gsdft_grid_density_workspace_size": [_i64, _i64, _i64, _int, _int, _psz],
+    "gsdft_grid_density": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp,
+                           _vp, _vp, _sz, _vp],
+    "gsdft_grid_density_vjp": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp,
+                               _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_profile_enable": [_int],
     "gsdft_profile_read": [_int, _pd, _pi64, _int],
     "gsdft_profile_read_work": [_int, ctypes.POINTER(ctypes.c_uint64), _int],

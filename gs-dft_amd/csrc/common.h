@@ -304,6 +304,47 @@ __device__ __forceinline__ void splat_chart(const double* __restrict__ q,
     *N = pow(8.0 * exp(l[0] + l[1] + l[2]) / kPi3, 0.25);
 }
 
+// Reverse of the chart for splat m: from acc = dE/dA (six slots, dE = sum over all nine entries),
+// dE/dmu (3) and dE/dN (1) to dE/dquat, dE/dlog_scale and dE/dcenters
+// (gs_dft/basis/spectral.py:33-40,72-82 under JAX autodiff).
+__device__ inline void chart_reverse(int64_t m, const double acc[10],
+                                     const double* __restrict__ quat,
+                                     const double* __restrict__ log_scale,
+                                     double* __restrict__ dquat, double* __restrict__ dlog_scale,
+                                     double* __restrict__ dcenters) {
+    const double* q = quat + 4 * m;
+    const double* l = log_scale + 3 * m;
+    double R[9], qn[4], nrm;
+    quat_rotation(q, R, qn, &nrm);
+    const double av[3] = {exp(l[0]), exp(l[1]), exp(l[2])};
+    const double Nm = pow(8.0 * exp(l[0] + l[1] + l[2]) / kPi3, 0.25);
+    const double G[9] = {acc[0], acc[3], acc[4], acc[3], acc[1], acc[5], acc[4], acc[5], acc[2]};
+    double GR[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c)
+            GR[3 * r + c] = G[3 * r] * R[c] + G[3 * r + 1] * R[3 + c] + G[3 * r + 2] * R[6 + c];
+    for (int jx = 0; jx < 3; ++jx) {
+        const double ga = R[jx] * GR[jx] + R[3 + jx] * GR[3 + jx] + R[6 + jx] * GR[6 + jx];
+        dlog_scale[3 * m + jx] = av[jx] * ga + acc[9] * Nm * 0.25;
+    }
+    double gR[9];
+    for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) gR[3 * r + c] = 2.0 * av[c] * GR[3 * r + c];
+    const double w = qn[0], x = qn[1], yq = qn[2], z = qn[3];
+    const double gqn[4] = {
+        2 * (-z * gR[1] + yq * gR[2] + z * gR[3] - x * gR[5] - yq * gR[6] + x * gR[7]),
+        2 * (yq * gR[1] + z * gR[2] + yq * gR[3] - 2 * x * gR[4] - w * gR[5] + z * gR[6]
+             + w * gR[7] - 2 * x * gR[8]),
+        2 * (-2 * yq * gR[0] + x * gR[1] + w * gR[2] + x * gR[3] + z * gR[5] - w * gR[6]
+             + z * gR[7] - 2 * yq * gR[8]),
+        2 * (-2 * z * gR[0] - w * gR[1] + x * gR[2] + w * gR[3] - 2 * z * gR[4] + yq * gR[5]
+             + x * gR[6] + yq * gR[7])};
+    const double den = nrm + 1e-12;
+    const double dot = q[0] * gqn[0] + q[1] * gqn[1] + q[2] * gqn[2] + q[3] * gqn[3];
+    for (int t = 0; t < 4; ++t) dquat[4 * m + t] = gqn[t] / den - q[t] * dot / (nrm * den * den);
+    for (int t = 0; t < 3; ++t) dcenters[3 * m + t] = acc[6 + t];
+}
+
 // ------------------------------------------------------------------ pair quantities
 // gs_dft/coulomb/stream.py:203-215: Ah = Ai + Aj, P = Ah^-1 (Ai mu_i + Aj mu_j),
 // KN = N_i N_j exp(-d . Ai Ah^-1 Aj d), d = mu_i - mu_j.

@@ -75,6 +75,9 @@ int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w);
 int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
                       hipStream_t s);
 
+// dfj.hip: the library's rocBLAS handle for the current device, bound to stream s.
+int blas_handle(hipStream_t s, struct _rocblas_handle** out);
+
 // screen.hip
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,
                  hipStream_t s);

@@ -214,3 +214,22 @@ def make_small(M: int, k: int, n_atoms: int = 4, seed: int = 0, spread: float = 
     return System(name=f"small{M}", atoms=atoms, quat=q, log_scale=log_scale, centers=centers,
                   C=C, occ=np.ones(k), scales=tuple(scales),
                   charges=np.resize(np.array([6.0, 1.0, 8.0]), n_atoms))
+
+
+def atom_grid(atoms: np.ndarray, n_rad: int = 24, n_ang: int = 110, r_max: float = 12.0,
+              seed: int = 0) -> np.ndarray:
+    """Synthetic atom-centred grid points (Bohr) for the density-on-grid workloads: per atom,
+    ``n_rad`` radii on a log-spaced ladder up to ``r_max`` times ``n_ang`` directions of a
+    Fibonacci sphere, randomly rotated per atom. Points only (the density needs no weights)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    radii = r_max * (np.expm1(np.linspace(0.05, 3.0, n_rad)) / np.expm1(3.0))
+    i = np.arange(n_ang) + 0.5
+    phi = np.arccos(1.0 - 2.0 * i / n_ang)
+    th = math.pi * (1.0 + 5.0 ** 0.5) * i
+    dirs = np.stack([np.cos(th) * np.sin(phi), np.sin(th) * np.sin(phi), np.cos(phi)], axis=1)
+    out = []
+    for a in atoms:
+        R = _random_rotation(rng)
+        out.append(a + (radii[:, None, None] * (dirs @ R.T)[None, :, :]).reshape(-1, 3))
+    return np.concatenate(out)
+

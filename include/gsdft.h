@@ -180,6 +180,30 @@ int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
                         double* dlog_scale, double* dcenters, double* dC, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Density on a grid for the exchange-correlation term, streamed over chunks of `chunk` points
+ * (<= 65535): rho (G) and, for mode >= 1, grad (G,3), and for mode 2 tau (G), of the orbitals
+ * C (M,k) with occupations occ at points (G,3). mode 0 replaces chunked_density, 1
+ * chunked_density_and_grad, 2 chunked_density_grad_tau (gs_dft/screening/grid.py:60-70,88-154;
+ * the dense eval_density_*_on_grid of gs_dft/integrals/dense.py give the same values). */
+int gsdft_grid_density_workspace_size(int64_t M, int64_t k, int64_t chunk, int mode, int reverse,
+                                      size_t* bytes);
+int gsdft_grid_density(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, int64_t k, const double* C, const double* occ,
+                       int64_t G, const double* points, int64_t chunk, int mode, double* rho,
+                       double* grad, double* tau, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Reverse of gsdft_grid_density for the cotangents v_rho (G), v_grad (G,3), v_tau (G) (null =
+ * zero): the gradients w.r.t. quat, log_scale, centers (M,4/3/3) and C (M,k); the points are held
+ * constant. Workspace query with reverse = 1. Replaces JAX's reverse pass through
+ * gs_dft/screening/grid.py:88-154. */
+int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t k, const double* C, const double* occ,
+                           int64_t G, const double* points, int64_t chunk, int mode,
+                           const double* v_rho, const double* v_grad, const double* v_tau,
+                           double* dquat, double* dlog_scale, double* dcenters, double* dC,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
  * 6 nuclear attraction per pair (values and splat moments), 7 nuclear attraction per nucleus

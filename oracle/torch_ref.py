@@ -269,3 +269,43 @@ def screened_coulomb_energy(quat, log_scale, centers, C, occ, pi, pj, valid):
     block = full_eri_block_schur(quat, log_scale, centers, pi, pj, pi, pj)
     return 0.5 * torch.sum((block @ Pw) * Pw)
 
+
+def full_eval_block(A, centers, norm, pts):
+    """gs_dft/screening/grid.py:52-70: splat values g (n, M) and gradients dg (n, M, 3) at pts."""
+    dx = pts[:, None, 0] - centers[None, :, 0]
+    dy = pts[:, None, 1] - centers[None, :, 1]
+    dz = pts[:, None, 2] - centers[None, :, 2]
+    a00, a11, a22 = A[None, :, 0, 0], A[None, :, 1, 1], A[None, :, 2, 2]
+    a01, a02, a12 = A[None, :, 0, 1], A[None, :, 0, 2], A[None, :, 1, 2]
+    Adr0 = a00 * dx + a01 * dy + a02 * dz
+    Adr1 = a01 * dx + a11 * dy + a12 * dz
+    Adr2 = a02 * dx + a12 * dy + a22 * dz
+    g = norm[None, :] * torch.exp(-(dx * Adr0 + dy * Adr1 + dz * Adr2))
+    dg = -2.0 * torch.stack([Adr0, Adr1, Adr2], dim=-1) * g[:, :, None]
+    return g, dg
+
+
+def chunked_density(quat, log_scale, centers, C, occ, pts, kind="gga", chunk=4096):
+    """gs_dft/screening/grid.py:88-154: (rho,), (rho, grad) or (rho, grad, tau) for kind
+    lda / gga / mgga, chunked over the points (the values do not depend on the chunking)."""
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    out = {"rho": [], "grad": [], "tau": []}
+    for s0 in range(0, pts.shape[0], chunk):
+        p = pts[s0:s0 + chunk]
+        g, dg = full_eval_block(A, centers, N, p)
+        psi = g @ C
+        out["rho"].append(torch.sum(occ[None, :] * psi ** 2, dim=1))
+        if kind == "gga":
+            phi = (psi * occ[None, :]) @ C.T
+            out["grad"].append(2.0 * torch.einsum("gm,gmd->gd", phi, dg))
+        elif kind == "mgga":
+            dpsi = torch.einsum("gmd,mn->gnd", dg, C)
+            out["grad"].append(2.0 * torch.einsum("n,gn,gnd->gd", occ, psi, dpsi))
+            out["tau"].append(0.5 * torch.einsum("n,gnd,gnd->g", occ, dpsi, dpsi))
+    res = (torch.cat(out["rho"]),)
+    if kind in ("gga", "mgga"):
+        res = res + (torch.cat(out["grad"]),)
+    if kind == "mgga":
+        res = res + (torch.cat(out["tau"]),)
+    return res
+

@@ -660,3 +660,59 @@ def test_exact_coulomb_invariances_and_autograd(orc, tr, wl):
             ed, _ = orc.exact_coulomb(v["quat"], v["log_scale"], v["centers"], v["C"], s.occ, pi, pj, w)
             fd = (eu - ed) / (2 * h)
             assert abs(fd - args[k].grad[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
+
+
+# ----------------------------------------------------------------------------- density on a grid
+
+def test_grid_density_integrates_to_the_orbital_overlaps(orc, tr, wl):
+    """gs_dft/screening/grid.py:52-70,88-112: on a fine Cartesian grid (the rectangle rule converges
+    spectrally for Gaussians), sum_r w psi_o psi_p reproduces C^T S C with S the normalised overlap
+    of the oracle (pairs.py:342-345), so the basis values, the norm and the contraction are pinned;
+    in particular each splat integrates to one."""
+    rng = np.random.default_rng(3)
+    M = 3
+    quat = rng.normal(size=(M, 4))
+    ls = rng.uniform(np.log(0.6), np.log(2.0), (M, 3))
+    mu = rng.normal(0, 0.5, (M, 3))
+    C = rng.normal(size=(M, 2))
+    h = 0.08
+    ax = np.arange(-6.0, 6.0 + h / 2, h)
+    X, Y, Z = np.meshgrid(ax, ax, ax, indexing="ij")
+    pts = _t(np.stack([X.ravel(), Y.ravel(), Z.ravel()], 1))
+    A, N = tr.splat_A(_t(quat), _t(ls)), tr.splat_norm(_t(ls))
+    g, _ = tr.full_eval_block(A, _t(mu), N, pts)
+    Sgrid = (g.T @ g).numpy() * h ** 3
+    pi = np.repeat(np.arange(M), M); pj = np.tile(np.arange(M), M)
+    S = orc.overlap_pairs(quat, ls, mu, pi, pj).reshape(M, M)
+    assert np.max(np.abs(np.diag(Sgrid) - 1.0)) < 1e-10
+    assert np.max(np.abs(Sgrid - S)) < 1e-10
+    rho, = tr.chunked_density(_t(quat), _t(ls), _t(mu), _t(C), _t(np.ones(2)), pts, kind="lda",
+                              chunk=200000)
+    assert abs(rho.sum().item() * h ** 3 - np.trace(C.T @ S @ C)) < 1e-9 * np.trace(C.T @ S @ C)
+
+
+def test_grid_density_gradient_and_tau_by_differences(tr, wl):
+    """grad rho against central differences of rho; tau = 1/2 sum_o occ_o |grad psi_o|^2 against
+    differences of psi; the GGA form (phi = (psi occ) C^T) equals the meta-GGA form
+    (2 sum occ psi grad psi); chunking changes nothing."""
+    s = wl.make_small(12, 3, n_atoms=2, seed=9)
+    pts = _t(np.random.default_rng(1).normal(0, 2.0, (40, 3)))
+    args = (_t(s.quat), _t(s.log_scale), _t(s.centers), _t(s.C), _t(s.occ))
+    rho, grad = tr.chunked_density(*args, pts, kind="gga")
+    rho2, grad2, tau = tr.chunked_density(*args, pts, kind="mgga", chunk=7)
+    assert torch.allclose(rho, rho2, rtol=1e-14, atol=0) and rel_max(grad2.numpy(), grad.numpy()) < 1e-13
+    h = 1e-5
+    A, N = tr.splat_A(args[0], args[1]), tr.splat_norm(args[1])
+    for d in range(3):
+        e = torch.zeros(3, dtype=torch.float64); e[d] = h
+        rp, = tr.chunked_density(*args, pts + e, kind="lda")
+        rm, = tr.chunked_density(*args, pts - e, kind="lda")
+        assert rel_max(((rp - rm) / (2 * h)).numpy(), grad[:, d].numpy()) < 1e-7
+    dpsi2 = torch.zeros(pts.shape[0], s.k, dtype=torch.float64)
+    for d in range(3):
+        e = torch.zeros(3, dtype=torch.float64); e[d] = h
+        gp, _ = tr.full_eval_block(A, args[2], N, pts + e)
+        gm, _ = tr.full_eval_block(A, args[2], N, pts - e)
+        dpsi2 += (((gp - gm) / (2 * h)) @ args[3]) ** 2
+    tau_fd = 0.5 * (dpsi2 * args[4][None, :]).sum(1)
+    assert rel_max(tau_fd.numpy(), tau.numpy()) < 1e-7
