@@ -46,11 +46,12 @@ def main() -> int:
                     help="benchmark system 1..5 (default 5; 3 for --term exact)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
-    ap.add_argument("--term", choices=("dfj", "nuclear", "exact"), default="dfj",
+    ap.add_argument("--term", choices=("dfj", "nuclear", "exact", "grid"), default="dfj",
                     help="dfj: the screened DF-J step (the headline); nuclear: the screened "
                          "nuclear attraction E_ext with every gradient on the same pair list; "
                          "exact: the exact screened Coulomb E_J with every gradient (O(n^2), "
-                         "system 3 unless --system is given)")
+                         "system 3 unless --system is given); grid: rho and grad rho on an "
+                         "atom-centred grid with every gradient")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 2 GiB device-to-device once (scales the HBM byte counters "
                          "FETCH_SIZE / WRITE_SIZE of a profiler run) and exit")
@@ -75,6 +76,8 @@ def main() -> int:
         return run_nuclear(args)
     if args.term == "exact":
         return run_exact(args)
+    if args.term == "grid":
+        return run_grid(args)
 
     import numpy as np
     import torch
@@ -496,6 +499,107 @@ def run_exact(args) -> int:
                     "forward_nodes_evaluated_frac": fwd_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
         "E_J": E.item(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_grid(args) -> int:
+    """(rho, grad rho) on an atom-centred grid with every gradient (splat leaves and C): one step =
+    the forward (basis values, psi = g C, phi = (psi occ) C^T) and the reverse (psi and grad psi,
+    dC += [g; dg]^T [Pbar; Pbar_d], [gbar; dgbar] = [Pbar; Pbar_d] C^T, basis reverse)."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as ge
+
+    g = ge.load_package()
+    import importlib
+    wl = importlib.import_module("gs_dft_amd.workloads")
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    s = wl.make_system(args.system)
+    pts_np = wl.atom_grid(s.atoms, n_rad=16, n_ang=50, r_max=10.0, seed=args.system)
+    G = int(pts_np.shape[0])
+    M, k = s.M, s.k
+    chunk = 8192
+    log(f"system {args.system} {s.name}: M={M} k={k}, grid {G} points ({len(s.atoms)} atoms x 16 "
+        f"radii x 50 directions), chunk {chunk}")
+    mk = lambda a: torch.tensor(a, device=dev, dtype=torch.float64)
+    quat, ls, cen, C0, occ, pts = (mk(a) for a in (s.quat, s.log_scale, s.centers, s.C, s.occ,
+                                                   pts_np))
+    v = mk(np.random.default_rng(0).uniform(0.5, 1.5, G))
+
+    def step():
+        b = g.Splat(quat=quat.clone().requires_grad_(), log_scale=ls.clone().requires_grad_(),
+                    centers=cen.clone().requires_grad_())
+        C = C0.clone().requires_grad_()
+        rho, grad = g.chunked_density_and_grad(b, C, occ, pts, chunk=chunk)
+        E = (v * rho).sum() + (grad * grad).sum()
+        E.backward()
+        return E
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        E = step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    with torch.no_grad():
+        b0 = g.Splat(quat=quat, log_scale=ls, centers=cen)
+        t1 = time.perf_counter()
+        g.chunked_density_and_grad(b0, C0, occ, pts, chunk=chunk)
+        torch.cuda.synchronize()
+        wall_f = time.perf_counter() - t1
+    # GEMM flops: forward psi = g C and phi = (psi occ) C^T; reverse [psi; dpsi] (4), dC (4),
+    # [gbar; dgbar] (4), each 2 G M k
+    gemm = 2.0 * G * M * k
+    flops_step = gemm * (2 + 12)
+    tf = flops_step / wall
+    log(f"E={E.item():.12e} step {wall * 1e3:.1f} ms (forward only {wall_f * 1e3:.1f} ms): "
+        f"{tf / 1e12:.2f} TFLOP/s of FP64 GEMM work through the step")
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import torch_ref as tr
+        torch.set_num_threads(max(1, os.cpu_count() or 1))
+        rng = np.random.default_rng(1)
+        args_t = [torch.as_tensor(a) for a in (s.quat, s.log_scale, s.centers, s.C, s.occ)]
+
+        def run(m):
+            sel = np.sort(rng.choice(G, size=min(m, G), replace=False))
+            t = time.perf_counter()
+            tr.chunked_density(*args_t, torch.as_tensor(pts_np[sel]), kind="gga", chunk=1024)
+            return time.perf_counter() - t, len(sel)
+
+        t_probe, m_probe = run(256)
+        m = max(1, min(G, int(m_probe * args.cpu_seconds / max(t_probe, 1e-6))))
+        t_cpu, m_cpu = run(m) if m > m_probe else (t_probe, m_probe)
+        cpu_ms = t_cpu / m_cpu * G * 1e3
+        cpu = {"value": cpu_ms, "unit": "ms per forward (rho, grad rho) evaluation, extrapolated "
+               "linearly in grid points", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{m_cpu} of {G} points, {t_cpu:.1f} s (torch float64 restatement of "
+                         f"the reference on the host, {torch.get_num_threads()} threads); "
+                         f"forward only"}
+        log(f"cpu baseline: {cpu_ms / 1e3:.1f} s per forward extrapolated from {m_cpu} points")
+    out = {
+        "metric": "grid density (rho, grad rho) fwd+bwd wall ms; FP64 GEMM TFLOP/s",
+        "value": tf / 1e12,
+        "unit": "TFLOP/s (FP64 GEMM work of the step)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"{s.name}: rho and grad rho with all gradients, M={M} splats, "
+                               f"k={k}, {G} grid points", "system": args.system, "M": M, "k": k,
+                   "grid_points": G, "chunk": chunk, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "FP64 GEMMs of the step (rocBLAS dgemm, MFMA)",
+                     "achieved": tf / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": tf / PEAK_FP64, "traffic": None,
+                     "note": "whole-step rate: the basis kernels and reductions are counted as "
+                             "time, not flops"},
+        "kernels": {"forward_only_ms": wall_f * 1e3},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0
