@@ -43,15 +43,17 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--system", type=int, default=None,
-                    help="benchmark system 1..5 (default 5; 3 for --term exact)")
+                    help="benchmark system 1..5 (default 5; 3 for --term exact / exchange)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
-    ap.add_argument("--term", choices=("dfj", "nuclear", "exact", "grid"), default="dfj",
+    ap.add_argument("--term", choices=("dfj", "nuclear", "exact", "grid", "exchange"),
+                    default="dfj",
                     help="dfj: the screened DF-J step (the headline); nuclear: the screened "
                          "nuclear attraction E_ext with every gradient on the same pair list; "
                          "exact: the exact screened Coulomb E_J with every gradient (O(n^2), "
                          "system 3 unless --system is given); grid: rho and grad rho on an "
-                         "atom-centred grid with every gradient")
+                         "atom-centred grid with every gradient; exchange: the screened RI-K "
+                         "E_K with every gradient (system 3 unless --system is given)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 2 GiB device-to-device once (scales the HBM byte counters "
                          "FETCH_SIZE / WRITE_SIZE of a profiler run) and exit")
@@ -71,13 +73,15 @@ def main() -> int:
         return 2
 
     if args.system is None:
-        args.system = 3 if args.term == "exact" else 5
+        args.system = 3 if args.term in ("exact", "exchange") else 5
     if args.term == "nuclear":
         return run_nuclear(args)
     if args.term == "exact":
         return run_exact(args)
     if args.term == "grid":
         return run_grid(args)
+    if args.term == "exchange":
+        return run_exchange(args)
 
     import numpy as np
     import torch
@@ -499,6 +503,166 @@ def run_exact(args) -> int:
                     "forward_nodes_evaluated_frac": fwd_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
         "E_J": E.item(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_exchange(args) -> int:
+    """Screened RI-K E_K = -||L^-1 D||^2 with every gradient (splat leaves and C) on the ordered
+    pair list and the frozen product aux: one step = per aux chunk the three-centre block, the
+    pair-sparse Y = T_P C and the FP64 GEMM D_P = C^T Y_P, one triangular solve over the
+    k(k+1)/2 packed columns, then the reverse (second solve, per chunk dC and Ybar GEMMs, the
+    sampled Tbar and the three-centre reverse). The refresh products are built beforehand."""
+    import numpy as np
+    import torch
+    import __graft_entry__ as ge
+
+    g = ge.load_package()
+    import importlib
+    wl = importlib.import_module("gs_dft_amd.workloads")
+    from gs_dft_amd import _lib
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    s = wl.make_system(args.system)
+    mk = lambda a: torch.tensor(a, device=dev, dtype=torch.float64)
+    quat, ls, cen, C0 = mk(s.quat), mk(s.log_scale), mk(s.centers), mk(s.C)
+    basis0 = g.Splat(quat=quat, log_scale=ls, centers=cen)
+    lam = 1e-8
+    pi, pj, w = g.neighbor_pairs(basis0, s.eps, unique=False)
+    index = g.build_pair_index(s.M, pi, pj, w)
+    aux = g.init_product_aux(basis0, scales=s.scales)
+    L = g.aux_cholesky(aux, lam)
+    torch.cuda.synchronize()
+    M, k, N, n = s.M, s.k, aux.n_basis, index.n_live
+    K2 = k * (k + 1) // 2
+    log(f"system {args.system} {s.name}: M={M} k={k} N_aux={N} ordered pairs n={n}")
+    integrals = float(N) * n
+    gemm_fwd = 2.0 * N * M * k * k                  # D_P = C^T Y_P
+    gemm_bwd = 2.0 * (2.0 * N * M * k * k)          # dC += 2 Y_P Dbar_P, Ybar_P = C Dbar_P
+    trsm = float(N) * N * K2                        # one solve over K2 columns
+    sparse = 2.0 * 2.0 * N * n * k                  # Y = T C and Tbar = Ybar . C (symmetric list)
+    flops = (gemm_fwd + gemm_bwd + 2 * trsm + sparse + integrals * (FLOPS_FWD + FLOPS_BWD))
+
+    def step():
+        b = g.Splat(quat=quat.clone().requires_grad_(), log_scale=ls.clone().requires_grad_(),
+                    centers=cen.clone().requires_grad_())
+        C = C0.clone().requires_grad_()
+        E = g.df_exchange_energy_screened(b, C, aux, pi, pj, lam=lam, valid=w, cholV=L,
+                                          index=index)
+        E.backward()
+        return E
+
+    ids = (_lib.PROF_EXCH_BLOCK, _lib.PROF_EXCH_BWD, _lib.PROF_EXCH_TRSM, _lib.PROF_EXCH_GEMM,
+           _lib.PROF_EXCH_SPARSE)
+    _lib.profile_enable(True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for kid in ids:
+        _lib.profile_read(kid, reset=True)
+        _lib.profile_read_work(kid, reset=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        E = step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    prof = {kid: _lib.profile_read(kid, reset=True) for kid in ids}
+    bwd_nodes = _lib.profile_read_work(_lib.PROF_EXCH_BWD, reset=True)
+    _lib.profile_enable(False)
+    per_step = {kid: prof[kid][0] / args.steps for kid in ids}
+    blk_ms, rev_ms = per_step[_lib.PROF_EXCH_BLOCK], per_step[_lib.PROF_EXCH_BWD]
+    trsm_ms, gemm_ms = per_step[_lib.PROF_EXCH_TRSM], per_step[_lib.PROF_EXCH_GEMM]
+    sparse_ms = per_step[_lib.PROF_EXCH_SPARSE]
+    trsm_tf = 2 * trsm / (trsm_ms * 1e-3)
+    gemm_tf = (gemm_fwd + gemm_bwd) / (gemm_ms * 1e-3)
+    with torch.no_grad():
+        t1 = time.perf_counter()
+        E0 = g.df_exchange_energy_screened(basis0, C0, aux, pi, pj, lam=lam, valid=w, cholV=L,
+                                           index=index)
+        torch.cuda.synchronize()
+        wall_e = time.perf_counter() - t1
+    log(f"E_K={E.item():.12e} (energy only {E0.item():.12e}); step {wall * 1e3:.1f} ms, energy "
+        f"only {wall_e * 1e3:.1f} ms; per step: trsm {trsm_ms:.1f} ms ({trsm_tf / 1e12:.1f} "
+        f"TFLOP/s), GEMMs {gemm_ms:.1f} ms ({gemm_tf / 1e12:.1f} TFLOP/s), three-centre block "
+        f"{blk_ms:.1f} ms, three-centre reverse {rev_ms:.1f} ms, pair-sparse products "
+        f"{sparse_ms:.1f} ms")
+    # the dominant kernel family of the step and its algorithmic flops per step (work that a
+    # recompute repeats is not counted again)
+    fams = [("three-centre block (k_exch_block)", blk_ms, integrals * FLOPS_FWD, "valu"),
+            ("three-centre reverse (k_gamma_bwd, per-(P,a) cotangent)", rev_ms,
+             integrals * FLOPS_BWD, "valu"),
+            ("pair-sparse products (k_exch_spmm, k_exch_sddmm)", sparse_ms, sparse, "valu"),
+            ("FP64 GEMMs (rocBLAS dgemm)", gemm_ms, gemm_fwd + gemm_bwd, "mfma"),
+            ("triangular solves (rocBLAS dtrsm)", trsm_ms, 2 * trsm, "mfma")]
+    dom = max(fams, key=lambda f: f[1])
+    dom_tf = dom[2] / (dom[1] * 1e-3)
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import oracle as orc
+        pin, pjn = pi.cpu().numpy(), pj.cpu().numpy()
+        la, ac = aux.log_alpha.cpu().numpy(), aux.centers.cpu().numpy()
+        rng = np.random.default_rng(1)
+
+        def per_pair(m):           # the reference's D accumulation over m pairs (ri.py:524-531)
+            sel = np.sort(rng.choice(n, size=min(m, n), replace=False))
+            t = time.perf_counter()
+            B = orc.three_center_block(s.quat, s.log_scale, s.centers, la, ac, pin[sel], pjn[sel])
+            np.einsum("Ap,po,pq->Aoq", B, s.C[pin[sel]], s.C[pjn[sel]], optimize=True)
+            return time.perf_counter() - t, len(sel)
+
+        m_probe, t_probe = 4, 0.0
+        while True:                 # grow the probe until it is long enough to scale from
+            t_probe, m_probe = per_pair(m_probe)
+            if t_probe > 0.5 or m_probe >= n:
+                break
+            m_probe *= 4
+        m = max(m_probe, min(n, int(m_probe * 0.5 * args.cpu_seconds / max(t_probe, 1e-6))))
+        t_pairs, m_pairs = per_pair(m) if m > m_probe else (t_probe, m_probe)
+        Dr = rng.normal(size=(N, k, k))
+        t = time.perf_counter()
+        Mm = np.einsum("Aoq,Boq->AB", Dr, Dr, optimize=True)       # ri.py:532
+        Vs = orc.aux_metric(la, ac, lam)
+        np.trace(np.linalg.solve(Vs, Mm))                           # ri.py:544
+        t_fixed = time.perf_counter() - t
+        cpu_ms = (t_pairs / m_pairs * n + t_fixed) * 1e3
+        cpu = {"value": cpu_ms, "unit": "ms per energy evaluation (pair part extrapolated "
+               "linearly in pairs, plus the measured M build and solve)",
+               "cores": orc.num_threads(), "kind": "port",
+               "sample": f"{m_pairs} of {n} pairs x all {N} aux ({t_pairs:.1f} s) + M = D D^T "
+                         f"and the dense solve at full size ({t_fixed:.1f} s) on "
+                         f"{orc.num_threads()} threads (C oracle three-centre block, numpy "
+                         f"einsum contractions as gs_dft/coulomb/ri.py:497-544); energy only"}
+        log(f"cpu baseline: {cpu_ms / 1e3:.1f} s per energy ({m_pairs} pairs sampled)")
+
+    out = {
+        "metric": "screened RI-K fwd+bwd wall ms; algorithmic FP64 FLOP/s",
+        "value": flops / wall,
+        "unit": "algorithmic FP64 FLOP/s (energy + all gradients)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"{s.name}: screened RI-K exchange, M={M} splats, k={k}, "
+                               f"N_aux={N}, eps={s.eps}, ordered pairs",
+                   "system": args.system, "M": M, "k": k, "N_aux": N, "n_pairs": n,
+                   "eps": s.eps, "parallelism": "single GPU"},
+        "roofline": {"bound": dom[3], "kernel": dom[0], "achieved": dom_tf / 1e12,
+                     "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom_tf / PEAK_FP64,
+                     "traffic": None, "flops_per_step": dom[2], "kernel_ms_per_step": dom[1],
+                     "note": "per step, summed over the chunk launches; algorithmic flops: "
+                             "N n x 419 (block), N n x 780 (reverse), 4 N n k (Y = T C and "
+                             "Tbar), 6 N M k^2 (GEMMs), 2 N^2 K2 (solves); FP64 peak 78.6 "
+                             "(vector and matrix)"},
+        "kernels": {"trsm_ms_per_step": trsm_ms, "trsm_tflops": trsm_tf / 1e12,
+                    "gemm_ms_per_step": gemm_ms, "gemm_tflops": gemm_tf / 1e12,
+                    "block_ms_per_step": blk_ms, "reverse_ms_per_step": rev_ms,
+                    "sparse_ms_per_step": sparse_ms,
+                    "reverse_nodes_evaluated_frac": bwd_nodes / args.steps / (NODES * integrals),
+                    "energy_only_ms": wall_e * 1e3},
+        "cpu_baseline": cpu,
+        "E_K": E.item(),
     }
     print(json.dumps(out), flush=True)
     return 0

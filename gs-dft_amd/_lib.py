@@ -22,7 +22,8 @@ GSDFT_ERR_LIB = 5
 GSDFT_ERR_WORKSPACE = 6
 
 (PROF_GAMMA_FWD, PROF_GAMMA_BWD, PROF_SCREEN, PROF_METRIC, PROF_CHOLESKY, PROF_SOLVE,
- PROF_NUC_PAIRS, PROF_NUC_ATOMS, PROF_ERI_FWD, PROF_ERI_BWD) = range(10)
+ PROF_NUC_PAIRS, PROF_NUC_ATOMS, PROF_ERI_FWD, PROF_ERI_BWD, PROF_EXCH_BLOCK, PROF_EXCH_BWD,
+ PROF_EXCH_TRSM, PROF_EXCH_GEMM, PROF_EXCH_SPARSE) = range(15)
 
 _i64, _i32, _int, _dbl, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_double, ctypes.c_size_t
 _vp = ctypes.c_void_p
@@ -63,6 +64,10 @@ SIGNATURES = {
     "gsdft_exact_coulomb_workspace_size": [_i64, _i64, _i64, _int, _psz],
     "gsdft_exact_coulomb": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "gsdft_exchange_workspace_size": [_i64, _i64, _i64, _i64, _int, _int, _i64, _int, _psz],
+    "gsdft_exchange": [_i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                       _vp, _vp, _vp, _vp, _int, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                       _vp],
     "gsdft_grid_density_workspace_size": [_i64, _i64, _i64, _int, _int, _psz],
     "gsdft_grid_density": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp,
                            _vp, _vp, _sz, _vp],

@@ -20,7 +20,8 @@ LIB = OUT_DIR / "libgsdft.so"
 ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("GSDFT_ARCH", "gfx950")
 
-SOURCES = ["abi.hip", "screen.hip", "dfj.hip", "solve.hip", "order.hip", "grid.hip"]
+SOURCES = ["abi.hip", "screen.hip", "dfj.hip", "solve.hip", "order.hip", "grid.hip",
+           "exchange.hip"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

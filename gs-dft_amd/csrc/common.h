@@ -373,4 +373,19 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
+// Centre-grouped slot order of a product aux of G = N / M exponent scales (scale-major,
+// P = s M + m): slot m G + s, so the scales sharing a centre are consecutive; G <= 1 keeps aux
+// order.
+__host__ __device__ __forceinline__ int64_t aux_slot(int64_t p, int64_t N, int64_t G) {
+    if (G <= 1) return p;
+    const int64_t Mg = N / G;
+    return (p % Mg) * G + p / Mg;
+}
+
+__host__ __device__ __forceinline__ int64_t aux_of_slot(int64_t q, int64_t N, int64_t G) {
+    if (G <= 1) return q;
+    const int64_t Mg = N / G;
+    return (q % G) * Mg + q / G;
+}
+
 }  // namespace gsdft

@@ -23,6 +23,7 @@
 #include <rocblas/rocblas.h>
 #include <rocsolver/rocsolver.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -316,17 +317,7 @@ __global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ 
 // m G + s, so the scales sharing a centre are consecutive; otherwise (N not a multiple of M) in
 // aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
 // the reverse kernel recomputes the centre-dependent terms only there, whatever the aux holds.
-__device__ __forceinline__ int64_t aux_slot(int64_t p, int64_t N, int64_t G) {
-    if (G <= 1) return p;
-    const int64_t Mg = N / G;
-    return (p % Mg) * G + p / Mg;
-}
-
-__device__ __forceinline__ int64_t aux_of_slot(int64_t q, int64_t N, int64_t G) {
-    if (G <= 1) return q;
-    const int64_t Mg = N / G;
-    return (q % G) * Mg + q / G;
-}
+// (aux_slot / aux_of_slot: common.h)
 
 __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
@@ -340,7 +331,7 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
     const int64_t slot = aux_slot(p, N, G);
     double* o = out + kAuxRec * slot;
     o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
-    o[3] = dgamma[p] * (dscale ? *dscale : 1.0) * kn[p];
+    o[3] = (dgamma ? dgamma[p] : 1.0) * (dscale ? *dscale : 1.0) * kn[p];
     bool first = true;
     if (slot > 0) {
         const int64_t q = aux_of_slot(slot - 1, N, G);
@@ -366,9 +357,13 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // f_t = wp_t y e^-z, y = Pn^(-1/2), z = s Qn / Pn, g_t = f_t / Pn and df/dPn = g_t (z - 1/2).
 // Records sharing a centre are consecutive, so d = R - Pa and the d-moments are formed once per
 // centre: C0..C2 = sum u dQ0..2 over the group, then Vc += C0 d, ..., Sb += C2 d d^T.
+// With kLaneU the cotangent of (P|a) is not separable: u = x[3] * ut[slot * ldu + p] per lane
+// (the exchange's dE/d(P|a), stored slot-major).
+template <bool kLaneU>
 __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
-    int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work) {
+    int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
+    const double* __restrict__ ut, int64_t ldu) {
     __shared__ double tab[256];
     // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
     // slot per lane, structure of arrays) rather than in registers across the loop.
@@ -416,7 +411,8 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     uint32_t nodes = 0;
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
-        const double u = x[3];
+        double u = x[3];
+        if constexpr (kLaneU) u *= live ? ut[a * ldu + p] : 0.0;
         if (p == p0 || x[5] != 0.0) {            // a new centre (wave-uniform)
             flush();
             const int l = threadIdx.x;
@@ -1092,6 +1088,82 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
     pair_reverse(n, a, i, j, A6, mu, Nrm, Gh, gP, gKN, contrib);
 }
 
+// ------------------------------------------------------------------ exchange three-centre block
+// Bt[a * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and every pair a in list
+// order, the pair record carrying q_a = w_a: the screened block of RI-K
+// (gs_dft/coulomb/ri.py:527-531, full_isobra_block), written rather than contracted. One lane per
+// aux slot, the pair records of a slab wave-uniform, as in k_gamma_fwd; each (a, l) is written once.
+__global__ __launch_bounds__(256) void k_exch_block(int64_t N, int64_t G, int64_t q0, int64_t W,
+                                                    const double* __restrict__ beta,
+                                                    const double* __restrict__ R,
+                                                    const double* __restrict__ kn, int64_t n,
+                                                    const double* __restrict__ rec,
+                                                    int64_t per_slab, int64_t ldb,
+                                                    double* __restrict__ Bt,
+                                                    unsigned long long* __restrict__ work) {
+    __shared__ double tab[256];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    __syncthreads();
+    const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = l < W;
+    const int64_t P = live ? aux_of_slot(q0 + l, N, G) : 0;
+    const double b = live ? beta[P] : 1.0;
+    const double Rx = live ? R[3 * P] : kFarAway, Ry = live ? R[3 * P + 1] : kFarAway,
+                 Rz = live ? R[3 * P + 2] : kFarAway;
+    const double knP = live ? kn[P] : 0.0;
+    double s[kNodes], wp[kNodes];
+    node_consts(b, s, wp);
+    const int64_t a0 = blockIdx.y * per_slab;
+    const int64_t a1 = min(n, a0 + per_slab);
+    uint32_t nodes = 0;
+    for (int64_t a = a0; a < a1; ++a) {
+        const double* __restrict__ r = rec + kRec * a;
+        const double I1 = r[0], I2 = r[1], I3 = r[2];
+        const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
+        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
+        const double coef = r[12];
+        const double ax = xx * dx + xy * dy + xz * dz;
+        const double ay = xy * dx + yy * dy + yz * dz;
+        const double az = xz * dx + yz * dy + zz * dz;
+        const double q0d = dx * dx + dy * dy + dz * dz;
+        const double q1 = dx * ax + dy * ay + dz * az;
+        const double q2 = ax * ax + ay * ay + az * az;
+        const double X0 = I3 * q0d;
+        const double rr = I1 * q1 - q2;
+        double F = 0.0;
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            const double st = s[t];
+            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
+            const NodeVal v = node_val(Pn, st * Qn);
+            F = __builtin_fma(wp[t] * v.y0, exp_neg_tab(v.arg, tab), F);
+            return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
+        F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
+        if (live) Bt[a * ldb + l] = (F * coef) * knP;
+    }
+    count_work(work, live, nodes);
+}
+
+// acc[c][slot] = (first ? 0 : acc[c][slot]) + sum over slabs of partial[slab][c][slot].
+__global__ void k_acc_fold(int64_t n, int64_t slabs, const double* __restrict__ partial,
+                           double* __restrict__ acc, int first) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= n * kAcc) return;
+    const int64_t c = t / n, slot = t % n;
+    double v = first ? 0.0 : acc[t];
+    for (int64_t k = 0; k < slabs; ++k) v += partial[(k * kAcc + c) * n + slot];
+    acc[t] = v;
+}
+
+// inv[perm[slot]] = slot.
+__global__ void k_inv_perm(int64_t n, const int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (slot < n) inv[perm[slot]] = (int32_t)slot;
+}
+
 // ------------------------------------------------------------------ work split
 
 struct Split {
@@ -1245,6 +1317,122 @@ int blas_handle(hipStream_t s, rocblas_handle* out) {
     if (rocblas_set_stream(g_blas[dev], s) != rocblas_status_success)
         return fail(GSDFT_ERR_LIB, "rocblas_set_stream failed");
     *out = g_blas[dev];
+    return GSDFT_OK;
+}
+
+
+// ------------------------------------------------------------------ exchange: three-centre passes
+
+int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
+                   ExchTcWs* w) {
+    *w = ExchTcWs{};
+    w->A6 = ar.take<double>(6 * M + 1);
+    w->Nrm = ar.take<double>(M + 1);
+    w->beta = ar.take<double>(N + 1);
+    w->kn = ar.take<double>(N + 1);
+    w->q = ar.take<double>(n + 1);
+    w->rec = ar.take<double>(kRec * n + kRec);
+    if (grads) {
+        // bwd_split(W, n).slabs for every chunk width W <= Pc stays within min(ceil(target /
+        // groups), (Pc + 15) / 16) (the count before its rounding to whole slabs)
+        const int64_t groups = n > 0 ? (n + 255) / 256 : 1;
+        int64_t slab_bound = (256 * 4 * 4 + groups - 1) / groups;
+        slab_bound = std::min<int64_t>(std::min<int64_t>(slab_bound, (Pc + 15) / 16), 65535);
+        if (slab_bound < 1) slab_bound = 1;
+        w->rec_sorted = ar.take<double>(kRec * n + kRec);
+        w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
+        w->part = ar.take<double>(slab_bound * kAcc * n + 1);
+        w->acc = ar.take<double>(kAcc * n + 1);
+        w->J = ar.take<double>(n + 1);
+        w->contrib = ar.take<double>(20 * n + 1);
+        w->inv_perm = ar.take<int32_t>(n + 1);
+        GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
+    }
+    return GSDFT_OK;
+}
+
+int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
+                     const double* centers, int64_t N, const double* log_alpha,
+                     const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s) {
+    GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
+    k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
+    GSDFT_HIP(hipGetLastError());
+    if (n <= 0) return GSDFT_OK;
+    if (weight) {
+        GSDFT_HIP(hipMemcpyAsync(w.q, weight, n * sizeof(double), hipMemcpyDeviceToDevice, s));
+    } else {
+        k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 1.0, w.q);
+        GSDFT_HIP(hipGetLastError());
+    }
+    k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec);
+    GSDFT_HIP(hipGetLastError());
+    if (!grads) return GSDFT_OK;
+    const int64_t G = (N % M == 0) ? N / M : 1;
+    k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
+                                                      nullptr, w.aux);
+    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
+    k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
+                                                            w.rec_sorted);
+    GSDFT_HIP(hipGetLastError());
+    k_inv_perm<<<blocks_for(n, 256), 256, 0, s>>>(n, w.pair_order.perm, w.inv_perm);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
+                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
+    if (n <= 0 || W <= 0) return GSDFT_OK;
+    const int64_t G = (N % M == 0) ? N / M : 1;
+    const int64_t gx = (W + 255) / 256;
+    int64_t slabs = (256 * 4 * 16 + gx - 1) / gx;
+    const int64_t max_slabs = (n + 7) / 8;
+    if (slabs > max_slabs) slabs = max_slabs;
+    if (slabs > 65535) slabs = 65535;
+    if (slabs < 1) slabs = 1;
+    const int64_t per = (n + slabs - 1) / slabs;
+    slabs = (n + per - 1) / per;
+    dim3 grid((unsigned)gx, (unsigned)slabs);
+    profile_begin(kProfExchBlock, s);
+    k_exch_block<<<grid, 256, 0, s>>>(N, G, q0, W, w.beta, aux_centers, w.kn, n, w.rec, per, ldb,
+                                      Bt, profile_work_counter(kProfExchBlock));
+    profile_end(kProfExchBlock, s);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* Tbar, int64_t ldt,
+                    bool first, const ExchTcWs& w, hipStream_t s) {
+    if (n <= 0 || W <= 0) return GSDFT_OK;
+    const Split sp = bwd_split(W, n);
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+    profile_begin(kProfExchBwd, s);
+    k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab,
+                                           w.part, profile_work_counter(kProfExchBwd), Tbar, ldt);
+    profile_end(kProfExchBwd, s);
+    GSDFT_HIP(hipGetLastError());
+    k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);
+    GSDFT_HIP(hipGetLastError());
+    (void)N;
+    return GSDFT_OK;
+}
+
+int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                   const double* weight, const double* quat, const double* log_scale,
+                   const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
+                   const int32_t* col_ptr, const int32_t* col_perm, double* dquat,
+                   double* dlog_scale, double* dcenters, const ExchTcWs& w, hipStream_t s) {
+    if (n > 0) {
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, kPref3c, w.pair_order.perm, pi,
+                                                           pj, weight, w.A6, centers, w.Nrm,
+                                                           w.rec_sorted, w.acc, w.J, w.contrib);
+        GSDFT_HIP(hipGetLastError());
+    }
+    k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
+                                                         col_perm, w.contrib, quat, log_scale,
+                                                         dquat, dlog_scale, dcenters);
+    GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }
 
@@ -1427,8 +1615,8 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         const Split sp = bwd_split(N, n);
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
-        k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
-                                         profile_work_counter(kProfGammaBwd));
+        k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
+                                                profile_work_counter(kProfGammaBwd), nullptr, 0);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
         k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPref3c, w.pair_order.perm, pi,
@@ -1479,8 +1667,9 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
     const Split sp = bwd_split(n_atoms, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfNucPairs, s);
-    k_gamma_bwd<<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab, w.g.acc,
-                                     profile_work_counter(kProfNucPairs));
+    k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab,
+                                            w.g.acc, profile_work_counter(kProfNucPairs), nullptr,
+                                            0);
     profile_end(kProfNucPairs, s);
     GSDFT_HIP(hipGetLastError());
     k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPrefNuc,

@@ -1,0 +1,511 @@
+// Screened exact exchange through density fitting (RI-K), gs_dft/coulomb/ri.py:497-544:
+//   D[P,o,o'] = sum over listed pairs a = (i, k) of w_a C_io C_ko' (P|a),
+//   E_K = -Tr((V + lam I)^-1 M),   M_PQ = sum_oo' D[P,o,o'] D[Q,o,o'].
+// With the Cholesky factor L L^T = V + lam I this is E_K = -||L^-1 D||_F^2 over the k^2 columns
+// (o, o'). An orthogonal change of the column basis keeps the norm, so the columns are stored as
+// the symmetric part, (D_oo' + D_o'o)/sqrt2 for o < o' and D_oo on the diagonal (k(k+1)/2
+// columns), followed by the antisymmetric part (D_oo' - D_o'o)/sqrt2 for o < o'. On a symmetric
+// pair list (every live (i, k, w) has its (k, i, w)) each D_P is symmetric up to round-off and the
+// antisymmetric columns are dropped.
+//
+// Forward, per chunk of W aux functions (centre-grouped slot order):
+//   Bt (n x W)          the screened three-centre block (k_exch_block, dfj.hip)
+//   Y[i][l][o']         = sum over pairs a of row i of Bt[a][l] C[k_a][o']     (k_exch_spmm, a
+//                         lane per aux, a wave per range of orbitals held in registers)
+//   D_P = C^T Y_P       one FP64 GEMM per chunk: k x (W k) x M
+//   Dt[:, P]            packed columns of D_P                                    (k_exch_pack)
+// then Wt = Dt L^-T (rocBLAS trsm over the packed-column right-hand sides) and E_K = -sum Wt^2.
+// Reverse with seed dE_K = 1: Dbar_t = -2 Wt L^-1 (trsm), then per chunk Dbar_P (k_exch_unpack),
+// with the forward's Y (and Y') kept in the workspace when they fit, else recomputed,
+//   dC    += Y_P Dbar_P^T + Y'_P Dbar_P      Y'[m][l][o] = sum over pairs a of column m of
+//                                            Bt[a][l] C[i_a][o] (= Y on a symmetric list)
+//   Ybar_P = C Dbar_P,   Tbar[a][l] = Ybar[i_a][l] . C[k_a]                   (k_exch_sddmm)
+//   and the three-centre reverse with the per-(P, a) cotangent Tbar (dfj.hip) for the splat
+//   gradients. Every sum runs in a fixed order (no atomics; rocBLAS runs with atomics off).
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+
+#include "common.h"
+#include "internal.h"
+
+namespace gsdft {
+
+namespace {
+
+inline unsigned nblk(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+#define GSDFT_BLAS(call)                                                                   \
+    do {                                                                                   \
+        rocblas_status st_ = (call);                                                       \
+        if (st_ != rocblas_status_success)                                                 \
+            return fail(GSDFT_ERR_LIB, "%s failed (rocBLAS status %d)", #call, (int)st_);  \
+    } while (0)
+
+constexpr double kRsqrt2 = 0.70710678118654752440;
+constexpr int kRedBlocks = 1024;
+constexpr double kChunkBytes = 8.0 * 1024 * 1024 * 1024;   // per-chunk buffers of the default chunk
+constexpr double kStoreBytes = 32.0 * 1024 * 1024 * 1024;   // Y (and Y') kept for the reverse
+constexpr int64_t kSplitMax = 32;                           // K slices of the dC GEMM
+
+// Y[i][l][o] = sum_{r in [ptr[i], ptr[i+1])} Bt[perm[r] * ldb + l] C[partner[perm[r]] * k + o] for
+// l < W, o < k. Grid (rows, ceil(W / 64), ceil(k / (4 ON))), 4 waves: lane = aux l, wave w owns the
+// ON orbitals o0 .. o0 + ON - 1 in registers. Per pair the lane reads one Bt entry (coalesced over
+// the wave) and the wave reads the pair's C row segment with wave-uniform (scalar) loads, so each
+// pair costs ON FMAs per lane.
+template <int ON>
+__global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t ldb,
+                                                   const int32_t* __restrict__ ptr,
+                                                   const int32_t* __restrict__ perm,
+                                                   const int32_t* __restrict__ partner,
+                                                   const double* __restrict__ Bt,
+                                                   const double* __restrict__ C,
+                                                   double* __restrict__ Y) {
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t l = (int64_t)blockIdx.y * 64 + lane;
+    const int64_t o0 = ((int64_t)blockIdx.z * 4 + wave) * ON;
+    if (o0 >= k) return;                                   // wave-uniform
+    const int on = (int)std::min<int64_t>(ON, k - o0);
+    const bool live = l < W;
+    const int64_t lc = live ? l : 0;
+    double acc[ON];
+#pragma unroll
+    for (int j = 0; j < ON; ++j) acc[j] = 0.0;
+    const int64_t r0 = ptr[i], r1 = ptr[i + 1];
+    if (on == ON) {
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t a = perm[r];
+            const double b = Bt[a * ldb + lc];
+            const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
+#pragma unroll
+            for (int j = 0; j < ON; ++j) acc[j] = __builtin_fma(b, crow[j], acc[j]);
+        }
+    } else {
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t a = perm[r];
+            const double b = Bt[a * ldb + lc];
+            const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
+#pragma unroll
+            for (int j = 0; j < ON; ++j)
+                if (j < on) acc[j] = __builtin_fma(b, crow[j], acc[j]);
+        }
+    }
+    if (!live) return;
+    double* __restrict__ out = Y + i * (W * k) + l * k + o0;
+#pragma unroll
+    for (int j = 0; j < ON; ++j)
+        if (j < on) out[j] = acc[j];
+}
+
+// Packed columns of D_P (P the aux of slot q0 + l): Dfull[o + k (l k + o')] = D_P[o][o'];
+// Dt[j + K2 P] with j = o'(o'+1)/2 + o for the symmetric part (o <= o') and
+// k(k+1)/2 + o'(o'-1)/2 + o for the antisymmetric part (o < o', only when !sym).
+__global__ void k_exch_pack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q0, int64_t N,
+                            int64_t G, const double* __restrict__ Dfull, double* __restrict__ Dt) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t kk = k * k;
+    if (t >= W * kk) return;
+    const int64_t l = t / kk, rem = t - l * kk;
+    const int64_t op = rem / k, o = rem - op * k;
+    if (o > op) return;
+    const int64_t P = aux_of_slot(q0 + l, N, G);
+    const double* Dl = Dfull + l * kk;
+    double* col = Dt + K2 * P;
+    const double d1 = Dl[o + k * op], d2 = Dl[op + k * o];
+    const int64_t js = op * (op + 1) / 2 + o;
+    if (o == op) {
+        col[js] = d1;
+    } else {
+        col[js] = (d1 + d2) * kRsqrt2;
+        if (!sym) col[k * (k + 1) / 2 + op * (op - 1) / 2 + o] = (d1 - d2) * kRsqrt2;
+    }
+}
+
+// Reverse of k_exch_pack: Dbar[o + k (l k + o')] = dE/dD_P[o][o'] and, for a non-null E, its
+// block transpose E[o' + k (l k + o)].
+__global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q0, int64_t N,
+                              int64_t G, const double* __restrict__ Dbt, double* __restrict__ Dbar,
+                              double* __restrict__ E) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t kk = k * k;
+    if (t >= W * kk) return;
+    const int64_t l = t / kk, rem = t - l * kk;
+    const int64_t op = rem / k, o = rem - op * k;
+    const int64_t P = aux_of_slot(q0 + l, N, G);
+    const double* col = Dbt + K2 * P;
+    const int64_t lo = o < op ? o : op, hi = o < op ? op : o;
+    double v = col[hi * (hi + 1) / 2 + lo];
+    if (o != op) {
+        v *= kRsqrt2;
+        if (!sym) {
+            const double a = col[k * (k + 1) / 2 + hi * (hi - 1) / 2 + lo] * kRsqrt2;
+            v += (o < op) ? a : -a;
+        }
+    }
+    Dbar[o + k * (l * k + op)] = v;
+    if (E) E[op + k * (l * k + o)] = v;
+}
+
+// Tbar[inv[a] * ldt + l] = sum_o Ybar[i][l][o] C[k_a][o] for the pairs a of row i and l < W.
+// Grid (rows, ceil(W / 64)), 4 waves: lane = aux l; per pass of 4 ON orbitals wave w holds
+// Ybar[i][l][o0 .. o0 + ON - 1] in registers and forms, for 16 pairs at a time (their C row
+// segments wave-uniform), its partial dot products into LDS; the four partials of a pair are then
+// summed in wave order and added to Tbar (set on the first pass). Passes run in order inside the
+// block, so every sum has a fixed order.
+constexpr int kPairGroup = 16;
+template <int ON>
+__global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_t ldt,
+                                                    const int32_t* __restrict__ ptr,
+                                                    const int32_t* __restrict__ perm,
+                                                    const int32_t* __restrict__ partner,
+                                                    const int32_t* __restrict__ inv,
+                                                    const double* __restrict__ Ybar,
+                                                    const double* __restrict__ C,
+                                                    double* __restrict__ Tbar) {
+    __shared__ double part[4][kPairGroup][64];
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t l = (int64_t)blockIdx.y * 64 + lane;
+    const bool live = l < W;
+    const int64_t lc = live ? l : 0;
+    const int64_t Wk = W * k;
+    const int64_t r0 = ptr[i], r1 = ptr[i + 1];
+    for (int64_t ob = 0; ob < k; ob += 4 * ON) {
+        const int64_t o0 = ob + (int64_t)wave * ON;
+        const int on = (int)std::max<int64_t>(0, std::min<int64_t>(ON, k - o0));
+        double y[ON];
+#pragma unroll
+        for (int j = 0; j < ON; ++j) y[j] = (j < on) ? Ybar[i * Wk + lc * k + o0 + j] : 0.0;
+        for (int64_t rb = r0; rb < r1; rb += kPairGroup) {
+            const int nr = (int)std::min<int64_t>(kPairGroup, r1 - rb);
+            for (int q = 0; q < nr; ++q) {
+                const int64_t a = perm[rb + q];
+                const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
+                double sacc = 0.0;
+                if (on == ON) {
+#pragma unroll
+                    for (int j = 0; j < ON; ++j) sacc = __builtin_fma(y[j], crow[j], sacc);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < ON; ++j)
+                        if (j < on) sacc = __builtin_fma(y[j], crow[j], sacc);
+                }
+                part[wave][q][lane] = sacc;
+            }
+            __syncthreads();
+            for (int q = wave; q < nr; q += 4) {
+                const double v = ((part[0][q][lane] + part[1][q][lane]) + part[2][q][lane]) +
+                                 part[3][q][lane];
+                if (live) {
+                    double* out = Tbar + (int64_t)inv[perm[rb + q]] * ldt + l;
+                    *out = (ob == 0) ? v : *out + v;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// part[b] = sum of x[i]^2 over block b's contiguous range (fixed order per block).
+__global__ __launch_bounds__(256) void k_sumsq_part(int64_t count, const double* __restrict__ x,
+                                                    double* __restrict__ part) {
+    __shared__ double red[256];
+    const int64_t per = (count + gridDim.x - 1) / gridDim.x;
+    const int64_t b0 = blockIdx.x * per;
+    const int64_t b1 = std::min<int64_t>(count, b0 + per);
+    double s = 0.0;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) s = __builtin_fma(x[i], x[i], s);
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(1024) void k_sum_scaled(int64_t m, const double* __restrict__ part,
+                                                     double scale, double* __restrict__ out) {
+    __shared__ double red[1024];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < m; i += 1024) s += part[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = scale * red[0];
+}
+
+// out[e] += sum over s < S of part[s * count + e], in order of s.
+__global__ void k_sum_slices(int64_t count, int64_t S, const double* __restrict__ part,
+                             double* __restrict__ out) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= count) return;
+    double v = out[e];
+    for (int64_t q = 0; q < S; ++q) v += part[q * count + e];
+    out[e] = v;
+}
+
+__global__ void k_fill0(int64_t n, double* __restrict__ out) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i < n) out[i] = 0.0;
+}
+
+// Aux functions per chunk: the caller's choice, else as many as keep the chunk's buffers that
+// grow with it (block, Y / Y', D_P blocks) near kChunkBytes, a multiple of 64. (The reverse
+// moments are bounded by the pair count alone.)
+int64_t exch_chunk(int64_t M, int64_t k, int64_t N, int64_t n, bool sym, bool grads,
+                   int64_t req) {
+    if (req > 0) return std::min(req, N);
+    const double ys = (grads && !sym) ? 2.0 : 1.0;
+    const double per = 8.0 * ((double)n + ys * (double)M * (double)k + ys * (double)k * (double)k);
+    int64_t Pc = (int64_t)(kChunkBytes / per);
+    Pc = (Pc / 64) * 64;
+    if (Pc < 64) Pc = 64;
+    return std::min(Pc, N);
+}
+
+// With gradients, the forward keeps Y (and Y' on a non-symmetric list) for every chunk when they
+// fit in kStoreBytes, so the reverse needs neither the block nor the pair-sparse products again.
+bool exch_store(int64_t M, int64_t k, int64_t N, bool sym, bool grads, bool recompute) {
+    return grads && !recompute &&
+           8.0 * (double)M * (double)N * (double)k * (sym ? 1.0 : 2.0) <= kStoreBytes;
+}
+
+// K slices of the dC GEMM (its k x M output is a handful of tiles; the K = W k dimension is long):
+// enough for ~512 tiles in flight, at most kSplitMax and one slice per aux function.
+int64_t dc_slices(int64_t k, int64_t M, int64_t W) {
+    const int64_t tiles = ((k + 127) / 128) * ((M + 127) / 128);
+    int64_t S = (512 + tiles - 1) / tiles;
+    S = std::min<int64_t>(std::min<int64_t>(S, kSplitMax), W);
+    return S < 1 ? 1 : S;
+}
+
+struct ExchWs {
+    ExchTcWs tc;
+    double *Dt, *Bt, *Y, *Yp, *Ys, *Yps, *Dfull, *Ebar, *part, *red;
+};
+
+int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool sym, bool grads,
+                    bool recompute, int64_t Pc, ExchWs* w) {
+    GSDFT_TRY(exch_tc_layout(ar, M, N, n, Pc, grads, &w->tc));
+    const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
+    const bool store = exch_store(M, k, N, sym, grads, recompute);
+    w->Dt = ar.take<double>(K2 * N + 1);
+    w->Bt = ar.take<double>(n * Pc + 1);
+    w->Y = ar.take<double>(M * Pc * k + 1);
+    w->Yp = (grads && !sym && !store) ? ar.take<double>(M * Pc * k + 1) : nullptr;
+    w->Ys = store ? ar.take<double>(M * N * k + 1) : nullptr;
+    w->Yps = (store && !sym) ? ar.take<double>(M * N * k + 1) : nullptr;
+    w->Dfull = ar.take<double>(k * k * Pc + 1);
+    w->Ebar = (grads && !sym) ? ar.take<double>(k * k * Pc + 1) : nullptr;
+    w->part = grads ? ar.take<double>(kSplitMax * k * M + 1) : nullptr;
+    w->red = ar.take<double>(kRedBlocks);
+    return GSDFT_OK;
+}
+
+// dC^T (k x M, column-major = row-major dC) += alpha Dbar (k x W k) Y^T-view (W k x M, ld W k),
+// as S K-slices of Ws = W / S aux functions (the remainder joins the last slice) into part, then
+// summed in slice order.
+int dc_gemm(rocblas_handle h, int64_t k, int64_t M, int64_t W, double alpha, const double* Dbar,
+            const double* Y, double* part, double* dC, hipStream_t s) {
+    const int64_t S = dc_slices(k, M, W), Ws = W / S, Wk = W * k;
+    const double one = 1.0, zero = 0.0;
+    const auto N_ = rocblas_operation_none;
+    GSDFT_BLAS(rocblas_dgemm_strided_batched_64(h, N_, N_, k, M, Ws * k, &alpha, Dbar, k,
+                                                k * Ws * k, Y, Wk, Ws * k, &zero, part, k, k * M,
+                                                S));
+    const int64_t rem = W - S * Ws;
+    if (rem > 0)
+        GSDFT_BLAS(rocblas_dgemm_64(h, N_, N_, k, M, rem * k, &alpha, Dbar + k * (S * Ws * k), k,
+                                    Y + S * Ws * k, Wk, &one, part + (S - 1) * k * M, k));
+    k_sum_slices<<<nblk(k * M, 256), 256, 0, s>>>(k * M, S, part, dC);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+// Orbitals per wave of the sparse kernels: the smallest of 8, 16, 24, 32 with 4 ON >= k, else 32
+// (several passes).
+int orbitals_per_wave(int64_t k) {
+    return k <= 32 ? 8 : k <= 64 ? 16 : k <= 96 ? 24 : 32;
+}
+
+int launch_spmm(int64_t M, int64_t W, int64_t k, int64_t ldb, const int32_t* ptr,
+                const int32_t* perm, const int32_t* partner, const double* Bt, const double* C,
+                double* Y, hipStream_t s) {
+    const int on = orbitals_per_wave(k);
+    dim3 grid((unsigned)M, nblk(W, 64), nblk(k, 4 * on));
+    profile_begin(kProfExchSparse, s);
+    switch (on) {
+    case 8: k_exch_spmm<8><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
+    case 16: k_exch_spmm<16><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
+    case 24: k_exch_spmm<24><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
+    default: k_exch_spmm<32><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
+    }
+    profile_end(kProfExchSparse, s);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+int launch_sddmm(int64_t M, int64_t W, int64_t k, int64_t ldt, const int32_t* ptr,
+                 const int32_t* perm, const int32_t* partner, const int32_t* inv,
+                 const double* Ybar, const double* C, double* Tbar, hipStream_t s) {
+    const int on = orbitals_per_wave(k);
+    dim3 grid((unsigned)M, nblk(W, 64));
+    profile_begin(kProfExchSparse, s);
+    switch (on) {
+    case 8:
+        k_exch_sddmm<8><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
+        break;
+    case 16:
+        k_exch_sddmm<16><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
+        break;
+    case 24:
+        k_exch_sddmm<24><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
+        break;
+    default:
+        k_exch_sddmm<32><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
+        break;
+    }
+    profile_end(kProfExchSparse, s);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+}  // namespace
+
+}  // namespace gsdft
+
+using namespace gsdft;
+
+extern "C" int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n,
+                                             int symmetric, int grads, int64_t aux_chunk,
+                                             int recompute, size_t* bytes) {
+    if (M <= 0 || k <= 0 || N <= 0 || n < 0 || aux_chunk < 0 || !bytes)
+        return fail(GSDFT_ERR_ARG, "exchange_workspace_size: bad arguments");
+    const bool sym = symmetric != 0, gr = grads != 0;
+    const int64_t Pc = exch_chunk(M, k, N, n, sym, gr, aux_chunk);
+    Arena ar{nullptr, 0, 0};
+    ExchWs w;
+    GSDFT_TRY(layout_exchange(ar, M, k, N, n, sym, gr, recompute != 0, Pc, &w));
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_scale,
+                              const double* centers, int64_t k, const double* C, int64_t N,
+                              const double* log_alpha, const double* aux_centers,
+                              const double* chol, int64_t n, const int32_t* pi, const int32_t* pj,
+                              const double* weight, const int32_t* row_ptr,
+                              const int32_t* row_perm, const int32_t* col_ptr,
+                              const int32_t* col_perm, int symmetric, int64_t aux_chunk,
+                              int recompute, double* energy, double* dquat, double* dlog_scale,
+                              double* dcenters, double* dC, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+    const bool grads = dquat != nullptr;
+    if (M <= 0 || k <= 0 || N <= 0 || n < 0 || aux_chunk < 0 || !quat || !log_scale ||
+        !centers || !C || !log_alpha || !aux_centers || !chol || !energy || !row_ptr ||
+        (n > 0 && (!pi || !pj || !row_perm)) ||
+        (grads && (!dlog_scale || !dcenters || !dC || !col_ptr || (n > 0 && !col_perm))))
+        return fail(GSDFT_ERR_ARG, "gsdft_exchange: bad arguments");
+    hipStream_t s = (hipStream_t)stream;
+    const bool sym = symmetric != 0;
+    const int64_t Pc = exch_chunk(M, k, N, n, sym, grads, aux_chunk);
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    ExchWs w;
+    GSDFT_TRY(layout_exchange(ar, M, k, N, n, sym, grads, recompute != 0, Pc, &w));
+    if (!w.red) return fail(GSDFT_ERR_WORKSPACE, "gsdft_exchange: workspace too small");
+    GSDFT_TRY(exch_tc_prologue(M, quat, log_scale, centers, N, log_alpha, aux_centers, n, pi, pj,
+                               weight, grads, w.tc, s));
+    if (n == 0) {                       // D = 0: E_K = 0 and every gradient vanishes
+        k_fill0<<<1, 1, 0, s>>>(1, energy);
+        GSDFT_HIP(hipGetLastError());
+        if (grads) {
+            k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
+            GSDFT_HIP(hipGetLastError());
+            GSDFT_TRY(exch_tc_finish(M, 0, pi, pj, weight, quat, log_scale, centers, row_ptr,
+                                     row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters,
+                                     w.tc, s));
+        }
+        return GSDFT_OK;
+    }
+    rocblas_handle h;
+    GSDFT_TRY(blas_handle(s, &h));
+    const int64_t G = (N % M == 0) ? N / M : 1;
+    const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
+    const double one = 1.0, zero = 0.0, mtwo = -2.0;
+    const auto N_ = rocblas_operation_none, T_ = rocblas_operation_transpose;
+
+    const bool store = exch_store(M, k, N, sym, grads, recompute != 0);
+    for (int64_t q0 = 0; q0 < N; q0 += Pc) {
+        const int64_t W = std::min(Pc, N - q0);
+        double* Yc = store ? w.Ys + M * q0 * k : w.Y;
+        GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
+        GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, pj, w.Bt, C, Yc, s));
+        if (store && !sym)
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, pi, w.Bt, C,
+                                  w.Yps + M * q0 * k, s));
+        profile_begin(kProfExchGemm, s);
+        GSDFT_BLAS(rocblas_dgemm_64(h, N_, T_, k, W * k, M, &one, C, k, Yc, W * k, &zero,
+                                    w.Dfull, k));
+        profile_end(kProfExchGemm, s);
+        k_exch_pack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, K2, sym ? 1 : 0, q0, N, G, w.Dfull,
+                                                         w.Dt);
+        GSDFT_HIP(hipGetLastError());
+    }
+    // Wt = Dt L^-T: chol is the row-major lower factor, i.e. the column-major upper L^T.
+    profile_begin(kProfExchTrsm, s);
+    GSDFT_BLAS(rocblas_dtrsm_64(h, rocblas_side_right, rocblas_fill_upper, N_,
+                                rocblas_diagonal_non_unit, K2, N, &one, chol, N, w.Dt, K2));
+    profile_end(kProfExchTrsm, s);
+    k_sumsq_part<<<kRedBlocks, 256, 0, s>>>(K2 * N, w.Dt, w.red);
+    GSDFT_HIP(hipGetLastError());
+    k_sum_scaled<<<1, 1024, 0, s>>>(kRedBlocks, w.red, -1.0, energy);
+    GSDFT_HIP(hipGetLastError());
+    if (!grads) return GSDFT_OK;
+
+    // Dbar_t = -2 Wt L^-1
+    profile_begin(kProfExchTrsm, s);
+    GSDFT_BLAS(rocblas_dtrsm_64(h, rocblas_side_right, rocblas_fill_upper, T_,
+                                rocblas_diagonal_non_unit, K2, N, &mtwo, chol, N, w.Dt, K2));
+    profile_end(kProfExchTrsm, s);
+    k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
+    GSDFT_HIP(hipGetLastError());
+    for (int64_t q0 = 0; q0 < N; q0 += Pc) {
+        const int64_t W = std::min(Pc, N - q0);
+        k_exch_unpack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, K2, sym ? 1 : 0, q0, N, G, w.Dt,
+                                                           w.Dfull, w.Ebar);
+        GSDFT_HIP(hipGetLastError());
+        const double* Yc = w.Y;
+        const double* Ypc = w.Yp;
+        if (store) {
+            Yc = w.Ys + M * q0 * k;
+            Ypc = sym ? nullptr : w.Yps + M * q0 * k;
+        } else {
+            GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, pj, w.Bt, C, w.Y, s));
+            if (!sym)
+                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, pi, w.Bt, C, w.Yp, s));
+        }
+        profile_begin(kProfExchGemm, s);
+        // dC += Y_P Dbar_P^T (+ Y'_P Dbar_P; the same term again on a symmetric list)
+        GSDFT_TRY(dc_gemm(h, k, M, W, sym ? 2.0 : 1.0, w.Dfull, Yc, w.part, dC, s));
+        if (!sym) GSDFT_TRY(dc_gemm(h, k, M, W, 1.0, w.Ebar, Ypc, w.part, dC, s));
+        // Ybar (Wk x M column-major, i.e. [i][l][o']) = Dbar^T C^T-view, into Y's buffer
+        GSDFT_BLAS(rocblas_dgemm_64(h, T_, N_, W * k, M, k, &one, w.Dfull, k, C, k, &zero, w.Y,
+                                    W * k));
+        profile_end(kProfExchGemm, s);
+        // Tbar (slot-major, ld Pc) into the block's buffer
+        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, pj, w.tc.inv_perm, w.Y, C, w.Bt,
+                               s));
+        GSDFT_TRY(exch_tc_reverse(N, q0, W, n, w.Bt, Pc, q0 == 0, w.tc, s));
+    }
+    GSDFT_TRY(exch_tc_finish(M, n, pi, pj, weight, quat, log_scale, centers, row_ptr, row_perm,
+                             col_ptr, col_perm, dquat, dlog_scale, dcenters, w.tc, s));
+    return GSDFT_OK;
+}

@@ -47,7 +47,9 @@ void profile_end(int id, hipStream_t s);
 unsigned long long* profile_work_counter(int id);
 enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMetric = 3,
                  kProfCholesky = 4, kProfSolve = 5, kProfNucPairs = 6, kProfNucAtoms = 7,
-                 kProfEriFwd = 8, kProfEriBwd = 9, kProfCount = 10 };
+                 kProfEriFwd = 8, kProfEriBwd = 9, kProfExchBlock = 10, kProfExchBwd = 11,
+                 kProfExchTrsm = 12, kProfExchGemm = 13, kProfExchSparse = 14,
+                 kProfCount = 15 };
 
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
@@ -77,6 +79,36 @@ int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOr
 
 // dfj.hip: the library's rocBLAS handle for the current device, bound to stream s.
 int blas_handle(hipStream_t s, struct _rocblas_handle** out);
+
+// dfj.hip: the three-centre passes of the screened exchange. Charts, aux quantities and pair
+// records (q_a = w_a) in list order; for the reverse also the slot order of the pairs, its
+// inverse, the aux records (u = KN_P, centre-grouped slots) and the moment accumulators.
+struct ExchTcWs {
+    double *A6, *Nrm, *beta, *kn, *q, *rec;
+    double *rec_sorted, *aux, *part, *acc, *J, *contrib;
+    int32_t* inv_perm;
+    PairOrderWs pair_order;
+};
+int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
+                   ExchTcWs* w);
+int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
+                     const double* centers, int64_t N, const double* log_alpha,
+                     const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
+                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s);
+// Bt[a * ldb + l] = (P|a) w_a for the aux of slots q0 .. q0 + W - 1 (slot order: the G = N / M
+// scales of one centre consecutive when N is a multiple of M, else aux order).
+int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
+                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
+// Adds (first: sets) the reverse moments of the aux slots q0 .. q0 + W - 1 with the cotangent
+// Tbar[slot * ldt + l] of (P_l|a_slot).
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* Tbar, int64_t ldt,
+                    bool first, const ExchTcWs& w, hipStream_t s);
+// Moments -> per-pair splat contributions -> dquat, dlog_scale, dcenters.
+int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                   const double* weight, const double* quat, const double* log_scale,
+                   const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
+                   const int32_t* col_ptr, const int32_t* col_perm, double* dquat,
+                   double* dlog_scale, double* dcenters, const ExchTcWs& w, hipStream_t s);
 
 // screen.hip
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,

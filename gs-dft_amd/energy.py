@@ -54,8 +54,10 @@ def train_pad_to(screen: Pairlist, n0: int, n_devices: int = 1) -> int:
 
 
 class SplatDFJ:
-    """E_J of a splat model through ``coulomb=df()`` (or ``exact()``) and
-    ``screen=pairlist(...)``."""
+    """The two-electron energy of a splat model through ``coulomb=df()`` (or ``exact()``) and
+    ``screen=pairlist(...)``: E_J, plus hf_coeff * E_K for a hybrid ``xc`` (an object with
+    ``exact_exchange_fraction`` or ``hf_coeff``; gs_dft/ks/energy.py:400-410 adds the same
+    term to the total)."""
 
     def __init__(self, *, coulomb: DFSpec | ExactSpec | None = None,
                  screen: Pairlist | None = None, xc=None, mesh=None):
@@ -71,6 +73,9 @@ class SplatDFJ:
         self.coulomb = _make_coulomb(spec, screened=True,
                                      a_x=hf_coeff(xc) if xc is not None else 0.0,
                                      skip_pad=bool(screen.skip_pad))
+        if screen.unique and self.coulomb.hf_coeff != 0.0:
+            raise ValueError("pairlist(unique=True) is PBE-class only: the screened RI-K "
+                             "contraction is not symmetric in the pair index")
         self.mesh = None
         self.cell_part = None
 
@@ -79,14 +84,20 @@ class SplatDFJ:
         if self.screen is not None and state.pairs is None:
             raise ValueError("this SplatKS screens: pass the refresh state "
                              "(state.pairs) -- see refresh(ks, basis).")
-        if isinstance(self.coulomb, ScreenedProductDFCoulomb) and state.aux is None:
-            raise ValueError("coulomb=df() needs the frozen product aux: "
-                             "pass the refresh state -- see refresh(ks, basis).")
+        if isinstance(self.coulomb, ScreenedProductDFCoulomb):
+            if state.aux is None:
+                raise ValueError("coulomb=df() needs the frozen product aux: "
+                                 "pass the refresh state -- see refresh(ks, basis).")
+            if self.coulomb.hf_coeff != 0.0 and state.aux_K is None:
+                raise ValueError("hybrid df() needs the K-aux: pass the refresh state "
+                                 "(state.aux_K) -- see refresh(ks, basis).")
 
     def __call__(self, model: SplatModel, state: SplatState | None = None) -> torch.Tensor:
         state = SplatState() if state is None else state
         self._check_state(state)
-        e_j, _e_k = self.coulomb.energy(model.basis, model.C, None, model.occupations, state)
+        e_j, e_k = self.coulomb.energy(model.basis, model.C, None, model.occupations, state)
+        if self.coulomb.hf_coeff != 0.0:
+            return e_j + self.coulomb.hf_coeff * e_k
         return e_j
 
 

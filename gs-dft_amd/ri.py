@@ -1,6 +1,7 @@
-"""Density-fitted Coulomb (RI-J) over the screened pair list, mirroring the DF-J half of
-gs_dft/coulomb/ri.py: the aux metric and its Cholesky factor, gamma = sum_a (P|a) q_a, and the
-robust-DF energy E_J = 1/2 gamma^T (V + lam I)^-1 gamma with a hand-written reverse pass.
+"""Density fitting over the screened pair list, mirroring gs_dft/coulomb/ri.py: the aux metric
+and its Cholesky factor, gamma = sum_a (P|a) q_a, the robust-DF energy
+E_J = 1/2 gamma^T (V + lam I)^-1 gamma, and the screened RI-K exchange energy, each with a
+hand-written reverse pass.
 
 Every value is computed by ``libgsdft``; torch autograd only routes cotangents. The aux and the
 metric factor are refresh products held constant, as the reference holds its ``SplatState``
@@ -21,8 +22,8 @@ def aux_metric(aux: IsotropicSplat, omega=None, *, lam: float = 0.0) -> torch.Te
     """V_PQ = (P|Q) (gs_dft/coulomb/ri.py:267-275); ``lam`` is added to the diagonal in the same
     kernel (the reference's ``shift_diag``)."""
     if omega:
-        raise NotImplementedError("aux_metric(omega=...): the range-separated metric belongs to "
-                                  "RI-K, which this library does not implement")
+        raise NotImplementedError("aux_metric(omega=...): the range-separated (erf) metric of "
+                                  "long-range exchange is not implemented")
     N = aux.n_basis
     dev = aux.log_alpha.device
     V = torch.empty((N, N), dtype=torch.float64, device=dev)
@@ -240,3 +241,122 @@ def coulomb_pairs(splats: Splat, C_occ, occ, aux: IsotropicSplat, pi, pj, lam: f
     gamma = _gamma_forward(x)
     d, _ = _cho_solve(L.detach().contiguous(), gamma, False)
     return _gamma_vjp(x, d, None)[0]
+
+
+# ------------------------------------------------------------------------------------ RI-K
+
+def _list_symmetric(M: int, pi: torch.Tensor, pj: torch.Tensor, w: torch.Tensor, n: int) -> bool:
+    """True when the live entries of the first ``n`` (weight 1) come in (i, j) / (j, i) pairs."""
+    if n == 0:
+        return True
+    live = w[:n] != 0
+    i, j = pi[:n][live].long(), pj[:n][live].long()
+    return bool(torch.equal(torch.sort(i * M + j).values, torch.sort(j * M + i).values))
+
+
+class _ExchangeInputs:
+    def __init__(self, splats: Splat, C_occ, aux: IsotropicSplat, pi, pj, valid, L, index,
+                 aux_chunk: int, recompute: bool):
+        dev = _lib.device()
+        self.M = splats.n_basis
+        self.quat, self.log_scale, self.centers = splats.quat, splats.log_scale, splats.centers
+        C = C_occ if isinstance(C_occ, torch.Tensor) else _lib.f64(C_occ, dev)
+        self.C = C.to(device=dev, dtype=torch.float64) if (C.device != dev or
+                                                           C.dtype != torch.float64) else C
+        if self.C.dim() != 2 or self.C.shape[0] != self.M or self.C.shape[1] == 0:
+            raise ValueError(f"C_occ must be (M, k) with M = {self.M} and k >= 1, got "
+                             f"{tuple(self.C.shape)}")
+        self.k = int(self.C.shape[1])
+        self.aux, self.N = aux, aux.n_basis
+        self.L = L.detach().contiguous()
+        if self.L.shape != (self.N, self.N):
+            raise ValueError(f"cholV must be ({self.N}, {self.N}), got {tuple(self.L.shape)}")
+        self.pi, self.pj = _lib.i32(pi, dev), _lib.i32(pj, dev)
+        n = self.pi.shape[0]
+        self.w = (torch.ones(n, dtype=torch.float64, device=dev) if valid is None
+                  else _lib.f64(valid, dev).reshape(-1))
+        if self.pj.shape[0] != n or self.w.shape[0] != n:
+            raise ValueError("pi, pj and valid must have the same length")
+        if n and not bool(torch.all((self.w == 0) | (self.w == 1))):
+            raise ValueError("RI-K reads valid as the 0/1 mask of the ordered pair list; "
+                             "unique-pair weights (pairlist(unique=True)) have no exchange "
+                             "path, as in gs_dft/ks/energy.py:240-241")
+        self.index = index if index is not None else build_pair_index(self.M, self.pi, self.pj,
+                                                                      self.w)
+        self.n = self.index.n_live
+        if index is None and self.n > 0:
+            lo = int(torch.minimum(self.pi[:self.n].min(), self.pj[:self.n].min()))
+            hi = int(torch.maximum(self.pi[:self.n].max(), self.pj[:self.n].max()))
+            if lo < 0 or hi >= self.M:
+                raise ValueError(f"pair indices must lie in [0, {self.M}), got [{lo}, {hi}]")
+        self.symmetric = _list_symmetric(self.M, self.pi, self.pj, self.w, self.n)
+        self.aux_chunk = int(aux_chunk)
+        self.recompute = int(bool(recompute))
+
+
+def _exchange(x: _ExchangeInputs, grads: bool):
+    """(E_K, dquat, dlog_scale, dcenters, dC) -- gradients None unless ``grads``."""
+    dev = x.C.device
+    M, k = x.M, x.k
+    Lb = _lib.lib()
+    ws = _lib.workspace(_lib.size_query(Lb.gsdft_exchange_workspace_size, M, k, x.N, x.n,
+                                        int(x.symmetric), int(grads), x.aux_chunk,
+                                        x.recompute), dev)
+    E = torch.empty((), dtype=torch.float64, device=dev)
+    out = [torch.empty(s, dtype=torch.float64, device=dev) if grads else None
+           for s in ((M, 4), (M, 3), (M, 3), (M, k))]
+    q, l, c, C = (t.detach().contiguous() for t in (x.quat, x.log_scale, x.centers, x.C))
+    idx = x.index
+    _lib.check(Lb.gsdft_exchange(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), k, _lib.ptr(C), x.N,
+                                 _lib.ptr(x.aux.log_alpha), _lib.ptr(x.aux.centers),
+                                 _lib.ptr(x.L), x.n, _lib.ptr(x.pi), _lib.ptr(x.pj),
+                                 _lib.ptr(x.w), _lib.ptr(idx.row_ptr), _lib.ptr(idx.row_perm),
+                                 _lib.ptr(idx.col_ptr), _lib.ptr(idx.col_perm),
+                                 int(x.symmetric), x.aux_chunk, x.recompute, _lib.ptr(E),
+                                 *[_lib.ptr(t) for t in out], _lib.ptr(ws), ws.numel(),
+                                 _lib.stream()), "df_exchange_energy_screened")
+    return (E, *out)
+
+
+class _ExchangeFn(torch.autograd.Function):
+    """E_K with its gradients formed in the same library call (the reverse needs the forward's
+    L^-1 D); backward scales them by the incoming cotangent."""
+
+    @staticmethod
+    def forward(ctx, quat, log_scale, centers, C, x):
+        grads = any(ctx.needs_input_grad[:4])
+        E, *g = _exchange(x, grads)
+        if grads:
+            ctx.save_for_backward(*g)
+        return E
+
+    @staticmethod
+    def backward(ctx, gE):
+        dq, dl, dc, dC = ctx.saved_tensors
+        return gE * dq, gE * dl, gE * dc, gE * dC, None
+
+
+def df_exchange_energy_screened(splats: Splat, C_occ, aux: IsotropicSplat, pi, pj,
+                                lam: float = 1e-8, chunk: int = 2048, valid=None,
+                                occ_chunk: int = 16, omega=None, *,
+                                cholV: torch.Tensor | None = None,
+                                index: PairIndex | None = None,
+                                aux_chunk: int = 0, recompute: bool = False) -> torch.Tensor:
+    """Screened RI-K exact-exchange energy E_K = -Tr((V + lam I)^-1 M),
+    M_PQ = sum_oo' D[P,o,o'] D[Q,o,o'], D[P,o,o'] = sum over the listed pairs (i, k) of
+    C_io C_ko' (P|ik) (gs_dft/coulomb/ri.py:497-544), differentiable w.r.t. the splat leaves and
+    C_occ (the aux is held constant).
+
+    ``valid`` is the 0/1 mask of the ordered pair list. ``chunk`` and ``occ_chunk`` bounded the
+    reference's memory and do not change its value; ``aux_chunk`` (aux functions per pass,
+    0 = automatic) and ``recompute`` (recompute the forward's (M, N, k) products in the reverse
+    instead of keeping them) are this library's memory knobs, likewise without effect on the
+    value. ``cholV`` = the Cholesky factor of V + lam I for this ``aux`` (built here when
+    absent)."""
+    del chunk, occ_chunk
+    if omega:
+        raise NotImplementedError("df_exchange_energy_screened(omega=...): the range-separated "
+                                  "(long-range erf) exchange is not implemented")
+    L = aux_cholesky(aux, lam) if cholV is None else cholV
+    x = _ExchangeInputs(splats, C_occ, aux, pi, pj, valid, L, index, aux_chunk, recompute)
+    return _ExchangeFn.apply(x.quat, x.log_scale, x.centers, x.C, x)

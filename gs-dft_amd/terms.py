@@ -1,4 +1,4 @@
-"""The Coulomb plugin surface of the screened paths, mirroring gs_dft/ks/terms.py.
+"""The Coulomb / exchange plugin surface of the screened paths, mirroring gs_dft/ks/terms.py.
 
 ``df()``, ``exact()`` and ``pairlist()`` build the same frozen spec values as the reference
 (terms.py:58-139) and ``_make_coulomb`` resolves ``df()`` + ``screen=pairlist(...)`` to
@@ -86,7 +86,9 @@ class CoulombTerm(abc.ABC):
 
 @dataclass(frozen=True)
 class ScreenedProductDFCoulomb(CoulombTerm):
-    """Frozen pair-product RI-J over the significant pairs (gs_dft/ks/terms.py:236-256)."""
+    """Frozen pair-product RI-J / RI-K over the significant pairs (gs_dft/ks/terms.py:236-264).
+    E_K (unscaled) is evaluated when ``hf_coeff`` != 0, on the K-aux ``state.aux_K``; the
+    long-range (erf) exchange of range-separated hybrids is not implemented."""
 
     hf_coeff: float = 0.0
     hf_coeff_lr: float = 0.0
@@ -104,9 +106,20 @@ class ScreenedProductDFCoulomb(CoulombTerm):
                                               cholV=state.cholV, skip_pad=self.skip_pad,
                                               index=getattr(state, "pair_index", None))
         if self.hf_coeff != 0.0:
-            raise NotImplementedError("screened RI-K (hybrid exchange) is not part of this "
-                                      "library; use a pure functional (hf_coeff = 0)")
-        return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
+            same = state.aux_K is state.aux
+            e_k = _cdf.df_exchange_energy_screened(
+                basis, C_orth, state.aux_K, pi, pj, lam=self.lam, chunk=self.chunk, valid=valid,
+                cholV=state.cholV if same else None,
+                index=getattr(state, "pair_index", None))
+        else:
+            e_k = torch.zeros((), dtype=torch.float64, device=e_j.device)
+        return e_j, e_k
+
+    def energy_lr(self, basis, C_orth, P, occ, state):
+        if self.hf_coeff_lr == 0.0:
+            return torch.zeros((), dtype=torch.float64, device=C_orth.device)
+        raise NotImplementedError("the long-range (erf) screened exchange of range-separated "
+                                  "hybrids (gs_dft/ks/terms.py:258-264) is not implemented")
 
 
 @dataclass(frozen=True)
@@ -139,9 +152,9 @@ def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
         if not screened:
             raise NotImplementedError("dense (unscreened) DF is not part of this library; pass "
                                       "screen=pairlist(eps=-1.0) for the full pair list")
-        if a_x != 0.0 or a_x_lr != 0.0:
-            raise NotImplementedError("screened RI-K (hybrid exchange) is not part of this "
-                                      "library; use a pure functional")
+        if a_x_lr != 0.0:
+            raise NotImplementedError("range-separated hybrids (hf_coeff_lr != 0) need the "
+                                      "long-range erf exchange, which is not implemented")
         return ScreenedProductDFCoulomb(hf_coeff=a_x, hf_coeff_lr=a_x_lr, omega=omega,
                                         lam=spec.lam, chunk=spec.chunk, scales=spec.scales,
                                         diagonal=spec.diagonal, skip_pad=bool(skip_pad))

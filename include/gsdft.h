@@ -204,13 +204,44 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
                            double* dquat, double* dlog_scale, double* dcenters, double* dC,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* Screened exact exchange through density fitting (RI-K): E_K = -Tr((V + lam I)^-1 M) with
+ * M_PQ = sum_oo' D[P,o,o'] D[Q,o,o'] and D[P,o,o'] = sum over the first n listed pairs
+ * a = (pi[a], pj[a]) of weight[a] C_io C_ko' (P|a) (weight null: all 1; the list is the ordered
+ * one, weights 0/1). Replaces gs_dft/coulomb/ri.py:497-544 (df_exchange_energy_screened and
+ * _exchange_M_streamed_screened) as called from gs_dft/ks/terms.py:250-253 with the frozen
+ * product aux (N functions: log_alpha, aux_centers) and chol = the row-major lower Cholesky factor
+ * of V + lam I (gsdft_cholesky). C is the (M, k) occupied block (occupation 2 folded into the
+ * prefactor, as in the reference). row_ptr/row_perm (and col_ptr/col_perm for gradients) are the
+ * CSR index of the list (gsdft_pair_index). symmetric = 1 asserts that every live entry (i, j, w)
+ * has its (j, i, w): D_P is then symmetric and only its k(k+1)/2 symmetric columns are solved
+ * (the antisymmetric part is round-off); with 0 all k^2 columns are kept. aux_chunk = aux
+ * functions per pass (0: the library's choice; the result does not depend on it beyond
+ * round-off). With gradients the forward keeps its (M, N, k) products for the reverse when they
+ * fit in 32 GiB; recompute = 1 forgoes that and recomputes them (less memory, more time), the
+ * role the reference's occ_chunk knob plays for its memory. Writes energy (one device double);
+ * with non-null dquat also dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
+int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, int symmetric,
+                                  int grads, int64_t aux_chunk, int recompute, size_t* bytes);
+int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                   int64_t k, const double* C, int64_t N, const double* log_alpha,
+                   const double* aux_centers, const double* chol, int64_t n, const int32_t* pi,
+                   const int32_t* pj, const double* weight, const int32_t* row_ptr,
+                   const int32_t* row_perm, const int32_t* col_ptr, const int32_t* col_perm,
+                   int symmetric, int64_t aux_chunk, int recompute, double* energy,
+                   double* dquat,
+                   double* dlog_scale, double* dcenters, double* dC, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
  * 6 nuclear attraction per pair (values and splat moments), 7 nuclear attraction per nucleus
  * (nuclear gradient), 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and
- * gradient moments). gsdft_profile_read synchronises the recorded events and returns the summed
- * milliseconds and the launch count since the last reset. gsdft_profile_read_work returns the
- * work units the kernels executed while profiling was on (ids 0, 1, 6-9: quadrature nodes
+ * gradient moments), 10 exchange three-centre block, 11 exchange three-centre reverse, 12
+ * exchange triangular solves (rocBLAS), 13 exchange GEMMs (rocBLAS), 14 exchange pair-sparse
+ * products (Y = T C and the sampled Tbar). gsdft_profile_read
+ * synchronises the recorded events and returns the summed milliseconds and the launch count since
+ * the last reset. gsdft_profile_read_work returns the
+ * work units the kernels executed while profiling was on (ids 0, 1, 6-11: quadrature nodes
  * evaluated, summed over live lanes, so at most 20 x (aux functions, nuclei or pairs) x pairs
  * per launch; other ids: 0). Profiling allocates a few bytes of
  * device memory on the device current when it is first enabled. */

@@ -285,5 +285,20 @@ def exact_coulomb(quat, log_scale, centers, C, occ, pi, pj, weight):
     return float(E), J
 
 
+def exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers, pi, pj, valid, lam):
+    """Screened RI-K energy following gs_dft/coulomb/ri.py:497-544:
+    D[P,o,o'] = sum over the valid listed pairs (i, k) of C_io C_ko' (P|ik) (``valid`` read as a
+    mask, ri.py:529), M = sum_oo' D[P,o,o'] D[Q,o,o'] (ri.py:532), and
+    E_K = -tr(solve(V + lam I, M)) with a dense solve (ri.py:544). Returns (E_K, D)."""
+    C = _f64(C)
+    pi_, pj_ = np.asarray(pi, dtype=np.int64), np.asarray(pj, dtype=np.int64)
+    B = three_center_block(quat, log_scale, centers, log_alpha, aux_centers, pi, pj)
+    m = (np.asarray(valid) != 0).astype(np.float64)
+    D = np.einsum("Ap,po,pq->Aoq", B, C[pi_] * m[:, None], C[pj_], optimize=True)
+    Mmat = np.einsum("Aoq,Boq->AB", D, D, optimize=True)
+    V = aux_metric(log_alpha, aux_centers, lam)
+    return -float(np.trace(np.linalg.solve(V, Mmat))), D
+
+
 def set_threads(n: int) -> None:
     os.environ["OMP_NUM_THREADS"] = str(int(n))

@@ -189,6 +189,30 @@ def gamma_screened(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi,
     return gamma
 
 
+def screened_exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers, pi, pj, valid,
+                             lam, chunk=2048, occ_chunk=16, table=None):
+    """gs_dft/coulomb/ri.py:497-544 as written: per occupied chunk, the pair stream builds
+    D[:, chunk, :] (ri.py:524-531) and M += D D^T (ri.py:532); E_K = -tr(solve(V + lam I, M)).
+    ``table`` replaces the 20-node rule of the three-centre block (for limit checks)."""
+    A, N = splat_A(quat, log_scale), splat_norm(log_scale)
+    aux_q = aux_quantities(log_alpha, aux_centers)
+    Na, n_occ, n = log_alpha.shape[0], C.shape[1], pi.shape[0]
+    mask = valid != 0
+    Mmat = torch.zeros((Na, Na), dtype=torch.float64)
+    for o0 in range(0, n_occ, occ_chunk):
+        o1 = min(n_occ, o0 + occ_chunk)
+        D = torch.zeros((Na, o1 - o0, n_occ), dtype=torch.float64)
+        for s in range(0, n, chunk):
+            ci, cj, cv = pi[s:s + chunk], pj[s:s + chunk], mask[s:s + chunk]
+            block = full_isobra_block(*aux_q, *full_pair_quantities(A, centers, N, ci, cj), table)
+            Ci = torch.where(cv[:, None], C[ci][:, o0:o1], torch.zeros((), dtype=torch.float64))
+            D = D + torch.einsum("Ap,po,pq->Aoq", block, Ci, C[cj])
+        Mmat = Mmat + torch.einsum("Aoq,Boq->AB", D, D)
+    V = aux_metric(log_alpha, aux_centers)
+    Vs = V + lam * torch.eye(Na, dtype=torch.float64)
+    return -torch.trace(torch.linalg.solve(Vs, Mmat))
+
+
 def coulomb_solve(gamma, L):
     """gs_dft/coulomb/ri.py:479 -- 0.5 gamma^T cho_solve((L, lower), gamma)."""
     d = torch.cholesky_solve(gamma[:, None], L, upper=False)[:, 0]

@@ -70,3 +70,9 @@ def test_workspace_queries_accept_empty_inputs(built):
                      (lib.gsdft_external_workspace_size, (4, 1, 10, 0))):
         rc = fn(*args, ctypes.byref(out))
         assert rc in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)
+    for sym in (0, 1):
+        for grads in (0, 1):
+            for n in (0, 100):
+                rc = lib.gsdft_exchange_workspace_size(4, 2, 8, n, sym, grads, 0, 0,
+                                                       ctypes.byref(out))
+                assert rc in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)

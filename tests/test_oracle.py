@@ -662,6 +662,143 @@ def test_exact_coulomb_invariances_and_autograd(orc, tr, wl):
             assert abs(fd - args[k].grad[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
 
 
+# ----------------------------------------------------------------------------- screened RI-K
+
+def _exch_system(wl, orc, M=14, k=3, seed=11, eps=1e-7, n_atoms=3):
+    s = wl.make_small(M, k, n_atoms=n_atoms, seed=seed)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, None, False)
+    return s, la, ac, pi, pj, w
+
+
+def test_exchange_single_orbital_is_minus_twice_dfj(orc, wl):
+    """k = 1: D_P = gamma_P at occupation 1, so E_K = -gamma^T (V + lam I)^-1 gamma = -2 E_J^DF on
+    the same list -- the RI-K chain against the DF-J chain, which is pinned on its own above."""
+    for seed in (11, 12):
+        s, la, ac, pi, pj, w = _exch_system(wl, orc, seed=seed)
+        C1 = s.C[:, :1]
+        EK, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, C1, la, ac, pi, pj, w, 1e-8)
+        EJ = orc.dfj_energy(s.quat, s.log_scale, s.centers, C1, np.ones(1), la, ac, pi, pj, w,
+                            1e-8)[0]
+        assert EK < 0 and abs(EK + 2 * EJ) < 1e-11 * abs(EK)
+
+
+def test_exchange_invariant_under_occupied_rotations(orc, wl):
+    """E_K of a closed-shell determinant depends on span(C) only: E_K(C U) = E_K(C) for orthogonal
+    U (a contraction that pairs o with itself, or drops the o != o' terms, is not invariant)."""
+    s, la, ac, pi, pj, w = _exch_system(wl, orc, k=4, seed=13)
+    U, _ = np.linalg.qr(np.random.default_rng(5).normal(size=(4, 4)))
+    E1, D1 = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, w, 1e-8)
+    E2, D2 = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C @ U, la, ac, pi, pj, w, 1e-8)
+    assert abs(E1 - E2) < 1e-12 * abs(E1)
+    # and D transforms as U^T D_P U
+    assert rel_max(np.einsum("ao,Pab,bq->Poq", U, D1, U), D2) < 1e-12
+
+
+def test_exchange_equals_density_matrix_form(orc, wl):
+    """Full ordered list: the occupied form equals the density-matrix form the reference gives
+    for SCF use (gs_dft/coulomb/ri.py:384-405), E_K = -1/4 sum_PQ (V + lam I)^-1_PQ Tr(Y_Q Y_P)
+    with Y_P = T_P P, P = 2 C C^T, T_P[i, k] = (P|ik): a different contraction order that a
+    transposed or self-paired index would break."""
+    M, k = 10, 3
+    s = wl.make_small(M, k, n_atoms=2, seed=17)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj = np.repeat(np.arange(M), M), np.tile(np.arange(M), M)
+    w = np.ones(M * M)
+    E, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, w, 1e-8)
+    T = orc.three_center_block(s.quat, s.log_scale, s.centers, la, ac, pi, pj).reshape(-1, M, M)
+    P = 2.0 * s.C @ s.C.T
+    Y = np.einsum("Ppr,rs->Pps", T, P)
+    Wm = np.einsum("Pba,Qab->PQ", Y, Y)
+    Ed = -0.25 * np.trace(np.linalg.solve(orc.aux_metric(la, ac, 1e-8), Wm))
+    assert abs(E - Ed) < 1e-11 * abs(E)
+
+
+def test_exchange_mask_drops_entries_and_padding(orc, wl):
+    """valid is a mask (gs_dft/coulomb/ri.py:529): zero entries add nothing, so deleting them or
+    appending zero-weight padding leaves E_K unchanged to the bit of the einsum order."""
+    s, la, ac, pi, pj, w = _exch_system(wl, orc, seed=19)
+    rng = np.random.default_rng(3)
+    wm = w * (rng.uniform(size=w.shape) > 0.2)
+    E1, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, wm, 1e-8)
+    keep = wm != 0
+    E2, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi[keep], pj[keep],
+                                wm[keep], 1e-8)
+    pp = np.concatenate([pi[keep], np.zeros(7, np.int32)])
+    qp = np.concatenate([pj[keep], np.zeros(7, np.int32)])
+    E3, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pp, qp,
+                                np.concatenate([wm[keep], np.zeros(7)]), 1e-8)
+    assert abs(E1 - E2) < 1e-13 * abs(E1) and abs(E2 - E3) < 1e-13 * abs(E2)
+
+
+def test_exchange_literal_restatement_matches_oracle(orc, tr, wl):
+    """The C-integral oracle against the torch line-by-line form (eigh three-centre block,
+    occupied-chunk stream with occ_chunk smaller than k)."""
+    s, la, ac, pi, pj, w = _exch_system(wl, orc, k=5, seed=23)
+    wm = w * (np.random.default_rng(4).uniform(size=w.shape) > 0.1)
+    E, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, wm, 1e-8)
+    Et = tr.screened_exchange_energy(_t(s.quat), _t(s.log_scale), _t(s.centers), _t(s.C), _t(la),
+                                     _t(ac), _idx(pi), _idx(pj), _t(wm), 1e-8, chunk=64,
+                                     occ_chunk=2).item()
+    assert abs(E - Et) < 1e-12 * abs(E)
+
+
+def test_exchange_is_exact_when_the_aux_spans_the_products(tr):
+    """Isotropic splats far apart, one orbital, aux = the self-products at scale 1: every listed
+    product g_i g_i is an aux function up to its norm, so the fit is exact and (with lam = 0)
+    E_K = -sum_ij C_i^2 C_j^2 (ii|jj), the closed-form Gaussian Coulomb integral. A 400-node rule
+    takes the three-centre quadrature error out; the metric is closed-form already."""
+    rng = np.random.default_rng(41)
+    M = 3
+    alpha = np.exp(rng.uniform(-0.5, 0.5, M))
+    quat = rng.normal(size=(M, 4))
+    ls = np.repeat(np.log(alpha)[:, None], 3, 1)
+    mu = np.array([[0.0, 0.0, 0.0], [30.0, 0.0, 0.0], [0.0, 40.0, 0.0]])
+    C = rng.normal(size=(M, 1))
+    la = np.log(2.0 * alpha)                  # det(A_i + A_i)^(1/3) = 2 alpha_i
+    pi = pj = np.arange(M)
+    x, wl_ = np.polynomial.legendre.leggauss(400)
+    sgl = (x + 1) / 2
+    table = ([float(v) for v in sgl / (1 - sgl)], [float(v) for v in (wl_ / 2) / (1 - sgl) ** 2])
+    E = tr.screened_exchange_energy(_t(quat), _t(ls), _t(mu), _t(C), _t(la), _t(mu), _idx(pi),
+                                    _idx(pj), _t(np.ones(M)), 0.0, table=table).item()
+    A, N = tr.splat_A(_t(quat), _t(ls)), tr.splat_norm(_t(ls))
+    _, _, KN = tr.full_pair_quantities(A, _t(mu), N, _idx(pi), _idx(pj))
+    KN = KN.numpy()
+    p = 2.0 * alpha
+    ref = 0.0
+    for a in range(M):
+        for b in range(M):
+            rho = p[a] * p[b] / (p[a] + p[b])
+            T = rho * np.sum((mu[a] - mu[b]) ** 2)
+            F0 = 0.5 * math.sqrt(math.pi / T) * erf(math.sqrt(T)) if T > 1e-12 else 1.0 - T / 3
+            eri = KN[a] * KN[b] * 2 * math.pi ** 2.5 / (p[a] * p[b] * math.sqrt(p[a] + p[b])) * F0
+            ref -= C[a, 0] ** 2 * C[b, 0] ** 2 * eri
+    assert abs(E - ref) < 1e-10 * abs(ref)
+
+
+def test_exchange_autograd_matches_finite_differences(orc, tr, wl):
+    """Autograd of the literal form against central differences of the oracle."""
+    s, la, ac, pi, pj, w = _exch_system(wl, orc, M=12, k=3, seed=29)
+    args = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*args, _t(la), _t(ac), _idx(pi), _idx(pj), _t(w), 1e-8)
+    Et.backward()
+    h = 1e-5
+    base = dict(quat=s.quat, log_scale=s.log_scale, centers=s.centers, C=s.C)
+    for k, name in enumerate(("quat", "log_scale", "centers", "C")):
+        arr = base[name]
+        for idx in [(0, 0), (arr.shape[0] - 1, 1), (5, 2)]:
+            vals = []
+            for sgn in (1, -1):
+                v = dict(base)
+                v[name] = arr.copy()
+                v[name][idx] += sgn * h
+                vals.append(orc.exchange_energy(v["quat"], v["log_scale"], v["centers"], v["C"],
+                                                la, ac, pi, pj, w, 1e-8)[0])
+            fd = (vals[0] - vals[1]) / (2 * h)
+            assert abs(fd - args[k].grad[idx].item()) < 1e-6 * max(1.0, abs(fd)), (name, idx)
+
+
 # ----------------------------------------------------------------------------- density on a grid
 
 def test_grid_density_integrates_to_the_orbital_overlaps(orc, tr, wl):
