@@ -593,7 +593,8 @@ def run_exchange(args) -> int:
     fams = [("three-centre block (k_exch_block)", blk_ms, integrals * FLOPS_FWD, "valu"),
             ("three-centre reverse (k_gamma_bwd, per-(P,a) cotangent)", rev_ms,
              integrals * FLOPS_BWD, "valu"),
-            ("pair-sparse products (k_exch_spmm, k_exch_sddmm)", sparse_ms, sparse, "valu"),
+            ("pair-sparse products (k_exch_spmm, k_exch_sddmm; FP64 MFMA)", sparse_ms, sparse,
+             "mfma"),
             ("FP64 GEMMs (rocBLAS dgemm)", gemm_ms, gemm_fwd + gemm_bwd, "mfma"),
             ("triangular solves (rocBLAS dtrsm)", trsm_ms, 2 * trsm, "mfma")]
     dom = max(fams, key=lambda f: f[1])

@@ -1092,7 +1092,8 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
 // Bt[a * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and every pair a in list
 // order, the pair record carrying q_a = w_a: the screened block of RI-K
 // (gs_dft/coulomb/ri.py:527-531, full_isobra_block), written rather than contracted. One lane per
-// aux slot, the pair records of a slab wave-uniform, as in k_gamma_fwd; each (a, l) is written once.
+// aux slot, the pair records of a slab wave-uniform, as in k_gamma_fwd; each (a, l) is written once
+// (consecutive lanes write consecutive columns).
 __global__ __launch_bounds__(256) void k_exch_block(int64_t N, int64_t G, int64_t q0, int64_t W,
                                                     const double* __restrict__ beta,
                                                     const double* __restrict__ R,

@@ -10,8 +10,8 @@
 //
 // Forward, per chunk of W aux functions (centre-grouped slot order):
 //   Bt (n x W)          the screened three-centre block (k_exch_block, dfj.hip)
-//   Y[i][l][o']         = sum over pairs a of row i of Bt[a][l] C[k_a][o']     (k_exch_spmm, a
-//                         lane per aux, a wave per range of orbitals held in registers)
+//   Y[i][l][o']         = sum over pairs a of row i of Bt[a][l] C[k_a][o']     (k_exch_spmm, FP64
+//                         MFMA over the row's block columns and gathered C rows)
 //   D_P = C^T Y_P       one FP64 GEMM per chunk: k x (W k) x M
 //   Dt[:, P]            packed columns of D_P                                    (k_exch_pack)
 // then Wt = Dt L^-T (rocBLAS trsm over the packed-column right-hand sides) and E_K = -sum Wt^2.
@@ -19,7 +19,7 @@
 // with the forward's Y (and Y') kept in the workspace when they fit, else recomputed,
 //   dC    += Y_P Dbar_P^T + Y'_P Dbar_P      Y'[m][l][o] = sum over pairs a of column m of
 //                                            Bt[a][l] C[i_a][o] (= Y on a symmetric list)
-//   Ybar_P = C Dbar_P,   Tbar[a][l] = Ybar[i_a][l] . C[k_a]                   (k_exch_sddmm)
+//   Ybar_P = C Dbar_P,   Tbar[a][l] = Ybar[i_a][l] . C[k_a]            (k_exch_sddmm, FP64 MFMA)
 //   and the three-centre reverse with the per-(P, a) cotangent Tbar (dfj.hip) for the splat
 //   gradients. Every sum runs in a fixed order (no atomics; rocBLAS runs with atomics off).
 #include <rocblas/rocblas.h>
@@ -48,55 +48,108 @@ constexpr double kChunkBytes = 8.0 * 1024 * 1024 * 1024;   // per-chunk buffers 
 constexpr double kStoreBytes = 32.0 * 1024 * 1024 * 1024;   // Y (and Y') kept for the reverse
 constexpr int64_t kSplitMax = 32;                           // K slices of the dC GEMM
 
-// Y[i][l][o] = sum_{r in [ptr[i], ptr[i+1])} Bt[perm[r] * ldb + l] C[partner[perm[r]] * k + o] for
-// l < W, o < k. Grid (rows, ceil(W / 64), ceil(k / (4 ON))), 4 waves: lane = aux l, wave w owns the
-// ON orbitals o0 .. o0 + ON - 1 in registers. Per pair the lane reads one Bt entry (coalesced over
-// the wave) and the wave reads the pair's C row segment with wave-uniform (scalar) loads, so each
-// pair costs ON FMAs per lane.
-template <int ON>
-__global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t ldb,
+// FP64 MFMA v_mfma_f64_16x16x4f64, D (16 x 16) += A (16 x 4) B (4 x 16), one wave: lane l supplies
+// A[l % 16][l / 16] and B[l / 16][l % 16] and holds D[l / 16 + 4 r][l % 16] in its register r
+// (checked with a one-wave probe of known operands on MI355X).
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4d mfma16x16x4(double a, double b, v4d c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+constexpr int kColPad = 16;     // entries of the per-position partner arrays past n (splat 0)
+constexpr int kMfAux = 32;      // aux per wave (two 16-row tiles)
+constexpr int kMfOrb = 96;      // orbitals per wave in the Y product (six 16-column tiles)
+constexpr int kMfK = 96;        // orbitals held in registers per pass of the Tbar product
+inline int64_t padded_cols(int64_t k) { return (k + 15) / 16 * 16; }
+
+// Y[i][l][o] = sum_{r in [ptr[i], ptr[i+1])} Bt[perm[r] * ldb + l] C[col[r] * k + o] for l < W,
+// o < k (col[r] = the partner splat of CSR position r), with C read from Cp, its rows padded to
+// kp = 16 ceil(k / 16) columns (zeros). Per row i this is the product of the row's block columns
+// (W x deg) and its gathered C rows (deg x kp): grid (rows, ceil(W / (4 kMfAux)), column
+// blocks), 4 waves, each wave a 32 x 16 NT tile of Y_i in 2 NT MFMA accumulators (NT = 6 for the
+// full 96-column blocks, the remainder in one more launch), K = 4
+// pairs per step (A: the Bt entries, one 128-byte row segment per quarter-wave; B: the C row
+// segments of the same 4 pairs), the next step's operands loaded before the current step's MFMAs.
+template <int NT>
+__global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t kp, int64_t ldb,
+                                                   int64_t obase,
                                                    const int32_t* __restrict__ ptr,
                                                    const int32_t* __restrict__ perm,
-                                                   const int32_t* __restrict__ partner,
+                                                   const int32_t* __restrict__ col,
                                                    const double* __restrict__ Bt,
-                                                   const double* __restrict__ C,
+                                                   const double* __restrict__ Cp,
                                                    double* __restrict__ Y) {
     const int64_t i = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t l = (int64_t)blockIdx.y * 64 + lane;
-    const int64_t o0 = ((int64_t)blockIdx.z * 4 + wave) * ON;
-    if (o0 >= k) return;                                   // wave-uniform
-    const int on = (int)std::min<int64_t>(ON, k - o0);
-    const bool live = l < W;
-    const int64_t lc = live ? l : 0;
-    double acc[ON];
+    const int wave = threadIdx.x >> 6;
+    const int kq = lane >> 4, c16 = lane & 15;
+    const int64_t lw = (int64_t)blockIdx.y * (4 * kMfAux) + (int64_t)wave * kMfAux;
+    const int64_t ob = obase + (int64_t)blockIdx.z * (16 * NT);
+    v4d acc[2][NT];
 #pragma unroll
-    for (int j = 0; j < ON; ++j) acc[j] = 0.0;
+    for (int ta = 0; ta < 2; ++ta)
+#pragma unroll
+        for (int to = 0; to < NT; ++to) acc[ta][to] = v4d{0.0, 0.0, 0.0, 0.0};
     const int64_t r0 = ptr[i], r1 = ptr[i + 1];
-    if (on == ON) {
-        for (int64_t r = r0; r < r1; ++r) {
-            const int64_t a = perm[r];
-            const double b = Bt[a * ldb + lc];
-            const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
+    // operands of the K step at rb (the 4 pairs rb .. rb + 3), loaded one step ahead
+    double av[2], bv[NT];
+    auto load = [&](int64_t rb) {
+        const bool has = rb + kq < r1;
+        const int64_t a = perm[has ? rb + kq : r0];
+        const int64_t cr = col[rb + kq];                  // padded past n
 #pragma unroll
-            for (int j = 0; j < ON; ++j) acc[j] = __builtin_fma(b, crow[j], acc[j]);
+        for (int ta = 0; ta < 2; ++ta) {
+            const int64_t l = lw + ta * 16 + c16;
+            av[ta] = (has && l < W) ? Bt[a * ldb + l] : 0.0;
         }
-    } else {
-        for (int64_t r = r0; r < r1; ++r) {
-            const int64_t a = perm[r];
-            const double b = Bt[a * ldb + lc];
-            const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
 #pragma unroll
-            for (int j = 0; j < ON; ++j)
-                if (j < on) acc[j] = __builtin_fma(b, crow[j], acc[j]);
+        for (int to = 0; to < NT; ++to) bv[to] = Cp[cr * kp + ob + to * 16 + c16];
+    };
+    if (r0 < r1) load(r0);
+    for (int64_t rb = r0; rb < r1; rb += 4) {
+        double ac[2], bc[NT];
+#pragma unroll
+        for (int ta = 0; ta < 2; ++ta) ac[ta] = av[ta];
+#pragma unroll
+        for (int to = 0; to < NT; ++to) bc[to] = bv[to];
+        if (rb + 4 < r1) load(rb + 4);
+#pragma unroll
+        for (int to = 0; to < NT; ++to) {
+            acc[0][to] = mfma16x16x4(ac[0], bc[to], acc[0][to]);
+            acc[1][to] = mfma16x16x4(ac[1], bc[to], acc[1][to]);
         }
     }
-    if (!live) return;
-    double* __restrict__ out = Y + i * (W * k) + l * k + o0;
+    const int64_t Wk = W * k;
 #pragma unroll
-    for (int j = 0; j < ON; ++j)
-        if (j < on) out[j] = acc[j];
+    for (int ta = 0; ta < 2; ++ta)
+#pragma unroll
+        for (int to = 0; to < NT; ++to) {
+            const int64_t o = ob + to * 16 + c16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t l = lw + ta * 16 + kq + 4 * r;
+                if (l < W && o < k) Y[i * Wk + l * k + o] = acc[ta][to][r];
+            }
+        }
+}
+
+// Cp[m][j] = C[m][j] for j < k, 0 for k <= j < kp.
+__global__ void k_pad_cols(int64_t M, int64_t k, int64_t kp, const double* __restrict__ C,
+                           double* __restrict__ Cp) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= M * kp) return;
+    const int64_t m = t / kp, j = t - m * kp;
+    Cp[t] = j < k ? C[m * k + j] : 0.0;
+}
+
+// col[r] = partner[perm[r]]: the partner splat of every CSR position, and splat 0 in the
+// kColPad padding entries after position n (read, never used, by the last pair tile).
+__global__ void k_csr_partner(int64_t n, const int32_t* __restrict__ perm,
+                              const int32_t* __restrict__ partner, int32_t* __restrict__ col) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r < n) col[r] = partner[perm[r]];
+    else if (r < n + kColPad) col[r] = 0;
 }
 
 // Packed columns of D_P (P the aux of slot q0 + l): Dfull[o + k (l k + o')] = D_P[o][o'];
@@ -148,63 +201,61 @@ __global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t
     if (E) E[op + k * (l * k + o)] = v;
 }
 
-// Tbar[inv[a] * ldt + l] = sum_o Ybar[i][l][o] C[k_a][o] for the pairs a of row i and l < W.
-// Grid (rows, ceil(W / 64)), 4 waves: lane = aux l; per pass of 4 ON orbitals wave w holds
-// Ybar[i][l][o0 .. o0 + ON - 1] in registers and forms, for 16 pairs at a time (their C row
-// segments wave-uniform), its partial dot products into LDS; the four partials of a pair are then
-// summed in wave order and added to Tbar (set on the first pass). Passes run in order inside the
-// block, so every sum has a fixed order.
-constexpr int kPairGroup = 16;
-template <int ON>
-__global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_t ldt,
+// Tbar[inv[a] * ldt + l] = sum_o Ybar[i][l][o] C[k_a][o] for the pairs a of row i and l < W
+// (k_a = col[r] for the CSR position r of a; C read from the padded Cp). Per row i this is the
+// product Ybar_i (W x kp) Cg^T (kp x deg) sampled at the row's pairs: grid (rows,
+// ceil(W / (4 kMfAux))), 4 waves, each wave 32 aux x 16 pairs per MFMA pair tile, K = 4 orbitals
+// per step. Per pass of 4 NS orbitals (NS = kMfK / 4 for the full passes, the remainder in one
+// more launch) the wave holds its Ybar block in registers and walks the row's pair tiles; a pass
+// after the first adds to Tbar (same lane, passes in order), so every sum has a fixed order.
+template <int NS>
+__global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_t kp, int64_t ldt,
+                                                    int64_t oc_begin, int64_t oc_end, int first,
                                                     const int32_t* __restrict__ ptr,
                                                     const int32_t* __restrict__ perm,
-                                                    const int32_t* __restrict__ partner,
+                                                    const int32_t* __restrict__ col,
                                                     const int32_t* __restrict__ inv,
                                                     const double* __restrict__ Ybar,
-                                                    const double* __restrict__ C,
+                                                    const double* __restrict__ Cp,
                                                     double* __restrict__ Tbar) {
-    __shared__ double part[4][kPairGroup][64];
     const int64_t i = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t l = (int64_t)blockIdx.y * 64 + lane;
-    const bool live = l < W;
-    const int64_t lc = live ? l : 0;
+    const int wave = threadIdx.x >> 6;
+    const int kq = lane >> 4, c16 = lane & 15;
+    const int64_t lw = (int64_t)blockIdx.y * (4 * kMfAux) + (int64_t)wave * kMfAux;
     const int64_t Wk = W * k;
     const int64_t r0 = ptr[i], r1 = ptr[i + 1];
-    for (int64_t ob = 0; ob < k; ob += 4 * ON) {
-        const int64_t o0 = ob + (int64_t)wave * ON;
-        const int on = (int)std::max<int64_t>(0, std::min<int64_t>(ON, k - o0));
-        double y[ON];
+    for (int64_t oc = oc_begin; oc < oc_end; oc += 4 * NS) {
+        const bool store = first && oc == oc_begin;
+        double ya[2][NS];
 #pragma unroll
-        for (int j = 0; j < ON; ++j) y[j] = (j < on) ? Ybar[i * Wk + lc * k + o0 + j] : 0.0;
-        for (int64_t rb = r0; rb < r1; rb += kPairGroup) {
-            const int nr = (int)std::min<int64_t>(kPairGroup, r1 - rb);
-            for (int q = 0; q < nr; ++q) {
-                const int64_t a = perm[rb + q];
-                const double* __restrict__ crow = C + (int64_t)partner[a] * k + o0;
-                double sacc = 0.0;
-                if (on == ON) {
+        for (int ta = 0; ta < 2; ++ta) {
+            const int64_t l = lw + ta * 16 + c16;
 #pragma unroll
-                    for (int j = 0; j < ON; ++j) sacc = __builtin_fma(y[j], crow[j], sacc);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < ON; ++j)
-                        if (j < on) sacc = __builtin_fma(y[j], crow[j], sacc);
-                }
-                part[wave][q][lane] = sacc;
+            for (int s4 = 0; s4 < NS; ++s4) {
+                const int64_t o = oc + 4 * s4 + kq;
+                ya[ta][s4] = (l < W && o < k) ? Ybar[i * Wk + l * k + o] : 0.0;
             }
-            __syncthreads();
-            for (int q = wave; q < nr; q += 4) {
-                const double v = ((part[0][q][lane] + part[1][q][lane]) + part[2][q][lane]) +
-                                 part[3][q][lane];
-                if (live) {
-                    double* out = Tbar + (int64_t)inv[perm[rb + q]] * ldt + l;
-                    *out = (ob == 0) ? v : *out + v;
-                }
+        }
+        for (int64_t rb = r0; rb < r1; rb += 16) {
+            const int64_t cr = col[rb + c16];                 // padded past n
+            v4d acc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+            for (int s4 = 0; s4 < NS; ++s4) {
+                const double bv = Cp[cr * kp + oc + 4 * s4 + kq];
+                acc[0] = mfma16x16x4(ya[0][s4], bv, acc[0]);
+                acc[1] = mfma16x16x4(ya[1][s4], bv, acc[1]);
             }
-            __syncthreads();
+            if (rb + c16 < r1) {
+                double* __restrict__ out = Tbar + (int64_t)inv[perm[rb + c16]] * ldt;
+#pragma unroll
+                for (int ta = 0; ta < 2; ++ta)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t l = lw + ta * 16 + kq + 4 * r;
+                        if (l < W) out[l] = store ? acc[ta][r] : out[l] + acc[ta][r];
+                    }
+            }
         }
     }
 }
@@ -289,6 +340,8 @@ int64_t dc_slices(int64_t k, int64_t M, int64_t W) {
 struct ExchWs {
     ExchTcWs tc;
     double *Dt, *Bt, *Y, *Yp, *Ys, *Yps, *Dfull, *Ebar, *part, *red;
+    int32_t *row_col, *col_row;       // partner splat per CSR position (rows: pj, columns: pi)
+    double* Cp;                       // C with rows padded to padded_cols(k) columns
 };
 
 int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool sym, bool grads,
@@ -306,6 +359,9 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
     w->Ebar = (grads && !sym) ? ar.take<double>(k * k * Pc + 1) : nullptr;
     w->part = grads ? ar.take<double>(kSplitMax * k * M + 1) : nullptr;
     w->red = ar.take<double>(kRedBlocks);
+    w->Cp = ar.take<double>(M * padded_cols(k) + 1);
+    w->row_col = ar.take<int32_t>(n + kColPad);
+    w->col_row = sym ? nullptr : ar.take<int32_t>(n + kColPad);
     return GSDFT_OK;
 }
 
@@ -329,23 +385,27 @@ int dc_gemm(rocblas_handle h, int64_t k, int64_t M, int64_t W, double alpha, con
     return GSDFT_OK;
 }
 
-// Orbitals per wave of the sparse kernels: the smallest of 8, 16, 24, 32 with 4 ON >= k, else 32
-// (several passes).
-int orbitals_per_wave(int64_t k) {
-    return k <= 32 ? 8 : k <= 64 ? 16 : k <= 96 ? 24 : 32;
-}
-
 int launch_spmm(int64_t M, int64_t W, int64_t k, int64_t ldb, const int32_t* ptr,
-                const int32_t* perm, const int32_t* partner, const double* Bt, const double* C,
+                const int32_t* perm, const int32_t* col, const double* Bt, const double* Cp,
                 double* Y, hipStream_t s) {
-    const int on = orbitals_per_wave(k);
-    dim3 grid((unsigned)M, nblk(W, 64), nblk(k, 4 * on));
+    const int64_t kp = padded_cols(k);
+    const int64_t full = kp / kMfOrb, tail = (kp % kMfOrb) / 16;
     profile_begin(kProfExchSparse, s);
-    switch (on) {
-    case 8: k_exch_spmm<8><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
-    case 16: k_exch_spmm<16><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
-    case 24: k_exch_spmm<24><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
-    default: k_exch_spmm<32><<<grid, 256, 0, s>>>(W, k, ldb, ptr, perm, partner, Bt, C, Y); break;
+    if (full > 0) {
+        dim3 grid((unsigned)M, nblk(W, 4 * kMfAux), (unsigned)full);
+        k_exch_spmm<kMfOrb / 16><<<grid, 256, 0, s>>>(W, k, kp, ldb, 0, ptr, perm, col, Bt, Cp,
+                                                      Y);
+    }
+    if (tail > 0) {
+        dim3 grid((unsigned)M, nblk(W, 4 * kMfAux), 1);
+        const int64_t ob = full * kMfOrb;
+        switch (tail) {
+        case 1: k_exch_spmm<1><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        case 2: k_exch_spmm<2><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        case 3: k_exch_spmm<3><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        case 4: k_exch_spmm<4><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        default: k_exch_spmm<5><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        }
     }
     profile_end(kProfExchSparse, s);
     GSDFT_HIP(hipGetLastError());
@@ -353,24 +413,28 @@ int launch_spmm(int64_t M, int64_t W, int64_t k, int64_t ldb, const int32_t* ptr
 }
 
 int launch_sddmm(int64_t M, int64_t W, int64_t k, int64_t ldt, const int32_t* ptr,
-                 const int32_t* perm, const int32_t* partner, const int32_t* inv,
-                 const double* Ybar, const double* C, double* Tbar, hipStream_t s) {
-    const int on = orbitals_per_wave(k);
-    dim3 grid((unsigned)M, nblk(W, 64));
+                 const int32_t* perm, const int32_t* col, const int32_t* inv,
+                 const double* Ybar, const double* Cp, double* Tbar, hipStream_t s) {
+    const int64_t kp = padded_cols(k);
+    const int64_t full = kp / kMfK * kMfK, tail = (kp - full) / 4;     // tail: K steps, 4 .. 20
+    dim3 grid((unsigned)M, nblk(W, 4 * kMfAux));
     profile_begin(kProfExchSparse, s);
-    switch (on) {
-    case 8:
-        k_exch_sddmm<8><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
-        break;
-    case 16:
-        k_exch_sddmm<16><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
-        break;
-    case 24:
-        k_exch_sddmm<24><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
-        break;
-    default:
-        k_exch_sddmm<32><<<grid, 256, 0, s>>>(W, k, ldt, ptr, perm, partner, inv, Ybar, C, Tbar);
-        break;
+    if (full > 0)
+        k_exch_sddmm<kMfK / 4><<<grid, 256, 0, s>>>(W, k, kp, ldt, 0, full, 1, ptr, perm, col, inv,
+                                                   Ybar, Cp, Tbar);
+    if (tail > 0) {
+        const int first = full == 0 ? 1 : 0;
+#define GSDFT_SDDMM_TAIL(NS)                                                                    \
+    k_exch_sddmm<NS><<<grid, 256, 0, s>>>(W, k, kp, ldt, full, kp, first, ptr, perm, col, inv, \
+                                          Ybar, Cp, Tbar)
+        switch (tail) {
+        case 4: GSDFT_SDDMM_TAIL(4); break;
+        case 8: GSDFT_SDDMM_TAIL(8); break;
+        case 12: GSDFT_SDDMM_TAIL(12); break;
+        case 16: GSDFT_SDDMM_TAIL(16); break;
+        default: GSDFT_SDDMM_TAIL(20); break;
+        }
+#undef GSDFT_SDDMM_TAIL
     }
     profile_end(kProfExchSparse, s);
     GSDFT_HIP(hipGetLastError());
@@ -436,6 +500,13 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     }
     rocblas_handle h;
     GSDFT_TRY(blas_handle(s, &h));
+    k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, row_perm, pj, w.row_col);
+    k_pad_cols<<<nblk(M * padded_cols(k), 256), 256, 0, s>>>(M, k, padded_cols(k), C, w.Cp);
+    GSDFT_HIP(hipGetLastError());
+    if (!sym) {
+        k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, col_perm, pi, w.col_row);
+        GSDFT_HIP(hipGetLastError());
+    }
     const int64_t G = (N % M == 0) ? N / M : 1;
     const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
     const double one = 1.0, zero = 0.0, mtwo = -2.0;
@@ -446,9 +517,9 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         const int64_t W = std::min(Pc, N - q0);
         double* Yc = store ? w.Ys + M * q0 * k : w.Y;
         GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
-        GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, pj, w.Bt, C, Yc, s));
+        GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.Bt, w.Cp, Yc, s));
         if (store && !sym)
-            GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, pi, w.Bt, C,
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, w.col_row, w.Bt, w.Cp,
                                   w.Yps + M * q0 * k, s));
         profile_begin(kProfExchGemm, s);
         GSDFT_BLAS(rocblas_dgemm_64(h, N_, T_, k, W * k, M, &one, C, k, Yc, W * k, &zero,
@@ -488,9 +559,9 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
             Ypc = sym ? nullptr : w.Yps + M * q0 * k;
         } else {
             GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
-            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, pj, w.Bt, C, w.Y, s));
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.Bt, w.Cp, w.Y, s));
             if (!sym)
-                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, pi, w.Bt, C, w.Yp, s));
+                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, w.col_row, w.Bt, w.Cp, w.Yp, s));
         }
         profile_begin(kProfExchGemm, s);
         // dC += Y_P Dbar_P^T (+ Y'_P Dbar_P; the same term again on a symmetric list)
@@ -501,7 +572,8 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
                                     W * k));
         profile_end(kProfExchGemm, s);
         // Tbar (slot-major, ld Pc) into the block's buffer
-        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, pj, w.tc.inv_perm, w.Y, C, w.Bt,
+        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.inv_perm, w.Y, w.Cp,
+                               w.Bt,
                                s));
         GSDFT_TRY(exch_tc_reverse(N, q0, W, n, w.Bt, Pc, q0 == 0, w.tc, s));
     }
