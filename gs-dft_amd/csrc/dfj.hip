@@ -14,12 +14,14 @@
 // all positive terms, no eigh, and differentiable at degenerate Ah.
 //
 // Work decomposition (no atomics anywhere):
-//   forward  -- one lane per aux function P; a workgroup walks a slab of pairs whose records are
-//               wave-uniform (scalar loads); per-slab partial gamma is summed in fixed order.
-//   reverse  -- one lane per pair; the wave walks the aux functions (uniform node tables); each
-//               lane accumulates its pair's 25 cotangent moments in registers; per-pair results
-//               are mapped to per-splat gradients by wave-per-splat segmented sums over the CSR
-//               pair index.
+//   forward  -- one lane per pair slot; the wave walks a block's aux records (uniform node
+//               tables, centre-grouped so the centre terms are shared by the exponent scales);
+//               each lane keeps its partial sums per record in LDS, the block adds them in lane
+//               order, and the per-block partials are summed in fixed order.
+//   reverse  -- one lane per pair slot; the wave walks the aux records the same way; each lane
+//               accumulates its pair's 25 cotangent moments in registers; per-pair results are
+//               mapped to per-splat gradients by wave-per-splat segmented sums over the CSR pair
+//               index.
 #include <rocblas/rocblas.h>
 #include <rocsolver/rocsolver.h>
 
@@ -245,68 +247,91 @@ __device__ __forceinline__ void count_work(unsigned long long* work, bool live, 
 
 // ------------------------------------------------------------------ forward
 
-__global__ __launch_bounds__(256) void k_gamma_fwd(int64_t N, const int32_t* __restrict__ order,
-                                                   const double* __restrict__ beta,
-                                                   const double* __restrict__ R,
-                                                   const double* __restrict__ kn, int64_t n,
-                                                   const double* __restrict__ rec,
-                                                   int64_t per_slab,
-                                                   double* __restrict__ partial,
-                                                   unsigned long long* __restrict__ work) {
+// Forward with one lane per pair slot (the reverse's slot order) and the aux records of the reverse
+// (centre-grouped, wave-uniform): block (g, s) sums the pair slots [g kFwdPairs, (g + 1) kFwdPairs)
+// against the kFwdRecs aux slots from s kFwdRecs on. The centre-dependent terms (d, Ah d, q0..q2)
+// are formed once per centre and shared by its exponent scales, and the wave's node screen acts on
+// 64 pairs in precision band + Morton order. Each lane keeps its running sums of coef_a F(P, a) for
+// the block's records in LDS; at the end the 256 lane sums of each record are added in lane order
+// and scaled by KN_P (the record's u): partial[g * N + slot].
+constexpr int kFwdRecs = 16;
+constexpr int64_t kFwdPairs = 8192;
+
+__global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
+                                                         const double* __restrict__ rec,
+                                                         int64_t N,
+                                                         const double* __restrict__ aux,
+                                                         double* __restrict__ partial,
+                                                         unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
+    __shared__ double acc[kFwdRecs][256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+#pragma unroll
+    for (int j = 0; j < kFwdRecs; ++j) acc[j][threadIdx.x] = 0.0;
     __syncthreads();
-    const int64_t lane_id = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = lane_id < N;
-    const int64_t P = live ? order[lane_id] : 0;
-    const double b = live ? beta[P] : 1.0;
-    const double Rx = live ? R[3 * P] : kFarAway, Ry = live ? R[3 * P + 1] : kFarAway,
-                 Rz = live ? R[3 * P + 2] : kFarAway;
-    double s[kNodes], wp[kNodes];
-    node_consts(b, s, wp);
-    const int64_t a0 = blockIdx.y * per_slab;
-    const int64_t a1 = min(n, a0 + per_slab);
-    double acc = 0.0;
+    const int64_t q0 = (int64_t)blockIdx.y * kFwdRecs;
+    const int nrec = (int)min((int64_t)kFwdRecs, N - q0);
+    const int64_t a_begin = (int64_t)blockIdx.x * kFwdPairs;
+    const int64_t a_end = min(n, a_begin + kFwdPairs);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t nodes = 0;
-    for (int64_t a = a0; a < a1; ++a) {
-        const double* __restrict__ r = rec + kRec * a;
+    for (int64_t a0 = a_begin + 64 * wave; a0 < a_end; a0 += 256) {      // wave-uniform
+        const int64_t a = a0 + lane;
+        const bool live = a < a_end;
+        const double* __restrict__ r = rec + kRec * (live ? a : a0);
         const double I1 = r[0], I2 = r[1], I3 = r[2];
         const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
-        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
-        const double coef = r[12];
-        const double ax = xx * dx + xy * dy + xz * dz;
-        const double ay = xy * dx + yy * dy + yz * dz;
-        const double az = xz * dx + yz * dy + zz * dz;
-        const double q0 = dx * dx + dy * dy + dz * dz;
-        const double q1 = dx * ax + dy * ay + dz * az;
-        const double q2 = ax * ax + ay * ay + az * az;
-        const double X0 = I3 * q0;
-        const double rr = I1 * q1 - q2;
-        double F = 0.0;
-        auto node = [&](auto tc) {
-            constexpr int t = decltype(tc)::value;
-            const double st = s[t];
-            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
-            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const NodeVal v = node_val(Pn, st * Qn);
-            F = __builtin_fma(wp[t] * v.y0, exp_neg_tab(v.arg, tab), F);
-            return screen_after(t) && wave_all_beyond(v.z);
-        };
-        nodes += node_loop<0>(node);
-        F = (q0 == q0) ? F : q0;                 // a NaN centre propagates, as in the reference
-        acc = __builtin_fma(F, coef, acc);
+        const double Px = live ? r[9] : kFarAway, Py = live ? r[10] : kFarAway,
+                     Pz = live ? r[11] : kFarAway;
+        const double coef = live ? r[12] : 0.0;
+        double q0d = 0, q1 = 0, X0 = 0, rr = 0;
+        for (int j = 0; j < nrec; ++j) {
+            const double* __restrict__ x = aux + kAuxRec * (q0 + j);
+            if (j == 0 || x[5] != 0.0) {             // a new centre (wave-uniform)
+                const double dx = x[0] - Px, dy = x[1] - Py, dz = x[2] - Pz;
+                const double ax = xx * dx + xy * dy + xz * dz;
+                const double ay = xy * dx + yy * dy + yz * dz;
+                const double az = xz * dx + yz * dy + zz * dz;
+                q0d = dx * dx + dy * dy + dz * dz;
+                q1 = dx * ax + dy * ay + dz * az;
+                const double q2 = ax * ax + ay * ay + az * az;
+                X0 = I3 * q0d;
+                rr = I1 * q1 - q2;
+            }
+            double F = 0.0;
+            auto node = [&](auto tc) {
+                constexpr int t = decltype(tc)::value;
+                const double st = x[8 + t];
+                const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+                const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
+                const NodeVal v = node_val(Pn, st * Qn);
+                F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
+                return screen_after(t) && wave_all_beyond(v.z);
+            };
+            nodes += node_loop<0>(node);
+            F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
+            acc[j][threadIdx.x] = __builtin_fma(F, coef, acc[j][threadIdx.x]);
+        }
     }
-    if (live) partial[blockIdx.y * N + P] = acc * kn[P];
-    count_work(work, live, nodes);
+    count_work(work, true, nodes);
+    __syncthreads();
+    if ((int)threadIdx.x < nrec) {
+        double sum = 0.0;
+        for (int l = 0; l < 256; ++l) sum += acc[threadIdx.x][l];
+        partial[(int64_t)blockIdx.x * N + q0 + threadIdx.x] =
+            sum * aux[kAuxRec * (q0 + threadIdx.x) + 3];
+    }
 }
 
-__global__ void k_slab_sum(int64_t N, int64_t slabs, const double* __restrict__ partial,
-                           double* __restrict__ out) {
+// gamma[p] = sum over pair groups of partial[g * N + slot(p)], in group order.
+__global__ void k_slot_sum(int64_t N, int64_t G, int64_t groups, const double* __restrict__ partial,
+                           double* __restrict__ gamma) {
     const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (p >= N) return;
+    const int64_t q = aux_slot(p, N, G);
     double s = 0.0;
-    for (int64_t k = 0; k < slabs; ++k) s += partial[k * N + p];
-    out[p] = s;
+    for (int64_t g = 0; g < groups; ++g) s += partial[g * N + q];
+    gamma[p] = s;
 }
 
 // ------------------------------------------------------------------ reverse
@@ -1172,19 +1197,6 @@ struct Split {
     int64_t per_slab;
 };
 
-// Forward: ceil(N/256) workgroups per slab; aim for ~16 resident rounds of 4 waves per SIMD.
-Split fwd_split(int64_t N, int64_t n) {
-    const int64_t groups = N > 0 ? (N + 255) / 256 : 1;
-    const int64_t target = 256 * 4 * 16;                   // workgroups (of 4 waves) wanted
-    int64_t slabs = (target + groups - 1) / groups;
-    slabs = slabs < 1 ? 1 : slabs;
-    const int64_t max_slabs = (n + 7) / 8;                  // at least 8 pairs per slab
-    if (slabs > max_slabs) slabs = max_slabs < 1 ? 1 : max_slabs;
-    if (slabs > 65535) slabs = 65535;
-    const int64_t per = (n + slabs - 1) / slabs;
-    return Split{(n + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
-}
-
 Split bwd_split(int64_t N, int64_t n) {
     const int64_t groups = n > 0 ? (n + 255) / 256 : 1;
     const int64_t target = 256 * 4 * 4;
@@ -1213,7 +1225,6 @@ Split atom_split(int64_t n_atoms, int64_t n) {
 struct GammaWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
     double *aux, *acc, *contrib, *rec_sorted;
-    AuxOrderWs order;
     PairOrderWs pair_order;
 };
 
@@ -1226,9 +1237,11 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
     w->rec = ar.take<double>(kRec * n + kRec);
     w->partial = w->aux = w->acc = w->contrib = w->rec_sorted = nullptr;
     if (!reverse) {
-        GSDFT_TRY(aux_order_layout(ar, N, &w->order));
-        const Split sp = fwd_split(N, n);
-        w->partial = ar.take<double>(sp.slabs * N + 1);
+        const int64_t groups = n > 0 ? (n + kFwdPairs - 1) / kFwdPairs : 1;
+        w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
+        w->rec_sorted = ar.take<double>(kRec * n + kRec);
+        GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
+        w->partial = ar.take<double>(groups * N + 1);
     } else {
         const Split sp = bwd_split(N, n);
         w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
@@ -1573,15 +1586,23 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
     }
     GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, N, log_alpha, n, pi, pj,
                              weight, w, s));
-    GSDFT_TRY(launch_aux_order(N, log_alpha, aux_centers, w.order, s));
-    const Split sp = fwd_split(N, n);
-    dim3 grid((unsigned)((N + 255) / 256), (unsigned)sp.slabs);
+    const int64_t G = (N % M == 0) ? N / M : 1;          // scales per centre of a product aux
+    k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
+                                                      nullptr, w.aux);
+    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
+    k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
+                                                            w.rec_sorted);
+    GSDFT_HIP(hipGetLastError());
+    const int64_t groups = (n + kFwdPairs - 1) / kFwdPairs;
+    if (N > 65535LL * kFwdRecs) return fail(GSDFT_ERR_ARG, "gsdft_gamma: N_aux too large");
+    dim3 grid((unsigned)groups, (unsigned)((N + kFwdRecs - 1) / kFwdRecs));
     profile_begin(kProfGammaFwd, s);
-    k_gamma_fwd<<<grid, 256, 0, s>>>(N, w.order.order, w.beta, aux_centers, w.kn, n, w.rec,
-                                     sp.per_slab, w.partial, profile_work_counter(kProfGammaFwd));
+    k_gamma_fwd_pairs<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, w.partial,
+                                           profile_work_counter(kProfGammaFwd));
     profile_end(kProfGammaFwd, s);
     GSDFT_HIP(hipGetLastError());
-    k_slab_sum<<<blocks_for(N, 256), 256, 0, s>>>(N, sp.slabs, w.partial, gamma);
+    k_slot_sum<<<blocks_for(N, 256), 256, 0, s>>>(N, G, groups, w.partial, gamma);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }

@@ -54,18 +54,7 @@ enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMet
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
 
-// order.hip: lane order of the forward three-centre pass (order[lane] = aux index).
-struct AuxOrderWs {
-    uint32_t *key_in, *key_out;
-    int32_t *idx_in, *order;
-    char* sort_tmp;
-    size_t sort_bytes;
-};
-int aux_order_layout(Arena& ar, int64_t N, AuxOrderWs* w);
-int launch_aux_order(int64_t N, const double* log_alpha, const double* aux_centers,
-                     const AuxOrderWs& w, hipStream_t s);
-
-// order.hip: slot order of the reverse three-centre pass (perm[slot] = pair index), built from
+// order.hip: slot order of the three-centre passes (perm[slot] = pair index), built from
 // pair records in list order whose first 12 doubles are I1 I2 I3 | Ah (6) | P (3).
 struct PairOrderWs {
     uint64_t *key_in, *key_out;
