@@ -1472,11 +1472,17 @@ extern "C" int gsdft_product_aux(int64_t M, const double* quat, const double* lo
     return GSDFT_OK;
 }
 
+// Blocked Cholesky: panels of kCholNb rows, trailing updates in column chunks of kCholW.
+constexpr int64_t kCholNb = 1024;
+constexpr int64_t kCholW = 4096;
+
+inline int64_t chol_steps(int64_t N) { return (N + kCholNb - 1) / kCholNb; }
+
 extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
     if (N < 0 || !bytes) return fail(GSDFT_ERR_ARG, "metric_workspace_size: bad arguments");
     Arena ar{nullptr, 0, 0};
     ar.take<double>(2 * N + 2);
-    ar.take<int64_t>(2);
+    ar.take<int64_t>(chol_steps(N) + 2);
     *bytes = ar.need();
     return GSDFT_OK;
 }
@@ -1500,6 +1506,102 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
     return GSDFT_OK;
 }
 
+constexpr int kPanelRows = 128;     // rows per substitution block of the panel solve
+constexpr int kPanelCols = 64;      // panel columns per workgroup
+
+// X <- U^-T X for one substitution block: U is ib x ib upper (column-major, leading dimension N;
+// U[c][r] at U[r N + c]), X is ib x T (column-major, leading dimension N). A workgroup stages 64
+// columns of X in LDS (coalesced: each column is contiguous), then wave 0 solves one column per
+// lane by substitution, x_r = (b_r - sum_{c<r} U[c][r] x_c) / U[r][r] (two partial sums over even
+// and odd c). The U entries are wave-uniform.
+__global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __restrict__ U,
+                                                     int ib, double* __restrict__ X, int64_t T) {
+    __shared__ double Xs[kPanelCols][kPanelRows + 1];
+    const int64_t j0 = (int64_t)blockIdx.x * kPanelCols;
+    const int nc = (int)min((int64_t)kPanelCols, T - j0);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int q0 = 0; q0 < kPanelCols; q0 += 4) {
+        const int q = q0 + wv;
+        if (q < nc) {
+            const double* col = X + (j0 + q) * N;
+            if (lane < ib) Xs[q][lane] = col[lane];
+            if (lane + 64 < ib) Xs[q][lane + 64] = col[lane + 64];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < nc) {
+        const int q = threadIdx.x;
+        for (int r = 0; r < ib; ++r) {
+            const double* ur = U + (int64_t)r * N;
+            double a0 = Xs[q][r], a1 = 0.0;
+            int c = 0;
+            for (; c + 1 < r; c += 2) {
+                a0 = __builtin_fma(-ur[c], Xs[q][c], a0);
+                a1 = __builtin_fma(-ur[c + 1], Xs[q][c + 1], a1);
+            }
+            if (c < r) a0 = __builtin_fma(-ur[c], Xs[q][c], a0);
+            Xs[q][r] = (a0 + a1) / ur[r];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q0 = 0; q0 < kPanelCols; q0 += 4) {
+        const int q = q0 + wv;
+        if (q < nc) {
+            double* col = X + (j0 + q) * N;
+            if (lane < ib) col[lane] = Xs[q][lane];
+            if (lane + 64 < ib) col[lane + 64] = Xs[q][lane + 64];
+        }
+    }
+}
+
+// Right-looking blocked upper Cholesky of the column-major view A (= V, symmetric), A = U^T U:
+// for each panel of kb <= kCholNb rows at k0, U_kk = potrf(A_kk) (rocSOLVER), the panel row
+// P = U_kk^-T A[k0:k0+kb, k0+kb:] by blocked substitution (128-row blocks solved by
+// k_panel_subst, each applied to the rest of the panel by an FP64 GEMM: backward stable, unlike a
+// solve through explicit inverses of the diagonal blocks, whose error grows with their condition
+// number), and the trailing upper triangle
+// A[k0+kb:, k0+kb:] -= P^T P as FP64 GEMMs over column chunks of kCholW, each chunk updating rows
+// 0 .. its last column (the chunk's own sub-diagonal part is computed too and is never read).
+// info[step] receives the panel's potrf status (0, or the failing minor within the panel).
+static int cholesky_blocked(rocblas_handle h, hipStream_t s, int64_t N, double* A, int64_t* info) {
+    const double one = 1.0, minus_one = -1.0;
+    int64_t step = 0;
+    for (int64_t k0 = 0; k0 < N; k0 += kCholNb, ++step) {
+        const int64_t kb = std::min(kCholNb, N - k0);
+        double* Akk = A + k0 * N + k0;
+        rocblas_status st = rocsolver_dpotrf_64(h, rocblas_fill_upper, kb, Akk, N, info + step);
+        if (st != rocblas_status_success)
+            return fail(GSDFT_ERR_LIB, "rocsolver_dpotrf failed (status %d)", (int)st);
+        const int64_t T = N - k0 - kb;
+        if (T == 0) break;
+        double* P = A + (k0 + kb) * N + k0;
+        for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
+            const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
+            k_panel_subst<<<(unsigned)((T + kPanelCols - 1) / kPanelCols), 256, 0, s>>>(
+                N, Akk + i0 * N + i0, ib, P + i0, T);
+            GSDFT_HIP(hipGetLastError());
+            if (i0 + ib < kb) {
+                st = rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none,
+                                      kb - i0 - ib, T, ib, &minus_one, Akk + (i0 + ib) * N + i0, N,
+                                      P + i0, N, &one, P + i0 + ib, N);
+                if (st != rocblas_status_success)
+                    return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
+            }
+        }
+        double* C = A + (k0 + kb) * N + (k0 + kb);
+        for (int64_t c0 = 0; c0 < T; c0 += kCholW) {
+            const int64_t w = std::min(kCholW, T - c0);
+            st = rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none, c0 + w, w,
+                                  kb, &minus_one, P, N, P + c0 * N, N, &one, C + c0 * N, N);
+            if (st != rocblas_status_success)
+                return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
+        }
+    }
+    return GSDFT_OK;
+}
+
 extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t workspace_bytes,
                               void* stream) {
     if (N <= 0 || !V) return fail(GSDFT_ERR_ARG, "gsdft_cholesky: bad arguments");
@@ -1507,26 +1609,27 @@ extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t work
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     ar.take<double>(2 * N + 2);
-    int64_t* info = ar.take<int64_t>(2);
+    const int64_t steps = chol_steps(N);
+    int64_t* info = ar.take<int64_t>(steps + 2);
     if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_cholesky: workspace too small");
     rocblas_handle h;
     GSDFT_TRY(blas_handle(s, &h));
-    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. The ILP64
-    // entry point: N * N exceeds the int32 range of the rocblas_int interface from N = 46341.
+    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. ILP64 entry
+    // points: N * N exceeds the int32 range of the rocblas_int interfaces from N = 46341.
     profile_begin(kProfCholesky, s);
-    rocblas_status st = rocsolver_dpotrf_64(h, rocblas_fill_upper, N, V, N, info);
+    GSDFT_TRY(cholesky_blocked(h, s, N, V, info));
     profile_end(kProfCholesky, s);
-    if (st != rocblas_status_success)
-        return fail(GSDFT_ERR_LIB, "rocsolver_dpotrf failed (status %d)", (int)st);
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     k_zero_upper<<<grid, 256, 0, s>>>(N, V);
     GSDFT_HIP(hipGetLastError());
-    int64_t h_info = 0;
-    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    std::vector<int64_t> h_info(steps);
+    GSDFT_HIP(hipMemcpyAsync(h_info.data(), info, sizeof(int64_t) * steps,
+                             hipMemcpyDeviceToHost, s));
     GSDFT_HIP(hipStreamSynchronize(s));
-    if (h_info != 0)
-        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not positive "
-                    "definite", (long long)h_info);
+    for (int64_t q = 0; q < steps; ++q)
+        if (h_info[q] != 0)
+            return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not "
+                        "positive definite", (long long)(q * kCholNb + h_info[q]));
     return GSDFT_OK;
 }
 
