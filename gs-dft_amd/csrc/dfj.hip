@@ -1473,16 +1473,14 @@ extern "C" int gsdft_product_aux(int64_t M, const double* quat, const double* lo
 }
 
 // Blocked Cholesky: panels of kCholNb rows, trailing updates in column chunks of kCholW.
-constexpr int64_t kCholNb = 1024;
-constexpr int64_t kCholW = 4096;
-
-inline int64_t chol_steps(int64_t N) { return (N + kCholNb - 1) / kCholNb; }
+constexpr int64_t kCholNb = 2048;
+constexpr int64_t kCholW = 2048;
 
 extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
     if (N < 0 || !bytes) return fail(GSDFT_ERR_ARG, "metric_workspace_size: bad arguments");
     Arena ar{nullptr, 0, 0};
     ar.take<double>(2 * N + 2);
-    ar.take<int64_t>(chol_steps(N) + 2);
+    ar.take<int64_t>(2);
     *bytes = ar.need();
     return GSDFT_OK;
 }
@@ -1506,98 +1504,193 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
     return GSDFT_OK;
 }
 
-constexpr int kPanelRows = 128;     // rows per substitution block of the panel solve
-constexpr int kPanelCols = 64;      // panel columns per workgroup
+constexpr int kPanelRows = 128;     // rows per diagonal block (inner factorisation, panel solve)
+constexpr int kPotfThreads = 1024;
+constexpr int kPackedTri = kPanelRows * (kPanelRows + 1) / 2;
 
-// X <- U^-T X for one substitution block: U is ib x ib upper (column-major, leading dimension N;
-// U[c][r] at U[r N + c]), X is ib x T (column-major, leading dimension N). A workgroup stages 64
-// columns of X in LDS (coalesced: each column is contiguous), then wave 0 solves one column per
-// lane by substitution, x_r = (b_r - sum_{c<r} U[c][r] x_c) / U[r][r] (two partial sums over even
-// and odd c). The U entries are wave-uniform.
+__global__ void k_info_reset(int64_t* __restrict__ info) { *info = 0; }
+
+// Unblocked upper Cholesky of one ib x ib diagonal block (ib <= 128; column-major, leading
+// dimension N, A(r, c) at A[c N + r] for r <= c), in place, staged in LDS (As[c][r] = A(r, c)).
+// Step j subtracts A(j, r) A(j, c) / A(j, j) from A(r, c) for j < r <= c (one barrier per step);
+// the rows are scaled at the end: U(j, j) = sqrt(A(j, j)), U(j, c) = A(j, c) / U(j, j). A pivot that
+// is not positive records base + j + 1 in *info unless an earlier minor has failed (the factor is
+// then meaningless, as with any failed factorisation).
+__global__ __launch_bounds__(kPotfThreads) void k_potf2(int64_t N, double* __restrict__ A, int ib,
+                                                        int64_t base,
+                                                        int64_t* __restrict__ info) {
+    __shared__ double As[kPanelRows][kPanelRows + 1];
+    __shared__ double sq[kPanelRows];
+    __shared__ int bad;
+    constexpr int kLoads = kPanelRows * kPanelRows / kPotfThreads;
+    const int t = threadIdx.x;
+    double v[kLoads];
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) {
+        const int e = t + q * kPotfThreads, c = e >> 7, r = e & (kPanelRows - 1);
+        v[q] = (c < ib && r <= c) ? A[c * N + r] : 0.0;
+    }
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) {
+        const int e = t + q * kPotfThreads;
+        As[e >> 7][e & (kPanelRows - 1)] = v[q];
+    }
+    if (t == 0) bad = 0;
+    __syncthreads();
+    const int cc = t & (kPanelRows - 1), rg = t >> 7;      // column, row group (8 groups)
+    for (int j = 0; j < ib; ++j) {
+        const double piv = As[j][j];
+        if (t == 0 && !(piv > 0.0) && bad == 0) bad = j + 1;
+        if (cc > j && cc < ib) {
+            const double uc = As[cc][j] / piv;
+            for (int r = j + 1 + rg; r <= cc; r += kPotfThreads / kPanelRows)
+                As[cc][r] = __builtin_fma(-As[r][j], uc, As[cc][r]);
+        }
+        __syncthreads();
+    }
+    if (t < ib) sq[t] = sqrt(As[t][t]);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kLoads; ++q) {
+        const int e = t + q * kPotfThreads, c = e >> 7, r = e & (kPanelRows - 1);
+        if (c < ib && r <= c) A[c * N + r] = r == c ? sq[r] : As[c][r] / sq[r];
+    }
+    if (t == 0 && bad != 0 && *info == 0) *info = base + bad;
+}
+
+constexpr int kSubstCols = 16;      // panel columns per wave of the panel solve
+
+// Offset of row c of a 128 x 128 upper triangle packed by rows (row c holds columns c..127).
+__device__ __forceinline__ int tri_row(int c) { return c * kPanelRows - c * (c - 1) / 2; }
+
+// X <- U^-T X for one diagonal block: U is ib x ib upper (column-major, leading dimension N; U(c, r)
+// at U[r N + c]), X is ib x T (column-major, leading dimension N). U's upper triangle is staged in
+// LDS packed by rows (zero past ib). Each wave solves 16 columns of X by column-oriented
+// substitution: lane l holds rows l and l + 64 of the 16 columns in registers; at step c the owner
+// lane's x_c = acc * (1 / U(c, c)) is broadcast with readlane and every row r > c takes
+// -U(c, r) x_c. Rows past ib carry zeros and a zero reciprocal, so all 128 steps run.
 __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __restrict__ U,
                                                      int ib, double* __restrict__ X, int64_t T) {
-    __shared__ double Xs[kPanelCols][kPanelRows + 1];
-    const int64_t j0 = (int64_t)blockIdx.x * kPanelCols;
-    const int nc = (int)min((int64_t)kPanelCols, T - j0);
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __shared__ double Us[kPackedTri];
+    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
-    for (int q0 = 0; q0 < kPanelCols; q0 += 4) {
-        const int q = q0 + wv;
-        if (q < nc) {
-            const double* col = X + (j0 + q) * N;
-            if (lane < ib) Xs[q][lane] = col[lane];
-            if (lane + 64 < ib) Xs[q][lane + 64] = col[lane + 64];
-        }
+    for (int r0 = 0; r0 < kPanelRows; r0 += 4) {
+        const int r = r0 + wv;
+        const double* ur = U + (int64_t)r * N;
+        if (l <= r) Us[tri_row(l) + r - l] = r < ib ? ur[l] : 0.0;
+        if (l + 64 <= r) Us[tri_row(l + 64) + r - l - 64] = r < ib ? ur[l + 64] : 0.0;
+    }
+    const int64_t jw = (int64_t)blockIdx.x * (4 * kSubstCols) + wv * kSubstCols;
+    const bool h0 = l < ib, h1 = l + 64 < ib;
+    double acc0[kSubstCols], acc1[kSubstCols];
+#pragma unroll
+    for (int k = 0; k < kSubstCols; ++k) {
+        const bool live = jw + k < T;
+        const double* col = X + (jw + k) * N;
+        acc0[k] = live && h0 ? col[l] : 0.0;
+        acc1[k] = live && h1 ? col[l + 64] : 0.0;
     }
     __syncthreads();
-    if (threadIdx.x < nc) {
-        const int q = threadIdx.x;
-        for (int r = 0; r < ib; ++r) {
-            const double* ur = U + (int64_t)r * N;
-            double a0 = Xs[q][r], a1 = 0.0;
-            int c = 0;
-            for (; c + 1 < r; c += 2) {
-                a0 = __builtin_fma(-ur[c], Xs[q][c], a0);
-                a1 = __builtin_fma(-ur[c + 1], Xs[q][c + 1], a1);
-            }
-            if (c < r) a0 = __builtin_fma(-ur[c], Xs[q][c], a0);
-            Xs[q][r] = (a0 + a1) / ur[r];
+    const double rd0 = h0 ? 1.0 / Us[tri_row(l)] : 0.0;
+    const double rd1 = h1 ? 1.0 / Us[tri_row(l + 64)] : 0.0;
+#pragma unroll 2
+    for (int c = 0; c < 64; ++c) {
+        const double u0 = l > c ? Us[tri_row(c) + l - c] : 0.0;
+        const double u1 = Us[tri_row(c) + l + 64 - c];
+#pragma unroll
+        for (int k = 0; k < kSubstCols; ++k) {
+            const double x = readlane_f64(acc0[k] * rd0, c);
+            acc0[k] = __builtin_fma(-u0, x, acc0[k]);
+            acc1[k] = __builtin_fma(-u1, x, acc1[k]);
         }
     }
-    __syncthreads();
+#pragma unroll 2
+    for (int c = 64; c < kPanelRows; ++c) {
+        const double u1 = l + 64 > c ? Us[tri_row(c) + l + 64 - c] : 0.0;
 #pragma unroll
-    for (int q0 = 0; q0 < kPanelCols; q0 += 4) {
-        const int q = q0 + wv;
-        if (q < nc) {
-            double* col = X + (j0 + q) * N;
-            if (lane < ib) col[lane] = Xs[q][lane];
-            if (lane + 64 < ib) col[lane + 64] = Xs[q][lane + 64];
+        for (int k = 0; k < kSubstCols; ++k) {
+            const double x = readlane_f64(acc1[k] * rd1, c - 64);
+            acc1[k] = __builtin_fma(-u1, x, acc1[k]);
         }
+    }
+#pragma unroll
+    for (int k = 0; k < kSubstCols; ++k) {
+        if (jw + k >= T) continue;
+        double* col = X + (jw + k) * N;
+        if (h0) col[l] = acc0[k] * rd0;
+        if (h1) col[l + 64] = acc1[k] * rd1;
     }
 }
 
-// Right-looking blocked upper Cholesky of the column-major view A (= V, symmetric), A = U^T U:
-// for each panel of kb <= kCholNb rows at k0, U_kk = potrf(A_kk) (rocSOLVER), the panel row
-// P = U_kk^-T A[k0:k0+kb, k0+kb:] by blocked substitution (128-row blocks solved by
-// k_panel_subst, each applied to the rest of the panel by an FP64 GEMM: backward stable, unlike a
-// solve through explicit inverses of the diagonal blocks, whose error grows with their condition
-// number), and the trailing upper triangle
-// A[k0+kb:, k0+kb:] -= P^T P as FP64 GEMMs over column chunks of kCholW, each chunk updating rows
-// 0 .. its last column (the chunk's own sub-diagonal part is computed too and is never read).
-// info[step] receives the panel's potrf status (0, or the failing minor within the panel).
-static int cholesky_blocked(rocblas_handle h, hipStream_t s, int64_t N, double* A, int64_t* info) {
+// P <- U^-T P for the kb x kb upper factor U at Akk and the kb x T panel P (both column-major,
+// leading dimension N), by blocked substitution: each 128-row block is solved by k_panel_subst and
+// applied to the rows below it by an FP64 GEMM. Backward stable, unlike a solve through explicit
+// inverses of the diagonal blocks, whose error grows with their condition number.
+static int panel_solve(rocblas_handle h, hipStream_t s, int64_t N, const double* Akk, int64_t kb,
+                       double* P, int64_t T) {
     const double one = 1.0, minus_one = -1.0;
-    int64_t step = 0;
-    for (int64_t k0 = 0; k0 < N; k0 += kCholNb, ++step) {
-        const int64_t kb = std::min(kCholNb, N - k0);
-        double* Akk = A + k0 * N + k0;
-        rocblas_status st = rocsolver_dpotrf_64(h, rocblas_fill_upper, kb, Akk, N, info + step);
-        if (st != rocblas_status_success)
-            return fail(GSDFT_ERR_LIB, "rocsolver_dpotrf failed (status %d)", (int)st);
-        const int64_t T = N - k0 - kb;
-        if (T == 0) break;
-        double* P = A + (k0 + kb) * N + k0;
-        for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
-            const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
-            k_panel_subst<<<(unsigned)((T + kPanelCols - 1) / kPanelCols), 256, 0, s>>>(
-                N, Akk + i0 * N + i0, ib, P + i0, T);
-            GSDFT_HIP(hipGetLastError());
-            if (i0 + ib < kb) {
-                st = rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none,
-                                      kb - i0 - ib, T, ib, &minus_one, Akk + (i0 + ib) * N + i0, N,
-                                      P + i0, N, &one, P + i0 + ib, N);
-                if (st != rocblas_status_success)
-                    return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
-            }
-        }
-        double* C = A + (k0 + kb) * N + (k0 + kb);
-        for (int64_t c0 = 0; c0 < T; c0 += kCholW) {
-            const int64_t w = std::min(kCholW, T - c0);
-            st = rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none, c0 + w, w,
-                                  kb, &minus_one, P, N, P + c0 * N, N, &one, C + c0 * N, N);
+    for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
+        const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
+        k_panel_subst<<<(unsigned)((T + 4 * kSubstCols - 1) / (4 * kSubstCols)), 256, 0, s>>>(
+            N, Akk + i0 * N + i0, ib, P + i0, T);
+        GSDFT_HIP(hipGetLastError());
+        if (i0 + ib < kb) {
+            const rocblas_status st = rocblas_dgemm_64(
+                h, rocblas_operation_transpose, rocblas_operation_none, kb - i0 - ib, T, ib,
+                &minus_one, Akk + (i0 + ib) * N + i0, N, P + i0, N, &one, P + i0 + ib, N);
             if (st != rocblas_status_success)
                 return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
         }
+    }
+    return GSDFT_OK;
+}
+
+// C (upper triangle, T x T at C, leading dimension N) -= P^T P for the kb x T panel P, as FP64
+// GEMMs over column chunks of width chunk, each chunk updating rows 0 .. its last column (the
+// chunk's own sub-diagonal part is computed too and never read).
+static int trailing_update(rocblas_handle h, int64_t N, const double* P, int64_t kb, double* C,
+                           int64_t T, int64_t chunk) {
+    const double one = 1.0, minus_one = -1.0;
+    for (int64_t c0 = 0; c0 < T; c0 += chunk) {
+        const int64_t w = std::min(chunk, T - c0);
+        const rocblas_status st = rocblas_dgemm_64(h, rocblas_operation_transpose,
+                                                   rocblas_operation_none, c0 + w, w, kb,
+                                                   &minus_one, P, N, P + c0 * N, N, &one,
+                                                   C + c0 * N, N);
+        if (st != rocblas_status_success)
+            return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
+    }
+    return GSDFT_OK;
+}
+
+// Right-looking blocked upper Cholesky of the column-major view A (= V, symmetric), A = U^T U, on
+// two levels with the same three steps: for each diagonal block, factor it, solve the panel to its
+// right (P = U_kk^-T A_k,rest) and update the trailing upper triangle (A_rest -= P^T P). The outer
+// level uses kCholNb-row panels (the trailing updates are large FP64 GEMMs); each kCholNb diagonal
+// block is factored the same way with 128-row blocks, whose factorisation is k_potf2. *info
+// receives the first failing leading minor (0 if none).
+static int cholesky_blocked(rocblas_handle h, hipStream_t s, int64_t N, double* A, int64_t* info) {
+    k_info_reset<<<1, 1, 0, s>>>(info);
+    GSDFT_HIP(hipGetLastError());
+    for (int64_t k0 = 0; k0 < N; k0 += kCholNb) {
+        const int64_t kb = std::min(kCholNb, N - k0);
+        double* Akk = A + k0 * N + k0;
+        for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
+            const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
+            double* Aii = Akk + i0 * N + i0;
+            k_potf2<<<1, kPotfThreads, 0, s>>>(N, Aii, ib, k0 + i0, info);
+            GSDFT_HIP(hipGetLastError());
+            const int64_t Ti = kb - i0 - ib;
+            if (Ti == 0) break;
+            double* Pi = Aii + (int64_t)ib * N;
+            GSDFT_TRY(panel_solve(h, s, N, Aii, ib, Pi, Ti));
+            GSDFT_TRY(trailing_update(h, N, Pi, ib, Pi + ib, Ti, Ti));
+        }
+        const int64_t T = N - k0 - kb;
+        if (T == 0) break;
+        double* P = Akk + kb * N;
+        GSDFT_TRY(panel_solve(h, s, N, Akk, kb, P, T));
+        GSDFT_TRY(trailing_update(h, N, P, kb, P + kb, T, kCholW));
     }
     return GSDFT_OK;
 }
@@ -1609,27 +1702,24 @@ extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t work
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     ar.take<double>(2 * N + 2);
-    const int64_t steps = chol_steps(N);
-    int64_t* info = ar.take<int64_t>(steps + 2);
+    int64_t* info = ar.take<int64_t>(2);
     if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_cholesky: workspace too small");
     rocblas_handle h;
     GSDFT_TRY(blas_handle(s, &h));
-    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. ILP64 entry
-    // points: N * N exceeds the int32 range of the rocblas_int interfaces from N = 46341.
+    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. ILP64 GEMMs:
+    // N * N exceeds the int32 range of the rocblas_int interfaces from N = 46341.
     profile_begin(kProfCholesky, s);
     GSDFT_TRY(cholesky_blocked(h, s, N, V, info));
     profile_end(kProfCholesky, s);
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     k_zero_upper<<<grid, 256, 0, s>>>(N, V);
     GSDFT_HIP(hipGetLastError());
-    std::vector<int64_t> h_info(steps);
-    GSDFT_HIP(hipMemcpyAsync(h_info.data(), info, sizeof(int64_t) * steps,
-                             hipMemcpyDeviceToHost, s));
+    int64_t h_info = 0;
+    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     GSDFT_HIP(hipStreamSynchronize(s));
-    for (int64_t q = 0; q < steps; ++q)
-        if (h_info[q] != 0)
-            return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not "
-                        "positive definite", (long long)(q * kCholNb + h_info[q]));
+    if (h_info != 0)
+        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not positive "
+                    "definite", (long long)h_info);
     return GSDFT_OK;
 }
 

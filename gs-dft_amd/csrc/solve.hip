@@ -20,13 +20,6 @@ namespace {
 constexpr int kNb = 128;        // block size
 constexpr int kLd = kNb + 1;    // padded LDS row
 
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
 // Solve the diagonal block rows [j0, j0 + nb) in place in x: forward L_jj y = x, or backward
 // L_jj^T d = x. Launched with 1024 threads: all stage the block (16 loads in flight per thread),
 // wave 0 solves. The sweep always runs all 128 steps: rows and columns past nb hold zeros in LDS
