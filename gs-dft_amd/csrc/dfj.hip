@@ -952,6 +952,95 @@ __global__ __launch_bounds__(256) void k_eri_fwd(int64_t n, const double* __rest
     if (live) partial[blockIdx.y * n + a] = acc;
 }
 
+// Symmetric forward over one band of bra slots [A0, A0 + H): (a|b) = (b|a), so each unordered
+// pair-pair is evaluated once, in the workgroup whose bra lanes hold a and whose ket slab holds
+// b >= a (a == b once, as a bra term). The bra lane accumulates c_b F_ab (c = h Pw) as in
+// k_eri_fwd; the ket side c_a F_ab is summed over the wave's lanes (fixed butterfly) for every ket,
+// kept per wave in LDS and written per workgroup (the four waves added in order) to
+// ket_part[x][b - A0] for the whole slab (zeros where a wave had no ket). Lanes with a > b (only
+// near the diagonal) contribute nothing and do not hold the wave in the node loop.
+constexpr int kEriSymSlab = 1024;        // kets per workgroup
+
+__global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __restrict__ rec,
+                                                     int64_t A0, int64_t H,
+                                                     double* __restrict__ bra_part,
+                                                     double* __restrict__ ket_part,
+                                                     unsigned long long* __restrict__ work) {
+    __shared__ double tab[256];
+    __shared__ double kw[4][kEriSymSlab];
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 4 * kEriSymSlab; i += blockDim.x) (&kw[0][0])[i] = 0.0;
+    __syncthreads();
+    const int wv = threadIdx.x >> 6;
+    const int64_t a = A0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t band_end = min(n, A0 + H);
+    const bool live = a < band_end;
+    const double* __restrict__ ra = rec + kEriRec * (live ? a : 0);
+    const double Ta[6] = {ra[0], ra[1], ra[2], ra[3], ra[4], ra[5]};
+    const double Px = live ? ra[6] : kFarAway, Py = live ? ra[7] : kFarAway,
+                 Pz = live ? ra[8] : kFarAway;
+    const double ca = live ? ra[9] * ra[10] : 0.0;
+    const int64_t kb0 = A0 + (int64_t)blockIdx.y * kEriSymSlab;
+    const int64_t kb1 = min(n, kb0 + kEriSymSlab);
+    const int64_t amin = A0 + (int64_t)blockIdx.x * 256 + wv * 64;
+    double acc = 0.0;
+    uint32_t nodes = 0;
+    auto ket = [&](int64_t b, auto maskc) {
+        constexpr bool kMask = decltype(maskc)::value;
+        const double* __restrict__ rb = rec + kEriRec * b;
+        const double cb = rb[9] * rb[10];              // h_b Pw_b, wave-uniform
+        if (cb == 0.0) return;                         // padding and zero weights: J_b is not used
+        const bool off = kMask && a > b;               // this lane's pair-pair is another's
+        const double T[6] = {Ta[0] + rb[0], Ta[1] + rb[1], Ta[2] + rb[2],
+                             Ta[3] + rb[3], Ta[4] + rb[4], Ta[5] + rb[5]};
+        const double d[3] = {Px - rb[6], Py - rb[7], Pz - rb[8]};
+        double adjT[6], Td[3];
+        const EriGeom G = eri_geom(T, d, adjT, Td);
+        double F = 0.0;
+        auto node = [&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr double st = quad_t(t) * quad_t(t);
+            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
+                                                              G.J1), 1.0);
+            const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
+            const NodeVal v = node_val(Es, st * num);
+            F = __builtin_fma(quad_w(t) * v.y0, exp_neg_tab(v.arg, tab), F);
+            if constexpr (kMask)
+                return screen_after(t) && wave_all_beyond(off ? kFarAway : v.z);
+            else
+                return screen_after(t) && wave_all_beyond(v.z);
+        };
+        nodes += node_loop<0>(node);
+        F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
+        if (!off) acc = __builtin_fma(F, cb, acc);
+        const double ks = wave_sum((off || a == b) ? 0.0 : ca * F);
+        if ((threadIdx.x & 63) == 0) kw[wv][b - kb0] = ks;
+    };
+    int64_t b = kb0 > amin ? kb0 : amin;
+    for (; b < kb1 && b < amin + 64; ++b) ket(b, std::true_type{});
+    for (; b < kb1; ++b) ket(b, std::false_type{});
+    count_work(work, live, nodes);
+    __syncthreads();
+    double* kp = ket_part + (int64_t)blockIdx.x * (n - A0) + (kb0 - A0);
+    for (int i = threadIdx.x; i < kb1 - kb0; i += blockDim.x)
+        kp[i] = ((kw[0][i] + kw[1][i]) + kw[2][i]) + kw[3][i];
+    if (live) bra_part[(int64_t)blockIdx.y * H + (a - A0)] = acc;
+}
+
+// Jacc[b] += sum_x ket_part[x][b - A0] (x in order) and, for b in the band, + sum_y
+// bra_part[y][b - A0] (y in order): the band's share of sum_b' c_b' F_bb'.
+__global__ void k_eri_sym_reduce(int64_t n, int64_t A0, int64_t H, int64_t groups, int64_t slabs,
+                                 int64_t acc_stride, const double* __restrict__ bra_part,
+                                 const double* __restrict__ ket_part, double* __restrict__ Jacc) {
+    const int64_t b = A0 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    double s = 0.0;
+    for (int64_t x = 0; x < groups; ++x) s += ket_part[x * (n - A0) + (b - A0)];
+    if (b < A0 + H)
+        for (int64_t y = 0; y < slabs; ++y) s += bra_part[y * acc_stride + (b - A0)];
+    Jacc[b] += s;
+}
+
 // Reverse: per bra slot the moments MJ = sum_b c_b F, MT = sum_b c_b dF/dT (six slots) and
 // Md = sum_b c_b dF/dd, c_b = h_b Pw_b, stored (slabs, 10, n).
 //   node sums: F, A_k = sum g (z - 1/2) s^k, B_k = sum g s^k (k = 1..3), g = f / E;
@@ -2012,8 +2101,18 @@ namespace {
 
 struct EriWs {
     double *A6, *Nrm, *q, *rec3, *rec, *partial, *contrib;
+    double *jacc, *bra_part, *ket_part;     // symmetric forward
+    int64_t band;
     PairOrderWs order;
 };
+
+// Bra band height of the symmetric forward: a multiple of 256, at most 16384, with the band's
+// ket partials ((band / 256) x n doubles) within 1 GiB.
+int64_t eri_band(int64_t n) {
+    const int64_t groups_cap = std::max<int64_t>(1, ((int64_t)1 << 27) / std::max<int64_t>(n, 1));
+    int64_t groups = std::min<int64_t>({(n + 255) / 256, 64, groups_cap});
+    return std::max<int64_t>(groups, 1) * 256;
+}
 
 int layout_eri(Arena& ar, int64_t M, int64_t n, bool grads, EriWs* w) {
     w->A6 = ar.take<double>(6 * M + 1);
@@ -2022,9 +2121,21 @@ int layout_eri(Arena& ar, int64_t M, int64_t n, bool grads, EriWs* w) {
     w->rec3 = ar.take<double>(kRec * n + kRec);
     w->rec = ar.take<double>(kEriRec * n + kEriRec);
     GSDFT_TRY(pair_order_layout(ar, n, &w->order));
-    const Split sp = bwd_split(n, n);
-    w->partial = ar.take<double>(sp.slabs * (grads ? kEriAcc : 1) * n + 1);
-    w->contrib = grads ? ar.take<double>(20 * n + 1) : nullptr;
+    w->jacc = w->bra_part = w->ket_part = nullptr;
+    w->band = 0;
+    if (grads) {
+        const Split sp = bwd_split(n, n);
+        w->partial = ar.take<double>(sp.slabs * kEriAcc * n + 1);
+        w->contrib = ar.take<double>(20 * n + 1);
+    } else {
+        w->band = eri_band(n);
+        const int64_t slabs = (n + kEriSymSlab - 1) / kEriSymSlab;
+        w->jacc = ar.take<double>(n + 1);
+        w->bra_part = ar.take<double>(slabs * w->band + 1);
+        w->ket_part = ar.take<double>((w->band / 256) * n + 1);
+        w->partial = w->jacc;
+        w->contrib = nullptr;
+    }
     return GSDFT_OK;
 }
 
@@ -2089,13 +2200,24 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
     const Split sp = bwd_split(n, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     if (!grads) {
+        // bands of bra slots, each against the kets from its own start on
+        if ((n + kEriSymSlab - 1) / kEriSymSlab > 65535)
+            return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the supported %lld pairs",
+                        (long long)65535 * kEriSymSlab);
+        k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 0.0, w.jacc);
         profile_begin(kProfEriFwd, s);
-        k_eri_fwd<<<grid, 256, 0, s>>>(n, w.rec, sp.per_slab, w.partial,
-                                       profile_work_counter(kProfEriFwd));
+        for (int64_t A0 = 0; A0 < n; A0 += w.band) {
+            const int64_t hb = std::min(w.band, n - A0);
+            dim3 g((unsigned)((hb + 255) / 256),
+                   (unsigned)((n - A0 + kEriSymSlab - 1) / kEriSymSlab));
+            k_eri_fwd_sym<<<g, 256, 0, s>>>(n, w.rec, A0, w.band, w.bra_part, w.ket_part,
+                                            profile_work_counter(kProfEriFwd));
+            k_eri_sym_reduce<<<blocks_for(n - A0, 256), 256, 0, s>>>(
+                n, A0, w.band, g.x, g.y, w.band, w.bra_part, w.ket_part, w.jacc);
+        }
         profile_end(kProfEriFwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_eri_finish<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.order.perm, w.rec,
-                                                        w.partial, J);
+        k_eri_finish<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, w.order.perm, w.rec, w.jacc, J);
     } else {
         profile_begin(kProfEriBwd, s);
         k_eri_bwd<<<grid, 256, 0, s>>>(n, w.rec, sp.per_slab, w.partial,

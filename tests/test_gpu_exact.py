@@ -160,3 +160,33 @@ def test_exact_water8_directional_derivative(g, wl, orc, cuda):
     print(f"[eri] water8 E {E.item():.10e}: directional derivative {dd:.10e} vs central "
           f"difference {fd:.10e}")
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
+
+
+def test_exact_water8_energy_paths_and_sampled_J(g, wl, orc, cuda):
+    """(H2O)8 at full size, where the energy-only pass runs in several bands of bra pairs and
+    evaluates each unordered pair-pair once: its E_J equals the reverse pass's (which evaluates
+    every ordered pair-pair) to round-off, and its J on sampled pairs matches oracle rows of
+    (a|b) Pw over the whole list."""
+    s = wl.make_system(2)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, s.eps, None, True)
+    print(f"[eri] water8 n={len(pi)}", flush=True)
+    basis = g.Splat(quat=_cu(s.quat, True), log_scale=_cu(s.log_scale, True),
+                    centers=_cu(s.centers, True))
+    C = _cu(s.C, True)
+    E_rev = g.screened_coulomb_energy(basis, C, s.occ, pi, pj, valid=w)
+    E_rev.backward()
+    with torch.no_grad():
+        E_fwd = g.screened_coulomb_energy(basis, C, s.occ, pi, pj, valid=w)
+        J = _np(g.screened_coulomb_J(basis, C, s.occ, pi, pj, valid=w))
+    rel = abs(E_fwd.item() - E_rev.item()) / abs(E_rev.item())
+    print(f"[eri] water8 E energy-only {E_fwd.item():.15e} reverse {E_rev.item():.15e} rel {rel:.2e}")
+    assert rel < 1e-12
+    Pw = w * np.sum(s.occ[None, :] * s.C[pi] * s.C[pj], axis=1)
+    rng = np.random.default_rng(7)
+    sel = np.sort(np.concatenate([rng.choice(len(pi), 24, replace=False),
+                                  [0, len(pi) - 1, 16383, 16384, 40000]]))
+    rows = orc.eri_block(s.quat, s.log_scale, s.centers, pi[sel], pj[sel], pi, pj)
+    Jref = rows @ Pw
+    err = float(np.max(np.abs(J[sel] - Jref) / np.abs(Jref)))
+    print(f"[eri] water8 sampled J max elementwise rel {err:.2e}")
+    assert err < 1e-12
