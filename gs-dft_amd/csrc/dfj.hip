@@ -906,56 +906,101 @@ __device__ __forceinline__ EriGeom eri_geom(const double T[6], const double d[3]
     return g;
 }
 
-// Jpart[slab][slot] = sum_{b in slab} Pw_b h_b F_ab (times h_a 2 pi^2.5 in k_eri_finish): one lane
-// per bra slot, the ket records of a slab wave-uniform.
-__global__ __launch_bounds__(256) void k_eri_fwd(int64_t n, const double* __restrict__ rec,
-                                                 int64_t per_slab, double* __restrict__ partial,
-                                                 unsigned long long* __restrict__ work) {
-    __shared__ double tab[256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
-    __syncthreads();
-    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = a < n;
-    const double* __restrict__ ra = rec + kEriRec * (live ? a : 0);
-    const double Ta[6] = {ra[0], ra[1], ra[2], ra[3], ra[4], ra[5]};
-    const double Px = live ? ra[6] : kFarAway, Py = live ? ra[7] : kFarAway,
-                 Pz = live ? ra[8] : kFarAway;
-    const int64_t b0 = blockIdx.y * per_slab;
-    const int64_t b1 = min(n, b0 + per_slab);
-    double acc = 0.0;
-    uint32_t nodes = 0;
-    for (int64_t b = b0; b < b1; ++b) {
-        const double* __restrict__ rb = rec + kEriRec * b;
-        const double cb = rb[9] * rb[10];              // h_b Pw_b, wave-uniform
-        if (cb == 0.0) continue;                       // padding adds exactly 0
-        const double T[6] = {Ta[0] + rb[0], Ta[1] + rb[1], Ta[2] + rb[2],
-                             Ta[3] + rb[3], Ta[4] + rb[4], Ta[5] + rb[5]};
-        const double d[3] = {Px - rb[6], Py - rb[7], Pz - rb[8]};
-        double adjT[6], Td[3];
-        const EriGeom G = eri_geom(T, d, adjT, Td);
-        double F = 0.0;
-        auto node = [&](auto tc) {
-            constexpr int t = decltype(tc)::value;
-            constexpr double st = quad_t(t) * quad_t(t);
-            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
-                                                              G.J1), 1.0);
-            const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
-            const NodeVal v = node_val(Es, st * num);
-            F = __builtin_fma(quad_w(t) * v.y0, exp_neg_tab(v.arg, tab), F);
-            return screen_after(t) && wave_all_beyond(v.z);
-        };
-        nodes += node_loop<0>(node);
-        F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
-        acc = __builtin_fma(F, cb, acc);
+// Cross-lane moves of doubles (two 32-bit halves each). swap32(x, y): x' = [x lanes 0-31, y lanes
+// 0-31], y' = [x lanes 32-63, y lanes 32-63]; swap16 does the same with the 16-lane rows of each
+// half (v_permlane32_swap / v_permlane16_swap); dpp<ctrl> reads the lane that a DPP control names
+// (0x140 row mirror: lane 15 - i of the row; 0x141 half-row mirror: 7 - i of the 8; 0x4e, 0xb1:
+// lane i ^ 2, i ^ 1).
+__device__ __forceinline__ void swap32(double& x, double& y) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
+                                                     false, false);
+    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
+    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
+}
+
+__device__ __forceinline__ void swap16(double& x, double& y) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
+                                                     false, false);
+    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
+    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp(double v) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)a, kCtrl, 0xf, 0xf,
+                                                              false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(a >> 32), kCtrl,
+                                                              0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sums of ten values over the 64 lanes of a wave by a transposing butterfly: at the exchanges
+// that pair lanes across bit 5 (swap32), bit 4 (swap16), bit 3 (row mirror) and bit 2 (half-row
+// mirror) of the lane index each lane keeps half of its partial sums and trades the other half
+// (5, 3, 2, 1 values), then two quad permutes finish. The total of value (b5 ? 5 : 0) + slot,
+// slot = (b4 ? 3 : 0) + (b3 ? 2 : 0) + b2, ends in the lanes with bits 1, 0 clear; returns it and
+// sets *idx to the value's index on the ten such lanes that hold one, -1 elsewhere. The
+// summation order is fixed.
+__device__ __forceinline__ double wave_sum10(const double v[10], int* idx) {
+    const int L = threadIdx.x & 63;
+    const bool b4 = L & 16, b3 = L & 8, b2 = L & 4;
+    double u[6];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        double x = v[i], y = v[5 + i];
+        swap32(x, y);
+        u[i] = x + y;
     }
-    count_work(work, live, nodes);
-    if (live) partial[blockIdx.y * n + a] = acc;
+    u[5] = 0.0;
+    double w[4];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        double x = u[j], y = u[3 + j];
+        swap16(x, y);
+        w[j] = x + y;
+    }
+    w[3] = 0.0;
+    double xk[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const double send = b3 ? w[k] : w[2 + k], keep = b3 ? w[2 + k] : w[k];
+        xk[k] = keep + dpp<0x140>(send);
+    }
+    const double send = b2 ? xk[0] : xk[1], keep = b2 ? xk[1] : xk[0];
+    double y = keep + dpp<0x141>(send);
+    y += dpp<0x4e>(y);
+    y += dpp<0xb1>(y);
+    const int bslot = (b3 ? 2 : 0) + (b2 ? 1 : 0);
+    const int aslot = (b4 ? 3 : 0) + bslot;
+    *idx = ((L & 3) == 0 && bslot <= 2 && aslot <= 4) ? ((L & 32) ? 5 : 0) + aslot : -1;
+    return y;
+}
+
+// Sum of v over the 64 lanes of a wave, in every lane, by the same exchanges as wave_sum10
+// (fixed order).
+__device__ __forceinline__ double wave_sum_x(double v) {
+    double x = v, y = v;
+    swap32(x, y);
+    v = x + y;
+    x = v; y = v;
+    swap16(x, y);
+    v = x + y;
+    v += dpp<0x140>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x4e>(v);
+    v += dpp<0xb1>(v);
+    return v;
 }
 
 // Symmetric forward over one band of bra slots [A0, A0 + H): (a|b) = (b|a), so each unordered
 // pair-pair is evaluated once, in the workgroup whose bra lanes hold a and whose ket slab holds
-// b >= a (a == b once, as a bra term). The bra lane accumulates c_b F_ab (c = h Pw) as in
-// k_eri_fwd; the ket side c_a F_ab is summed over the wave's lanes (fixed butterfly) for every ket,
+// b >= a (a == b once, as a bra term). The bra lane accumulates c_b F_ab (c = h Pw); the ket
+// side c_a F_ab is summed over the wave's lanes (wave_sum_x) for every ket,
 // kept per wave in LDS and written per workgroup (the four waves added in order) to
 // ket_part[x][b - A0] for the whole slab (zeros where a wave had no ket). Lanes with a > b (only
 // near the diagonal) contribute nothing and do not hold the wave in the node loop.
@@ -1013,7 +1058,7 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
         nodes += node_loop<0>(node);
         F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
         if (!off) acc = __builtin_fma(F, cb, acc);
-        const double ks = wave_sum((off || a == b) ? 0.0 : ca * F);
+        const double ks = wave_sum_x((off || a == b) ? 0.0 : ca * F);
         if ((threadIdx.x & 63) == 0) kw[wv][b - kb0] = ks;
     };
     int64_t b = kb0 > amin ? kb0 : amin;
@@ -1041,8 +1086,8 @@ __global__ void k_eri_sym_reduce(int64_t n, int64_t A0, int64_t H, int64_t group
     Jacc[b] += s;
 }
 
-// Reverse: per bra slot the moments MJ = sum_b c_b F, MT = sum_b c_b dF/dT (six slots) and
-// Md = sum_b c_b dF/dd, c_b = h_b Pw_b, stored (slabs, 10, n).
+// Reverse moments of a pair a: MJ = sum_b c_b F, MT = sum_b c_b dF/dT (six slots) and
+// Md = sum_b c_b dF/dd, c_b = h_b Pw_b.
 //   node sums: F, A_k = sum g (z - 1/2) s^k, B_k = sum g s^k (k = 1..3), g = f / E;
 //   dF/dJ_k = A_k, dF/dp_k = -B_(k+1); with p1 = J1 p0 - d.T d and p2 = |T d|^2 - J1 d.T d + J2 p0:
 //   dF/dT = gJ1 I + gJ2 (J1 I - T) + gJ3 adj T - gp1' d d^T
@@ -1050,26 +1095,50 @@ __global__ void k_eri_sym_reduce(int64_t n, int64_t A0, int64_t H, int64_t group
 //   dF/dd = 2 (gp0' d + gp1'' T d + gp2 adj(T) d), primes folding the p1 chain.
 constexpr int kEriAcc = 10;
 
-__global__ __launch_bounds__(256) void k_eri_bwd(int64_t n, const double* __restrict__ rec,
-                                                 int64_t per_slab, double* __restrict__ partial,
-                                                 unsigned long long* __restrict__ work) {
+// Symmetric reverse over one band of bra slots [A0, A0 + H), as k_eri_fwd_sym: each unordered
+// pair-pair once. Per pair-pair the node sums and the chain above give F, gT = dF/dT (six
+// slots) and gd = dF/dd (d = P_a - P_b); the bra lane accumulates c_b (F, gT, gd),
+// and the ket's moments c_a (F, gT, -gd) (T is symmetric in a and b, d changes sign) are summed over
+// the wave (wave_sum10) and written per wave to ket_part[(4 x + wave) * 10 + c][b - A0] for every
+// ket of the workgroup's slab (zeros where the wave had no ket).
+constexpr int kEriSymSlabB = 1024;       // kets per workgroup (reverse)
+
+__global__ __launch_bounds__(256) void k_eri_bwd_sym(int64_t n, const double* __restrict__ rec,
+                                                     int64_t A0, int64_t H,
+                                                     double* __restrict__ bra_part,
+                                                     double* __restrict__ ket_part,
+                                                     unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
-    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = a < n;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t a = A0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t band_end = min(n, A0 + H);
+    const bool live = a < band_end;
     const double* __restrict__ ra = rec + kEriRec * (live ? a : 0);
     const double Ta[6] = {ra[0], ra[1], ra[2], ra[3], ra[4], ra[5]};
     const double Px = live ? ra[6] : kFarAway, Py = live ? ra[7] : kFarAway,
                  Pz = live ? ra[8] : kFarAway;
-    const int64_t b0 = blockIdx.y * per_slab;
-    const int64_t b1 = min(n, b0 + per_slab);
+    const double ca = live ? ra[9] * ra[10] : 0.0;
+    const int64_t kb0 = A0 + (int64_t)blockIdx.y * kEriSymSlabB;
+    const int64_t kb1 = min(n, kb0 + kEriSymSlabB);
+    const int64_t amin = A0 + (int64_t)blockIdx.x * 256 + wv * 64;
+    const int64_t nk = n - A0;
+    double* __restrict__ kp = ket_part + ((int64_t)blockIdx.x * 4 + wv) * kEriAcc * nk;
+    // kets before the wave's first bra: zeros
+    for (int64_t b = kb0 + lane; b < kb1 && b < amin; b += 64)
+        for (int c = 0; c < kEriAcc; ++c) kp[c * nk + (b - A0)] = 0.0;
     double MJ = 0.0, MT[6] = {0, 0, 0, 0, 0, 0}, Md[3] = {0, 0, 0};
     uint32_t nodes = 0;
-    for (int64_t b = b0; b < b1; ++b) {
+    auto ket = [&](int64_t b, auto maskc) {
+        constexpr bool kMask = decltype(maskc)::value;
         const double* __restrict__ rb = rec + kEriRec * b;
         const double cb = rb[9] * rb[10];
-        if (cb == 0.0) continue;
+        if (cb == 0.0) {                               // no moments needed for this ket
+            if (lane < kEriAcc) kp[lane * nk + (b - A0)] = 0.0;
+            return;
+        }
+        const bool off = kMask && a > b;
         const double T[6] = {Ta[0] + rb[0], Ta[1] + rb[1], Ta[2] + rb[2],
                              Ta[3] + rb[3], Ta[4] + rb[4], Ta[5] + rb[5]};
         const double d[3] = {Px - rb[6], Py - rb[7], Pz - rb[8]};
@@ -1093,21 +1162,23 @@ __global__ __launch_bounds__(256) void k_eri_bwd(int64_t n, const double* __rest
             B1 = __builtin_fma(g, st, B1);
             B2 = __builtin_fma(g, st * st, B2);
             B3 = __builtin_fma(g, st * st * st, B3);
-            return screen_after(t) && wave_all_beyond(v.z);
+            if constexpr (kMask)
+                return screen_after(t) && wave_all_beyond(off ? kFarAway : v.z);
+            else
+                return screen_after(t) && wave_all_beyond(v.z);
         };
         nodes += node_loop<0>(node);
         F = (G.p0 == G.p0) ? F : G.p0;
-        // chain to T and d
         const double gp1 = -B2, gp2 = -B3;
-        const double gJ1 = __builtin_fma(gp1, G.p0, A1);             // p1 = J1 p0 - d.T d
+        const double gJ1 = __builtin_fma(gp1, G.p0, A1);
         const double gp0 = __builtin_fma(gp1, G.J1, -B1);
         const double gJ2 = A2, gJ3 = A3;
         const double dTd = __builtin_fma(d[0], Td[0], __builtin_fma(d[1], Td[1], d[2] * Td[2]));
-        // diagonal part: (gJ1 + gJ2 J1 - gp2 dTd + gp2 p0 J1) I
         const double diag = gJ1 + G.J1 * __builtin_fma(gp2, G.p0, gJ2) - gp2 * dTd;
-        const double cT = -__builtin_fma(gp2, G.p0, gJ2);           // coefficient of T
-        const double cdd = -__builtin_fma(gp2, G.J1, gp1);          // coefficient of d d^T
+        const double cT = -__builtin_fma(gp2, G.p0, gJ2);
+        const double cdd = -__builtin_fma(gp2, G.J1, gp1);
         const int rr_[6] = {0, 1, 2, 0, 0, 1}, cc_[6] = {0, 1, 2, 1, 2, 2};
+        double gT[6];
 #pragma unroll
         for (int k = 0; k < 6; ++k) {
             const int r = rr_[k], c = cc_[k];
@@ -1115,23 +1186,67 @@ __global__ __launch_bounds__(256) void k_eri_bwd(int64_t n, const double* __rest
             gt = __builtin_fma(cdd, d[r] * d[c], gt);
             gt = __builtin_fma(gp2, __builtin_fma(Td[r], d[c], d[r] * Td[c]), gt);
             if (r == c) gt += diag;
-            MT[k] = __builtin_fma(cb, gt, MT[k]);
+            gT[k] = gt;
         }
         const double ax = __builtin_fma(adjT[0], d[0], __builtin_fma(adjT[3], d[1], adjT[4] * d[2]));
         const double ay = __builtin_fma(adjT[3], d[0], __builtin_fma(adjT[1], d[1], adjT[5] * d[2]));
         const double az = __builtin_fma(adjT[4], d[0], __builtin_fma(adjT[5], d[1], adjT[2] * d[2]));
-        const double c2 = 2.0 * cb;
-        Md[0] = __builtin_fma(c2, __builtin_fma(gp0, d[0], __builtin_fma(-gp1, Td[0], gp2 * ax)), Md[0]);
-        Md[1] = __builtin_fma(c2, __builtin_fma(gp0, d[1], __builtin_fma(-gp1, Td[1], gp2 * ay)), Md[1]);
-        Md[2] = __builtin_fma(c2, __builtin_fma(gp0, d[2], __builtin_fma(-gp1, Td[2], gp2 * az)), Md[2]);
-        MJ = __builtin_fma(F, cb, MJ);
-    }
+        const double gd[3] = {2.0 * __builtin_fma(gp0, d[0], __builtin_fma(-gp1, Td[0], gp2 * ax)),
+                              2.0 * __builtin_fma(gp0, d[1], __builtin_fma(-gp1, Td[1], gp2 * ay)),
+                              2.0 * __builtin_fma(gp0, d[2], __builtin_fma(-gp1, Td[2], gp2 * az))};
+        const double cbra = off ? 0.0 : cb;
+        MJ = __builtin_fma(F, cbra, MJ);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) MT[k] = __builtin_fma(cbra, gT[k], MT[k]);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) Md[k] = __builtin_fma(cbra, gd[k], Md[k]);
+        const double cket = (off || a == b) ? 0.0 : ca;
+        const double v[kEriAcc] = {cket * F, cket * gT[0], cket * gT[1], cket * gT[2],
+                                   cket * gT[3], cket * gT[4], cket * gT[5],
+                                   -cket * gd[0], -cket * gd[1], -cket * gd[2]};
+        int idx;
+        const double tot = wave_sum10(v, &idx);
+        if (idx >= 0) kp[idx * nk + (b - A0)] = tot;
+    };
+    int64_t b = kb0 > amin ? kb0 : amin;
+    for (; b < kb1 && b < amin + 64; ++b) ket(b, std::true_type{});
+    for (; b < kb1; ++b) ket(b, std::false_type{});
     count_work(work, live, nodes);
     if (!live) return;
-    double* o = partial + (int64_t)blockIdx.y * kEriAcc * n + a;
-    const double v[kEriAcc] = {MJ, MT[0], MT[1], MT[2], MT[3], MT[4], MT[5], Md[0], Md[1], Md[2]};
+    double* o = bra_part + (int64_t)blockIdx.y * kEriAcc * H + (a - A0);
+    const double mv[kEriAcc] = {MJ, MT[0], MT[1], MT[2], MT[3], MT[4], MT[5], Md[0], Md[1], Md[2]};
 #pragma unroll
-    for (int c = 0; c < kEriAcc; ++c) o[(int64_t)c * n] = v[c];
+    for (int c = 0; c < kEriAcc; ++c) o[(int64_t)c * H] = mv[c];
+}
+
+// The band's share of every pair's ten reverse moments, in a fixed order: first
+// macc[c][b] += sum_x ket_part[x * 10 + c][b - A0] (x in order) for every b >= A0 (one thread per b),
+// then macc[c][b] += sum_y bra_part[y * 10 + c][b - A0] (y in order) for b in the band (one thread per
+// (c, b)).
+__global__ void k_eri_sym_reduce10_ket(int64_t n, int64_t A0, int64_t waves,
+                                       const double* __restrict__ ket_part,
+                                       double* __restrict__ macc) {
+    const int64_t b = A0 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    const int64_t nk = n - A0;
+#pragma unroll
+    for (int c = 0; c < kEriAcc; ++c) {
+        double s = 0.0;
+        for (int64_t x = 0; x < waves; ++x) s += ket_part[(x * kEriAcc + c) * nk + (b - A0)];
+        macc[(int64_t)c * n + b] += s;
+    }
+}
+
+__global__ void k_eri_sym_reduce10_bra(int64_t n, int64_t A0, int64_t H, int64_t slabs,
+                                       const double* __restrict__ bra_part,
+                                       double* __restrict__ macc) {
+    const int64_t hb = min(H, n - A0);
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= kEriAcc * hb) return;
+    const int64_t c = t / hb, i = t % hb;
+    double s = 0.0;
+    for (int64_t y = 0; y < slabs; ++y) s += bra_part[(y * kEriAcc + c) * H + i];
+    macc[c * n + A0 + i] += s;
 }
 
 // J[perm[slot]] = h_a 2 pi^2.5 sum_slabs Jpart (0 on zero-weight entries).
@@ -2101,7 +2216,7 @@ namespace {
 
 struct EriWs {
     double *A6, *Nrm, *q, *rec3, *rec, *partial, *contrib;
-    double *jacc, *bra_part, *ket_part;     // symmetric forward
+    double *jacc, *bra_part, *ket_part;     // symmetric passes (jacc: J, or the ten moments)
     int64_t band;
     PairOrderWs order;
 };
@@ -2111,6 +2226,14 @@ struct EriWs {
 int64_t eri_band(int64_t n) {
     const int64_t groups_cap = std::max<int64_t>(1, ((int64_t)1 << 27) / std::max<int64_t>(n, 1));
     int64_t groups = std::min<int64_t>({(n + 255) / 256, 64, groups_cap});
+    return std::max<int64_t>(groups, 1) * 256;
+}
+
+// The same for the reverse, whose ket partials are (band / 64) x 10 x n doubles, within 8 GiB
+// (fewer, fuller band launches: the reverse is the longer pass).
+int64_t eri_band10(int64_t n) {
+    const int64_t waves_cap = ((int64_t)1 << 30) / (kEriAcc * std::max<int64_t>(n, 1));
+    const int64_t groups = std::min<int64_t>({(n + 255) / 256, 64, waves_cap / 4});
     return std::max<int64_t>(groups, 1) * 256;
 }
 
@@ -2124,8 +2247,12 @@ int layout_eri(Arena& ar, int64_t M, int64_t n, bool grads, EriWs* w) {
     w->jacc = w->bra_part = w->ket_part = nullptr;
     w->band = 0;
     if (grads) {
-        const Split sp = bwd_split(n, n);
-        w->partial = ar.take<double>(sp.slabs * kEriAcc * n + 1);
+        w->band = eri_band10(n);
+        const int64_t slabs = (n + kEriSymSlabB - 1) / kEriSymSlabB;
+        w->jacc = ar.take<double>(kEriAcc * n + 1);
+        w->bra_part = ar.take<double>(slabs * kEriAcc * w->band + 1);
+        w->ket_part = ar.take<double>((w->band / 64) * kEriAcc * n + 1);
+        w->partial = w->jacc;
         w->contrib = ar.take<double>(20 * n + 1);
     } else {
         w->band = eri_band(n);
@@ -2197,8 +2324,6 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
     k_eri_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, w.order.perm, pi, pj, w.A6, centers, w.Nrm,
                                                  w.q, w.rec);
     GSDFT_HIP(hipGetLastError());
-    const Split sp = bwd_split(n, n);
-    dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     if (!grads) {
         // bands of bra slots, each against the kets from its own start on
         if ((n + kEriSymSlab - 1) / kEriSymSlab > 65535)
@@ -2219,14 +2344,27 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
         GSDFT_HIP(hipGetLastError());
         k_eri_finish<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, w.order.perm, w.rec, w.jacc, J);
     } else {
+        if ((n + kEriSymSlabB - 1) / kEriSymSlabB > 65535)
+            return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the supported %lld pairs",
+                        (long long)65535 * kEriSymSlabB);
+        k_fill<<<blocks_for(kEriAcc * n, 256), 256, 0, s>>>(kEriAcc * n, 0.0, w.jacc);
         profile_begin(kProfEriBwd, s);
-        k_eri_bwd<<<grid, 256, 0, s>>>(n, w.rec, sp.per_slab, w.partial,
-                                       profile_work_counter(kProfEriBwd));
+        for (int64_t A0 = 0; A0 < n; A0 += w.band) {
+            const int64_t hb = std::min(w.band, n - A0);
+            dim3 g((unsigned)((hb + 255) / 256),
+                   (unsigned)((n - A0 + kEriSymSlabB - 1) / kEriSymSlabB));
+            k_eri_bwd_sym<<<g, 256, 0, s>>>(n, w.rec, A0, w.band, w.bra_part, w.ket_part,
+                                            profile_work_counter(kProfEriBwd));
+            k_eri_sym_reduce10_ket<<<blocks_for(n - A0, 256), 256, 0, s>>>(
+                n, A0, 4 * (int64_t)g.x, w.ket_part, w.jacc);
+            k_eri_sym_reduce10_bra<<<blocks_for(kEriAcc * hb, 256), 256, 0, s>>>(
+                n, A0, w.band, g.y, w.bra_part, w.jacc);
+        }
         profile_end(kProfEriBwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_eri_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, w.order.perm, pi, pj,
-                                                          w.A6, centers, w.Nrm, w.rec,
-                                                          w.partial, J, w.contrib);
+        k_eri_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, w.order.perm, pi, pj, w.A6,
+                                                          centers, w.Nrm, w.rec, w.jacc, J,
+                                                          w.contrib);
     }
     GSDFT_HIP(hipGetLastError());
     // E_J = 1/2 sum_a Pw_a J_a (gs_dft/coulomb/stream.py:319-320), fixed summation order
