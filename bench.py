@@ -258,12 +258,11 @@ def main() -> int:
     return 0
 
 
-# Nuclear attraction, per (nucleus, pair) integral at 20 nodes: the pair pass is the three-centre
-# reverse kernel (the same per-integral figure); the nuclear-gradient pass evaluates each node's
-# value and three moments (Pn, Qn, 1/sqrt, 1/Pn, exp as in the forward, then g = f/Pn and three
-# fma: 17 + 2 + 7 flops) after a prologue of d, A d, A^2 d, q0..q2 (51) and an epilogue of 12.
-NUC_ATOM_PER_INTEGRAL, NUC_ATOM_PER_NODE = 63, 26
-FLOPS_NUC_ATOM = NUC_ATOM_PER_INTEGRAL + NODES * NUC_ATOM_PER_NODE     # 583
+# Nuclear attraction, per (nucleus, pair) integral at 20 nodes: one pass of the three-centre
+# reverse kernel over point-charge records (the same per-integral figure) that also forms the
+# nucleus' force from its node sums: A^2 d (15), the three coefficients (3) and the scaled vector
+# (18), 36 flops per integral; the cross-lane sums are per wave, not per integral.
+FLOPS_NUC_PAIR = FLOPS_BWD + 36                                        # 816
 
 
 def run_nuclear(args) -> int:
@@ -316,20 +315,16 @@ def run_nuclear(args) -> int:
     pair_ms, pair_k = _lib.profile_read(_lib.PROF_NUC_PAIRS, reset=True)
     atom_ms, atom_k = _lib.profile_read(_lib.PROF_NUC_ATOMS, reset=True)
     pair_nodes = _lib.profile_read_work(_lib.PROF_NUC_PAIRS, reset=True) / max(pair_k, 1)
-    atom_nodes = _lib.profile_read_work(_lib.PROF_NUC_ATOMS, reset=True) / max(atom_k, 1)
+    _lib.profile_read_work(_lib.PROF_NUC_ATOMS, reset=True)
     _lib.profile_enable(False)
     pair_ms /= max(pair_k, 1)
     atom_ms /= max(atom_k, 1)
-    pair_tf = integrals * FLOPS_BWD / (pair_ms * 1e-3)
-    atom_tf = integrals * FLOPS_NUC_ATOM / (atom_ms * 1e-3)
-    log(f"E_ext={E.item():.12e} step {wall * 1e3:.2f} ms; pair pass {pair_ms:.2f} ms "
-        f"({pair_tf / 1e12:.2f} TFLOP/s, {pair_nodes / (NODES * integrals):.3f} of nodes), "
-        f"nuclear-gradient pass {atom_ms:.2f} ms ({atom_tf / 1e12:.2f} TFLOP/s, "
-        f"{atom_nodes / (NODES * integrals):.3f} of nodes)")
-    if pair_ms >= atom_ms:
-        dom = ("pair pass (k_gamma_bwd over point-charge records)", pair_ms, FLOPS_BWD, pair_tf)
-    else:
-        dom = ("nuclear-gradient pass (k_vne_atom_grad)", atom_ms, FLOPS_NUC_ATOM, atom_tf)
+    pair_tf = integrals * FLOPS_NUC_PAIR / (pair_ms * 1e-3)
+    log(f"E_ext={E.item():.12e} step {wall * 1e3:.2f} ms; pair pass with nuclear forces "
+        f"{pair_ms:.2f} ms ({pair_tf / 1e12:.2f} TFLOP/s, {pair_nodes / (NODES * integrals):.3f} "
+        f"of nodes), force sums over pair blocks {atom_ms:.2f} ms")
+    dom = ("pair pass with nuclear forces (k_gamma_bwd<false, true> over point-charge records)",
+           pair_ms, FLOPS_NUC_PAIR, pair_tf)
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -372,9 +367,8 @@ def run_nuclear(args) -> int:
                      "traffic": None, "flops_per_integral": dom[2],
                      "integrals_per_launch": integrals, "kernel_ms": dom[1],
                      "note": "FP64 vector bound; fixed per-integral work at 20 nodes"},
-        "kernels": {"pair_pass_ms": pair_ms, "nuclear_gradient_ms": atom_ms,
-                    "pair_nodes_evaluated_frac": pair_nodes / (NODES * integrals),
-                    "nuclear_nodes_evaluated_frac": atom_nodes / (NODES * integrals)},
+        "kernels": {"pair_pass_ms": pair_ms, "force_sums_ms": atom_ms,
+                    "pair_nodes_evaluated_frac": pair_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
         "E_ext": E.item(),
     }

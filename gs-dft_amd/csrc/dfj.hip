@@ -336,6 +336,62 @@ __global__ void k_slot_sum(int64_t N, int64_t G, int64_t groups, const double* _
 
 // ------------------------------------------------------------------ reverse
 
+// Cross-lane moves of doubles (two 32-bit halves each). swap32(x, y): x' = [x lanes 0-31, y lanes
+// 0-31], y' = [x lanes 32-63, y lanes 32-63]; swap16 does the same with the 16-lane rows of each
+// half (v_permlane32_swap / v_permlane16_swap); dpp<ctrl> reads the lane that a DPP control names
+// (0x140 row mirror: lane 15 - i of the row; 0x141 half-row mirror: 7 - i of the 8; 0x4e, 0xb1:
+// lane i ^ 2, i ^ 1).
+__device__ __forceinline__ void swap32(double& x, double& y) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
+    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
+                                                     false, false);
+    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
+    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
+}
+
+__device__ __forceinline__ void swap16(double& x, double& y) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
+    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
+                                                     false, false);
+    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
+    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp(double v) {
+    const uint64_t a = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)a, kCtrl, 0xf, 0xf,
+                                                              false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(a >> 32), kCtrl,
+                                                              0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sums of three values over the 64 lanes of a wave (v0, v1 paired across lane bit 5, v2 with a
+// zero; then across bit 4; then the row steps of wave_sum_x): the totals of v0, v2 and v1 end in
+// lanes 0, 16 and 32. Returns this lane's total and sets *comp to its component there, -1
+// elsewhere. Fixed order.
+__device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
+    double x = v[0], y = v[1];
+    swap32(x, y);
+    double u0 = x + y;
+    x = v[2]; y = 0.0;
+    swap32(x, y);
+    double u1 = x + y;
+    swap16(u0, u1);
+    double w = u0 + u1;
+    w += dpp<0x140>(w);
+    w += dpp<0x141>(w);
+    w += dpp<0x4e>(w);
+    w += dpp<0xb1>(w);
+    const int L = threadIdx.x & 63;
+    *comp = L == 0 ? 0 : L == 32 ? 1 : L == 16 ? 2 : -1;
+    return w;
+}
+
+
 // Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wp_t | s_t^2 |
 // s_t^3. Records are stored centre-grouped: with G = N / M exponent scales (the product aux is
 // scale-major, P = s M + m, every scale of splat m at one centre), the record of P sits at slot
@@ -384,12 +440,21 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // centre: C0..C2 = sum u dQ0..2 over the group, then Vc += C0 d, ..., Sb += C2 d d^T.
 // With kLaneU the cotangent of (P|a) is not separable: u = x[3] * ut[slot * ldu + p] per lane
 // (the exchange's dE/d(P|a), stored slot-major).
-template <bool kLaneU>
+// With kAtomF the records are nuclei (point charges) and the pass also forms every nucleus' force
+// from the same node sums: per (nucleus p, pair a) the vector 2 KN_a q_a (f0 d + f1 Ah d + f2 Ah^2 d),
+// f0 = -I3 sum g s, f1 = -(I1 sum g s^2 + sum g s^3), f2 = sum g s^2 (dF/dR of
+// gs_dft/ks/forces.py:53-77 through pairs.py:348-370), summed over the wave (wave_sum3), then over
+// the four waves in LDS per chunk of 64 nuclei, into atom_part[pair block][p][3] (times -Z_p 2 pi
+// later).
+constexpr int kAtomChunk = 64;
+
+template <bool kLaneU, bool kAtomF = false>
 __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
-    const double* __restrict__ ut, int64_t ldu) {
+    const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part) {
     __shared__ double tab[256];
+    __shared__ double af[kAtomF ? 4 : 1][kAtomF ? kAtomChunk : 1][3];
     // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
     // slot per lane, structure of arrays) rather than in registers across the loop.
     __shared__ double geo[9][256];
@@ -409,6 +474,9 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     double Sa[6] = {0, 0, 0, 0, 0, 0}, Sb[6] = {0, 0, 0, 0, 0, 0};
     double C0 = 0, C1 = 0, C2 = 0;
     double d[3] = {0, 0, 0}, q0 = 0, q1 = 0, X0 = 0, rr = 0;
+    double ad[3] = {0, 0, 0}, a2d[3] = {0, 0, 0};      // Ah d, Ah^2 d (kAtomF)
+    const double cq2 = kAtomF && live ? 2.0 * r[13] * r[14] : 0.0;
+    int64_t chunk0 = blockIdx.y * per_slab;
     auto flush = [&]() {
         const double e1x = C1 * d[0], e1y = C1 * d[1], e1z = C1 * d[2];
         const double e2x = C2 * d[0], e2y = C2 * d[1], e2z = C2 * d[2];
@@ -452,6 +520,12 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             const double q2 = ax * ax + ay * ay + az * az;
             X0 = I3 * q0;
             rr = I1 * q1 - q2;
+            if constexpr (kAtomF) {
+                ad[0] = ax; ad[1] = ay; ad[2] = az;
+                a2d[0] = xx * ax + xy * ay + xz * az;
+                a2d[1] = xy * ax + yy * ay + yz * az;
+                a2d[2] = xz * ax + yz * ay + zz * az;
+            }
         }
         double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
         auto node = [&](auto tc) {
@@ -481,6 +555,25 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         C0 = __builtin_fma(u, -gs1, C0);
         C1 = __builtin_fma(u, -gs2, C1);
         C2 = __builtin_fma(u, -gs3, C2);
+        if constexpr (kAtomF) {
+            const double f0 = -I3 * gs1, f1 = -__builtin_fma(I1, gs2, gs3), f2 = gs2;
+            double fv[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                fv[c] = cq2 * __builtin_fma(f0, d[c], __builtin_fma(f1, ad[c], f2 * a2d[c]));
+            int comp;
+            const double tot = wave_sum3(fv, &comp);
+            if (comp >= 0) af[threadIdx.x >> 6][p - chunk0][comp] = tot;
+            if (p - chunk0 == kAtomChunk - 1 || p == p1 - 1) {     // workgroup-uniform
+                __syncthreads();
+                const int i = threadIdx.x / 3, c = threadIdx.x % 3;
+                if (threadIdx.x < 3 * kAtomChunk && chunk0 + i <= p)
+                    atom_part[((int64_t)blockIdx.x * N + chunk0 + i) * 3 + c] =
+                        ((af[0][i][c] + af[1][i][c]) + af[2][i][c]) + af[3][i][c];
+                __syncthreads();
+                chunk0 = p + 1;
+            }
+        }
     }
     flush();
     count_work(work, live, nodes);
@@ -754,86 +847,6 @@ __global__ void k_atom_rec(int64_t n_atoms, const double* __restrict__ coords,
     }
 }
 
-// dE/dR_A of E = sum_a q_a V_a: one lane per atom, the pairs of a slab wave-uniform (scalar loads
-// of the list-order records); per-slab partial sums (slabs, n_atoms, 3), summed in fixed order.
-// With F = sum_t w_t Pn^(-1/2) e^(-s Qn/Pn) and g_t = f_t / Pn: dF/dq0 = -I3 sum g s,
-// dF/dq1 = -(I1 sum g s^2 + sum g s^3), dF/dq2 = sum g s^2, and dF/dR = 2 (dF/dq0 d + dF/dq1 Ah d
-// + dF/dq2 Ah^2 d) for d = R - Pa.
-__global__ __launch_bounds__(256) void k_vne_atom_grad(int64_t n_atoms,
-                                                       const double* __restrict__ coords,
-                                                       const double* __restrict__ charges,
-                                                       int64_t n, const double* __restrict__ rec,
-                                                       int64_t per_slab,
-                                                       double* __restrict__ partial,
-                                                       unsigned long long* __restrict__ work) {
-    __shared__ double tab[256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
-    __syncthreads();
-    const int64_t A = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = A < n_atoms;
-    const double Rx = live ? coords[3 * A] : kFarAway, Ry = live ? coords[3 * A + 1] : kFarAway,
-                 Rz = live ? coords[3 * A + 2] : kFarAway;
-    const int64_t a0 = blockIdx.y * per_slab;
-    const int64_t a1 = min(n, a0 + per_slab);
-    double gx = 0.0, gy = 0.0, gz = 0.0;
-    uint32_t nodes = 0;
-    for (int64_t a = a0; a < a1; ++a) {
-        const double* __restrict__ r = rec + kRec * a;
-        const double c = r[13] * r[14];          // KN_a q_a, wave-uniform
-        if (c == 0.0) continue;                  // zero weight or zero density: adds exactly 0
-        const double I1 = r[0], I2 = r[1], I3 = r[2];
-        const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
-        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
-        const double ax = xx * dx + xy * dy + xz * dz;
-        const double ay = xy * dx + yy * dy + yz * dz;
-        const double az = xz * dx + yz * dy + zz * dz;
-        const double bx = xx * ax + xy * ay + xz * az;
-        const double by = xy * ax + yy * ay + yz * az;
-        const double bz = xz * ax + yz * ay + zz * az;
-        const double q0 = dx * dx + dy * dy + dz * dz;
-        const double q1 = dx * ax + dy * ay + dz * az;
-        const double q2 = ax * ax + ay * ay + az * az;
-        const double X0 = I3 * q0;
-        const double rr = I1 * q1 - q2;
-        double gs1 = 0.0, gs2 = 0.0, gs3 = 0.0;
-        auto node = [&](auto tc) {
-            constexpr int t = decltype(tc)::value;
-            constexpr double st = quad_t(t) * quad_t(t);
-            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
-            const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const NodeVal v = node_val(Pn, st * Qn);
-            const double g = ((quad_w(t) * v.y0) * exp_neg_tab(v.arg, tab)) * v.ip;
-            gs1 = __builtin_fma(g, st, gs1);
-            gs2 = __builtin_fma(g, st * st, gs2);
-            gs3 = __builtin_fma(g, st * st * st, gs3);
-            return screen_after(t) && wave_all_beyond(v.z);
-        };
-        nodes += node_loop<0>(node);
-        const double f0 = -I3 * gs1, f1 = -(I1 * gs2 + gs3), f2 = gs2;
-        const double s2 = 2.0 * c;
-        gx = __builtin_fma(s2, f0 * dx + f1 * ax + f2 * bx, gx);
-        gy = __builtin_fma(s2, f0 * dy + f1 * ay + f2 * by, gy);
-        gz = __builtin_fma(s2, f0 * dz + f1 * az + f2 * bz, gz);
-    }
-    count_work(work, live, nodes);
-    if (!live) return;
-    const double u = -charges[A] * kPrefNuc;
-    double* o = partial + ((int64_t)blockIdx.y * n_atoms + A) * 3;
-    o[0] = u * gx;
-    o[1] = u * gy;
-    o[2] = u * gz;
-}
-
-// out[i] (i < count) = sum over slabs of partial[slab * count + i], fixed order.
-__global__ void k_slab_sum_flat(int64_t count, int64_t slabs, const double* __restrict__ partial,
-                                double* __restrict__ out) {
-    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (i >= count) return;
-    double s = 0.0;
-    for (int64_t k = 0; k < slabs; ++k) s += partial[k * count + i];
-    out[i] = s;
-}
-
 // ------------------------------------------------------------------ exact pair-pair Coulomb
 // gs_dft/coulomb/stream.py:249-281,296-320: (a|b) = KN_a KN_b (2/sqrt(pi)) sum_t w_t pi^3
 // det(G_t)^(-1/2) exp(-quad_t), G_t the 6x6 block precision [[A_a + sI, -sI], [-sI, A_b + sI]]
@@ -904,39 +917,6 @@ __device__ __forceinline__ EriGeom eri_geom(const double T[6], const double d[3]
     const double az = __builtin_fma(adjT[4], d[0], __builtin_fma(adjT[5], d[1], adjT[2] * d[2]));
     g.p2 = __builtin_fma(d[0], ax, __builtin_fma(d[1], ay, d[2] * az));
     return g;
-}
-
-// Cross-lane moves of doubles (two 32-bit halves each). swap32(x, y): x' = [x lanes 0-31, y lanes
-// 0-31], y' = [x lanes 32-63, y lanes 32-63]; swap16 does the same with the 16-lane rows of each
-// half (v_permlane32_swap / v_permlane16_swap); dpp<ctrl> reads the lane that a DPP control names
-// (0x140 row mirror: lane 15 - i of the row; 0x141 half-row mirror: 7 - i of the 8; 0x4e, 0xb1:
-// lane i ^ 2, i ^ 1).
-__device__ __forceinline__ void swap32(double& x, double& y) {
-    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
-    const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)b, false, false);
-    const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
-                                                     false, false);
-    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
-    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
-}
-
-__device__ __forceinline__ void swap16(double& x, double& y) {
-    const uint64_t a = __builtin_bit_cast(uint64_t, x), b = __builtin_bit_cast(uint64_t, y);
-    const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)b, false, false);
-    const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32),
-                                                     false, false);
-    x = __builtin_bit_cast(double, ((uint64_t)hi[0] << 32) | lo[0]);
-    y = __builtin_bit_cast(double, ((uint64_t)hi[1] << 32) | lo[1]);
-}
-
-template <int kCtrl>
-__device__ __forceinline__ double dpp(double v) {
-    const uint64_t a = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)a, kCtrl, 0xf, 0xf,
-                                                              false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(a >> 32), kCtrl,
-                                                              0xf, 0xf, false);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
 // Sums of ten values over the 64 lanes of a wave by a transposing butterfly: at the exchanges
@@ -1413,19 +1393,6 @@ Split bwd_split(int64_t N, int64_t n) {
     return Split{(N + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
 }
 
-// Atom-gradient pass of the nuclear attraction: ceil(n_atoms/256) workgroups per slab of pairs.
-Split atom_split(int64_t n_atoms, int64_t n) {
-    const int64_t groups = n_atoms > 0 ? (n_atoms + 255) / 256 : 1;
-    const int64_t target = 256 * 4 * 4;
-    int64_t slabs = (target + groups - 1) / groups;
-    const int64_t max_slabs = (n + 63) / 64;                // at least 64 pairs per slab
-    if (slabs > max_slabs) slabs = max_slabs;
-    if (slabs < 1) slabs = 1;
-    if (slabs > 65535) slabs = 65535;
-    const int64_t per = n > 0 ? (n + slabs - 1) / slabs : 1;
-    return Split{n > 0 ? (n + per - 1) / per : 1, per};
-}
-
 struct GammaWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
     double *aux, *acc, *contrib, *rec_sorted;
@@ -1627,7 +1594,8 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* T
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfExchBwd, s);
     k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab,
-                                           w.part, profile_work_counter(kProfExchBwd), Tbar, ldt);
+                                           w.part, profile_work_counter(kProfExchBwd), Tbar, ldt,
+                                           nullptr);
     profile_end(kProfExchBwd, s);
     GSDFT_HIP(hipGetLastError());
     k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);
@@ -2035,7 +2003,8 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
         k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
-                                                profile_work_counter(kProfGammaBwd), nullptr, 0);
+                                                profile_work_counter(kProfGammaBwd), nullptr, 0,
+                                                nullptr);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
         k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPref3c, w.pair_order.perm, pi,
@@ -2058,14 +2027,45 @@ namespace {
 
 struct ExternalWs {
     GammaWs g;
-    double* atom_partial;
+    double* atom_partial;       // (pair blocks, n_atoms, 3) from the pair pass
+    double* atom_groups;        // (ceil(pair blocks / 256), n_atoms, 3)
 };
+
+constexpr int64_t kAtomGroup = 256;   // pair blocks per first-stage sum of the nuclear forces
+
+inline int64_t pair_blocks(int64_t n) { return n > 0 ? (n + 255) / 256 : 1; }
 
 int layout_external(Arena& ar, int64_t M, int64_t n, int64_t n_atoms, ExternalWs* w) {
     GSDFT_TRY(layout_gamma(ar, M, n_atoms, n, true, &w->g));
-    const Split sa = atom_split(n_atoms, n);
-    w->atom_partial = ar.take<double>(sa.slabs * n_atoms * 3 + 3);
+    const int64_t blocks = pair_blocks(n);
+    w->atom_partial = ar.take<double>(blocks * n_atoms * 3 + 3);
+    w->atom_groups = ar.take<double>(((blocks + kAtomGroup - 1) / kAtomGroup) * n_atoms * 3 + 3);
     return GSDFT_OK;
+}
+
+// out[g][i] = sum of part[b][i] over the pair blocks b of group g (kAtomGroup each), in order.
+__global__ void k_atom_sum_groups(int64_t count, int64_t blocks, const double* __restrict__ part,
+                                  double* __restrict__ out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t groups = (blocks + kAtomGroup - 1) / kAtomGroup;
+    if (t >= groups * count) return;
+    const int64_t g = t / count, i = t % count;
+    const int64_t b1 = min(blocks, (g + 1) * kAtomGroup);
+    double s = 0.0;
+    for (int64_t b = g * kAtomGroup; b < b1; ++b) s += part[b * count + i];
+    out[g * count + i] = s;
+}
+
+// datoms[A][c] = -Z_A 2 pi sum_g groups[g][A][c], in group order.
+__global__ void k_atom_force_finish(int64_t n_atoms, int64_t groups,
+                                    const double* __restrict__ gsum,
+                                    const double* __restrict__ charges,
+                                    double* __restrict__ datoms) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= 3 * n_atoms) return;
+    double s = 0.0;
+    for (int64_t g = 0; g < groups; ++g) s += gsum[g * 3 * n_atoms + i];
+    datoms[i] = -charges[i / 3] * kPrefNuc * s;
 }
 
 // V (n) = the nuclear attraction of every listed pair (J of the reverse kernel with the nuclei as
@@ -2074,7 +2074,7 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
                   int64_t k, const double* C, const double* occ, int64_t n, const int32_t* pi,
                   const int32_t* pj, const double* weight, int64_t n_atoms,
                   const double* atom_coords, const double* atom_charges, double* V,
-                  ExternalWs& w, hipStream_t s) {
+                  ExternalWs& w, bool atom_forces, hipStream_t s) {
     GSDFT_TRY(gamma_prologue(M, quat, log_scale, centers, k, C, occ, n_atoms, nullptr, n, pi, pj,
                              weight, w.g, s));
     k_atom_rec<<<blocks_for(n_atoms, 256), 256, 0, s>>>(n_atoms, atom_coords, atom_charges,
@@ -2086,9 +2086,15 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
     const Split sp = bwd_split(n_atoms, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfNucPairs, s);
-    k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab,
-                                            w.g.acc, profile_work_counter(kProfNucPairs), nullptr,
-                                            0);
+    if (atom_forces)
+        k_gamma_bwd<false, true><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux,
+                                                      sp.per_slab, w.g.acc,
+                                                      profile_work_counter(kProfNucPairs),
+                                                      nullptr, 0, w.atom_partial);
+    else
+        k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab,
+                                                w.g.acc, profile_work_counter(kProfNucPairs),
+                                                nullptr, 0, nullptr);
     profile_end(kProfNucPairs, s);
     GSDFT_HIP(hipGetLastError());
     k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPrefNuc,
@@ -2135,7 +2141,7 @@ extern "C" int gsdft_nuclear_pairs(int64_t M, const double* quat, const double* 
     GSDFT_TRY(layout_external(ar, M, n, n_atoms, &w));
     if (!w.atom_partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_nuclear_pairs: workspace too small");
     return external_pass(M, quat, log_scale, centers, 0, nullptr, nullptr, n, pi, pj, nullptr,
-                         n_atoms, atom_coords, atom_charges, V, w, s);
+                         n_atoms, atom_coords, atom_charges, V, w, false, s);
 }
 
 extern "C" int gsdft_external_energy(
@@ -2172,7 +2178,7 @@ extern "C" int gsdft_external_energy(
         return GSDFT_OK;
     }
     GSDFT_TRY(external_pass(M, quat, log_scale, centers, k, C, occ, n, pi, pj, weight, n_atoms,
-                            atom_coords, atom_charges, V, w, s));
+                            atom_coords, atom_charges, V, w, datoms != nullptr, s));
     // E = sum_a q_a V_a (gs_dft/screening/pairs.py:429-432), fixed summation order
     k_scaled_dot<<<1, 1024, 0, s>>>(n, w.g.q, V, 1.0, energy);
     GSDFT_HIP(hipGetLastError());
@@ -2186,16 +2192,14 @@ extern "C" int gsdft_external_energy(
                             dC, s));
     }
     if (datoms) {
-        const Split sa = atom_split(n_atoms, n);
-        dim3 grid((unsigned)((n_atoms + 255) / 256), (unsigned)sa.slabs);
+        // the pair pass left each pair block's force on every nucleus: sum them in fixed order
+        const int64_t blocks = pair_blocks(n), groups = (blocks + kAtomGroup - 1) / kAtomGroup;
         profile_begin(kProfNucAtoms, s);
-        k_vne_atom_grad<<<grid, 256, 0, s>>>(n_atoms, atom_coords, atom_charges, n, w.g.rec,
-                                             sa.per_slab, w.atom_partial,
-                                             profile_work_counter(kProfNucAtoms));
+        k_atom_sum_groups<<<blocks_for(groups * 3 * n_atoms, 256), 256, 0, s>>>(
+            3 * n_atoms, blocks, w.atom_partial, w.atom_groups);
+        k_atom_force_finish<<<blocks_for(3 * n_atoms, 256), 256, 0, s>>>(
+            n_atoms, groups, w.atom_groups, atom_charges, datoms);
         profile_end(kProfNucAtoms, s);
-        GSDFT_HIP(hipGetLastError());
-        k_slab_sum_flat<<<blocks_for(3 * n_atoms, 256), 256, 0, s>>>(3 * n_atoms, sa.slabs,
-                                                                     w.atom_partial, datoms);
         GSDFT_HIP(hipGetLastError());
     }
     return GSDFT_OK;

@@ -234,8 +234,8 @@ int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const
 
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
- * 6 nuclear attraction per pair (values and splat moments), 7 nuclear attraction per nucleus
- * (nuclear gradient), 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and
+ * 6 nuclear attraction per pair (values, splat moments and, with nuclear gradients, each pair
+ * block's forces on the nuclei), 7 nuclear attraction per nucleus (the fixed-order force sums), 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and
  * gradient moments), 10 exchange three-centre block, 11 exchange three-centre reverse, 12
  * exchange triangular solves (rocBLAS), 13 exchange GEMMs (rocBLAS), 14 exchange pair-sparse
  * products (Y = T C and the sampled Tbar). gsdft_profile_read
