@@ -1298,63 +1298,78 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
 }
 
 // ------------------------------------------------------------------ exchange three-centre block
-// Bt[a * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and every pair a in list
-// order, the pair record carrying q_a = w_a: the screened block of RI-K
+// Bt[perm[slot] * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and the pair of each
+// pair slot, the pair record carrying q_a = w_a: the screened block of RI-K
 // (gs_dft/coulomb/ri.py:527-531, full_isobra_block), written rather than contracted. One lane per
-// aux slot, the pair records of a slab wave-uniform, as in k_gamma_fwd; each (a, l) is written once
-// (consecutive lanes write consecutive columns).
-__global__ __launch_bounds__(256) void k_exch_block(int64_t N, int64_t G, int64_t q0, int64_t W,
-                                                    const double* __restrict__ beta,
-                                                    const double* __restrict__ R,
-                                                    const double* __restrict__ kn, int64_t n,
-                                                    const double* __restrict__ rec,
-                                                    int64_t per_slab, int64_t ldb,
-                                                    double* __restrict__ Bt,
-                                                    unsigned long long* __restrict__ work) {
+// pair slot (the pair order of the reverse, so the 64 pairs of a wave are close in space and width
+// and the node screen fires for whole waves) and the aux records
+// of slots q0 + l wave-uniform and centre-grouped (d, A d, q0..q2 formed once per centre, x[3] =
+// KN_P): block (x, y) covers the pair slots [256 x, 256 x + 256) and the sixteen aux slots from
+// 16 y on; each lane's sixteen values go through LDS and are written as one row segment
+// Bt[perm[slot] * ldb + 16 y ...] (16-byte stores when kPair: ldb even, Bt 16-byte aligned).
+constexpr int kBlockRecs = 16;
+
+template <bool kPair>
+__global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
+                                                          const double* __restrict__ rec,
+                                                          const int32_t* __restrict__ perm,
+                                                          int64_t W, const double* __restrict__ aux,
+                                                          int64_t ldb, double* __restrict__ Bt,
+                                                          unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
+    __shared__ double val[kBlockRecs][256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
     __syncthreads();
-    const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = l < W;
-    const int64_t P = live ? aux_of_slot(q0 + l, N, G) : 0;
-    const double b = live ? beta[P] : 1.0;
-    const double Rx = live ? R[3 * P] : kFarAway, Ry = live ? R[3 * P + 1] : kFarAway,
-                 Rz = live ? R[3 * P + 2] : kFarAway;
-    const double knP = live ? kn[P] : 0.0;
-    double s[kNodes], wp[kNodes];
-    node_consts(b, s, wp);
-    const int64_t a0 = blockIdx.y * per_slab;
-    const int64_t a1 = min(n, a0 + per_slab);
+    const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const bool live = slot < n;
+    const double* __restrict__ r = rec + kRec * (live ? slot : 0);
+    const double I1 = r[0], I2 = r[1], I3 = r[2];
+    const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
+    const double Px = live ? r[9] : kFarAway, Py = live ? r[10] : kFarAway,
+                 Pz = live ? r[11] : kFarAway;
+    const double coef = r[12];
+    const int64_t l0 = (int64_t)blockIdx.y * kBlockRecs;
+    const int nrec = (int)min((int64_t)kBlockRecs, W - l0);
+    double q0d = 0, q1 = 0, X0 = 0, rr = 0;
     uint32_t nodes = 0;
-    for (int64_t a = a0; a < a1; ++a) {
-        const double* __restrict__ r = rec + kRec * a;
-        const double I1 = r[0], I2 = r[1], I3 = r[2];
-        const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
-        const double dx = Rx - r[9], dy = Ry - r[10], dz = Rz - r[11];
-        const double coef = r[12];
-        const double ax = xx * dx + xy * dy + xz * dz;
-        const double ay = xy * dx + yy * dy + yz * dz;
-        const double az = xz * dx + yz * dy + zz * dz;
-        const double q0d = dx * dx + dy * dy + dz * dz;
-        const double q1 = dx * ax + dy * ay + dz * az;
-        const double q2 = ax * ax + ay * ay + az * az;
-        const double X0 = I3 * q0d;
-        const double rr = I1 * q1 - q2;
+    for (int j = 0; j < nrec; ++j) {
+        const double* __restrict__ x = aux + kAuxRec * (l0 + j);
+        if (j == 0 || x[5] != 0.0) {             // a new centre (wave-uniform)
+            const double dx = x[0] - Px, dy = x[1] - Py, dz = x[2] - Pz;
+            const double ax = xx * dx + xy * dy + xz * dz;
+            const double ay = xy * dx + yy * dy + yz * dz;
+            const double az = xz * dx + yz * dy + zz * dz;
+            q0d = dx * dx + dy * dy + dz * dz;
+            q1 = dx * ax + dy * ay + dz * az;
+            const double q2 = ax * ax + ay * ay + az * az;
+            X0 = I3 * q0d;
+            rr = I1 * q1 - q2;
+        }
         double F = 0.0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = s[t];
+            const double st = x[8 + t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeVal v = node_val(Pn, st * Qn);
-            F = __builtin_fma(wp[t] * v.y0, exp_neg_tab(v.arg, tab), F);
+            F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
             return screen_after(t) && wave_all_beyond(v.z);
         };
         nodes += node_loop<0>(node);
         F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
-        if (live) Bt[a * ldb + l] = (F * coef) * knP;
+        val[j][threadIdx.x] = (F * coef) * x[3];
     }
     count_work(work, live, nodes);
+    if (!live) return;
+    double* row = Bt + (int64_t)perm[slot] * ldb + l0;
+    if (kPair && nrec == kBlockRecs) {
+#pragma unroll
+        for (int j = 0; j < kBlockRecs; j += 2)
+            *reinterpret_cast<double2*>(row + j) = make_double2(val[j][threadIdx.x],
+                                                                val[j + 1][threadIdx.x]);
+    } else {
+        for (int j = 0; j < nrec; ++j) row[j] = val[j][threadIdx.x];
+    }
 }
 
 // acc[c][slot] = (first ? 0 : acc[c][slot]) + sum over slabs of partial[slab][c][slot].
@@ -1517,6 +1532,9 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
     w->kn = ar.take<double>(N + 1);
     w->q = ar.take<double>(n + 1);
     w->rec = ar.take<double>(kRec * n + kRec);
+    w->rec_sorted = ar.take<double>(kRec * n + kRec);
+    w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
+    GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
     if (grads) {
         // bwd_split(W, n).slabs for every chunk width W <= Pc stays within min(ceil(target /
         // groups), (Pc + 15) / 16) (the count before its rounding to whole slabs)
@@ -1524,14 +1542,11 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
         int64_t slab_bound = (256 * 4 * 4 + groups - 1) / groups;
         slab_bound = std::min<int64_t>(std::min<int64_t>(slab_bound, (Pc + 15) / 16), 65535);
         if (slab_bound < 1) slab_bound = 1;
-        w->rec_sorted = ar.take<double>(kRec * n + kRec);
-        w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
         w->part = ar.take<double>(slab_bound * kAcc * n + 1);
         w->acc = ar.take<double>(kAcc * n + 1);
         w->J = ar.take<double>(n + 1);
         w->contrib = ar.take<double>(20 * n + 1);
         w->inv_perm = ar.take<int32_t>(n + 1);
-        GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
     }
     return GSDFT_OK;
 }
@@ -1552,7 +1567,6 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     }
     k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec);
     GSDFT_HIP(hipGetLastError());
-    if (!grads) return GSDFT_OK;
     const int64_t G = (N % M == 0) ? N / M : 1;
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
                                                       nullptr, w.aux);
@@ -1561,6 +1575,7 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
                                                             w.rec_sorted);
     GSDFT_HIP(hipGetLastError());
+    if (!grads) return GSDFT_OK;
     k_inv_perm<<<blocks_for(n, 256), 256, 0, s>>>(n, w.pair_order.perm, w.inv_perm);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -1569,19 +1584,20 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
 int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
                   int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
     if (n <= 0 || W <= 0) return GSDFT_OK;
-    const int64_t G = (N % M == 0) ? N / M : 1;
-    const int64_t gx = (W + 255) / 256;
-    int64_t slabs = (256 * 4 * 16 + gx - 1) / gx;
-    const int64_t max_slabs = (n + 7) / 8;
-    if (slabs > max_slabs) slabs = max_slabs;
-    if (slabs > 65535) slabs = 65535;
-    if (slabs < 1) slabs = 1;
-    const int64_t per = (n + slabs - 1) / slabs;
-    slabs = (n + per - 1) / per;
-    dim3 grid((unsigned)gx, (unsigned)slabs);
+    (void)M; (void)N; (void)aux_centers;
+    const int64_t gy = (W + kBlockRecs - 1) / kBlockRecs;
+    if (gy > 65535) return fail(GSDFT_ERR_ARG, "exchange: aux chunk too wide");
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)gy);
+    const bool pair = ldb % 2 == 0 && reinterpret_cast<uintptr_t>(Bt) % 16 == 0;
     profile_begin(kProfExchBlock, s);
-    k_exch_block<<<grid, 256, 0, s>>>(N, G, q0, W, w.beta, aux_centers, w.kn, n, w.rec, per, ldb,
-                                      Bt, profile_work_counter(kProfExchBlock));
+    if (pair)
+        k_exch_block_pairs<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, w.pair_order.perm, W,
+                                                      w.aux + kAuxRec * q0, ldb, Bt,
+                                                      profile_work_counter(kProfExchBlock));
+    else
+        k_exch_block_pairs<false><<<grid, 256, 0, s>>>(n, w.rec_sorted, w.pair_order.perm, W,
+                                                       w.aux + kAuxRec * q0, ldb, Bt,
+                                                       profile_work_counter(kProfExchBlock));
     profile_end(kProfExchBlock, s);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;

@@ -9,7 +9,7 @@
 // antisymmetric columns are dropped.
 //
 // Forward, per chunk of W aux functions (centre-grouped slot order):
-//   Bt (n x W)          the screened three-centre block (k_exch_block, dfj.hip)
+//   Bt (n x W)          the screened three-centre block (k_exch_block_pairs, dfj.hip)
 //   Y[i][l][o']         = sum over pairs a of row i of Bt[a][l] C[k_a][o']     (k_exch_spmm, FP64
 //                         MFMA over the row's block columns and gathered C rows)
 //   D_P = C^T Y_P       one FP64 GEMM per chunk: k x (W k) x M
