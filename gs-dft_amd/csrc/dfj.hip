@@ -530,20 +530,21 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[8 + t];
+            const double st = x[8 + t], wp = x[8 + kNodes + t], s2 = x[8 + 2 * kNodes + t],
+                         s3 = x[8 + 3 * kNodes + t];
             const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeVal v = node_val(Pn, st * Qn);
-            const double f = (x[8 + kNodes + t] * v.y0) * exp_neg_tab(v.arg, tab);
+            const double f = (wp * v.y0) * exp_neg_tab(v.arg, tab);
             F += f;
             const double g = f * v.ip;
             const double gh = g * (v.z - 0.5);          // df/dPn
             dP0 += gh;
             dP1 = __builtin_fma(gh, st, dP1);
-            dP2 = __builtin_fma(gh, x[8 + 2 * kNodes + t], dP2);
+            dP2 = __builtin_fma(gh, s2, dP2);
             gs1 = __builtin_fma(g, st, gs1);
-            gs2 = __builtin_fma(g, x[8 + 2 * kNodes + t], gs2);
-            gs3 = __builtin_fma(g, x[8 + 3 * kNodes + t], gs3);
+            gs2 = __builtin_fma(g, s2, gs2);
+            gs3 = __builtin_fma(g, s3, gs3);
             return screen_after(t) && wave_all_beyond(v.z);
         };
         nodes += node_loop<0>(node);
