@@ -408,6 +408,61 @@ def test_system3_sampled_gamma_and_directional_derivative(g, wl, orc, cuda):
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
 
 
+def test_system4_sampled_gamma_J_and_directional_derivative(g, wl, orc, cuda):
+    """The 300-atom CH2 globule (M = 12000, N_aux = 48000, k = 600: 64-bit offsets in the factor and
+    the solves, several slabs and Cholesky panels): gamma on sampled aux functions and J on sampled
+    pairs against the oracle over the whole list, and the gradient's directional derivative
+    through the plugin surface against central differences of the GPU energy."""
+    from gs_dft_amd import ri as _ri
+    s = wl.make_system(4)
+    basis = _splat(g, s)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(s.eps, unique=True))
+    state = g.refresh(ks, basis)
+    pi, pj, w = state.pairs
+    C = torch.tensor(s.C, device="cuda")
+    print(f"[system4] n={pi.shape[0]} N={state.aux.n_basis}", flush=True)
+    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
+                                          index=state.pair_index))
+    pin, pjn, wn = _np(pi), _np(pj), _np(w)
+    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
+    rng = np.random.default_rng(4)
+    sel = np.sort(rng.choice(len(la), 6, replace=False))
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
+    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
+    print(f"[system4] sampled gamma max elementwise rel {err:.2e}", flush=True)
+    assert err < 1e-12
+    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
+    x = _ri._Inputs(basis, C, s.occ, state.aux, pi, pj, w, state.pair_index)
+    J = _np(_ri._gamma_vjp(x, dg, None)[0])
+    psel = np.sort(rng.choice(len(pin), 32, replace=False))
+    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
+                       wn[psel], _np(dg))[0]
+    errJ = rel_max(J[psel], Jo)
+    print(f"[system4] sampled J rel-to-max {errJ:.2e}", flush=True)
+    assert errJ < 1e-11
+    b2 = _splat(g, s, grad=True)
+    Cg = C.clone().requires_grad_()
+    occ = torch.tensor(s.occ, device="cuda")
+    E = ks(g.SplatModel(basis=b2, C=Cg, occupations=occ), state)
+    E.backward()
+    leaves = (b2.quat, b2.log_scale, b2.centers, Cg)
+    gen = torch.Generator(device="cpu").manual_seed(44)
+    dirs = [torch.randn(t.shape, generator=gen, dtype=torch.float64).cuda() for t in leaves]
+    dd = sum((t.grad * d).sum().item() for t, d in zip(leaves, dirs))
+    h = 1e-5
+
+    def e_at(sign):
+        with torch.no_grad():
+            b = g.Splat(quat=b2.quat + sign * h * dirs[0], log_scale=b2.log_scale + sign * h * dirs[1],
+                        centers=b2.centers + sign * h * dirs[2])
+            return ks(g.SplatModel(basis=b, C=Cg + sign * h * dirs[3], occupations=occ),
+                      state).item()
+    fd = (e_at(1) - e_at(-1)) / (2 * h)
+    print(f"[system4] E {E.item():.12e}: directional derivative {dd:.10e} vs central difference "
+          f"{fd:.10e}")
+    assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
+
+
 def test_globule700_sampled_gamma_and_J(g, wl, orc, cuda):
     """The headline shape (globule700: M = 20000, N_aux = 80000, ~1.1e7 unique pairs, every slab
     and screen path of the full-size launch): gamma on sampled aux functions and J = sum_P
