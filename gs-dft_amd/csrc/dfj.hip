@@ -138,6 +138,53 @@ __global__ __launch_bounds__(1024) void k_scaled_dot(int64_t N, const double* __
     if (threadIdx.x == 0) *out = scale * part[0];
 }
 
+// The same as two fixed-order stages for long vectors: block b of the first stage sums the
+// elements [b kDotChunk, (b + 1) kDotChunk) (thread-strided, then a tree), the second adds the
+// block sums. The partition does not depend on N, so appended zero entries change nothing.
+constexpr int64_t kDotChunk = 8192;
+inline int64_t dot_blocks(int64_t N) { return std::max<int64_t>(1, (N + kDotChunk - 1) / kDotChunk); }
+
+__global__ __launch_bounds__(256) void k_dot_part(int64_t N, int64_t chunk,
+                                                  const double* __restrict__ a,
+                                                  const double* __restrict__ b,
+                                                  double* __restrict__ part) {
+    __shared__ double red[256];
+    const int64_t i0 = blockIdx.x * chunk, i1 = min(N, i0 + chunk);
+    double s = 0.0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) s = __builtin_fma(a[i], b[i], s);
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(256) void k_dot_finish(int64_t blocks, const double* __restrict__ part,
+                                                    double scale, double* __restrict__ out) {
+    __shared__ double red[256];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < blocks; i += 256) s += part[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = scale * red[0];
+}
+
+// scale * a.b into *out (device), with part holding dot_blocks(N) doubles of scratch.
+int launch_scaled_dot(int64_t N, const double* a, const double* b, double scale, double* out,
+                      double* part, hipStream_t s) {
+    const int64_t blocks = dot_blocks(N);
+    k_dot_part<<<(unsigned)blocks, 256, 0, s>>>(N, kDotChunk, a, b, part);
+    k_dot_finish<<<1, 256, 0, s>>>(blocks, part, scale, out);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
 // ------------------------------------------------------------------ pair records
 
 // q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456; w_a = 1 for a null weight); G lanes
@@ -763,9 +810,10 @@ __global__ __launch_bounds__(256) void k_splat_grad(
 
 // dE/dC_mo = occ_o [sum_{a: i_a=m} J_a w_a C_{j_a o} + sum_{a: j_a=m} J_a w_a C_{i_a o}]
 // (gs_dft/coulomb/ri.py:456 reverse). One workgroup per splat; thread t owns orbitals
-// o = t + 256 c for c < CH, so each pair's scale and partner index are read once per workgroup
-// and the partner's C row is streamed coalesced. Orbitals beyond 256 CH are covered by further
-// passes over the splat's pairs.
+// o = t + 256 c for c < CH, and the partner's C row is streamed coalesced. The splat's pairs (its
+// CSR row, then its column) are taken 256 at a time: each thread resolves one pair's partner and
+// scale J_a w_a into LDS, so the streaming loop carries no dependent index loads. Orbitals beyond
+// 256 CH are covered by further passes over the pairs.
 template <int CH>
 __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
                                             const int32_t* __restrict__ row_ptr,
@@ -779,31 +827,34 @@ __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
                                             const double* __restrict__ C,
                                             const double* __restrict__ occ,
                                             double* __restrict__ dC) {
+    __shared__ int32_t partner[256];
+    __shared__ double scale[256];
     const int64_t m = blockIdx.x;
     const int64_t r0 = row_ptr[m], r1 = row_ptr[m + 1], c0 = col_ptr[m], c1 = col_ptr[m + 1];
+    const int64_t nr = r1 - r0, total = nr + (c1 - c0);
     for (int64_t base = 0; base < k; base += 256 * CH) {
         double acc[CH];
 #pragma unroll
         for (int c = 0; c < CH; ++c) acc[c] = 0.0;
-        for (int64_t p = r0; p < r1; ++p) {
-            const int64_t a = row_perm[p];
-            const double sc = J[a] * weight[a];
-            const double* __restrict__ row = C + (int64_t)pj[a] * k;
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int64_t o = base + threadIdx.x + 256 * c;
-                if (o < k) acc[c] = __builtin_fma(sc, row[o], acc[c]);
+        for (int64_t b0 = 0; b0 < total; b0 += 256) {
+            const int64_t e = b0 + threadIdx.x;
+            if (e < total) {
+                const int64_t a = e < nr ? row_perm[r0 + e] : col_perm[c0 + e - nr];
+                partner[threadIdx.x] = e < nr ? pj[a] : pi[a];
+                scale[threadIdx.x] = J[a] * weight[a];
             }
-        }
-        for (int64_t p = c0; p < c1; ++p) {
-            const int64_t a = col_perm[p];
-            const double sc = J[a] * weight[a];
-            const double* __restrict__ row = C + (int64_t)pi[a] * k;
+            __syncthreads();
+            const int cnt = (int)min((int64_t)256, total - b0);
+            for (int q = 0; q < cnt; ++q) {
+                const double sc = scale[q];
+                const double* __restrict__ row = C + (int64_t)partner[q] * k;
 #pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int64_t o = base + threadIdx.x + 256 * c;
-                if (o < k) acc[c] = __builtin_fma(sc, row[o], acc[c]);
+                for (int c = 0; c < CH; ++c) {
+                    const int64_t o = base + threadIdx.x + 256 * c;
+                    if (o < k) acc[c] = __builtin_fma(sc, row[o], acc[c]);
+                }
             }
+            __syncthreads();
         }
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
@@ -2046,6 +2097,7 @@ struct ExternalWs {
     GammaWs g;
     double* atom_partial;       // (pair blocks, n_atoms, 3) from the pair pass
     double* atom_groups;        // (ceil(pair blocks / 256), n_atoms, 3)
+    double* dot_part;           // dot_blocks(n)
 };
 
 constexpr int64_t kAtomGroup = 256;   // pair blocks per first-stage sum of the nuclear forces
@@ -2057,6 +2109,7 @@ int layout_external(Arena& ar, int64_t M, int64_t n, int64_t n_atoms, ExternalWs
     const int64_t blocks = pair_blocks(n);
     w->atom_partial = ar.take<double>(blocks * n_atoms * 3 + 3);
     w->atom_groups = ar.take<double>(((blocks + kAtomGroup - 1) / kAtomGroup) * n_atoms * 3 + 3);
+    w->dot_part = ar.take<double>(dot_blocks(n));
     return GSDFT_OK;
 }
 
@@ -2197,8 +2250,7 @@ extern "C" int gsdft_external_energy(
     GSDFT_TRY(external_pass(M, quat, log_scale, centers, k, C, occ, n, pi, pj, weight, n_atoms,
                             atom_coords, atom_charges, V, w, datoms != nullptr, s));
     // E = sum_a q_a V_a (gs_dft/screening/pairs.py:429-432), fixed summation order
-    k_scaled_dot<<<1, 1024, 0, s>>>(n, w.g.q, V, 1.0, energy);
-    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_scaled_dot(n, w.g.q, V, 1.0, energy, w.dot_part, s));
     if (splat_grad) {
         k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
                                                              col_perm, w.g.contrib, quat,
@@ -2238,6 +2290,7 @@ namespace {
 struct EriWs {
     double *A6, *Nrm, *q, *rec3, *rec, *partial, *contrib;
     double *jacc, *bra_part, *ket_part;     // symmetric passes (jacc: J, or the ten moments)
+    double* dot_part;                       // dot_blocks(n)
     int64_t band;
     PairOrderWs order;
 };
@@ -2265,6 +2318,7 @@ int layout_eri(Arena& ar, int64_t M, int64_t n, bool grads, EriWs* w) {
     w->rec3 = ar.take<double>(kRec * n + kRec);
     w->rec = ar.take<double>(kEriRec * n + kEriRec);
     GSDFT_TRY(pair_order_layout(ar, n, &w->order));
+    w->dot_part = ar.take<double>(dot_blocks(n));
     w->jacc = w->bra_part = w->ket_part = nullptr;
     w->band = 0;
     if (grads) {
@@ -2389,8 +2443,7 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
     }
     GSDFT_HIP(hipGetLastError());
     // E_J = 1/2 sum_a Pw_a J_a (gs_dft/coulomb/stream.py:319-320), fixed summation order
-    k_scaled_dot<<<1, 1024, 0, s>>>(n, w.q, J, 0.5, energy);
-    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(launch_scaled_dot(n, w.q, J, 0.5, energy, w.dot_part, s));
     if (grads) {
         k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
                                                              col_perm, w.contrib, quat,
