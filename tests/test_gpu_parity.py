@@ -408,6 +408,48 @@ def test_system3_sampled_gamma_and_directional_derivative(g, wl, orc, cuda):
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
 
 
+@pytest.mark.parametrize("eps", [1e-5, 1e-9])
+def test_system3_eps_sweep_sampled_gamma_and_J(g, wl, orc, cuda, eps):
+    """C20H42 at the other two screening thresholds of its configuration (1e-5: ~4x fewer pairs,
+    1e-9: ~2x more): gamma on sampled aux functions and J on sampled pairs against the oracle over
+    the whole list, and E_J against the same factor's solve of the oracle's gamma on a 1e-5 list."""
+    from gs_dft_amd import ri as _ri
+    s = wl.make_system(3, eps=eps)
+    basis = _splat(g, s)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(eps, unique=True))
+    state = g.refresh(ks, basis)
+    pi, pj, w = state.pairs
+    C = torch.tensor(s.C, device="cuda")
+    print(f"[eps {eps:g}] n={pi.shape[0]}", flush=True)
+    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
+                                          index=state.pair_index))
+    pin, pjn, wn = _np(pi), _np(pj), _np(w)
+    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
+    rng = np.random.default_rng(int(-np.log10(eps)))
+    sel = np.sort(rng.choice(len(la), 24, replace=False))
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
+    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
+    print(f"[eps {eps:g}] sampled gamma max elementwise rel {err:.2e}", flush=True)
+    assert err < 1e-12
+    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
+    x = _ri._Inputs(basis, C, s.occ, state.aux, pi, pj, w, state.pair_index)
+    J = _np(_ri._gamma_vjp(x, dg, None)[0])
+    psel = np.sort(rng.choice(len(pin), 48, replace=False))
+    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
+                       wn[psel], _np(dg))[0]
+    errJ = rel_max(J[psel], Jo)
+    print(f"[eps {eps:g}] sampled J rel-to-max {errJ:.2e}", flush=True)
+    assert errJ < 1e-11
+    if eps == 1e-5:                     # the whole gamma from the oracle is affordable here
+        go_all = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin, pjn, wn)
+        E = g.df_coulomb_energy_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
+                                         cholV=state.cholV, index=state.pair_index).item()
+        E_o = g.df_coulomb_solve(torch.tensor(go_all, device="cuda"), state.aux,
+                                 cholV=state.cholV).item()
+        print(f"[eps {eps:g}] E_J {E:.15e} vs solve of the oracle's gamma {E_o:.15e}")
+        assert abs(E - E_o) < 1e-10 * abs(E_o)
+
+
 def test_system4_sampled_gamma_J_and_directional_derivative(g, wl, orc, cuda):
     """The 300-atom CH2 globule (M = 12000, N_aux = 48000, k = 600: 64-bit offsets in the factor and
     the solves, several slabs and Cholesky panels): gamma on sampled aux functions and J on sampled
