@@ -321,10 +321,11 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
     const int64_t a_begin = (int64_t)blockIdx.x * kFwdPairs;
     const int64_t a_end = min(n, a_begin + kFwdPairs);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t nodes = 0;
+    uint64_t lane_nodes = 0;                 // profiling: node evaluations over live lanes
     for (int64_t a0 = a_begin + 64 * wave; a0 < a_end; a0 += 256) {      // wave-uniform
         const int64_t a = a0 + lane;
         const bool live = a < a_end;
+        const uint64_t lanes = __builtin_popcountll(__builtin_amdgcn_ballot_w64(live));
         const double* __restrict__ r = rec + kRec * (live ? a : a0);
         const double I1 = r[0], I2 = r[1], I3 = r[2];
         const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
@@ -355,12 +356,12 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
                 return screen_after(t) && wave_all_beyond(v.z);
             };
-            nodes += node_loop<0>(node);
+            lane_nodes += lanes * node_loop<0>(node);
             F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
             acc[j][threadIdx.x] = __builtin_fma(F, coef, acc[j][threadIdx.x]);
         }
     }
-    count_work(work, true, nodes);
+    if (work && (threadIdx.x & 63) == 0) atomicAdd(work, (unsigned long long)lane_nodes);
     __syncthreads();
     if ((int)threadIdx.x < nrec) {
         double sum = 0.0;
