@@ -67,7 +67,7 @@ __device__ __forceinline__ double exp_fast(double x) {
     return __builtin_ldexp(p, (int)kf);
 }
 
-// e^-z for the three-centre node loops, z >= 0 (Tang's table-driven method): z is reduced as
+// e^-z for the three-centre node loops, z >= -1 (Tang's table-driven method): z is reduced as
 // -z = (256 m + j) ln2/256 + r with |r| <= ln2/512, e^r comes from its degree-4 Taylor polynomial
 // (truncation < 4e-17 relative) and 2^(j/256) from a 256-entry table held in LDS. z is capped at
 // 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308 stands in for the
@@ -115,6 +115,29 @@ __device__ __forceinline__ NodeVal node_val(double P, double sQ) {
     v.ip = __builtin_fma(h, eps, h);
     v.z = sQ * v.ip;
     v.arg = __builtin_fma(eps, -0.5, v.z);
+    return v;
+}
+
+// The node in the scaled form of the three-centre passes: with Pr = Pn(s)/s and Q = Qn(s), so that
+// z = Q/Pr = s Qn/Pn without the product s Qn, returns y0 ~ Pr^(-1/2) and ip = 1/Pr (as node_val),
+// zh = z - 1/2 and arg = zh - eps/2: y0 e^-arg = e^(1/2) Pr^(-1/2) e^-z (the records fold
+// s^(-1/2) e^(-1/2) into the node weight). zh is what the reverse needs, s df/dPn = G zh with
+// G = f/Pr.
+struct NodeValH {
+    double y0;   // hardware estimate of Pr^(-1/2)
+    double zh;   // Q / Pr - 1/2
+    double ip;   // 1 / Pr
+    double arg;  // zh - eps/2
+};
+
+__device__ __forceinline__ NodeValH node_val_h(double P, double Q) {
+    NodeValH v;
+    v.y0 = __builtin_amdgcn_rsq(P);
+    const double h = v.y0 * v.y0;
+    const double eps = __builtin_fma(-P, h, 1.0);
+    v.ip = __builtin_fma(h, eps, h);
+    v.zh = __builtin_fma(Q, v.ip, -0.5);
+    v.arg = __builtin_fma(eps, -0.5, v.zh);
     return v;
 }
 

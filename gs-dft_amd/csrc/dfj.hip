@@ -272,6 +272,22 @@ __device__ __forceinline__ bool wave_all_beyond(double z) {
     return __builtin_amdgcn_ballot_w64(!(z > kSkipZ)) == 0;
 }
 
+// The same test on zh = z - 1/2 (node_val_h).
+__device__ __forceinline__ bool wave_all_beyond_h(double zh) {
+    return __builtin_amdgcn_ballot_w64(!(zh > kSkipZ - 0.5)) == 0;
+}
+
+// Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2), s_t^2 and
+// 1/s_t, for the scaled node form (node_val_h) of the forward and reverse passes.
+constexpr double kExpMinusHalf = 0x1.368b2fc6f960ap-1;     // e^(-1/2), correctly rounded
+
+__device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp) {
+    o[8 + t] = s;
+    o[8 + kNodes + t] = wp / sqrt(s) * kExpMinusHalf;
+    o[8 + 2 * kNodes + t] = s * s;
+    o[8 + 3 * kNodes + t] = 1.0 / s;
+}
+
 // body(std::integral_constant<int, t>) for t = 0, 1, ..., kNodes - 1 until it returns true: a
 // fully unrolled node loop with early exits (node tables stay in registers). Returns the number
 // of nodes evaluated (wave-uniform).
@@ -349,12 +365,12 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
             double F = 0.0;
             auto node = [&](auto tc) {
                 constexpr int t = decltype(tc)::value;
-                const double st = x[8 + t];
-                const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+                const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
+                const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
                 const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-                const NodeVal v = node_val(Pn, st * Qn);
+                const NodeValH v = node_val_h(Pr, Qn);
                 F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
-                return screen_after(t) && wave_all_beyond(v.z);
+                return screen_after(t) && wave_all_beyond_h(v.zh);
             };
             lane_nodes += lanes * node_loop<0>(node);
             F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
@@ -440,11 +456,11 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 }
 
 
-// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wp_t | s_t^2 |
-// s_t^3. Records are stored centre-grouped: with G = N / M exponent scales (the product aux is
-// scale-major, P = s M + m, every scale of splat m at one centre), the record of P sits at slot
-// m G + s, so the scales sharing a centre are consecutive; otherwise (N not a multiple of M) in
-// aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
+// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wh_t | s_t^2 |
+// 1/s_t (put_node_consts). Records are stored centre-grouped: with G = N / M exponent scales (the
+// product aux is scale-major, P = s M + m, every scale of splat m at one centre), the record of P
+// sits at slot m G + s, so the scales sharing a centre are consecutive; otherwise (N not a
+// multiple of M) in aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
 // the reverse kernel recomputes the centre-dependent terms only there, whatever the aux holds.
 // (aux_slot / aux_of_slot: common.h)
 
@@ -471,12 +487,7 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
                       __builtin_bit_cast(uint64_t, R[3 * p + 2]));
     }
     o[4] = b; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
-    for (int t = 0; t < kNodes; ++t) {
-        o[8 + t] = s[t];
-        o[8 + kNodes + t] = wp[t];
-        o[8 + 2 * kNodes + t] = s[t] * s[t];
-        o[8 + 3 * kNodes + t] = s[t] * s[t] * s[t];
-    }
+    for (int t = 0; t < kNodes; ++t) put_node_consts(o, t, s[t], wp[t]);
 }
 
 // One lane per pair slot; accumulates over a slab of aux records (u = dgamma_P KN_P)
@@ -486,6 +497,8 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // f_t = wp_t y e^-z, y = Pn^(-1/2), z = s Qn / Pn, g_t = f_t / Pn and df/dPn = g_t (z - 1/2).
 // Records sharing a centre are consecutive, so d = R - Pa and the d-moments are formed once per
 // centre: C0..C2 = sum u dQ0..2 over the group, then Vc += C0 d, ..., Sb += C2 d d^T.
+// Each node runs in the scaled form Pr = Pn/s (node_val_h): G = f/Pr = g s, so the node sums are
+// gs1..3 = sum G (1, s, s^2) = sum g s^(1..3) and dP0..2 = sum G (z - 1/2) (1/s, 1, s).
 // With kLaneU the cotangent of (P|a) is not separable: u = x[3] * ut[slot * ldu + p] per lane
 // (the exchange's dE/d(P|a), stored slot-major).
 // With kAtomF the records are nuclei (point charges) and the pass also forms every nucleus' force
@@ -578,22 +591,22 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[8 + t], wp = x[8 + kNodes + t], s2 = x[8 + 2 * kNodes + t],
-                         s3 = x[8 + 3 * kNodes + t];
-            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double st = x[8 + t], wh = x[8 + kNodes + t], s2 = x[8 + 2 * kNodes + t],
+                         is = x[8 + 3 * kNodes + t];
+            const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const NodeVal v = node_val(Pn, st * Qn);
-            const double f = (wp * v.y0) * exp_neg_tab(v.arg, tab);
+            const NodeValH v = node_val_h(Pr, Qn);
+            const double f = (wh * v.y0) * exp_neg_tab(v.arg, tab);
             F += f;
-            const double g = f * v.ip;
-            const double gh = g * (v.z - 0.5);          // df/dPn
-            dP0 += gh;
-            dP1 = __builtin_fma(gh, st, dP1);
-            dP2 = __builtin_fma(gh, s2, dP2);
-            gs1 = __builtin_fma(g, st, gs1);
-            gs2 = __builtin_fma(g, s2, gs2);
-            gs3 = __builtin_fma(g, s3, gs3);
-            return screen_after(t) && wave_all_beyond(v.z);
+            const double G = f * v.ip;                  // g s
+            const double Gh = G * v.zh;                 // s df/dPn
+            dP0 = __builtin_fma(Gh, is, dP0);
+            dP1 += Gh;
+            dP2 = __builtin_fma(Gh, st, dP2);
+            gs1 += G;
+            gs2 = __builtin_fma(G, st, gs2);
+            gs3 = __builtin_fma(G, s2, gs3);
+            return screen_after(t) && wave_all_beyond_h(v.zh);
         };
         nodes += node_loop<0>(node);
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
@@ -891,13 +904,7 @@ __global__ void k_atom_rec(int64_t n_atoms, const double* __restrict__ coords,
                   __builtin_bit_cast(uint64_t, coords[3 * A - 1]) ==
                       __builtin_bit_cast(uint64_t, coords[3 * A + 2]));
     o[4] = 0.0; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
-    for (int t = 0; t < kNodes; ++t) {
-        const double t2 = quad_t(t) * quad_t(t);
-        o[8 + t] = t2;
-        o[8 + kNodes + t] = quad_w(t);
-        o[8 + 2 * kNodes + t] = t2 * t2;
-        o[8 + 3 * kNodes + t] = t2 * t2 * t2;
-    }
+    for (int t = 0; t < kNodes; ++t) put_node_consts(o, t, quad_t(t) * quad_t(t), quad_w(t));
 }
 
 // ------------------------------------------------------------------ exact pair-pair Coulomb
@@ -1401,12 +1408,12 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
         double F = 0.0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[8 + t];
-            const double Pn = __builtin_fma(st, __builtin_fma(st, I1 + st, I2), I3);
+            const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
+            const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const NodeVal v = node_val(Pn, st * Qn);
+            const NodeValH v = node_val_h(Pr, Qn);
             F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
-            return screen_after(t) && wave_all_beyond(v.z);
+            return screen_after(t) && wave_all_beyond_h(v.zh);
         };
         nodes += node_loop<0>(node);
         F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
