@@ -93,6 +93,32 @@ __device__ __forceinline__ double exp_neg_tab(double z, const double* __restrict
     return __builtin_ldexp(tab[k & 255] * p, k >> 8);
 }
 
+// 24 e^-z for the three-centre passes: the reduction of exp_neg_tab with two changes. The
+// polynomial is scaled by 24, 24 e^r = (((r + 4) r + 12) r + 24) r + 24, whose coefficients are
+// exact and whose first step adds an inline constant (no coefficient has to sit in a vector
+// register; the node weights carry the 1/24). And 2^m 2^(j/256) is formed by one integer add on the
+// high word: the table `lead` holds 2^(j/256) with j << 12 taken off its high word
+// (exp2_frac_lead), so adding k << 12 = (m << 20) + (j << 12) leaves 2^(j/256) with m added to
+// its exponent field -- exact while the result stays normal, which the cap at z = 708.3 ensures
+// (m >= -1022 and 2^(j/256) >= 1).
+__device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __restrict__ lead) {
+    constexpr double kShift = 0x1.8p52;
+    z = __builtin_fmin(z, 708.3);
+    const double sh = __builtin_fma(z, -0x1.71547652b82fep+8, kShift);  // -z * 256/ln2 + shift
+    const double kf = sh - kShift;
+    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
+    const double r = __builtin_fma(-kf, 0x1.62e42fefa39efp-9, -z);      // ln2 / 256
+    double p = r + 4.0;
+    p = __builtin_fma(p, r, 12.0);
+    p = __builtin_fma(p, r, 24.0);
+    p = __builtin_fma(p, r, 24.0);
+    struct Words { uint32_t lo, hi; };
+    Words w = __builtin_bit_cast(Words, lead[k & 255]);
+    // a 32-bit add on the high word (written out: the compiler otherwise forms a 64-bit add)
+    asm("v_lshl_add_u32 %0, %1, 12, %2" : "=v"(w.hi) : "v"(k), "v"(w.hi));
+    return __builtin_bit_cast(double, w) * p;
+}
+
 // One node of the three-centre quadrature: with P = Pn(s) > 0 and sQ = s Qn(s), returns
 // y0 e^(-sQ/P + eps/2) (= P^(-1/2) e^(-sQ/P)) and sets z = sQ/P and ip = 1/P, from the hardware
 // 1/sqrt estimate y0 without a separate Newton step. The estimate's relative error is below
@@ -129,6 +155,23 @@ struct NodeValH {
     double ip;   // 1 / Pr
     double arg;  // zh - eps/2
 };
+
+// The forward passes need only y0 and the exponent argument: with a = Q h - 1/2,
+// arg = a (1 + eps) = Q h (1 + eps) - 1/2 - eps/2, node_val_h's arg without forming 1/Pr.
+struct NodeArgH {
+    double y0;   // hardware estimate of Pr^(-1/2)
+    double arg;  // z - 1/2 - eps/2, |eps| < 1.1e-7
+};
+
+__device__ __forceinline__ NodeArgH node_arg_h(double P, double Q) {
+    NodeArgH v;
+    v.y0 = __builtin_amdgcn_rsq(P);
+    const double h = v.y0 * v.y0;
+    const double eps = __builtin_fma(-P, h, 1.0);
+    const double a = __builtin_fma(Q, h, -0.5);
+    v.arg = __builtin_fma(a, eps, a);
+    return v;
+}
 
 __device__ __forceinline__ NodeValH node_val_h(double P, double Q) {
     NodeValH v;
@@ -210,6 +253,12 @@ __host__ __device__ constexpr double exp2_frac(int j) {
     0x1.fa7c1819e90d8p+0, 0x1.fbdba3692d514p+0, 0x1.fd3c22b8f71f1p+0, 0x1.fe9d96b2a23d9p+0,
     };
     return t[j];
+}
+
+// exp2_frac(j) with j << 12 taken off its high word (the table of exp_neg_tab_x24).
+__host__ __device__ inline double exp2_frac_lead(int j) {
+    return __builtin_bit_cast(double, __builtin_bit_cast(uint64_t, exp2_frac(j)) -
+                                          ((uint64_t)j << 44));
 }
 
 // 1/sqrt(x) for positive normal x: the hardware estimate (relative error ~5e-8) refined by one

@@ -272,18 +272,19 @@ __device__ __forceinline__ bool wave_all_beyond(double z) {
     return __builtin_amdgcn_ballot_w64(!(z > kSkipZ)) == 0;
 }
 
-// The same test on zh = z - 1/2 (node_val_h).
+// The same test on zh = z - 1/2 (node_val_h), or on the forward's arg = zh - eps/2 (node_arg_h),
+// which differs from zh by less than 6e-8.
 __device__ __forceinline__ bool wave_all_beyond_h(double zh) {
     return __builtin_amdgcn_ballot_w64(!(zh > kSkipZ - 0.5)) == 0;
 }
 
-// Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2), s_t^2 and
-// 1/s_t, for the scaled node form (node_val_h) of the forward and reverse passes.
+// Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / 24, s_t^2
+// and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes.
 constexpr double kExpMinusHalf = 0x1.368b2fc6f960ap-1;     // e^(-1/2), correctly rounded
 
 __device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp) {
     o[8 + t] = s;
-    o[8 + kNodes + t] = wp / sqrt(s) * kExpMinusHalf;
+    o[8 + kNodes + t] = wp / sqrt(s) * (kExpMinusHalf / 24.0);
     o[8 + 2 * kNodes + t] = s * s;
     o[8 + 3 * kNodes + t] = 1.0 / s;
 }
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                                                          unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     __shared__ double acc[kFwdRecs][256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
 #pragma unroll
     for (int j = 0; j < kFwdRecs; ++j) acc[j][threadIdx.x] = 0.0;
     __syncthreads();
@@ -368,9 +369,9 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
                 const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
                 const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-                const NodeValH v = node_val_h(Pr, Qn);
-                F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
-                return screen_after(t) && wave_all_beyond_h(v.zh);
+                const NodeArgH v = node_arg_h(Pr, Qn);
+                F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+                return screen_after(t) && wave_all_beyond_h(v.arg);
             };
             lane_nodes += lanes * node_loop<0>(node);
             F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
@@ -519,7 +520,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
     // slot per lane, structure of arrays) rather than in registers across the loop.
     __shared__ double geo[9][256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = a < n;
     const double* r = rec + kRec * (live ? a : 0);
@@ -596,7 +597,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeValH v = node_val_h(Pr, Qn);
-            const double f = (wh * v.y0) * exp_neg_tab(v.arg, tab);
+            const double f = (wh * v.y0) * exp_neg_tab_x24(v.arg, tab);
             F += f;
             const double G = f * v.ip;                  // g s
             const double Gh = G * v.zh;                 // s df/dPn
@@ -1378,7 +1379,7 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
                                                           unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     __shared__ double val[kBlockRecs][256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     __syncthreads();
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const bool live = slot < n;
@@ -1411,9 +1412,9 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-            const NodeValH v = node_val_h(Pr, Qn);
-            F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab(v.arg, tab), F);
-            return screen_after(t) && wave_all_beyond_h(v.zh);
+            const NodeArgH v = node_arg_h(Pr, Qn);
+            F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            return screen_after(t) && wave_all_beyond_h(v.arg);
         };
         nodes += node_loop<0>(node);
         F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
