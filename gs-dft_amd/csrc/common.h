@@ -67,40 +67,24 @@ __device__ __forceinline__ double exp_fast(double x) {
     return __builtin_ldexp(p, (int)kf);
 }
 
-// e^-z for the three-centre node loops, z >= -1 (Tang's table-driven method): z is reduced as
+// 24 e^-z for the quadrature node loops, z >= -1 (Tang's table-driven method): z is reduced as
 // -z = (256 m + j) ln2/256 + r with |r| <= ln2/512, e^r comes from its degree-4 Taylor polynomial
-// (truncation < 4e-17 relative) and 2^(j/256) from a 256-entry table held in LDS. z is capped at
-// 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308 stands in for the
-// smaller values, whose contribution to any node sum is far below round-off). A NaN z is lost
-// here; callers check their inputs for NaN once per integral instead of once per node.
-// The integer 256 m + j = round(-z 256/ln2) is formed by adding 1.5 * 2^52 in the same fma: the
-// sum's unit in the last place is 1, so it is rounded to an integer, which then sits in the low
-// 32 bits of the mantissa as a two's-complement int (|256 m + j| <= 261581 < 2^51).
+// (truncation < 4e-17 relative) scaled by 24, 24 e^r = (((r + 4) r + 12) r + 24) r + 24, whose
+// coefficients are exact and whose first step adds an inline constant (no coefficient has to sit
+// in a vector register; the node weights carry the 1/24), and 2^(j/256) from a 256-entry table in
+// LDS. z is capped at 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308
+// stands in for the smaller values, whose contribution to any node sum is far below round-off). A
+// NaN z is lost here; callers check their inputs for NaN once per integral instead of per node.
+// The integer k = 256 m + j = round(-z 256/ln2) is formed by adding 1.5 * 2^52 in the same fma:
+// the sum's unit in the last place is 1, so it is rounded to an integer, which then sits in the
+// low 32 bits of the mantissa as a two's-complement int (|k| <= 261581 < 2^51).
 // The reduction uses ln2/256 rounded to one double (relative error d <= 2^-53) instead of a
 // hi/lo pair: r then carries an absolute error ~z d, so e^-z is off by a relative z d, i.e. by
 // at most z e^-z d <= 0.37 d ~ 4e-17 of the node's prefactor -- below the round-off of the sum.
-__device__ __forceinline__ double exp_neg_tab(double z, const double* __restrict__ tab) {
-    constexpr double kShift = 0x1.8p52;
-    z = __builtin_fmin(z, 708.3);
-    const double sh = __builtin_fma(z, -0x1.71547652b82fep+8, kShift);  // -z * 256/ln2 + shift
-    const double kf = sh - kShift;
-    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
-    const double r = __builtin_fma(-kf, 0x1.62e42fefa39efp-9, -z);      // ln2 / 256
-    double p = __builtin_fma(r, 4.16666666666666666667e-02, 1.66666666666666666667e-01);
-    p = __builtin_fma(p, r, 0.5);
-    p = __builtin_fma(p, r, 1.0);
-    p = __builtin_fma(p, r, 1.0);
-    return __builtin_ldexp(tab[k & 255] * p, k >> 8);
-}
-
-// 24 e^-z for the three-centre passes: the reduction of exp_neg_tab with two changes. The
-// polynomial is scaled by 24, 24 e^r = (((r + 4) r + 12) r + 24) r + 24, whose coefficients are
-// exact and whose first step adds an inline constant (no coefficient has to sit in a vector
-// register; the node weights carry the 1/24). And 2^m 2^(j/256) is formed by one integer add on the
-// high word: the table `lead` holds 2^(j/256) with j << 12 taken off its high word
-// (exp2_frac_lead), so adding k << 12 = (m << 20) + (j << 12) leaves 2^(j/256) with m added to
-// its exponent field -- exact while the result stays normal, which the cap at z = 708.3 ensures
-// (m >= -1022 and 2^(j/256) >= 1).
+// 2^m 2^(j/256) is one integer add on the high word: the table `lead` holds 2^(j/256) with j << 12
+// taken off its high word (exp2_frac_lead), so adding k << 12 = (m << 20) + (j << 12) leaves
+// 2^(j/256) with m added to its exponent field -- exact while the result stays normal, which the
+// cap ensures (m >= -1022 and 2^(j/256) >= 1).
 __device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __restrict__ lead) {
     constexpr double kShift = 0x1.8p52;
     z = __builtin_fmin(z, 708.3);
@@ -119,47 +103,38 @@ __device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __rest
     return __builtin_bit_cast(double, w) * p;
 }
 
-// One node of the three-centre quadrature: with P = Pn(s) > 0 and sQ = s Qn(s), returns
-// y0 e^(-sQ/P + eps/2) (= P^(-1/2) e^(-sQ/P)) and sets z = sQ/P and ip = 1/P, from the hardware
-// 1/sqrt estimate y0 without a separate Newton step. The estimate's relative error is below
-// 5.3e-8 (measured on MI355X over x in [1e-6, 1e8]), so |eps| < 1.1e-7 for eps = 1 - P y0^2.
-// With h = y0^2: 1/P = h (1 + eps) + O(eps^2) (relative error eps^2 < 1.2e-14, which moves the
-// node by z eps^2 e^-z <= 4.4e-15 of its prefactor) and P^(-1/2) = y0 e^(eps/2 + eps^2/4 + ...)
-// (relative error eps^2/4 < 3e-15 whatever z is).
-struct NodeVal {
+// One quadrature node in scaled form: with P = Pn(s)/s > 0 (Pn the node's determinant
+// polynomial) and Q = Qn(s), so that the exponent is z = Q/P = s Qn/Pn without the product s Qn,
+// returns y0 ~ P^(-1/2), ip = 1/P, zh = z - 1/2 and arg = zh - eps/2, so that
+// y0 e^-arg = e^(1/2) P^(-1/2) e^-z (callers fold s^(-1/2) e^(-1/2) into the node weight); zh is
+// what a reverse pass needs, s df/dPn = (f/P) zh. y0 is the hardware 1/sqrt estimate without a
+// separate Newton step: its relative error is below 5.3e-8 (measured on MI355X over x in
+// [1e-6, 1e8]), so |eps| < 1.1e-7 for eps = 1 - P y0^2. With h = y0^2: 1/P = h (1 + eps) +
+// O(eps^2) (relative error eps^2 < 1.2e-14, which moves the node by z eps^2 e^-z <= 4.4e-15 of its
+// prefactor) and P^(-1/2) = y0 e^(eps/2 + eps^2/4 + ...) (relative error eps^2/4 < 3e-15 whatever z
+// is).
+struct NodeValH {
     double y0;   // hardware estimate of P^(-1/2)
-    double z;    // s Qn / Pn
-    double ip;   // 1 / Pn
-    double arg;  // z - eps/2: y0 e^-arg = P^(-1/2) e^-z
+    double zh;   // Q / P - 1/2
+    double ip;   // 1 / P
+    double arg;  // zh - eps/2
 };
 
-__device__ __forceinline__ NodeVal node_val(double P, double sQ) {
-    NodeVal v;
+__device__ __forceinline__ NodeValH node_val_h(double P, double Q) {
+    NodeValH v;
     v.y0 = __builtin_amdgcn_rsq(P);
     const double h = v.y0 * v.y0;
     const double eps = __builtin_fma(-P, h, 1.0);
     v.ip = __builtin_fma(h, eps, h);
-    v.z = sQ * v.ip;
-    v.arg = __builtin_fma(eps, -0.5, v.z);
+    v.zh = __builtin_fma(Q, v.ip, -0.5);
+    v.arg = __builtin_fma(eps, -0.5, v.zh);
     return v;
 }
 
-// The node in the scaled form of the three-centre passes: with Pr = Pn(s)/s and Q = Qn(s), so that
-// z = Q/Pr = s Qn/Pn without the product s Qn, returns y0 ~ Pr^(-1/2) and ip = 1/Pr (as node_val),
-// zh = z - 1/2 and arg = zh - eps/2: y0 e^-arg = e^(1/2) Pr^(-1/2) e^-z (the records fold
-// s^(-1/2) e^(-1/2) into the node weight). zh is what the reverse needs, s df/dPn = G zh with
-// G = f/Pr.
-struct NodeValH {
-    double y0;   // hardware estimate of Pr^(-1/2)
-    double zh;   // Q / Pr - 1/2
-    double ip;   // 1 / Pr
-    double arg;  // zh - eps/2
-};
-
 // The forward passes need only y0 and the exponent argument: with a = Q h - 1/2,
-// arg = a (1 + eps) = Q h (1 + eps) - 1/2 - eps/2, node_val_h's arg without forming 1/Pr.
+// arg = a (1 + eps) = Q h (1 + eps) - 1/2 - eps/2, node_val_h's arg without forming 1/P.
 struct NodeArgH {
-    double y0;   // hardware estimate of Pr^(-1/2)
+    double y0;   // hardware estimate of P^(-1/2)
     double arg;  // z - 1/2 - eps/2, |eps| < 1.1e-7
 };
 
@@ -173,18 +148,7 @@ __device__ __forceinline__ NodeArgH node_arg_h(double P, double Q) {
     return v;
 }
 
-__device__ __forceinline__ NodeValH node_val_h(double P, double Q) {
-    NodeValH v;
-    v.y0 = __builtin_amdgcn_rsq(P);
-    const double h = v.y0 * v.y0;
-    const double eps = __builtin_fma(-P, h, 1.0);
-    v.ip = __builtin_fma(h, eps, h);
-    v.zh = __builtin_fma(Q, v.ip, -0.5);
-    v.arg = __builtin_fma(eps, -0.5, v.zh);
-    return v;
-}
-
-// 2^(j/256), j = 0..255, correctly rounded (the table of exp_neg_tab).
+// 2^(j/256), j = 0..255, correctly rounded.
 __host__ __device__ constexpr double exp2_frac(int j) {
     constexpr double t[256] = {
     0x1.0000000000000p+0, 0x1.00b1afa5abcbfp+0, 0x1.0163da9fb3335p+0, 0x1.02168143b0281p+0,

@@ -1054,7 +1054,7 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
                                                      unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
     __shared__ double kw[4][kEriSymSlab];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     for (int i = threadIdx.x; i < 4 * kEriSymSlab; i += blockDim.x) (&kw[0][0])[i] = 0.0;
     __syncthreads();
     const int wv = threadIdx.x >> 6;
@@ -1085,16 +1085,16 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
         double F = 0.0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            constexpr double st = quad_t(t) * quad_t(t);
-            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
-                                                              G.J1), 1.0);
+            constexpr double st = quad_t(t) * quad_t(t), is = 1.0 / st;
+            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / 24.0);
+            const double Er = __builtin_fma(st, __builtin_fma(st, G.J3, G.J2), G.J1) + is;
             const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
-            const NodeVal v = node_val(Es, st * num);
-            F = __builtin_fma(quad_w(t) * v.y0, exp_neg_tab(v.arg, tab), F);
+            const NodeArgH v = node_arg_h(Er, num);
+            F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
             if constexpr (kMask)
-                return screen_after(t) && wave_all_beyond(off ? kFarAway : v.z);
+                return screen_after(t) && wave_all_beyond_h(off ? kFarAway : v.arg);
             else
-                return screen_after(t) && wave_all_beyond(v.z);
+                return screen_after(t) && wave_all_beyond_h(v.arg);
         };
         nodes += node_loop<0>(node);
         F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(256) void k_eri_bwd_sym(int64_t n, const double* __
                                                      double* __restrict__ ket_part,
                                                      unsigned long long* __restrict__ work) {
     __shared__ double tab[256];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac(i);
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     __syncthreads();
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t a = A0 + (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1188,25 +1188,25 @@ __global__ __launch_bounds__(256) void k_eri_bwd_sym(int64_t n, const double* __
         double F = 0, A1 = 0, A2 = 0, A3 = 0, B1 = 0, B2 = 0, B3 = 0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            constexpr double st = quad_t(t) * quad_t(t);
-            const double Es = __builtin_fma(st, __builtin_fma(st, __builtin_fma(st, G.J3, G.J2),
-                                                              G.J1), 1.0);
+            constexpr double st = quad_t(t) * quad_t(t), is = 1.0 / st;
+            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / 24.0);
+            const double Er = __builtin_fma(st, __builtin_fma(st, G.J3, G.J2), G.J1) + is;
             const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
-            const NodeVal v = node_val(Es, st * num);
-            const double f = (quad_w(t) * v.y0) * exp_neg_tab(v.arg, tab);
+            const NodeValH v = node_val_h(Er, num);
+            const double f = (wh * v.y0) * exp_neg_tab_x24(v.arg, tab);
             F += f;
-            const double g = f * v.ip;
-            const double gh = g * (v.z - 0.5);
-            A1 = __builtin_fma(gh, st, A1);
-            A2 = __builtin_fma(gh, st * st, A2);
-            A3 = __builtin_fma(gh, st * st * st, A3);
-            B1 = __builtin_fma(g, st, B1);
-            B2 = __builtin_fma(g, st * st, B2);
-            B3 = __builtin_fma(g, st * st * st, B3);
+            const double gs = f * v.ip;                 // g s, g = f / Es
+            const double ghs = gs * v.zh;               // gh s, gh = g (z - 1/2)
+            A1 += ghs;
+            A2 = __builtin_fma(ghs, st, A2);
+            A3 = __builtin_fma(ghs, st * st, A3);
+            B1 += gs;
+            B2 = __builtin_fma(gs, st, B2);
+            B3 = __builtin_fma(gs, st * st, B3);
             if constexpr (kMask)
-                return screen_after(t) && wave_all_beyond(off ? kFarAway : v.z);
+                return screen_after(t) && wave_all_beyond_h(off ? kFarAway : v.zh);
             else
-                return screen_after(t) && wave_all_beyond(v.z);
+                return screen_after(t) && wave_all_beyond_h(v.zh);
         };
         nodes += node_loop<0>(node);
         F = (G.p0 == G.p0) ? F : G.p0;
