@@ -279,12 +279,14 @@ __device__ __forceinline__ bool wave_all_beyond_h(double zh) {
 }
 
 // Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / 24, s_t^2
-// and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes.
+// and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes;
+// `scale` multiplies the weight (the record's u, for the reverse pass that folds it in).
 constexpr double kExpMinusHalf = 0x1.368b2fc6f960ap-1;     // e^(-1/2), correctly rounded
 
-__device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp) {
+__device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp,
+                                                double scale = 1.0) {
     o[8 + t] = s;
-    o[8 + kNodes + t] = wp / sqrt(s) * (kExpMinusHalf / 24.0);
+    o[8 + kNodes + t] = wp / sqrt(s) * (kExpMinusHalf / 24.0) * scale;
     o[8 + 2 * kNodes + t] = s * s;
     o[8 + 3 * kNodes + t] = 1.0 / s;
 }
@@ -458,7 +460,7 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 
 
 // Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wh_t | s_t^2 |
-// 1/s_t (put_node_consts). Records are stored centre-grouped: with G = N / M exponent scales (the
+// 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored centre-grouped: with G = N / M exponent scales (the
 // product aux is scale-major, P = s M + m, every scale of splat m at one centre), the record of P
 // sits at slot m G + s, so the scales sharing a centre are consecutive; otherwise (N not a
 // multiple of M) in aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
@@ -468,7 +470,8 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
                                const double* __restrict__ dgamma,
-                               const double* __restrict__ dscale, double* __restrict__ out) {
+                               const double* __restrict__ dscale, int fold,
+                               double* __restrict__ out) {
     const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (p >= N) return;
     const double b = beta[p];
@@ -477,7 +480,8 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
     const int64_t slot = aux_slot(p, N, G);
     double* o = out + kAuxRec * slot;
     o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
-    o[3] = (dgamma ? dgamma[p] : 1.0) * (dscale ? *dscale : 1.0) * kn[p];
+    const double u = (dgamma ? dgamma[p] : 1.0) * (dscale ? *dscale : 1.0) * kn[p];
+    o[3] = u;
     bool first = true;
     if (slot > 0) {
         const int64_t q = aux_of_slot(slot - 1, N, G);
@@ -488,7 +492,7 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
                       __builtin_bit_cast(uint64_t, R[3 * p + 2]));
     }
     o[4] = b; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
-    for (int t = 0; t < kNodes; ++t) put_node_consts(o, t, s[t], wp[t]);
+    for (int t = 0; t < kNodes; ++t) put_node_consts(o, t, s[t], wp[t], fold ? u : 1.0);
 }
 
 // One lane per pair slot; accumulates over a slab of aux records (u = dgamma_P KN_P)
@@ -500,6 +504,9 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // centre: C0..C2 = sum u dQ0..2 over the group, then Vc += C0 d, ..., Sb += C2 d d^T.
 // Each node runs in the scaled form Pr = Pn/s (node_val_h): G = f/Pr = g s, so the node sums are
 // gs1..3 = sum G (1, s, s^2) = sum g s^(1..3) and dP0..2 = sum G (z - 1/2) (1/s, 1, s).
+// With kFold the record weights already carry u (k_aux_bwd_prep with fold): the node sums then run
+// over all records of a centre and are turned into jt, T1..T3 and C0..C2 once per centre (flush),
+// since every per-record term is linear in u and q0, q1 are the centre's.
 // With kLaneU the cotangent of (P|a) is not separable: u = x[3] * ut[slot * ldu + p] per lane
 // (the exchange's dE/d(P|a), stored slot-major).
 // With kAtomF the records are nuclei (point charges) and the pass also forms every nucleus' force
@@ -510,7 +517,7 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // later).
 constexpr int kAtomChunk = 64;
 
-template <bool kLaneU, bool kAtomF = false>
+template <bool kLaneU, bool kAtomF = false, bool kFold = false>
 __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
@@ -539,7 +546,16 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     double ad[3] = {0, 0, 0}, a2d[3] = {0, 0, 0};      // Ah d, Ah^2 d (kAtomF)
     const double cq2 = kAtomF && live ? 2.0 * r[13] * r[14] : 0.0;
     int64_t chunk0 = blockIdx.y * per_slab;
+    double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;      // node sums
     auto flush = [&]() {
+        if constexpr (kFold) {           // the node sums span the centre's records, u folded in
+            jt += (q0 == q0) ? F : q0;   // a NaN centre propagates
+            T3 += __builtin_fma(q0, -gs1, dP0);
+            T2 += dP1;
+            T1 += __builtin_fma(q1, -gs2, dP2);
+            C0 = -gs1; C1 = -gs2; C2 = -gs3;
+            F = 0; dP0 = 0; dP1 = 0; dP2 = 0; gs1 = 0; gs2 = 0; gs3 = 0;
+        }
         const double e1x = C1 * d[0], e1y = C1 * d[1], e1z = C1 * d[2];
         const double e2x = C2 * d[0], e2y = C2 * d[1], e2z = C2 * d[2];
         Vc[0] = __builtin_fma(C0, d[0], Vc[0]);
@@ -589,7 +605,9 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
                 a2d[2] = xz * ax + yz * ay + zz * az;
             }
         }
-        double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;
+        if constexpr (!kFold) {
+            F = 0; dP0 = 0; dP1 = 0; dP2 = 0; gs1 = 0; gs2 = 0; gs3 = 0;
+        }
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
             const double st = x[8 + t], wh = x[8 + kNodes + t], s2 = x[8 + 2 * kNodes + t],
@@ -610,6 +628,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             return screen_after(t) && wave_all_beyond_h(v.zh);
         };
         nodes += node_loop<0>(node);
+        if constexpr (kFold) continue;
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
         jt = __builtin_fma(u, F, jt);
         T3 = __builtin_fma(u, __builtin_fma(q0, -gs1, dP0), T3);
@@ -1630,7 +1649,7 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     GSDFT_HIP(hipGetLastError());
     const int64_t G = (N % M == 0) ? N / M : 1;
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, w.aux);
+                                                      nullptr, 0, w.aux);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
@@ -2030,7 +2049,7 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
                              weight, w, s));
     const int64_t G = (N % M == 0) ? N / M : 1;          // scales per centre of a product aux
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, w.aux);
+                                                      nullptr, 0, w.aux);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
@@ -2072,16 +2091,17 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     if (n > 0) {
         const int64_t G = (N % M == 0) ? N / M : 1;      // scales per centre of a product aux
         k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers,
-                                                          dgamma, dgamma_scale, w.aux);
+                                                          dgamma, dgamma_scale, 1, w.aux);
         GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
         k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
                                                                 w.rec_sorted);
         const Split sp = bwd_split(N, n);
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
-        k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
-                                                profile_work_counter(kProfGammaBwd), nullptr, 0,
-                                                nullptr);
+        k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
+                                                             sp.per_slab, w.acc,
+                                                             profile_work_counter(kProfGammaBwd),
+                                                             nullptr, 0, nullptr);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
         k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPref3c, w.pair_order.perm, pi,
