@@ -278,6 +278,12 @@ __device__ __forceinline__ bool wave_all_beyond_h(double zh) {
     return __builtin_amdgcn_ballot_w64(!(zh > kSkipZ - 0.5)) == 0;
 }
 
+// The record's "first" flag (1.0 or 0.0): tested on its bits, so the wave-uniform test is a scalar
+// compare rather than a vector one.
+__device__ __forceinline__ bool new_centre(const double* __restrict__ x) {
+    return __builtin_bit_cast(uint64_t, x[5]) != 0;
+}
+
 // Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / 24, s_t^2
 // and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes;
 // `scale` multiplies the weight (the record's u, for the reverse pass that folds it in).
@@ -351,10 +357,10 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
         const double Px = live ? r[9] : kFarAway, Py = live ? r[10] : kFarAway,
                      Pz = live ? r[11] : kFarAway;
         const double coef = live ? r[12] : 0.0;
-        double q0d = 0, q1 = 0, X0 = 0, rr = 0;
+        double q0d = 0, q1 = 0, X0 = 0, rr = 0, cf = coef;
         for (int j = 0; j < nrec; ++j) {
             const double* __restrict__ x = aux + kAuxRec * (q0 + j);
-            if (j == 0 || x[5] != 0.0) {             // a new centre (wave-uniform)
+            if (j == 0 || new_centre(x)) {           // wave-uniform
                 const double dx = x[0] - Px, dy = x[1] - Py, dz = x[2] - Pz;
                 const double ax = xx * dx + xy * dy + xz * dz;
                 const double ay = xy * dx + yy * dy + yz * dz;
@@ -364,6 +370,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 const double q2 = ax * ax + ay * ay + az * az;
                 X0 = I3 * q0d;
                 rr = I1 * q1 - q2;
+                cf = (q0d == q0d) ? coef : q0d;      // a NaN centre propagates
             }
             double F = 0.0;
             auto node = [&](auto tc) {
@@ -376,8 +383,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 return screen_after(t) && wave_all_beyond_h(v.arg);
             };
             lane_nodes += lanes * node_loop<0>(node);
-            F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
-            acc[j][threadIdx.x] = __builtin_fma(F, coef, acc[j][threadIdx.x]);
+            acc[j][threadIdx.x] = __builtin_fma(F, cf, acc[j][threadIdx.x]);
         }
     }
     if (work && (threadIdx.x & 63) == 0) atomicAdd(work, (unsigned long long)lane_nodes);
@@ -584,7 +590,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         const double* __restrict__ x = aux + kAuxRec * p;
         double u = x[3];
         if constexpr (kLaneU) u *= live ? ut[a * ldu + p] : 0.0;
-        if (p == p0 || x[5] != 0.0) {            // a new centre (wave-uniform)
+        if (p == p0 || new_centre(x)) {          // wave-uniform
             flush();
             const int l = threadIdx.x;
             const double xx = geo[0][l], yy = geo[1][l], zz = geo[2][l], xy = geo[3][l],
@@ -1410,11 +1416,11 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
     const double coef = r[12];
     const int64_t l0 = (int64_t)blockIdx.y * kBlockRecs;
     const int nrec = (int)min((int64_t)kBlockRecs, W - l0);
-    double q0d = 0, q1 = 0, X0 = 0, rr = 0;
+    double q0d = 0, q1 = 0, X0 = 0, rr = 0, cf = coef;
     uint32_t nodes = 0;
     for (int j = 0; j < nrec; ++j) {
         const double* __restrict__ x = aux + kAuxRec * (l0 + j);
-        if (j == 0 || x[5] != 0.0) {             // a new centre (wave-uniform)
+        if (j == 0 || new_centre(x)) {           // wave-uniform
             const double dx = x[0] - Px, dy = x[1] - Py, dz = x[2] - Pz;
             const double ax = xx * dx + xy * dy + xz * dz;
             const double ay = xy * dx + yy * dy + yz * dz;
@@ -1424,6 +1430,7 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             const double q2 = ax * ax + ay * ay + az * az;
             X0 = I3 * q0d;
             rr = I1 * q1 - q2;
+            cf = (q0d == q0d) ? coef : q0d;          // a NaN centre propagates
         }
         double F = 0.0;
         auto node = [&](auto tc) {
@@ -1436,8 +1443,7 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             return screen_after(t) && wave_all_beyond_h(v.arg);
         };
         nodes += node_loop<0>(node);
-        F = (q0d == q0d) ? F : q0d;              // a NaN centre propagates
-        val[j][threadIdx.x] = (F * coef) * x[3];
+        val[j][threadIdx.x] = (F * cf) * x[3];
     }
     count_work(work, live, nodes);
     if (!live) return;
