@@ -416,6 +416,8 @@ extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* l
 
 extern "C" int gsdft_pair_index_workspace_size(int64_t M, int64_t n, size_t* bytes) {
     if (M < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "pair_index_workspace_size: bad arguments");
+    if (n >= INT32_MAX)
+        return fail(GSDFT_ERR_ARG, "pair_index_workspace_size: n exceeds the int32 range");
     size_t sb = 0;
     if (hipcub::DeviceRadixSort::SortPairs(nullptr, sb, (const int32_t*)nullptr,
                                            (int32_t*)nullptr, (const int32_t*)nullptr,
@@ -435,6 +437,7 @@ extern "C" int gsdft_pair_index(int64_t M, int64_t n, const int32_t* pi, const i
                                 void* stream) {
     if (M <= 0 || n < 0 || !row_ptr || !col_ptr)
         return fail(GSDFT_ERR_ARG, "gsdft_pair_index: bad arguments");
+    if (n >= INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_pair_index: n exceeds the int32 range");
     hipStream_t s = (hipStream_t)stream;
     size_t sb = 0;
     if (hipcub::DeviceRadixSort::SortPairs(nullptr, sb, (const int32_t*)nullptr,

@@ -76,3 +76,17 @@ def test_workspace_queries_accept_empty_inputs(built):
                 rc = lib.gsdft_exchange_workspace_size(4, 2, 8, n, sym, grads, 0, 0,
                                                        ctypes.byref(out))
                 assert rc in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)
+
+
+def test_pair_index_refuses_counts_past_int32(built):
+    """The pair index sorts with 32-bit counts: a pair count past the int32 range is refused with
+    an argument error before any library call, by the size query and by the builder itself."""
+    lib = built.lib()
+    out = ctypes.c_size_t(0)
+    big = 2 ** 31
+    assert lib.gsdft_pair_index_workspace_size(4, big, ctypes.byref(out)) == built.GSDFT_ERR_ARG
+    assert b"int32" in lib.gsdft_last_error()
+    dummy = ctypes.c_int32(0)
+    p = ctypes.byref(dummy)
+    rc = lib.gsdft_pair_index(4, big, p, p, p, p, p, p, None, 0, None)
+    assert rc == built.GSDFT_ERR_ARG
