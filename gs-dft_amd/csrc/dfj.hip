@@ -187,6 +187,18 @@ int launch_scaled_dot(int64_t N, const double* a, const double* b, double scale,
 
 // ------------------------------------------------------------------ pair records
 
+// Workgroups are dispatched to the 8 XCDs in turn (workgroup b to XCD b mod 8). A launch of
+// xcd_grid(nb) workgroups in which workgroup b takes logical block xcd_block(nb) = (b mod 8) chunk
+// + b / 8 (chunk = ceil(nb / 8); -1 past nb) gives each XCD one contiguous range of the nb logical
+// blocks, so neighbouring blocks' reads of shared rows meet in that XCD's L2.
+inline unsigned xcd_grid(int64_t nb) { return (unsigned)(8 * ((nb + 7) / 8)); }
+
+__device__ __forceinline__ int64_t xcd_block(int64_t nb) {
+    const int64_t chunk = (nb + 7) / 8;
+    const int64_t lb = (int64_t)(blockIdx.x % 8) * chunk + blockIdx.x / 8;
+    return lb < nb ? lb : -1;
+}
+
 // q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456; w_a = 1 for a null weight); G lanes
 // per pair.
 template <int G>
@@ -869,7 +881,8 @@ __global__ __launch_bounds__(256) void k_dC(int64_t M, int64_t k,
                                             double* __restrict__ dC) {
     __shared__ int32_t partner[256];
     __shared__ double scale[256];
-    const int64_t m = blockIdx.x;
+    const int64_t m = xcd_block(M);             // XCD-contiguous ranges of splats
+    if (m < 0) return;
     const int64_t r0 = row_ptr[m], r1 = row_ptr[m + 1], c0 = col_ptr[m], c1 = col_ptr[m + 1];
     const int64_t nr = r1 - r0, total = nr + (c1 - c0);
     for (int64_t base = 0; base < k; base += 256 * CH) {
@@ -1546,13 +1559,13 @@ int launch_dC(int64_t M, int64_t k, const int32_t* row_ptr, const int32_t* row_p
               const int32_t* pj, const double* J, const double* weight, const double* C,
               const double* occ, double* dC, hipStream_t s) {
     if (k <= 256)
-        k_dC<1><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+        k_dC<1><<<xcd_grid(M), 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
                                             weight, C, occ, dC);
     else if (k <= 1024)
-        k_dC<4><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+        k_dC<4><<<xcd_grid(M), 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
                                             weight, C, occ, dC);
     else
-        k_dC<8><<<(unsigned)M, 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+        k_dC<8><<<xcd_grid(M), 256, 0, s>>>(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
                                             weight, C, occ, dC);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
