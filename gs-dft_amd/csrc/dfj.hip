@@ -332,8 +332,10 @@ __device__ __forceinline__ void count_work(unsigned long long* work, bool live, 
 // ------------------------------------------------------------------ forward
 
 // Forward with one lane per pair slot (the reverse's slot order) and the aux records of the reverse
-// (centre-grouped, wave-uniform): block (g, s) sums the pair slots [g kFwdPairs, (g + 1) kFwdPairs)
-// against the kFwdRecs aux slots from s kFwdRecs on. The centre-dependent terms (d, Ah d, q0..q2)
+// (centre-grouped, wave-uniform): block g nrb + s (nrb = ceil(N / kFwdRecs)) sums the pair slots
+// [g kFwdPairs, (g + 1) kFwdPairs) against the kFwdRecs aux slots from s kFwdRecs on. The record
+// blocks run fastest, so the workgroups dispatched together share their pair slots (read once
+// into L2) and differ only in their aux records. The centre-dependent terms (d, Ah d, q0..q2)
 // are formed once per centre and shared by its exponent scales, and the wave's node screen acts on
 // 64 pairs in precision band + Morton order. Each lane keeps its running sums of coef_a F(P, a) for
 // the block's records in LDS; at the end the 256 lane sums of each record are added in lane order
@@ -353,9 +355,10 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
 #pragma unroll
     for (int j = 0; j < kFwdRecs; ++j) acc[j][threadIdx.x] = 0.0;
     __syncthreads();
-    const int64_t q0 = (int64_t)blockIdx.y * kFwdRecs;
+    const int64_t nrb = (N + kFwdRecs - 1) / kFwdRecs;
+    const int64_t q0 = ((int64_t)blockIdx.x % nrb) * kFwdRecs, g = (int64_t)blockIdx.x / nrb;
     const int nrec = (int)min((int64_t)kFwdRecs, N - q0);
-    const int64_t a_begin = (int64_t)blockIdx.x * kFwdPairs;
+    const int64_t a_begin = g * kFwdPairs;
     const int64_t a_end = min(n, a_begin + kFwdPairs);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint64_t lane_nodes = 0;                 // profiling: node evaluations over live lanes
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
     if ((int)threadIdx.x < nrec) {
         double sum = 0.0;
         for (int l = 0; l < 256; ++l) sum += acc[threadIdx.x][l];
-        partial[(int64_t)blockIdx.x * N + q0 + threadIdx.x] =
+        partial[g * N + q0 + threadIdx.x] =
             sum * aux[kAuxRec * (q0 + threadIdx.x) + 3];
     }
 }
@@ -2075,8 +2078,9 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
                                                             w.rec_sorted);
     GSDFT_HIP(hipGetLastError());
     const int64_t groups = (n + kFwdPairs - 1) / kFwdPairs;
-    if (N > 65535LL * kFwdRecs) return fail(GSDFT_ERR_ARG, "gsdft_gamma: N_aux too large");
-    dim3 grid((unsigned)groups, (unsigned)((N + kFwdRecs - 1) / kFwdRecs));
+    const int64_t blocks = groups * ((N + kFwdRecs - 1) / kFwdRecs);
+    if (blocks > INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_gamma: n x N_aux too large");
+    const dim3 grid((unsigned)blocks);
     profile_begin(kProfGammaFwd, s);
     k_gamma_fwd_pairs<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, w.partial,
                                            profile_work_counter(kProfGammaFwd));
