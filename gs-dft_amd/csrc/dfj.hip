@@ -280,12 +280,8 @@ __host__ __device__ constexpr bool screen_after(int t) {
 // kFirstSkip on), so they never keep a wave in the loop and need no mask of their own.
 constexpr double kFarAway = 1e20;
 
-__device__ __forceinline__ bool wave_all_beyond(double z) {
-    return __builtin_amdgcn_ballot_w64(!(z > kSkipZ)) == 0;
-}
-
-// The same test on zh = z - 1/2 (node_val_h), or on the forward's arg = zh - eps/2 (node_arg_h),
-// which differs from zh by less than 6e-8.
+// True once every lane of the wave has z > kSkipZ, tested on zh = z - 1/2 (node_val_h) or on the
+// forward's arg = zh - eps/2 (node_arg_h), which differs from zh by less than 6e-8.
 __device__ __forceinline__ bool wave_all_beyond_h(double zh) {
     return __builtin_amdgcn_ballot_w64(!(zh > kSkipZ - 0.5)) == 0;
 }
