@@ -37,6 +37,28 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo) and its logical CPU count."""
+    name = "unknown"
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
+
+
+def counter_record(workload: str, kernel: str):
+    """The FP64 VALU counter figures of ``kernel`` at ``workload`` from the rocprofv3 counter runs
+    summarised in profiles/three_centre_fp64_counters.json (None when not recorded)."""
+    f = ROOT / "profiles" / "three_centre_fp64_counters.json"
+    if not f.exists():
+        return None
+    return json.loads(f.read_text()).get(workload, {}).get(kernel)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,9 +231,10 @@ def main() -> int:
         cpu_step_ms = per_pair * n * 1e3
         cpu = {"value": cpu_step_ms, "unit": "ms per fwd+bwd step (three-centre gamma + reverse, "
                "extrapolated linearly in pairs)", "cores": orc.num_threads(), "kind": "port",
-               "sample": f"{m_cpu} of {n} pairs x all {N} aux functions, {t_cpu:.1f} s on "
-                         f"{orc.num_threads()} threads (C oracle, OpenMP); metric, Cholesky "
-                         f"and solves excluded",
+               "sample": f"{m_cpu} of {n} pairs ({100.0 * m_cpu / n:.3g}%) x all {N} aux "
+                         f"functions, {t_cpu:.1f} s on {orc.num_threads()} threads (C oracle, "
+                         f"OpenMP); metric, Cholesky and solves excluded",
+               "sample_frac": m_cpu / n, "cpu_model": cpu_model(),
                "integrals_per_s": integrals / (cpu_step_ms * 1e-3)}
         log(f"cpu baseline: {cpu_step_ms / 1e3:.1f} s per step extrapolated from {m_cpu} pairs")
 
@@ -232,16 +255,22 @@ def main() -> int:
                                f"N_aux={N}, k={s.k}, eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "N_aux": N, "k": s.k, "n_pairs": n,
                    "pad_to": pad_to, "eps": s.eps, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": f"three-centre {dom[0]} ({dom[1]})",
+        "roofline": {"bound": "valu", "kernel": f"three-centre {dom[0]} ({dom[1]})",
                      "achieved": dom[4] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
-                     "frac": dom[4] / PEAK_FP64, "traffic": traffic,
+                     "frac": dom[4] / PEAK_FP64, "frac_basis": "algorithmic",
+                     "traffic": traffic,
                      "flops_per_integral": dom[3], "integrals_per_launch": integrals,
                      "kernel_ms": dom[2],
                      "executed_achieved": dom[5] / 1e12, "executed_frac": dom[5] / PEAK_FP64,
                      "nodes_evaluated_frac": dom[6],
-                     "note": "FP64 compute bound on the vector ALUs (MI355X FP64 vector peak = "
-                             "FP64 matrix peak = 78.6 TFLOP/s); achieved counts the fixed "
-                             "per-integral work, executed_* only the nodes the screen kept"},
+                     "fp64_counters": counter_record(s.name, dom[1]),
+                     "note": "FP64 compute bound on the vector ALUs (VALU; MI355X FP64 vector "
+                             "peak 78.6 TFLOP/s, no MFMA: the work is elementwise). frac is "
+                             "algorithmic: it credits every integral with all 20 nodes, so the "
+                             "nodes the screen skips count as done; executed_* count only the "
+                             "nodes evaluated; fp64_counters holds the hardware FP64 VALU "
+                             "instruction rate of the same kernel at this workload from the "
+                             "rocprofv3 counter runs in profiles/"},
         "kernels": {"three_centre_fwd_ms": fwd_ms, "three_centre_bwd_ms": bwd_ms,
                     "fwd_frac_fp64": fwd_tf / PEAK_FP64, "bwd_frac_fp64": bwd_tf / PEAK_FP64,
                     "fwd_executed_frac_fp64": fwd_exec_tf / PEAK_FP64,
@@ -347,7 +376,7 @@ def run_nuclear(args) -> int:
         t_cpu, m_cpu = run(m) if m > m_probe else (t_probe, m_probe)
         cpu_ms = t_cpu / m_cpu * n * 1e3
         cpu = {"value": cpu_ms, "unit": "ms per energy evaluation (extrapolated linearly in "
-               "pairs)", "cores": orc.num_threads(), "kind": "port",
+               "pairs)", "cores": orc.num_threads(), "kind": "port", "cpu_model": cpu_model(),
                "sample": f"{m_cpu} of {n} pairs x all {A} nuclei, {t_cpu:.1f} s on "
                          f"{orc.num_threads()} threads (C oracle, OpenMP); energy only: the "
                          f"oracle has no hand-written reverse pass for this term",
@@ -365,11 +394,13 @@ def run_nuclear(args) -> int:
                                f"{A} nuclei, k={s.k}, eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "n_atoms": A, "k": s.k, "n_pairs": n,
                    "eps": s.eps, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": dom[0], "achieved": dom[3] / 1e12,
+        "roofline": {"bound": "valu", "kernel": dom[0], "achieved": dom[3] / 1e12,
                      "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom[3] / PEAK_FP64,
+                     "frac_basis": "algorithmic",
                      "traffic": None, "flops_per_integral": dom[2],
                      "integrals_per_launch": integrals, "kernel_ms": dom[1],
-                     "note": "FP64 vector bound; fixed per-integral work at 20 nodes"},
+                     "note": "FP64 vector (VALU) bound; algorithmic: every integral credited "
+                             "with all 20 nodes, including the nodes the screen skips"},
         "kernels": {"pair_pass_ms": pair_ms, "force_sums_ms": atom_ms,
                     "pair_nodes_evaluated_frac": pair_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
@@ -475,6 +506,7 @@ def run_exact(args) -> int:
         cpu_ms = t_cpu / m_cpu * n * 1e3
         cpu = {"value": cpu_ms, "unit": "ms per energy evaluation (all (a|b), extrapolated "
                "linearly in bra pairs)", "cores": orc.num_threads(), "kind": "port",
+               "cpu_model": cpu_model(),
                "sample": f"{m_cpu} of {n} bra pairs x all {n} ket pairs, {t_cpu:.1f} s on "
                          f"{orc.num_threads()} threads (C oracle, OpenMP, the reference's Schur "
                          f"node form); energy only",
@@ -492,13 +524,14 @@ def run_exact(args) -> int:
                                f"eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "k": s.k, "n_pairs": n, "eps": s.eps,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "exact pair-pair reverse (k_eri_bwd_sym, all bands)",
+        "roofline": {"bound": "valu", "kernel": "exact pair-pair reverse (k_eri_bwd_sym, all bands)",
                      "achieved": bwd_tf / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
-                     "frac": bwd_tf / PEAK_FP64, "traffic": None,
+                     "frac": bwd_tf / PEAK_FP64, "frac_basis": "algorithmic", "traffic": None,
                      "flops_per_integral": FLOPS_ERI_BWD, "integrals_per_launch": sym_integrals,
                      "kernel_ms": bwd_ms,
-                     "note": "FP64 vector bound; fixed per-integral work at 20 nodes over the "
-                             "n(n+1)/2 unordered pair-pairs each pass evaluates ((a|b) = (b|a)); "
+                     "note": "FP64 vector (VALU) bound; algorithmic: every integral credited "
+                             "with all 20 nodes, over the n(n+1)/2 unordered pair-pairs each "
+                             "pass evaluates ((a|b) = (b|a)); "
                              "kernel_ms spans every band launch and its reductions"},
         "kernels": {"reverse_ms": bwd_ms, "forward_ms": fwd_ms,
                     "energy_only_ms": wall_e * 1e3,
@@ -636,7 +669,7 @@ def run_exchange(args) -> int:
         cpu_ms = (t_pairs / m_pairs * n + t_fixed) * 1e3
         cpu = {"value": cpu_ms, "unit": "ms per energy evaluation (pair part extrapolated "
                "linearly in pairs, plus the measured M build and solve)",
-               "cores": orc.num_threads(), "kind": "port",
+               "cores": orc.num_threads(), "kind": "port", "cpu_model": cpu_model(),
                "sample": f"{m_pairs} of {n} pairs x all {N} aux ({t_pairs:.1f} s) + M = D D^T "
                          f"and the dense solve at full size ({t_fixed:.1f} s) on "
                          f"{orc.num_threads()} threads (C oracle three-centre block, numpy "
@@ -749,6 +782,7 @@ def run_grid(args) -> int:
         cpu_ms = t_cpu / m_cpu * G * 1e3
         cpu = {"value": cpu_ms, "unit": "ms per forward (rho, grad rho) evaluation, extrapolated "
                "linearly in grid points", "cores": torch.get_num_threads(), "kind": "port",
+               "cpu_model": cpu_model(),
                "sample": f"{m_cpu} of {G} points, {t_cpu:.1f} s (torch float64 restatement of "
                          f"the reference on the host, {torch.get_num_threads()} threads); "
                          f"forward only"}

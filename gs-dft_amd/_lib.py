@@ -43,6 +43,8 @@ SIGNATURES = {
     "gsdft_pair_index_workspace_size": [_i64, _i64, _psz],
     "gsdft_pair_index": [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_product_aux": [_i64, _vp, _vp, _vp, _pd, _int, _vp, _vp, _vp, _sz, _vp],
+    "gsdft_product_aux_pairs": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _pd, _int, _vp, _vp,
+                                _vp, _sz, _vp],
     "gsdft_metric_workspace_size": [_i64, _psz],
     "gsdft_aux_metric": [_i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp],
     "gsdft_cholesky": [_i64, _vp, _vp, _sz, _vp],

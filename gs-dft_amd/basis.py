@@ -98,13 +98,11 @@ def _has_splat_interface(basis) -> bool:
 
 def init_product_aux(basis: Splat, pi=None, pj=None, valid=None, *, scales=(1.0,),
                      diagonal_only: bool = True) -> IsotropicSplat:
-    """Frozen density-fitting aux from the splats' self-products (gs_dft/basis/isotropic.py:81-116):
-    one isotropic aux per splat and scale at the product centre with exponent
-    det(2 A_i)^(1/3) * s, concatenated scale-major."""
-    if not diagonal_only:
-        raise NotImplementedError("init_product_aux(diagonal_only=False): the off-diagonal "
-                                  "product aux is not part of this library; df(diagonal=True) "
-                                  "is the production setting")
+    """Frozen density-fitting aux from the splats' pair products (gs_dft/basis/isotropic.py:81-116):
+    one isotropic aux per kept pair and scale at the product centre with exponent
+    det(A_i + A_j)^(1/3) * s, concatenated scale-major. With ``diagonal_only`` (or no ``pi``) the
+    pairs are the self-products (i, i); otherwise they are the listed ``(pi, pj)``, and entries whose
+    ``valid`` is 0 (padding) get the inert exponent s."""
     if not _has_splat_interface(basis):
         raise NotImplementedError(f"init_product_aux: {type(basis).__name__} is not a Splat")
     scales = tuple(float(s) for s in scales)
@@ -112,11 +110,33 @@ def init_product_aux(basis: Splat, pi=None, pj=None, valid=None, *, scales=(1.0,
         raise ValueError("init_product_aux needs at least one exponent scale")
     M = basis.n_basis
     dev = basis.centers.device
-    la = torch.empty(len(scales) * M, dtype=torch.float64, device=dev)
-    cen = torch.empty((len(scales) * M, 3), dtype=torch.float64, device=dev)
     sc = (ctypes.c_double * len(scales))(*scales)
     q, l, c = (t.detach().contiguous() for t in (basis.quat, basis.log_scale, basis.centers))
-    _lib.check(_lib.lib().gsdft_product_aux(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), sc,
-                                            len(scales), _lib.ptr(la), _lib.ptr(cen), None, 0,
-                                            _lib.stream()), "gsdft_product_aux")
+    L = _lib.lib()
+    if diagonal_only or pi is None:
+        la = torch.empty(len(scales) * M, dtype=torch.float64, device=dev)
+        cen = torch.empty((len(scales) * M, 3), dtype=torch.float64, device=dev)
+        _lib.check(L.gsdft_product_aux(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), sc, len(scales),
+                                       _lib.ptr(la), _lib.ptr(cen), None, 0, _lib.stream()),
+                   "gsdft_product_aux")
+        return IsotropicSplat(log_alpha=la, centers=cen)
+    from .screening import check_pair_indices
+    if pj is None:
+        raise ValueError("init_product_aux(diagonal_only=False) with pi needs pj as well")
+    pi_t, pj_t = _lib.i32(pi, dev).reshape(-1), _lib.i32(pj, dev).reshape(-1)
+    check_pair_indices(pi_t, pj_t, M, "init_product_aux")
+    n = pi_t.shape[0]
+    v = None
+    if valid is not None:
+        v = _lib.f64(torch.as_tensor(valid).to(torch.float64) if not isinstance(valid, torch.Tensor)
+                     else valid.detach().to(torch.float64), dev).reshape(-1)
+        if v.shape[0] != n:
+            raise ValueError("init_product_aux: valid must have one entry per listed pair")
+    la = torch.empty(len(scales) * n, dtype=torch.float64, device=dev)
+    cen = torch.empty((len(scales) * n, 3), dtype=torch.float64, device=dev)
+    ws = _lib.workspace(_lib.size_query(L.gsdft_screen_workspace_size, M, 0, 0), dev)
+    _lib.check(L.gsdft_product_aux_pairs(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), n,
+                                         _lib.ptr(pi_t), _lib.ptr(pj_t), _lib.ptr(v), sc,
+                                         len(scales), _lib.ptr(la), _lib.ptr(cen), _lib.ptr(ws),
+                                         ws.numel(), _lib.stream()), "gsdft_product_aux_pairs")
     return IsotropicSplat(log_alpha=la, centers=cen)

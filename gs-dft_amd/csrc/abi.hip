@@ -38,6 +38,14 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(GSDFT_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+int read_back(void* host, const void* dev, size_t bytes, hipStream_t s, const char* what) {
+    const hipError_t ec = hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, s);
+    const hipError_t es = hipStreamSynchronize(s);
+    if (ec != hipSuccess) return hip_fail(ec, what);
+    if (es != hipSuccess) return hip_fail(es, what);
+    return GSDFT_OK;
+}
+
 void profile_begin(int id, hipStream_t s) {
     std::lock_guard<std::mutex> lk(g_prof_mu);
     if (!g_prof_on) return;
@@ -107,16 +115,24 @@ extern "C" int gsdft_profile_read(int id, double* total_ms, int64_t* launches, i
     if (id < 0 || id >= kProfCount || !total_ms || !launches)
         return fail(GSDFT_ERR_ARG, "gsdft_profile_read: bad id");
     std::lock_guard<std::mutex> lk(g_prof_mu);
+    // Every recorded pair is read and destroyed, and the list is emptied, on every path: a pair
+    // left behind after an error would be read again after its events were destroyed.
+    hipError_t first = hipSuccess;
     for (auto& ev : g_open[id]) {
-        GSDFT_HIP(hipEventSynchronize(ev.stop));
+        hipError_t e = hipEventSynchronize(ev.stop);
         float ms = 0.f;
-        GSDFT_HIP(hipEventElapsedTime(&ms, ev.start, ev.stop));
-        g_total_ms[id] += ms;
-        g_launches[id] += 1;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.start, ev.stop);
+        if (e == hipSuccess) {
+            g_total_ms[id] += ms;
+            g_launches[id] += 1;
+        } else if (first == hipSuccess) {
+            first = e;
+        }
         (void)hipEventDestroy(ev.start);
         (void)hipEventDestroy(ev.stop);
     }
     g_open[id].clear();
+    if (first != hipSuccess) return hip_fail(first, "gsdft_profile_read");
     *total_ms = g_total_ms[id];
     *launches = g_launches[id];
     if (reset) {

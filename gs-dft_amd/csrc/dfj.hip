@@ -45,12 +45,15 @@ inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) /
 
 // ------------------------------------------------------------------ aux
 
+// Up to 16 exponent scales by value; longer ladders are launched in chunks (s0 = first scale of
+// the chunk, so output block s0 + s holds scale sc.v[s]).
 struct Scales {
     double v[16];
     int n;
+    int s0;
 };
 
-// gs_dft/basis/isotropic.py:269-281, diagonal_only: the self-product of each splat.
+// gs_dft/basis/isotropic.py:81-116, diagonal_only: the self-product of each splat.
 __global__ void k_product_aux(int64_t M, const double* __restrict__ quat,
                               const double* __restrict__ log_scale,
                               const double* __restrict__ centers, Scales sc,
@@ -64,7 +67,37 @@ __global__ void k_product_aux(int64_t M, const double* __restrict__ quat,
     pair_quantities(A, A, mu, mu, N, N, &Ah, P, &KN);
     const double alpha0 = pow(det3(Ah), 1.0 / 3.0);
     for (int s = 0; s < sc.n; ++s) {
-        const int64_t o = (int64_t)s * M + m;
+        const int64_t o = (int64_t)(sc.s0 + s) * M + m;
+        log_alpha[o] = log(alpha0 * sc.v[s]);
+        aux_centers[3 * o] = P[0];
+        aux_centers[3 * o + 1] = P[1];
+        aux_centers[3 * o + 2] = P[2];
+    }
+}
+
+// gs_dft/basis/isotropic.py:106-116 with diagonal_only=False: one aux per listed pair a at its
+// product centre, alpha_0 = det3(A_i + A_j)^(1/3), and the inert alpha_0 = 1 where valid[a] is 0
+// (valid null: every entry live). The charts come from k_chart (A6 slots xx,yy,zz,xy,xz,yz).
+__global__ void k_product_aux_pairs(int64_t n, const int32_t* __restrict__ pi,
+                                    const int32_t* __restrict__ pj,
+                                    const double* __restrict__ valid,
+                                    const double* __restrict__ A6, const double* __restrict__ Nrm,
+                                    const double* __restrict__ centers, Scales sc,
+                                    double* __restrict__ log_alpha,
+                                    double* __restrict__ aux_centers) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    const int64_t i = pi[a], j = pj[a];
+    const Sym3 Ai = load_sym(A6 + 6 * i), Aj = load_sym(A6 + 6 * j);
+    const double mi[3] = {centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]};
+    const double mj[3] = {centers[3 * j], centers[3 * j + 1], centers[3 * j + 2]};
+    Sym3 Ah;
+    double P[3], KN;
+    pair_quantities(Ai, Aj, mi, mj, Nrm[i], Nrm[j], &Ah, P, &KN);
+    double alpha0 = pow(det3(Ah), 1.0 / 3.0);
+    if (valid && valid[a] == 0.0) alpha0 = 1.0;
+    for (int s = 0; s < sc.n; ++s) {
+        const int64_t o = (int64_t)(sc.s0 + s) * n + a;
         log_alpha[o] = log(alpha0 * sc.v[s]);
         aux_centers[3 * o] = P[0];
         aux_centers[3 * o + 1] = P[1];
@@ -1740,21 +1773,57 @@ int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
 
 using namespace gsdft;
 
+static Scales scale_chunk(const double* scales, int n_scales, int s0) {
+    Scales sc{};
+    sc.s0 = s0;
+    sc.n = std::min(16, n_scales - s0);
+    for (int i = 0; i < sc.n; ++i) sc.v[i] = scales[s0 + i];
+    return sc;
+}
+
 extern "C" int gsdft_product_aux(int64_t M, const double* quat, const double* log_scale,
                                  const double* centers, const double* scales, int n_scales,
                                  double* log_alpha, double* aux_centers, void* workspace,
                                  size_t workspace_bytes, void* stream) {
     (void)workspace;
     (void)workspace_bytes;
-    if (M <= 0 || n_scales <= 0 || n_scales > 16 || !scales)
-        return fail(GSDFT_ERR_ARG, "gsdft_product_aux: need 1..16 scales and M > 0");
-    Scales sc{};
-    sc.n = n_scales;
-    for (int i = 0; i < n_scales; ++i) sc.v[i] = scales[i];
+    if (M <= 0 || n_scales <= 0 || !scales || !quat || !log_scale || !centers || !log_alpha ||
+        !aux_centers)
+        return fail(GSDFT_ERR_ARG, "gsdft_product_aux: need M > 0, at least one scale and every "
+                    "array");
     hipStream_t s = (hipStream_t)stream;
-    k_product_aux<<<blocks_for(M, 256), 256, 0, s>>>(M, quat, log_scale, centers, sc, log_alpha,
-                                                      aux_centers);
-    GSDFT_HIP(hipGetLastError());
+    for (int s0 = 0; s0 < n_scales; s0 += 16) {
+        k_product_aux<<<blocks_for(M, 256), 256, 0, s>>>(M, quat, log_scale, centers,
+                                                          scale_chunk(scales, n_scales, s0),
+                                                          log_alpha, aux_centers);
+        GSDFT_HIP(hipGetLastError());
+    }
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_product_aux_pairs(int64_t M, const double* quat, const double* log_scale,
+                                       const double* centers, int64_t n, const int32_t* pi,
+                                       const int32_t* pj, const double* valid,
+                                       const double* scales, int n_scales, double* log_alpha,
+                                       double* aux_centers, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+    if (M <= 0 || n < 0 || n_scales <= 0 || !scales || !quat || !log_scale || !centers ||
+        (n > 0 && (!pi || !pj || !log_alpha || !aux_centers)))
+        return fail(GSDFT_ERR_ARG, "gsdft_product_aux_pairs: need M > 0, n >= 0, at least one "
+                    "scale and every array");
+    if (n == 0) return GSDFT_OK;
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    double* A6 = ar.take<double>(6 * M + 1);
+    double* Nrm = ar.take<double>(M + 1);
+    if (!A6 || !Nrm) return fail(GSDFT_ERR_WORKSPACE, "gsdft_product_aux_pairs: workspace too small");
+    GSDFT_TRY(launch_chart(M, quat, log_scale, A6, Nrm, s));
+    for (int s0 = 0; s0 < n_scales; s0 += 16) {
+        k_product_aux_pairs<<<blocks_for(n, 256), 256, 0, s>>>(
+            n, pi, pj, valid, A6, Nrm, centers, scale_chunk(scales, n_scales, s0), log_alpha,
+            aux_centers);
+        GSDFT_HIP(hipGetLastError());
+    }
     return GSDFT_OK;
 }
 
@@ -1994,15 +2063,15 @@ extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t work
     GSDFT_TRY(blas_handle(s, &h));
     // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. ILP64 GEMMs:
     // N * N exceeds the int32 range of the rocblas_int interfaces from N = 46341.
-    profile_begin(kProfCholesky, s);
-    GSDFT_TRY(cholesky_blocked(h, s, N, V, info));
-    profile_end(kProfCholesky, s);
+    {
+        ProfileScope prof(kProfCholesky, s);
+        GSDFT_TRY(cholesky_blocked(h, s, N, V, info));
+    }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     k_zero_upper<<<grid, 256, 0, s>>>(N, V);
     GSDFT_HIP(hipGetLastError());
     int64_t h_info = 0;
-    GSDFT_HIP(hipMemcpyAsync(&h_info, info, sizeof(int64_t), hipMemcpyDeviceToHost, s));
-    GSDFT_HIP(hipStreamSynchronize(s));
+    GSDFT_TRY(read_back(&h_info, info, sizeof(int64_t), s, "gsdft_cholesky: status"));
     if (h_info != 0)
         return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not positive "
                     "definite", (long long)h_info);
@@ -2014,9 +2083,10 @@ extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, 
     if (N <= 0 || !L || !gamma || !d) return fail(GSDFT_ERR_ARG, "gsdft_cho_solve: bad arguments");
     hipStream_t s = (hipStream_t)stream;
     GSDFT_HIP(hipMemcpyAsync(d, gamma, sizeof(double) * N, hipMemcpyDeviceToDevice, s));
-    profile_begin(kProfSolve, s);
-    GSDFT_TRY(launch_trsv_pair(N, L, d, s));
-    profile_end(kProfSolve, s);
+    {
+        ProfileScope prof(kProfSolve, s);
+        GSDFT_TRY(launch_trsv_pair(N, L, d, s));
+    }
     if (energy) {
         k_scaled_dot<<<1, 1024, 0, s>>>(N, gamma, d, 0.5, energy);
         GSDFT_HIP(hipGetLastError());

@@ -39,9 +39,23 @@ struct Arena {
     size_t need() const { return (used + 255) & ~size_t(255); }
 };
 
+// Copies `bytes` from device memory into host memory and waits on stream s before returning,
+// whatever the outcome, so no copy into the host buffer (often a stack local) is ever left in
+// flight behind an early return.
+int read_back(void* host, const void* dev, size_t bytes, hipStream_t s, const char* what);
+
 // Optional per-kernel timing with HIP events on the launch stream.
 void profile_begin(int id, hipStream_t s);
 void profile_end(int id, hipStream_t s);
+// Brackets a scope with profile_begin / profile_end, so every return path closes the interval.
+struct ProfileScope {
+    int id;
+    hipStream_t s;
+    ProfileScope(int id_, hipStream_t s_) : id(id_), s(s_) { profile_begin(id, s); }
+    ~ProfileScope() { profile_end(id, s); }
+    ProfileScope(const ProfileScope&) = delete;
+    ProfileScope& operator=(const ProfileScope&) = delete;
+};
 // Device counter of work units for kernel id while profiling is on (current device only), else
 // nullptr; kernels given a counter add their executed units to it.
 unsigned long long* profile_work_counter(int id);

@@ -270,11 +270,8 @@ int screen_scan(int64_t M, const double* quat, const double* log_scale, const do
     GSDFT_HIP(hipcub::DeviceScan::ExclusiveSum(w.scan_tmp, sb, w.counts, w.offsets, (int)T, s));
     int64_t last_off = 0;
     int32_t last_cnt = 0;
-    GSDFT_HIP(hipMemcpyAsync(&last_off, w.offsets + (T - 1), sizeof(int64_t),
-                             hipMemcpyDeviceToHost, s));
-    GSDFT_HIP(hipMemcpyAsync(&last_cnt, w.counts + (T - 1), sizeof(int32_t),
-                             hipMemcpyDeviceToHost, s));
-    GSDFT_HIP(hipStreamSynchronize(s));
+    GSDFT_TRY(read_back(&last_off, w.offsets + (T - 1), sizeof(int64_t), s, "screen: offsets"));
+    GSDFT_TRY(read_back(&last_cnt, w.counts + (T - 1), sizeof(int32_t), s, "screen: counts"));
     *n_sig = last_off + last_cnt;
     return GSDFT_OK;
 }
@@ -343,10 +340,8 @@ extern "C" int gsdft_screen_count(int64_t M, const double* quat, const double* l
     GSDFT_TRY(layout_screen(ar, M, 0, &w));
     if (!w.scan_tmp) return fail(GSDFT_ERR_WORKSPACE, "gsdft_screen_count: workspace too small");
     TileGeom g{M, (M + kTile - 1) / kTile, unique ? 1 : 0, 0, eps};
-    profile_begin(kProfScreen, s);
-    int rc = screen_scan(M, quat, log_scale, centers, g, w, s, n_sig);
-    profile_end(kProfScreen, s);
-    return rc;
+    ProfileScope prof(kProfScreen, s);
+    return screen_scan(M, quat, log_scale, centers, g, w, s, n_sig);
 }
 
 extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* log_scale,
@@ -367,7 +362,7 @@ extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* l
     const int all = (eps < 0.0 && pad_to >= n_all) ? 1 : 0;
     TileGeom g{M, (M + kTile - 1) / kTile, unique ? 1 : 0, all, eps};
     const int64_t T = n_tiles(M);
-    profile_begin(kProfScreen, s);
+    ProfileScope prof(kProfScreen, s);
     GSDFT_TRY(screen_scan(M, quat, log_scale, centers, g, w, s, n_sig));
     const int64_t ns = *n_sig;
     if (ns <= pad_to) {
@@ -377,11 +372,9 @@ extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* l
         if (pad_to > ns)
             k_fill_tail<<<blocks_for(pad_to - ns, 256), 256, 0, s>>>(ns, pad_to, pi, pj, weight);
         GSDFT_HIP(hipGetLastError());
-        profile_end(kProfScreen, s);
         return GSDFT_OK;
     }
     if (ns > 2 * pad_to) {
-        profile_end(kProfScreen, s);
         return fail(GSDFT_ERR_OVERFLOW,
                     "neighbor_pairs: %lld significant pairs exceed 2x the pad (%lld). Raise "
                     "screen.pad -- the run's pair list has outgrown the shape frozen at step 0.",
@@ -391,11 +384,9 @@ extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* l
     Arena ar2{(char*)workspace, workspace_bytes, 0};
     ScreenWs w2;
     GSDFT_TRY(layout_screen(ar2, M, ns, &w2));
-    if (!w2.sort_tmp) {
-        profile_end(kProfScreen, s);
+    if (!w2.sort_tmp)
         return fail(GSDFT_ERR_WORKSPACE, "gsdft_screen_build: the keep-largest path needs "
                     "gsdft_screen_workspace_size(M, unique, %lld)", (long long)ns);
-    }
     // the scan results live at the same offsets in both layouts
     k_screen_emit<<<(unsigned)T, kTile, 0, s>>>(g, w.A6, centers, w.N, w.offsets, 1, ns, nullptr,
                                                  nullptr, nullptr, w2.flat_in, w2.val_in);
@@ -410,7 +401,6 @@ extern "C" int gsdft_screen_build(int64_t M, const double* quat, const double* l
     k_decode<<<blocks_for(pad_to, 256), 256, 0, s>>>(pad_to, w2.flat_in, M, unique ? 1 : 0, pi,
                                                       pj, weight);
     GSDFT_HIP(hipGetLastError());
-    profile_end(kProfScreen, s);
     return GSDFT_OK;
 }
 

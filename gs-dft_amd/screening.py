@@ -21,6 +21,19 @@ def _splat_args(splats):
     return q, l, c
 
 
+def check_pair_indices(pi: torch.Tensor, pj: torch.Tensor, bound: int, what: str) -> None:
+    """Refuses a pair list whose indices leave [0, bound): the kernels read the splat (or C) rows
+    they name without a range check. One host sync."""
+    if pi.shape[0] != pj.shape[0]:
+        raise ValueError(f"{what}: pi and pj must have the same length")
+    if pi.shape[0] == 0:
+        return
+    lo = int(torch.minimum(pi.min(), pj.min()))
+    hi = int(torch.maximum(pi.max(), pj.max()))
+    if lo < 0 or hi >= bound:
+        raise ValueError(f"{what}: pair indices must lie in [0, {bound}), got [{lo}, {hi}]")
+
+
 def _pair_weights(pi: torch.Tensor, pj: torch.Tensor, unique: bool) -> torch.Tensor:
     """Third output of ``neighbor_pairs`` (gs_dft/screening/pairs.py:318-322)."""
     if not unique:
@@ -96,6 +109,7 @@ def screened_overlap_pairs(splats, pi, pj) -> torch.Tensor:
     M = splats.n_basis
     q, l, c = _splat_args(splats)
     pi, pj = _lib.i32(pi, q.device), _lib.i32(pj, q.device)
+    check_pair_indices(pi, pj, M, "screened_overlap_pairs")
     S = torch.empty(pi.shape[0], dtype=torch.float64, device=q.device)
     L = _lib.lib()
     ws = _lib.workspace(_lib.size_query(L.gsdft_screen_workspace_size, M, 0, 0), q.device)
@@ -161,6 +175,7 @@ def density_pairs(C_orth, occ, pi, pj) -> torch.Tensor:
     pi, pj = _lib.i32(pi, dev), _lib.i32(pj, dev)
     if C.dim() != 2 or o.shape[0] != C.shape[1]:
         raise ValueError("density_pairs: C_orth must be (M, k) with one occupation per column")
+    check_pair_indices(pi, pj, C.shape[0], "density_pairs")
     out = torch.empty(pi.shape[0], dtype=torch.float64, device=dev)
     _lib.check(_lib.lib().gsdft_density_pairs(pi.shape[0], _lib.ptr(pi), _lib.ptr(pj), C.shape[1],
                                               _lib.ptr(C), _lib.ptr(o), _lib.ptr(out),
@@ -177,6 +192,7 @@ def screened_nuclear_pairs(splats, pi, pj, atom_coords, atom_charges) -> torch.T
     q, l, c = _splat_args(splats)
     dev = q.device
     pi, pj = _lib.i32(pi, dev), _lib.i32(pj, dev)
+    check_pair_indices(pi, pj, M, "screened_nuclear_pairs")
     R, Z = _atoms(atom_coords, atom_charges, dev)
     n = pi.shape[0]
     V = torch.empty(n, dtype=torch.float64, device=dev)
@@ -258,11 +274,7 @@ def screened_external_energy(splats, C_orth, occ, pi, pj, atom_coords, atom_char
     if pj_t.shape[0] != pi_t.shape[0] or w.shape[0] != pi_t.shape[0]:
         raise ValueError("pi, pj and valid must have the same length")
     n = live_length(w)
-    if n > 0:
-        lo = int(torch.minimum(pi_t[:n].min(), pj_t[:n].min()))
-        hi = int(torch.maximum(pi_t[:n].max(), pj_t[:n].max()))
-        if lo < 0 or hi >= M:
-            raise ValueError(f"pair indices must lie in [0, {M}), got [{lo}, {hi}]")
+    check_pair_indices(pi_t[:n], pj_t[:n], M, "screened_external_energy")
     R_in = atom_coords if isinstance(atom_coords, torch.Tensor) else _lib.f64(atom_coords, dev)
     R, Z = _atoms(R_in.detach(), atom_charges, dev)
     Rg = R_in if (isinstance(R_in, torch.Tensor) and R_in.requires_grad) else R

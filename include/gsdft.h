@@ -76,13 +76,26 @@ int gsdft_pair_index(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
                      int32_t* row_ptr, int32_t* row_perm, int32_t* col_ptr, int32_t* col_perm,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-/* Frozen diagonal product aux: log_alpha (n_scales*M) and centres, scale-major. scales is a
- * HOST array. Replaces init_product_aux(diagonal_only=True), gs_dft/basis/isotropic.py:81-116.
- * Workspace: gsdft_screen_workspace_size(M,0,0). */
+/* Frozen diagonal product aux: log_alpha (n_scales*M) and centres, scale-major: one isotropic aux
+ * per splat and scale at the self-product centre with exponent det(A_i + A_i)^(1/3) * scale.
+ * scales is a HOST array of any length >= 1. The workspace is not used (pass NULL, 0). Replaces
+ * init_product_aux(diagonal_only=True, or pi=None), gs_dft/basis/isotropic.py:81-116. */
 int gsdft_product_aux(int64_t M, const double* quat, const double* log_scale,
                       const double* centers, const double* scales, int n_scales,
                       double* log_alpha, double* aux_centers, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* Frozen product aux of a listed set of pairs: log_alpha (n_scales*n) and centres, scale-major,
+ * one aux per entry a at the product centre of (pi[a], pj[a]) with exponent
+ * det(A_pi + A_pj)^(1/3) * scale, and exponent scale (alpha_0 = 1) where valid[a] == 0 (valid
+ * may be NULL: every entry live). scales is a HOST array. Workspace:
+ * gsdft_screen_workspace_size(M,0,0) (the charts). Replaces init_product_aux(basis, pi, pj, valid,
+ * diagonal_only=False), gs_dft/basis/isotropic.py:106-116. */
+int gsdft_product_aux_pairs(int64_t M, const double* quat, const double* log_scale,
+                            const double* centers, int64_t n, const int32_t* pi,
+                            const int32_t* pj, const double* valid, const double* scales,
+                            int n_scales, double* log_alpha, double* aux_centers,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace for gsdft_aux_metric and gsdft_cholesky. */
 int gsdft_metric_workspace_size(int64_t N, size_t* bytes);

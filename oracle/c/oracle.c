@@ -28,6 +28,7 @@
 
 static const double PI15 = 5.568327996831708;        /* math.pi ** 1.5 */
 
+/* The worker count of the OpenMP loops (1 when built without OpenMP). */
 int orc_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();
@@ -262,6 +263,18 @@ static void decode(const int64_t* flat, int64_t k, int64_t M, int64_t pad_to, in
     for (int64_t a = k; a < pad_to; ++a) { pi[a] = 0; pj[a] = 0; w[a] = 0.0; }
 }
 
+/* Per-row significant counts of the candidate space (pairs.py:103-118, one row at a time). */
+static void row_counts(int64_t M, const Chart* c, const double* centers, double eps, int unique,
+                       int64_t* cnt) {
+#pragma omp parallel for schedule(dynamic, 8)
+    for (int64_t i = 0; i < M; ++i) {
+        int64_t k = 0;
+        for (int64_t j = unique ? i : 0; j < M; ++j)
+            if (fabs(overlap_one(c->A9, centers, c->norm, (int)i, (int)j)) > eps) ++k;
+        cnt[i] = k;
+    }
+}
+
 int orc_neighbor_pairs(int64_t M, const double* quat, const double* log_scale,
                        const double* centers, double eps, int64_t pad_to, int unique,
                        int32_t* pi, int32_t* pj, double* weight, int64_t* n_out, int64_t* n_sig) {
@@ -282,19 +295,27 @@ int orc_neighbor_pairs(int64_t M, const double* quat, const double* log_scale,
         return 0;
     }
     Chart c = chart_alloc(M, quat, log_scale);
-    /* ascending flat i*M + j with their |S| (pairs.py:50-87 emits exactly this order) */
-    int64_t cap = 1024, cnt = 0;
-    FlatVal* sig = (FlatVal*)malloc(sizeof(FlatVal) * cap);
-    for (int64_t i = 0; i < M; ++i)
+    /* ascending flat i*M + j with their |S| (pairs.py:50-87 emits exactly this order): per-row
+     * counts, their prefix sum, then every row fills its own segment in column order */
+    int64_t* off = (int64_t*)malloc(sizeof(int64_t) * (size_t)(M + 1));
+    row_counts(M, &c, centers, eps, unique, off + 1);
+    off[0] = 0;
+    for (int64_t i = 0; i < M; ++i) off[i + 1] += off[i];
+    const int64_t cnt = off[M];
+    FlatVal* sig = (FlatVal*)malloc(sizeof(FlatVal) * (size_t)(cnt > 0 ? cnt : 1));
+#pragma omp parallel for schedule(dynamic, 8)
+    for (int64_t i = 0; i < M; ++i) {
+        int64_t a = off[i];
         for (int64_t j = unique ? i : 0; j < M; ++j) {
             double s = fabs(overlap_one(c.A9, centers, c.norm, (int)i, (int)j));
             if (s > eps) {
-                if (cnt == cap) { cap *= 2; sig = (FlatVal*)realloc(sig, sizeof(FlatVal) * cap); }
-                sig[cnt].flat = i * M + j;
-                sig[cnt].val = s;
-                ++cnt;
+                sig[a].flat = i * M + j;
+                sig[a].val = s;
+                ++a;
             }
         }
+    }
+    free(off);
     chart_free(&c);
     *n_sig = cnt;
     if (pad_to < 0) pad_to = cnt;                         /* pairs.py:278-282 */
@@ -321,9 +342,80 @@ int orc_neighbor_pairs(int64_t M, const double* quat, const double* log_scale,
     return rc;
 }
 
+/* Knife-edge audit of the threshold: over every candidate (j >= i when unique), the number with
+ * ||S| - eps| <= rel_tol * eps and the smallest ||S| - eps| / eps. */
+void orc_screen_margin(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, double rel_tol,
+                       int64_t* n_close, double* min_gap) {
+    Chart c = chart_alloc(M, quat, log_scale);
+    int64_t close = 0;
+    double gap = INFINITY;
+#pragma omp parallel for schedule(dynamic, 8) reduction(+ : close) reduction(min : gap)
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = unique ? i : 0; j < M; ++j) {
+            double r = fabs(fabs(overlap_one(c.A9, centers, c.norm, (int)i, (int)j)) - eps) / eps;
+            if (r <= rel_tol) ++close;
+            if (r < gap) gap = r;
+        }
+    chart_free(&c);
+    *n_close = close;
+    *min_gap = gap;
+}
+
+/* The spatial candidate rules against the significant set, by brute force over the candidate
+ * space (j >= i when unique), with L = max(-ln eps, 1e-12) and lmin_i = exp(min_k l_ik):
+ *   reference rule (pairs.py:167-197, grid.py:76-82): |mu_i - mu_j| < safety (rc_i + rc_j),
+ *     rc_i = sqrt(L / lmin_i);
+ *   bound rule: |mu_i - mu_j|^2 < L (1/lmin_i + 1/lmin_j).
+ * Outputs: significant pairs, candidates of each rule, significant pairs each rule misses, and
+ * the largest |d|^2 / (L (1/lmin_i + 1/lmin_j)) over the significant pairs. */
+void orc_spatial_audit(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, double safety,
+                       int64_t* n_sig, int64_t* n_cand_ref, int64_t* n_miss_ref,
+                       int64_t* n_cand_bound, int64_t* n_miss_bound, double* max_ratio) {
+    Chart c = chart_alloc(M, quat, log_scale);
+    const double L = fmax(-log(eps), 1e-12);
+    double* inv = (double*)malloc(sizeof(double) * (size_t)(M > 0 ? M : 1));
+    for (int64_t m = 0; m < M; ++m) {
+        const double* l = log_scale + 3 * m;
+        inv[m] = 1.0 / exp(fmin(l[0], fmin(l[1], l[2])));
+    }
+    int64_t ns = 0, cr = 0, mr = 0, cb = 0, mb = 0;
+    double mx = 0.0;
+#pragma omp parallel for schedule(dynamic, 8) reduction(+ : ns, cr, mr, cb, mb) reduction(max : mx)
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = unique ? i : 0; j < M; ++j) {
+            const double* a = centers + 3 * i;
+            const double* b = centers + 3 * j;
+            const double d2 = (a[0] - b[0]) * (a[0] - b[0]) + (a[1] - b[1]) * (a[1] - b[1])
+                            + (a[2] - b[2]) * (a[2] - b[2]);
+            const int ref = sqrt(d2) < safety * (sqrt(L * inv[i]) + sqrt(L * inv[j]));
+            const double ratio = d2 / (L * (inv[i] + inv[j]));
+            const int bnd = ratio < 1.0;
+            const int sig = fabs(overlap_one(c.A9, centers, c.norm, (int)i, (int)j)) > eps;
+            cr += ref;
+            cb += bnd;
+            if (sig) {
+                ++ns;
+                mr += !ref;
+                mb += !bnd;
+                if (ratio > mx) mx = ratio;
+            }
+        }
+    free(inv);
+    chart_free(&c);
+    *n_sig = ns;
+    *n_cand_ref = cr;
+    *n_miss_ref = mr;
+    *n_cand_bound = cb;
+    *n_miss_bound = mb;
+    *max_ratio = mx;
+}
+
 /* ---------------------------------------------------------------- product aux */
 
-/* gs_dft/basis/isotropic.py:269-281 with diagonal_only: pi = pj = arange(M). */
+/* gs_dft/basis/isotropic.py:81-116 with diagonal_only (pi = pj = arange(M)): alpha_0 =
+ * det3(A_i + A_i)^(1/3) at the product centre of the self-pair. */
 void orc_product_aux(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, const double* scales, int n_scales,
                      double* log_alpha, double* aux_centers) {
@@ -335,6 +427,32 @@ void orc_product_aux(int64_t M, const double* quat, const double* log_scale,
         double alpha0 = pow(det3(Ah), 1.0 / 3.0);
         for (int s = 0; s < n_scales; ++s) {
             int64_t o = (int64_t)s * M + m;
+            log_alpha[o] = log(alpha0 * scales[s]);
+            aux_centers[3 * o] = Pc[0];
+            aux_centers[3 * o + 1] = Pc[1];
+            aux_centers[3 * o + 2] = Pc[2];
+        }
+    }
+    chart_free(&c);
+}
+
+/* gs_dft/basis/isotropic.py:106-116 with diagonal_only=False and a pair list: one aux per listed
+ * pair a at its product centre with alpha_0 = det3(A_i + A_j)^(1/3), alpha_0 = 1 where valid[a]
+ * is 0 (valid may be NULL: every entry live), scale-major over the n_scales scales. */
+void orc_product_aux_pairs(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t n, const int32_t* pi,
+                           const int32_t* pj, const double* valid, const double* scales,
+                           int n_scales, double* log_alpha, double* aux_centers) {
+    Chart c = chart_alloc(M, quat, log_scale);
+    for (int64_t a = 0; a < n; ++a) {
+        const int i = pi[a], j = pj[a];
+        double Ah[9], Pc[3], KN;
+        pair_q(c.A9 + 9 * i, c.A9 + 9 * j, centers + 3 * i, centers + 3 * j, c.norm[i],
+               c.norm[j], Ah, Pc, &KN, NULL);
+        double alpha0 = pow(det3(Ah), 1.0 / 3.0);
+        if (valid && valid[a] == 0.0) alpha0 = 1.0;
+        for (int s = 0; s < n_scales; ++s) {
+            int64_t o = (int64_t)s * n + a;
             log_alpha[o] = log(alpha0 * scales[s]);
             aux_centers[3 * o] = Pc[0];
             aux_centers[3 * o + 1] = Pc[1];
@@ -525,21 +643,29 @@ void orc_gamma(int64_t M, const double* quat, const double* log_scale, const dou
     AuxQ aq = aux_alloc(N, log_alpha);
     PairRec* pr = (PairRec*)malloc(sizeof(PairRec) * (n > 0 ? n : 1));
     double* qa = (double*)malloc(sizeof(double) * (n > 0 ? n : 1));
+#pragma omp parallel for schedule(static)
     for (int64_t a = 0; a < n; ++a) {
         pair_rec(c.A9, centers, c.norm, pi[a], pj[a], pr + a);
         qa[a] = weight[a] * pair_density(k, C, occ, pi[a], pj[a]);
     }
     double pref = pref3c();
+    /* Pair blocks that stay in cache while every aux row sweeps them; each gamma_P still sums its
+     * pairs in list order. */
+    const int64_t kBlk = 2048;
+    for (int64_t p = 0; p < N; ++p) gamma[p] = 0.0;
+    for (int64_t a0 = 0; a0 < n; a0 += kBlk) {
+        const int64_t a1 = a0 + kBlk < n ? a0 + kBlk : n;
 #pragma omp parallel for schedule(static)
-    for (int64_t p = 0; p < N; ++p) {
-        double g = 0.0;
-        for (int64_t a = 0; a < n; ++a) {
-            if (qa[a] == 0.0) continue;          /* zero-weight (padding) pairs add exactly 0 */
-            double blk = (aq.KN[p] * pr[a].KN) * pref
-                       * node_sum(tq, wq, aq.beta[p], aux_centers + 3 * p, pr + a);
-            g += blk * qa[a];
+        for (int64_t p = 0; p < N; ++p) {
+            double g = gamma[p];
+            for (int64_t a = a0; a < a1; ++a) {
+                if (qa[a] == 0.0) continue;      /* zero-weight (padding) pairs add exactly 0 */
+                double blk = (aq.KN[p] * pr[a].KN) * pref
+                           * node_sum(tq, wq, aq.beta[p], aux_centers + 3 * p, pr + a);
+                g += blk * qa[a];
+            }
+            gamma[p] = g;
         }
-        gamma[p] = g;
     }
     free(qa);
     free(pr);

@@ -51,11 +51,31 @@ int orc_neighbor_pairs(int64_t M, const double* quat, const double* log_scale,
                        const double* centers, double eps, int64_t pad_to, int unique,
                        int32_t* pi, int32_t* pj, double* weight, int64_t* n_out, int64_t* n_sig);
 
+/* Knife-edge audit: candidates with ||S| - eps| <= rel_tol eps, and min ||S| - eps| / eps. */
+void orc_screen_margin(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, double rel_tol,
+                       int64_t* n_close, double* min_gap);
+
+/* gs_dft/screening/pairs.py:167-197 (+ grid.py:76-82) -- the spatial candidate rules checked
+ * against the significant set by brute force (see oracle.c). */
+void orc_spatial_audit(int64_t M, const double* quat, const double* log_scale,
+                       const double* centers, double eps, int unique, double safety,
+                       int64_t* n_sig, int64_t* n_cand_ref, int64_t* n_miss_ref,
+                       int64_t* n_cand_bound, int64_t* n_miss_bound, double* max_ratio);
+
 /* gs_dft/basis/isotropic.py:81-116 -- diagonal product aux: log_alpha (S*M), centres (S*M,3),
  * scale-major. */
 void orc_product_aux(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, const double* scales, int n_scales,
                      double* log_alpha, double* aux_centers);
+
+/* gs_dft/basis/isotropic.py:106-116 -- product aux of listed pairs (diagonal_only=False):
+ * log_alpha (S*n), centres (S*n,3), scale-major; alpha_0 = 1 where valid[a] == 0 (valid may be
+ * NULL). */
+void orc_product_aux_pairs(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t n, const int32_t* pi,
+                           const int32_t* pj, const double* valid, const double* scales,
+                           int n_scales, double* log_alpha, double* aux_centers);
 
 /* gs_dft/coulomb/ri.py:63-76,267-275 (+ shift_diag :243-250 when lam != 0) -- metric V (N,N). */
 void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, double lam,
@@ -93,7 +113,6 @@ void orc_gamma_vjp(int64_t M, const double* quat, const double* log_scale, const
                    const double* dgamma, double* J, double* dquat, double* dlog_scale,
                    double* dcenters, double* dC);
 
-/* The worker count the OpenMP loops above use (1 when built without OpenMP). */
 /* V (n) of gs_dft/screening/pairs.py:348-370 for the listed pairs and nuclei (coords (n_atoms,3),
  * charges (n_atoms)), in the reference's B = A + t^2 I form. */
 void orc_nuclear_pairs(int64_t M, const double* quat, const double* log_scale,
@@ -119,6 +138,7 @@ double orc_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
                          int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
                          double* J);
 
+/* The worker count the OpenMP loops above use (1 when built without OpenMP). */
 int orc_num_threads(void);
 
 #ifdef __cplusplus

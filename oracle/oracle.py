@@ -144,6 +144,34 @@ def neighbor_pairs(quat, log_scale, centers, eps, pad_to=None, unique=False):
     return pi[:m], pj[:m], w[:m], int(n_sig.value)
 
 
+def screen_margin(quat, log_scale, centers, eps, unique, rel_tol=1e-10):
+    """(number of candidates with ||S| - eps| <= rel_tol eps, min ||S| - eps| / eps)."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    n_close = ctypes.c_int64()
+    gap = ctypes.c_double()
+    lib().orc_screen_margin(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                            ctypes.c_double(eps), ctypes.c_int(int(unique)),
+                            ctypes.c_double(rel_tol), ctypes.byref(n_close), ctypes.byref(gap))
+    return int(n_close.value), float(gap.value)
+
+
+def spatial_audit(quat, log_scale, centers, eps, unique, safety=1.25):
+    """Brute-force check of the spatial candidate rules (gs_dft/screening/pairs.py:167-197):
+    dict with the significant count, each rule's candidate count and the significant pairs it
+    misses, and the largest |d|^2 / (L (1/lmin_i + 1/lmin_j)) over the significant pairs."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    out = [ctypes.c_int64() for _ in range(5)]
+    mx = ctypes.c_double()
+    lib().orc_spatial_audit(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                            ctypes.c_double(eps), ctypes.c_int(int(unique)),
+                            ctypes.c_double(safety), *(ctypes.byref(o) for o in out),
+                            ctypes.byref(mx))
+    keys = ("n_sig", "n_cand_ref", "n_miss_ref", "n_cand_bound", "n_miss_bound")
+    r = {k: int(o.value) for k, o in zip(keys, out)}
+    r["max_ratio"] = float(mx.value)
+    return r
+
+
 def product_aux(quat, log_scale, centers, scales):
     quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
     sc = _f64(np.asarray(scales, float))
@@ -152,6 +180,23 @@ def product_aux(quat, log_scale, centers, scales):
     cen = np.empty((len(sc) * M, 3))
     lib().orc_product_aux(_i64(M), _d(quat), _d(log_scale), _d(centers), _d(sc),
                           ctypes.c_int(len(sc)), _d(la), _d(cen))
+    return la, cen
+
+
+def product_aux_pairs(quat, log_scale, centers, pi, pj, valid, scales):
+    """Product aux of the listed pairs (gs_dft/basis/isotropic.py:106-116, diagonal_only=False):
+    (log_alpha (S*n,), centres (S*n, 3)), scale-major; ``valid`` None or per-entry weights."""
+    quat, log_scale, centers = _f64(quat), _f64(log_scale), _f64(centers)
+    pi, pj = _i32(pi), _i32(pj)
+    v = None if valid is None else _f64(np.asarray(valid, dtype=np.float64))
+    sc = _f64(np.asarray(scales, float))
+    n = pi.shape[0]
+    la = np.empty(len(sc) * n)
+    cen = np.empty((len(sc) * n, 3))
+    lib().orc_product_aux_pairs(_i64(quat.shape[0]), _d(quat), _d(log_scale), _d(centers),
+                                _i64(n), pi.ctypes.data_as(_I32), pj.ctypes.data_as(_I32),
+                                None if v is None else _d(v), _d(sc), ctypes.c_int(len(sc)),
+                                _d(la), _d(cen))
     return la, cen
 
 

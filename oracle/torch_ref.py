@@ -105,7 +105,7 @@ def full_overlap_pairs(quat, log_scale, centers, pi, pj):
 
 
 def init_product_aux(quat, log_scale, centers, scales=(1.0,)):
-    """gs_dft/basis/isotropic.py:269-281 (diagonal_only=True) -> (log_alpha, centers)."""
+    """gs_dft/basis/isotropic.py:81-116 (diagonal_only=True) -> (log_alpha, centers)."""
     A, N = splat_A(quat, log_scale), splat_norm(log_scale)
     idx = torch.arange(A.shape[0])
     Aij, Pa, _ = full_pair_quantities(A, centers, N, idx, idx)

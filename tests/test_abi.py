@@ -90,3 +90,43 @@ def test_pair_index_refuses_counts_past_int32(built):
     p = ctypes.byref(dummy)
     rc = lib.gsdft_pair_index(4, big, p, p, p, p, p, p, None, 0, None)
     assert rc == built.GSDFT_ERR_ARG
+
+
+def _header_params():
+    """name -> list of parameter C types, parsed from include/gsdft.h."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:int|const char\*)\s+(gsdft_\w+)\((.*?)\);", text, re.M | re.S):
+        args = " ".join(m.group(2).split())
+        if args in ("void", ""):
+            out[m.group(1)] = []
+            continue
+        types = []
+        for a in args.split(","):
+            a = a.strip()
+            name = re.findall(r"(\w+)$", a)[0]
+            types.append(a[: -len(name)].replace(" ", ""))
+        out[m.group(1)] = types
+    return out
+
+
+def test_ctypes_signatures_match_the_header(built):
+    """Every argtypes entry of the Python binding has the width and kind of the header's
+    parameter: a 32-bit int where the header says int64_t, or a missing argument, would pass
+    garbage across the ABI."""
+    kind = {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "double": ctypes.c_double,
+            "size_t": ctypes.c_size_t}
+    params = _header_params()
+    for name, argtypes in built.SIGNATURES.items():
+        want = params[name]
+        assert len(argtypes) == len(want), (name, len(argtypes), len(want))
+        for k, (c, t) in enumerate(zip(want, argtypes)):
+            if c.endswith("*"):
+                assert t is ctypes.c_void_p or issubclass(t, ctypes._Pointer), (name, k, c, t)
+                if c.rstrip("*").replace("const", "") in ("int64_t", "size_t", "double",
+                                                          "uint64_t") and t is not ctypes.c_void_p:
+                    base = {"int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
+                            "double": ctypes.c_double, "uint64_t": ctypes.c_uint64}
+                    assert t._type_ is base[c.rstrip("*").replace("const", "")], (name, k, c, t)
+            else:
+                assert t is kind[c], (name, k, c, t)

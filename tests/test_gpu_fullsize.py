@@ -1,0 +1,188 @@
+"""Full-size parity of the HIP path against the CPU oracle at the three largest benchmark systems.
+
+The reference checks its device pair list element for element against a host build
+(gs-dft tests/unit/test_device_pairs.py:50) and its screened gradients against the unscreened
+ones (tests/unit/test_screening.py:167); these are the same checks at the benchmark sizes:
+
+* the pair list bit for bit (indices, order, weights) at the 300- and 700-atom globules, with a
+  knife-edge audit of the threshold on every benchmark system;
+* gradients per splat: a splat's rows of dE/d(quat, log_scale, centers, C) depend only on the list
+  entries that contain it, so the oracle's reverse pass over just those entries, driven by the
+  GPU's own d = (V + lam I)^-1 gamma, reproduces those rows exactly; 8 random splats per case,
+  each row within 1e-9 of its largest entry, and J on those entries within 1e-10;
+* gamma on sampled aux rows, elementwise within 1e-12;
+* E_J: against 1/2 gamma_o . (L L^T)^-1 gamma_o with the oracle's whole gamma_o where the CPU can
+  afford it (C20H42 at every screening threshold); at the globules, where the oracle's whole gamma
+  would take hours of CPU, E_J = 1/2 gamma . d is pinned through (a) the sampled gamma rows, (b)
+  the adjoint identity v . gamma = sum_a q_a J_a(v) between the forward and the reverse kernels
+  for a random v, and (c) the normwise backward error of the solve against a freshly built metric.
+
+cond(V + lam I) is estimated per system (power and inverse iteration) and printed beside the
+E_J figures.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_max
+
+pytestmark = pytest.mark.gpu
+
+REL_E = 1e-10
+REL_G = 1e-9
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _splat(g, s):
+    mk = lambda a: torch.tensor(a, device="cuda", dtype=torch.float64)
+    return g.Splat(quat=mk(s.quat), log_scale=mk(s.log_scale), centers=mk(s.centers))
+
+
+# ----------------------------------------------------------------------------- pair list
+
+@pytest.mark.parametrize("system,unique", [(4, True), (4, False), (5, True)])
+def test_pair_list_bit_exact_globules(g, wl, orc, cuda, system, unique):
+    """The 300-atom (7.2e7 / 1.4e8 candidates) and 700-atom (2.0e8 candidates) globules at
+    eps = 1e-7: the GPU list equals the oracle's element for element."""
+    s = wl.make_system(system)
+    print(f"[pairs] system {system} M={s.M} eps={s.eps} unique={unique}", flush=True)
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=s.eps, unique=unique)
+    ri, rj, rw, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, s.eps, None, unique)
+    assert len(ri) == n_sig == pi.shape[0]
+    assert np.array_equal(_np(pi), ri) and np.array_equal(_np(pj), rj)
+    if unique:
+        assert np.array_equal(_np(v), rw)
+    else:
+        assert bool(v.all())
+    print(f"[pairs] system {system}: {len(ri)} pairs bit-exact", flush=True)
+
+
+@pytest.mark.parametrize("system,eps", [(3, 1e-5), (3, 1e-7), (3, 1e-9), (4, 1e-7), (5, 1e-7)])
+def test_threshold_knife_edge_audit(g, wl, orc, cuda, system, eps):
+    """No candidate's |S| lies within 1e-12 of eps (relative), so the few-ulp differences between
+    the GPU's and glibc's exp/pow cannot move a pair across the threshold; the smallest margin
+    is printed."""
+    s = wl.make_system(system, eps=eps)
+    n_close, gap = orc.screen_margin(s.quat, s.log_scale, s.centers, eps, True, rel_tol=1e-12)
+    n10, _ = orc.screen_margin(s.quat, s.log_scale, s.centers, eps, True, rel_tol=1e-10)
+    print(f"[knife-edge] system {system} eps {eps:g}: smallest ||S| - eps| / eps = {gap:.3e}; "
+          f"{n_close} candidates within 1e-12, {n10} within 1e-10", flush=True)
+    assert n_close == 0
+
+
+# ----------------------------------------------------------------------------- E_J and gradients
+
+def _cond_estimate(V, d_solve, iters=60):
+    """(lambda_max, lambda_min) of the SPD matrix V by power iteration and inverse iteration
+    (d_solve(x) = V^-1 x)."""
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(V.shape[0], generator=gen, dtype=torch.float64).cuda()
+    x /= x.norm()
+    lmax = 0.0
+    for _ in range(iters):
+        y = torch.mv(V, x)
+        lmax = float(y.norm())
+        x = y / lmax
+    x = torch.randn(V.shape[0], generator=gen, dtype=torch.float64).cuda()
+    x /= x.norm()
+    inv = 0.0
+    for _ in range(iters):
+        y = d_solve(x)
+        inv = float(y.norm())
+        x = y / inv
+    return lmax, 1.0 / inv
+
+
+def _splat_rows_parity(orc, s, la, ac, pin, pjn, wn, d, got, J, n_splats, seed, tag):
+    """Oracle reverse pass over the entries that contain n_splats random splats, with the GPU's
+    own d as the cotangent, against those splats' gradient rows and the entries' J."""
+    rng = np.random.default_rng(seed)
+    splats = np.sort(rng.choice(s.M, n_splats, replace=False))
+    live = wn != 0
+    idx = np.nonzero(live & (np.isin(pin, splats) | np.isin(pjn, splats)))[0]
+    print(f"[{tag}] splats {splats.tolist()}: {len(idx)} list entries x {len(la)} aux", flush=True)
+    ref = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[idx], pjn[idx],
+                        wn[idx], d)
+    errJ = rel_max(J[idx], ref[0])
+    print(f"[{tag}] J on those entries rel-to-max {errJ:.2e}", flush=True)
+    assert errJ < REL_E
+    worst = 0.0
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"), got, ref[1:]):
+        for m in splats:
+            scale = np.max(np.abs(b[m]))
+            err = float(np.max(np.abs(a[m] - b[m])) / scale) if scale > 0 else float(np.max(np.abs(a[m])))
+            worst = max(worst, err)
+            assert err < REL_G, (name, int(m), err)
+    print(f"[{tag}] gradient rows of {n_splats} splats: worst rel-to-row-max {worst:.2e}",
+          flush=True)
+
+
+@pytest.mark.parametrize("system,eps", [(3, 1e-5), (3, 1e-7), (3, 1e-9), (4, 1e-7), (5, 1e-7)])
+def test_energy_gamma_and_gradient_rows_full_size(g, wl, orc, cuda, system, eps):
+    from gs_dft_amd import ri as _ri
+    from gs_dft_amd import screening as _scr
+    tag = f"system {system} eps {eps:g}"
+    s = wl.make_system(system, eps=eps)
+    basis = _splat(g, s)
+    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(eps, unique=True))
+    state = g.refresh(ks, basis)
+    pi, pj, w = state.pairs
+    N = state.aux.n_basis
+    C = torch.tensor(s.C, device="cuda")
+    print(f"[{tag}] M={s.M} N_aux={N} k={s.k} n={pi.shape[0]}", flush=True)
+    # the calls _EnergyFn makes: gamma, the solve with the energy, the reverse with dE/dgamma = d
+    x = _ri._Inputs(basis, C, s.occ, state.aux, pi, pj, w, state.pair_index)
+    gam = _ri._gamma_forward(x)
+    d, E = _ri._cho_solve(state.cholV, gam, True)
+    J, dq, dl, dc, dC = _ri._gamma_vjp(x, d, None)
+    torch.cuda.synchronize()
+    E = E.item()
+    gam_n, d_n, J_n = _np(gam), _np(d), _np(J)
+    got = [_np(t) for t in (dq, dl, dc, dC)]
+    pin, pjn, wn = _np(pi), _np(pj), _np(w)
+    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
+    # E_J is the scaled dot of the solve's own outputs
+    assert abs(E - 0.5 * float(np.dot(gam_n, d_n))) < 1e-13 * abs(E)
+    # gamma: every row at C20H42, sampled rows at the globules
+    rng = np.random.default_rng(system * 10 + int(-np.log10(eps)))
+    sel = np.arange(N) if system == 3 else np.sort(rng.choice(N, 32, replace=False))
+    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
+    err = float(np.max(np.abs(gam_n[sel] - go) / np.abs(go)))
+    print(f"[{tag}] {len(sel)} gamma rows: max elementwise rel {err:.2e}", flush=True)
+    assert err < 1e-12
+    # per-splat gradient rows and J
+    _splat_rows_parity(orc, s, la, ac, pin, pjn, wn, d_n, got, J_n, 8, system * 100 + 7, tag)
+    # E_J
+    V = _ri.aux_metric(state.aux, lam=s.lam)
+    lmax, lmin = _cond_estimate(V, lambda v: _ri._cho_solve(state.cholV, v, False)[0])
+    print(f"[{tag}] cond(V + lam I) ~ {lmax / lmin:.3e} (lambda_max {lmax:.3e}, "
+          f"lambda_min {lmin:.3e})", flush=True)
+    if system == 3:
+        d_o, E_o = _ri._cho_solve(state.cholV, torch.tensor(go, device="cuda"), True)
+        E_o = E_o.item()
+        print(f"[{tag}] E_J {E:.15e} vs 1/2 gamma_o . solve(gamma_o) {E_o:.15e} "
+              f"rel {abs(E - E_o) / abs(E_o):.2e}", flush=True)
+        assert abs(E - E_o) < REL_E * abs(E_o)
+    else:
+        # (b) adjoint identity between the forward and reverse kernels
+        v = torch.tensor(rng.normal(size=N), device="cuda")
+        Jv = _ri._gamma_vjp(x, v, None)[0]
+        q = _scr.density_pairs(C, s.occ, pi, pj) * w
+        lhs = float(torch.dot(v, gam))
+        terms = q * Jv
+        rhs = float(terms.sum())
+        scale = float(terms.abs().sum())
+        print(f"[{tag}] v.gamma {lhs:.15e} vs sum_a q_a J_a(v) {rhs:.15e}: "
+              f"diff / sum|terms| {abs(lhs - rhs) / scale:.2e}", flush=True)
+        assert abs(lhs - rhs) < 1e-12 * scale
+        # (c) normwise backward error of the solve against the metric built afresh
+        r = torch.mv(V, d) - gam
+        eta = float(r.abs().max()) / (float(V.abs().sum(1).max()) * float(d.abs().max())
+                                     + float(gam.abs().max()))
+        print(f"[{tag}] solve backward error {eta:.2e}; E_J {E:.15e}", flush=True)
+        assert eta < 1e-12
+    del V
+    torch.cuda.empty_cache()

@@ -161,3 +161,22 @@ def test_system3_energy_and_directional_derivative(g, wl, orc, cuda):
     fd = (e_at(1) - e_at(-1)) / (2 * h)
     print(f"[vne] system3 directional derivative {dd:.10e} vs central difference {fd:.10e}")
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
+
+
+def test_out_of_range_pair_indices_are_refused(g, wl, cuda):
+    """screened_overlap_pairs, density_pairs and screened_nuclear_pairs refuse an index outside
+    the splat (or C) rows on the host, before any launch."""
+    import pytest
+    s = wl.make_small(12, 3, seed=2)
+    basis = g.Splat(quat=s.quat, log_scale=s.log_scale, centers=s.centers)
+    bad_i = torch.tensor([0, 12], dtype=torch.int32, device="cuda")
+    bad_j = torch.tensor([-1, 3], dtype=torch.int32, device="cuda")
+    ok = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    C = torch.tensor(s.C, device="cuda")
+    for pi, pj in ((bad_i, ok), (ok, bad_j)):
+        with pytest.raises(ValueError, match="pair indices"):
+            g.screened_overlap_pairs(basis, pi, pj)
+        with pytest.raises(ValueError, match="pair indices"):
+            g.density_pairs(C, s.occ, pi, pj)
+        with pytest.raises(ValueError, match="pair indices"):
+            g.screened_nuclear_pairs(basis, pi, pj, s.atoms, s.charges)

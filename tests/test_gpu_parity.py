@@ -137,6 +137,45 @@ def test_product_aux_and_metric_match_oracle(g, wl, orc, cuda):
     assert np.array_equal(V, V.T)
 
 
+def test_product_aux_of_listed_pairs_matches_oracle(g, wl, orc, cuda):
+    """init_product_aux(basis, pi, pj, valid, diagonal_only=False) (gs_dft/basis/isotropic.py:
+    106-116) on a padded pair list with bool and float weights and a 20-rung scale ladder (more
+    than one launch of scales), and the reference's diagonal fallbacks: diagonal_only=True, or no
+    pi, give the self-product aux."""
+    s = _small(wl, SMALL[1])
+    basis = _splat(g, s)
+    pi, pj, w = g.neighbor_pairs(basis, eps=1e-5, pad_to=None, unique=True)
+    n = pi.shape[0]
+    pad = torch.zeros(17, dtype=torch.int32, device="cuda")
+    pi, pj = torch.cat([pi, pad]), torch.cat([pj, pad])
+    w = torch.cat([w, torch.zeros(17, dtype=torch.float64, device="cuda")])
+    scales = tuple(0.25 * 1.2 ** k for k in range(20))
+    for valid in (w, w != 0, None):
+        aux = g.init_product_aux(basis, pi, pj, valid, scales=scales, diagonal_only=False)
+        vo = None if valid is None else _np(valid).astype(float)
+        la, ac = orc.product_aux_pairs(s.quat, s.log_scale, s.centers, _np(pi), _np(pj), vo,
+                                       scales)
+        assert aux.n_basis == 20 * (n + 17)
+        assert rel_max(_np(aux.log_alpha), la) < 1e-15 and rel_max(_np(aux.centers), ac) < 1e-14
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, scales)
+    for aux in (g.init_product_aux(basis, pi, pj, w, scales=scales, diagonal_only=True),
+                g.init_product_aux(basis, scales=scales, diagonal_only=False)):
+        assert rel_max(_np(aux.log_alpha), la) < 1e-15 and rel_max(_np(aux.centers), ac) < 1e-14
+
+
+def test_refresh_with_off_diagonal_df_builds_the_self_product_aux(g, wl, orc, cuda):
+    """refresh passes no pair list to init_product_aux (gs_dft/ks/energy.py:465-466), so
+    df(diagonal=False) refreshes to the self-product aux, as df(diagonal=True) does."""
+    s = wl.make_system(1)
+    basis = _splat(g, s)
+    states = [g.refresh(g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam, diagonal=dg),
+                                   screen=g.pairlist(s.eps, unique=True)), basis)
+              for dg in (True, False)]
+    assert torch.equal(states[0].aux.log_alpha, states[1].aux.log_alpha)
+    assert torch.equal(states[0].aux.centers, states[1].aux.centers)
+    assert torch.equal(states[0].cholV, states[1].cholV)
+
+
 def test_cholesky_and_solve(g, wl, orc, cuda):
     """L L^T reproduces V + lam I to backward-stable accuracy, and the solve matches LAPACK for a
     right-hand side in the range of V (the physical case: gamma is the Coulomb projection of a
@@ -408,80 +447,17 @@ def test_system3_sampled_gamma_and_directional_derivative(g, wl, orc, cuda):
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
 
 
-@pytest.mark.parametrize("eps", [1e-5, 1e-9])
-def test_system3_eps_sweep_sampled_gamma_and_J(g, wl, orc, cuda, eps):
-    """C20H42 at the other two screening thresholds of its configuration (1e-5: ~4x fewer pairs,
-    1e-9: ~2x more): gamma on sampled aux functions and J on sampled pairs against the oracle over
-    the whole list, and E_J against the same factor's solve of the oracle's gamma on a 1e-5 list."""
-    from gs_dft_amd import ri as _ri
-    s = wl.make_system(3, eps=eps)
-    basis = _splat(g, s)
-    ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(eps, unique=True))
-    state = g.refresh(ks, basis)
-    pi, pj, w = state.pairs
-    C = torch.tensor(s.C, device="cuda")
-    print(f"[eps {eps:g}] n={pi.shape[0]}", flush=True)
-    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
-                                          index=state.pair_index))
-    pin, pjn, wn = _np(pi), _np(pj), _np(w)
-    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
-    rng = np.random.default_rng(int(-np.log10(eps)))
-    sel = np.sort(rng.choice(len(la), 24, replace=False))
-    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
-    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
-    print(f"[eps {eps:g}] sampled gamma max elementwise rel {err:.2e}", flush=True)
-    assert err < 1e-12
-    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
-    x = _ri._Inputs(basis, C, s.occ, state.aux, pi, pj, w, state.pair_index)
-    J = _np(_ri._gamma_vjp(x, dg, None)[0])
-    psel = np.sort(rng.choice(len(pin), 48, replace=False))
-    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
-                       wn[psel], _np(dg))[0]
-    errJ = rel_max(J[psel], Jo)
-    print(f"[eps {eps:g}] sampled J rel-to-max {errJ:.2e}", flush=True)
-    assert errJ < 1e-11
-    if eps == 1e-5:                     # the whole gamma from the oracle is affordable here
-        go_all = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin, pjn, wn)
-        E = g.df_coulomb_energy_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
-                                         cholV=state.cholV, index=state.pair_index).item()
-        E_o = g.df_coulomb_solve(torch.tensor(go_all, device="cuda"), state.aux,
-                                 cholV=state.cholV).item()
-        print(f"[eps {eps:g}] E_J {E:.15e} vs solve of the oracle's gamma {E_o:.15e}")
-        assert abs(E - E_o) < 1e-10 * abs(E_o)
-
-
-def test_system4_sampled_gamma_J_and_directional_derivative(g, wl, orc, cuda):
+def test_system4_directional_derivative(g, wl, orc, cuda):
     """The 300-atom CH2 globule (M = 12000, N_aux = 48000, k = 600: 64-bit offsets in the factor and
-    the solves, several slabs and Cholesky panels): gamma on sampled aux functions and J on sampled
-    pairs against the oracle over the whole list, and the gradient's directional derivative
-    through the plugin surface against central differences of the GPU energy."""
-    from gs_dft_amd import ri as _ri
+    the solves, several slabs and Cholesky panels): the gradient's directional derivative through
+    the plugin surface against central differences of the GPU energy (element-level parity at
+    this size is in test_gpu_fullsize.py)."""
     s = wl.make_system(4)
     basis = _splat(g, s)
     ks = g.SplatDFJ(coulomb=g.df(scales=s.scales, lam=s.lam), screen=g.pairlist(s.eps, unique=True))
     state = g.refresh(ks, basis)
-    pi, pj, w = state.pairs
     C = torch.tensor(s.C, device="cuda")
-    print(f"[system4] n={pi.shape[0]} N={state.aux.n_basis}", flush=True)
-    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, state.aux, pi, pj, valid=w,
-                                          index=state.pair_index))
-    pin, pjn, wn = _np(pi), _np(pj), _np(w)
-    la, ac = _np(state.aux.log_alpha), _np(state.aux.centers)
-    rng = np.random.default_rng(4)
-    sel = np.sort(rng.choice(len(la), 6, replace=False))
-    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
-    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
-    print(f"[system4] sampled gamma max elementwise rel {err:.2e}", flush=True)
-    assert err < 1e-12
-    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
-    x = _ri._Inputs(basis, C, s.occ, state.aux, pi, pj, w, state.pair_index)
-    J = _np(_ri._gamma_vjp(x, dg, None)[0])
-    psel = np.sort(rng.choice(len(pin), 32, replace=False))
-    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
-                       wn[psel], _np(dg))[0]
-    errJ = rel_max(J[psel], Jo)
-    print(f"[system4] sampled J rel-to-max {errJ:.2e}", flush=True)
-    assert errJ < 1e-11
+    print(f"[system4] n={state.pairs[0].shape[0]} N={state.aux.n_basis}", flush=True)
     b2 = _splat(g, s, grad=True)
     Cg = C.clone().requires_grad_()
     occ = torch.tensor(s.occ, device="cuda")
@@ -503,35 +479,3 @@ def test_system4_sampled_gamma_J_and_directional_derivative(g, wl, orc, cuda):
     print(f"[system4] E {E.item():.12e}: directional derivative {dd:.10e} vs central difference "
           f"{fd:.10e}")
     assert abs(fd - dd) < 1e-6 * max(1.0, abs(dd))
-
-
-def test_globule700_sampled_gamma_and_J(g, wl, orc, cuda):
-    """The headline shape (globule700: M = 20000, N_aux = 80000, ~1.1e7 unique pairs, every slab
-    and screen path of the full-size launch): gamma on sampled aux functions and J = sum_P
-    dgamma_P (P|a) on sampled pairs, for a random dgamma, against the oracle over all pairs and
-    all aux functions respectively."""
-    from gs_dft_amd import ri as _ri
-    s = wl.make_system(5)
-    basis = _splat(g, s)
-    pi, pj, w = g.neighbor_pairs(basis, s.eps, unique=True)
-    aux = g.init_product_aux(basis, scales=s.scales)
-    C = torch.tensor(s.C, device="cuda")
-    print(f"[globule700] n={pi.shape[0]} N={aux.n_basis}", flush=True)
-    gam = _np(g.df_coulomb_gamma_screened(basis, C, s.occ, aux, pi, pj, valid=w))
-    pin, pjn, wn = _np(pi), _np(pj), _np(w)
-    la, ac = _np(aux.log_alpha), _np(aux.centers)
-    rng = np.random.default_rng(5)
-    sel = np.sort(rng.choice(len(la), 6, replace=False))
-    go = orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la[sel], ac[sel], pin, pjn, wn)
-    err = float(np.max(np.abs(gam[sel] - go) / np.abs(go)))
-    print(f"[globule700] sampled gamma max elementwise rel {err:.2e}", flush=True)
-    assert err < 1e-12
-    dg = torch.tensor(rng.normal(size=len(la)), device="cuda")
-    x = _ri._Inputs(basis, C, s.occ, aux, pi, pj, w, None)
-    J = _np(_ri._gamma_vjp(x, dg, None)[0])
-    psel = np.sort(rng.choice(len(pin), 64, replace=False))
-    Jo = orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pin[psel], pjn[psel],
-                       wn[psel], _np(dg))[0]
-    errJ = rel_max(J[psel], Jo)
-    print(f"[globule700] sampled J rel-to-max {errJ:.2e}", flush=True)
-    assert errJ < 1e-11

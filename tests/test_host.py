@@ -88,3 +88,19 @@ def test_workloads_are_deterministic_and_sized(wl):
     assert (s3.M, s3.k, s3.n_aux) == (2000, 81, 8000) and s3.atoms.shape == (62, 3)
     import numpy as np
     assert abs(np.linalg.norm(s3.C, axis=0).mean() - np.sqrt(2000 / 81)) < 0.5
+
+
+def test_pair_index_range_check(g):
+    """The host check every pair-list entry point runs before a launch: indices outside
+    [0, bound) raise ValueError, since the kernels read the rows they name unchecked."""
+    import torch
+    from gs_dft_amd.screening import check_pair_indices
+    ok = torch.tensor([0, 3, 4], dtype=torch.int32)
+    check_pair_indices(ok, ok.flip(0), 5, "t")
+    check_pair_indices(ok[:0], ok[:0], 5, "t")
+    with pytest.raises(ValueError, match=r"\[0, 5\)"):
+        check_pair_indices(ok, torch.tensor([0, 5, 1], dtype=torch.int32), 5, "t")
+    with pytest.raises(ValueError, match=r"got \[-1, 4\]"):
+        check_pair_indices(torch.tensor([-1, 0, 4], dtype=torch.int32), ok, 5, "t")
+    with pytest.raises(ValueError, match="same length"):
+        check_pair_indices(ok, ok[:2], 5, "t")

@@ -146,6 +146,21 @@ def test_pairs_are_the_thresholded_set_lexsorted(orc, tr, wl, unique, eps):
     assert orc.count_significant(s.quat, s.log_scale, s.centers, eps, unique) == len(want)
 
 
+@pytest.mark.parametrize("seed,spread", [(8, 4.0), (9, 10.0), (10, 2.0)])
+def test_spatial_candidate_rules_cover_the_significant_set(orc, wl, seed, spread):
+    """gs_dft/screening/pairs.py:167-197: the spatial candidates must be a superset of the
+    significant pairs. Brute force over every candidate: neither the reference's radius rule
+    (|d| < 1.25 (rc_i + rc_j), rc = sqrt(-ln eps / lambda_min), grid.py:76-82) nor the tighter
+    bound |d|^2 < -ln eps (1/lambda_min,i + 1/lambda_min,j) that the GPU spatial path uses misses a
+    significant pair; the largest |d|^2 / bound over the significant pairs is below 1."""
+    s = wl.make_small(120, 3, n_atoms=6, spread=spread, seed=seed)
+    for eps in (1e-3, 1e-7, 1e-11):
+        r = orc.spatial_audit(s.quat, s.log_scale, s.centers, eps, False)
+        assert r["n_sig"] == orc.count_significant(s.quat, s.log_scale, s.centers, eps, False)
+        assert r["n_miss_ref"] == 0 and r["n_miss_bound"] == 0 and r["max_ratio"] < 1.0
+        assert r["n_sig"] <= r["n_cand_bound"] <= r["n_cand_ref"]
+
+
 def test_unique_covers_ordered_with_weights(orc, wl):
     """gs-dft tests/unit/test_pair_tricks.py:44."""
     s = wl.make_small(48, 3, n_atoms=6, spread=3.0, seed=9)
@@ -214,6 +229,39 @@ def test_product_aux_closed_form_and_literal(orc, tr, wl):
         assert np.max(np.abs(la[k * M:(k + 1) * M] - (base + np.log(sc)))) < 1e-10
         assert np.max(np.abs(ac[k * M:(k + 1) * M] - s.centers)) < 1e-12
     assert len(la) == 3 * M                       # N_aux = mult * M (test_aux_mult.py:29)
+
+
+def test_product_aux_of_listed_pairs(orc, wl):
+    """Off-diagonal product aux (gs_dft/basis/isotropic.py:106-116): on the self-pairs it is the
+    diagonal aux; for isotropic splats A = a I the product exponent det(A_i + A_j)^(1/3) is
+    a_i + a_j at the centre (a_i mu_i + a_j mu_j) / (a_i + a_j); for anisotropic splats the
+    exponent is numpy's det of the summed chart precisions; entries with valid 0 take
+    alpha_0 = 1 (exponent = the scale) at their pair's product centre."""
+    s = wl.make_small(30, 3, seed=12)
+    M = s.M
+    scales = (0.5, 1.0, 2.0)
+    idx = np.arange(M)
+    la, ac = orc.product_aux_pairs(s.quat, s.log_scale, s.centers, idx, idx, None, scales)
+    ld, acd = orc.product_aux(s.quat, s.log_scale, s.centers, scales)
+    assert np.array_equal(la, ld) and np.array_equal(ac, acd)
+    rng = np.random.default_rng(3)
+    a = np.exp(rng.uniform(-1, 1, M))
+    quat = np.tile([1.0, 0, 0, 0], (M, 1))
+    ls = np.repeat(np.log(a)[:, None], 3, 1)
+    pi = rng.integers(0, M, 50).astype(np.int32)
+    pj = rng.integers(0, M, 50).astype(np.int32)
+    valid = (rng.uniform(size=50) > 0.2).astype(float) * 2.0
+    la, ac = orc.product_aux_pairs(quat, ls, s.centers, pi, pj, valid, scales)
+    n = len(pi)
+    want_c = (a[pi, None] * s.centers[pi] + a[pj, None] * s.centers[pj]) / (a[pi] + a[pj])[:, None]
+    for k, sc in enumerate(scales):
+        blk = slice(k * n, (k + 1) * n)
+        want = np.where(valid != 0, np.log((a[pi] + a[pj]) * sc), np.log(sc))
+        assert np.max(np.abs(la[blk] - want)) < 1e-14
+        assert np.max(np.abs(ac[blk] - want_c)) < 1e-13
+    A, _ = orc.chart(s.quat, s.log_scale)
+    la, _ = orc.product_aux_pairs(s.quat, s.log_scale, s.centers, pi, pj, None, (1.0,))
+    assert np.max(np.abs(la - np.log(np.linalg.det(A[pi] + A[pj])) / 3.0)) < 1e-13
 
 
 def _gauss_coulomb(a, A, b, B):
