@@ -20,6 +20,7 @@ GSDFT_ERR_NOT_PD = 3
 GSDFT_ERR_HIP = 4
 GSDFT_ERR_LIB = 5
 GSDFT_ERR_WORKSPACE = 6
+GSDFT_ERR_FALLBACK = 7
 
 (PROF_GAMMA_FWD, PROF_GAMMA_BWD, PROF_SCREEN, PROF_METRIC, PROF_CHOLESKY, PROF_SOLVE,
  PROF_NUC_PAIRS, PROF_NUC_ATOMS, PROF_ERI_FWD, PROF_ERI_BWD, PROF_EXCH_BLOCK, PROF_EXCH_BWD,
@@ -40,6 +41,9 @@ SIGNATURES = {
     "gsdft_screen_count": [_i64, _vp, _vp, _vp, _dbl, _int, _vp, _sz, _pi64, _vp],
     "gsdft_screen_build": [_i64, _vp, _vp, _vp, _dbl, _int, _i64, _vp, _vp, _vp, _vp, _sz,
                            _pi64, _vp],
+    "gsdft_screen_spatial_workspace_size": [_i64, _psz],
+    "gsdft_screen_spatial": [_i64, _vp, _vp, _vp, _dbl, _int, _i64, _vp, _vp, _vp, _vp, _sz,
+                             _pi64, _vp],
     "gsdft_pair_index_workspace_size": [_i64, _i64, _psz],
     "gsdft_pair_index": [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_product_aux": [_i64, _vp, _vp, _vp, _pd, _int, _vp, _vp, _vp, _sz, _vp],

@@ -276,6 +276,339 @@ int screen_scan(int64_t M, const double* quat, const double* log_scale, const do
     return GSDFT_OK;
 }
 
+// ------------------------------------------------------------------ spatial candidates
+// gs_dft/screening/pairs.py:167-222 builds a superset of the significant pairs from the splat
+// centres (a KD-tree ball query with r_cut from grid.py:76-82) and compacts the significant ones in
+// ascending flat order. Here the superset comes from a bound that holds for every splat pair:
+// S_ij = p_ij exp(-e_ij) with p_ij <= 1 (det(A_i + A_j) >= 8 sqrt(det A_i det A_j)) and
+// e_ij = d^T (A_i^-1 + A_j^-1)^-1 d >= |d|^2 / (1/lmin_i + 1/lmin_j), so |S_ij| > eps needs
+// |d|^2 < L (1/lmin_i + 1/lmin_j), L = -ln eps. With b_i = kSpatialMargin L / lmin_i the candidate
+// test is |d|^2 < b_i + b_j (the margin covers rounding). lmin_i is a lower bound of the smallest
+// eigenvalue of the chart's A_i: the chart rotates by q/(|q| + 1e-12), whose rotation matrix is
+// nu^2 R(u) + (1 - nu^2) I (nu the norm of the divided quaternion), so by Weyl's inequality the
+// eigenvalues sit within 4 eps (1 + eps) a_max of the a_k = e^(l_k), eps = |1 - nu^2|; a splat
+// whose bound is not positive is a candidate for every pair.
+//
+// Splats are sorted by the Morton code of their centre and cut into blocks of 64 with bounding
+// boxes. One workgroup per row i: waves test whole blocks against the box (one lane per block),
+// expand the live ones (one lane per member), append the candidates to an LDS list and evaluate
+// S_ij on the list with every lane busy, setting bit j of the row's LDS bitmap when |S_ij| > eps.
+// S_ij is the same function on the same operands (i the row) as in the dense scan, so the bitmap
+// is exactly the dense scan's row; its popcount gives the row count, the exclusive scan the row
+// offsets, and the emit pass writes each row's set bits in ascending j, i.e. in flat order.
+
+constexpr double kSpatialMargin = 1.0625;
+constexpr int kSpBlock = 64;              // splats per Morton block
+constexpr int kSpList = 4096;             // LDS candidate list per round
+constexpr int kSpExpand = kSpList / 256;  // live blocks each wave expands per round
+constexpr int64_t kSpMaxM = 262144;       // bitmap row (M / 8 bytes) must fit in LDS
+
+inline int64_t sp_words(int64_t M) { return (M + 31) / 32; }
+
+__global__ void k_sp_prep(int64_t M, const double* __restrict__ quat,
+                          const double* __restrict__ log_scale, double L,
+                          double* __restrict__ b) {
+    const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (m >= M) return;
+    const double* q = quat + 4 * m;
+    const double nrm = sqrt(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+    const double nu = nrm / (nrm + 1e-12);
+    const double e = fabs(1.0 - nu * nu);
+    const double* l = log_scale + 3 * m;
+    const double amin = exp(fmin(l[0], fmin(l[1], l[2])));
+    const double amax = exp(fmax(l[0], fmax(l[1], l[2])));
+    const double lmin = amin - (4.0 * e * (1.0 + e) + 1e-14) * amax;
+    b[m] = lmin > 0.0 ? kSpatialMargin * L / lmin : INFINITY;
+}
+
+// Bounding box of the centres (one workgroup, strided): lo (3), hi (3).
+__global__ __launch_bounds__(1024) void k_sp_bbox(int64_t M, const double* __restrict__ mu,
+                                                  double* __restrict__ box) {
+    __shared__ double red[6][1024 / 64];
+    double v[6] = {INFINITY, INFINITY, INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    for (int64_t m = threadIdx.x; m < M; m += blockDim.x)
+        for (int c = 0; c < 3; ++c) {
+            v[c] = fmin(v[c], mu[3 * m + c]);
+            v[3 + c] = fmax(v[3 + c], mu[3 * m + c]);
+        }
+    for (int off = 32; off > 0; off >>= 1)
+        for (int c = 0; c < 3; ++c) {
+            v[c] = fmin(v[c], __shfl_xor(v[c], off, 64));
+            v[3 + c] = fmax(v[3 + c], __shfl_xor(v[3 + c], off, 64));
+        }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0)
+        for (int c = 0; c < 6; ++c) red[c][wave] = v[c];
+    __syncthreads();
+    if (threadIdx.x < 6) {
+        const int c = threadIdx.x;
+        double r = red[c][0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+            r = c < 3 ? fmin(r, red[c][w]) : fmax(r, red[c][w]);
+        box[c] = r;
+    }
+}
+
+__device__ __forceinline__ uint32_t spread3(uint32_t x) {      // 10 bits -> every third bit
+    x &= 0x3ff;
+    x = (x | (x << 16)) & 0x030000ff;
+    x = (x | (x << 8)) & 0x0300f00f;
+    x = (x | (x << 4)) & 0x030c30c3;
+    x = (x | (x << 2)) & 0x09249249;
+    return x;
+}
+
+__global__ void k_sp_morton(int64_t M, const double* __restrict__ mu,
+                            const double* __restrict__ box, uint32_t* __restrict__ key,
+                            int32_t* __restrict__ idx) {
+    const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (m >= M) return;
+    uint32_t k = 0;
+    for (int c = 0; c < 3; ++c) {
+        const double ext = box[3 + c] - box[c];
+        const double t = ext > 0.0 ? (mu[3 * m + c] - box[c]) / ext : 0.0;
+        const uint32_t g = (uint32_t)fmin(fmax(t * 1024.0, 0.0), 1023.0);
+        k |= spread3(g) << c;
+    }
+    key[m] = k;
+    idx[m] = (int32_t)m;
+}
+
+// Per Morton block: members' (x, y, z, b) in sorted order, the box (lo, hi) and the largest b.
+__global__ __launch_bounds__(256) void k_sp_blocks(int64_t M, const int32_t* __restrict__ perm,
+                                                   const double* __restrict__ mu,
+                                                   const double* __restrict__ b,
+                                                   double4* __restrict__ member,
+                                                   double* __restrict__ blk) {
+    const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t B = m / kSpBlock;
+    const bool live = m < M;
+    double x = 0.0, y = 0.0, z = 0.0, bb = -INFINITY;
+    if (live) {
+        const int64_t j = perm[m];
+        x = mu[3 * j]; y = mu[3 * j + 1]; z = mu[3 * j + 2]; bb = b[j];
+        member[m] = make_double4(x, y, z, bb);
+    }
+    double v[7] = {live ? x : INFINITY, live ? y : INFINITY, live ? z : INFINITY,
+                   live ? x : -INFINITY, live ? y : -INFINITY, live ? z : -INFINITY, bb};
+    for (int off = 32; off > 0; off >>= 1)
+        for (int c = 0; c < 7; ++c) {
+            const double o = __shfl_xor(v[c], off, 64);
+            v[c] = c < 3 ? fmin(v[c], o) : fmax(v[c], o);
+        }
+    if ((threadIdx.x & 63) == 0 && B * kSpBlock < M)
+        for (int c = 0; c < 7; ++c) blk[8 * B + c] = v[c];
+}
+
+struct SpGeom {
+    int64_t M;
+    int64_t n_blocks;
+    int64_t words;      // bitmap words per row
+    int unique;
+    double eps;
+};
+
+// One workgroup (256 lanes) per row i; dynamic LDS = the row's bitmap (words x 4 bytes).
+__global__ __launch_bounds__(256) void k_sp_rows(SpGeom g, const double* __restrict__ A6,
+                                                 const double* __restrict__ mu,
+                                                 const double* __restrict__ Nrm,
+                                                 const double* __restrict__ b,
+                                                 const int32_t* __restrict__ perm,
+                                                 const double4* __restrict__ member,
+                                                 const double* __restrict__ blk,
+                                                 uint32_t* __restrict__ bitmap,
+                                                 int32_t* __restrict__ counts) {
+    extern __shared__ uint32_t bits[];
+    __shared__ int32_t list[kSpList];
+    __shared__ int list_n;
+    __shared__ int wave_cnt[4];
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int64_t w = threadIdx.x; w < g.words; w += 256) bits[w] = 0u;
+    const double mx = mu[3 * i], my = mu[3 * i + 1], mz = mu[3 * i + 2];
+    const double bi = b[i];
+    const Sym3 Ai = load_sym(A6 + 6 * i);
+    const double mui[3] = {mx, my, mz};
+    const double Ni = Nrm[i];
+    int64_t next = (int64_t)wave * 64;   // next chunk of 64 blocks this wave tests
+    int64_t base = 0;                     // block index of bit 0 of `pending`
+    uint64_t pending = 0;                 // live blocks of the current chunk not yet expanded
+    bool done = false;
+    bool all_done = false;
+    while (!all_done) {
+        if (threadIdx.x == 0) list_n = 0;
+        __syncthreads();
+        for (int budget = kSpExpand; budget > 0 && !done;) {
+            if (pending == 0) {
+                if (next >= g.n_blocks) { done = true; break; }
+                const int64_t B = next + lane;
+                bool live = false;
+                if (B < g.n_blocks) {
+                    const double* bx = blk + 8 * B;
+                    const double dx = fmax(fmax(bx[0] - mx, mx - bx[3]), 0.0);
+                    const double dy = fmax(fmax(bx[1] - my, my - bx[4]), 0.0);
+                    const double dz = fmax(fmax(bx[2] - mz, mz - bx[5]), 0.0);
+                    live = dx * dx + dy * dy + dz * dz < (bi + bx[6]) * (1.0 + 1e-10);
+                }
+                pending = __ballot(live);
+                base = next;
+                next += 4 * 64;
+                continue;
+            }
+            const int bit = __builtin_ctzll(pending);
+            pending &= pending - 1;
+            --budget;
+            const int64_t m = (base + bit) * kSpBlock + lane;
+            bool cand = false;
+            int32_t j = 0;
+            if (m < g.M) {
+                j = perm[m];
+                const double4 o = member[m];
+                const double dx = o.x - mx, dy = o.y - my, dz = o.z - mz;
+                cand = (!g.unique || j >= i) && dx * dx + dy * dy + dz * dz < bi + o.w;
+            }
+            const uint64_t cm = __ballot(cand);
+            const int k = __popcll(cm);
+            if (k == 0) continue;
+            int at = 0;
+            if (lane == 0) at = atomicAdd(&list_n, k);
+            at = __shfl(at, 0, 64);
+            const uint64_t lower = lane == 0 ? 0ull : (cm & (~0ull >> (64 - lane)));
+            if (cand) list[at + __popcll(lower)] = j;
+        }
+        __syncthreads();
+        const int n = list_n;
+        for (int e = threadIdx.x; e < n; e += 256) {
+            const int32_t j = list[e];
+            Sym3 Aj;
+            double muj[3], Nj;
+            load_splat(A6, mu, Nrm, j, &Aj, muj, &Nj);
+            if (fabs(overlap(Ai, Aj, mui, muj, Ni, Nj)) > g.eps)
+                atomicOr(&bits[j >> 5], 1u << (j & 31));
+        }
+        all_done = __syncthreads_and(done ? 1 : 0) != 0;
+    }
+    int c = 0;
+    uint32_t* row = bitmap + i * g.words;
+    for (int64_t w = threadIdx.x; w < g.words; w += 256) {
+        const uint32_t v = bits[w];
+        row[w] = v;
+        c += __popc(v);
+    }
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if (lane == 0) wave_cnt[wave] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) counts[i] = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+}
+
+// One wave per row: the row's set bits, in ascending j, at the row's offset.
+__global__ __launch_bounds__(256) void k_sp_emit(SpGeom g, const uint32_t* __restrict__ bitmap,
+                                                 const int64_t* __restrict__ offsets,
+                                                 int32_t* __restrict__ pi,
+                                                 int32_t* __restrict__ pj,
+                                                 double* __restrict__ weight) {
+    const int64_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= g.M) return;
+    const int lane = threadIdx.x & 63;
+    const uint32_t* row = bitmap + i * g.words;
+    int64_t pos = offsets[i];
+    for (int64_t w0 = 0; w0 < g.words; w0 += 64) {
+        const int64_t w = w0 + lane;
+        uint32_t v = w < g.words ? row[w] : 0u;
+        const int c = __popc(v);
+        int incl = c;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        int64_t p = pos + incl - c;
+        while (v) {
+            const int bit = __builtin_ctz(v);
+            v &= v - 1;
+            const int32_t j = (int32_t)(w * 32 + bit);
+            pi[p] = (int32_t)i;
+            pj[p] = j;
+            weight[p] = g.unique ? (i == j ? 1.0 : 2.0) : 1.0;
+            ++p;
+        }
+        pos += __shfl(incl, 63, 64);
+    }
+}
+
+struct SpatialWs {
+    double* A6;
+    double* N;
+    double* b;
+    double* box;
+    uint32_t* key_in;
+    uint32_t* key_out;
+    int32_t* idx_in;
+    int32_t* perm;
+    double4* member;
+    double* blk;
+    uint32_t* bitmap;
+    int32_t* counts;
+    int64_t* offsets;
+    void* tmp;
+    size_t tmp_bytes;
+};
+
+int layout_spatial(Arena& ar, int64_t M, SpatialWs* w) {
+    const int64_t Mx = M > 0 ? M : 1;
+    const int64_t nb = (Mx + kSpBlock - 1) / kSpBlock;
+    w->A6 = ar.take<double>(6 * Mx);
+    w->N = ar.take<double>(Mx);
+    w->b = ar.take<double>(Mx);
+    w->box = ar.take<double>(8);
+    w->key_in = ar.take<uint32_t>(Mx);
+    w->key_out = ar.take<uint32_t>(Mx);
+    w->idx_in = ar.take<int32_t>(Mx);
+    w->perm = ar.take<int32_t>(Mx);
+    w->member = ar.take<double4>(Mx);
+    w->blk = ar.take<double>(8 * nb);
+    w->bitmap = ar.take<uint32_t>(Mx * sp_words(Mx));
+    w->counts = ar.take<int32_t>(Mx);
+    w->offsets = ar.take<int64_t>(Mx);
+    size_t b1 = 0, b2 = 0;
+    if (hipcub::DeviceRadixSort::SortPairs(nullptr, b1, (const uint32_t*)nullptr,
+                                           (uint32_t*)nullptr, (const int32_t*)nullptr,
+                                           (int32_t*)nullptr, (int)Mx) != hipSuccess ||
+        hipcub::DeviceScan::ExclusiveSum(nullptr, b2, (const int32_t*)nullptr,
+                                         (int64_t*)nullptr, (int)Mx) != hipSuccess)
+        return fail(GSDFT_ERR_LIB, "hipcub size query failed");
+    w->tmp_bytes = b1 > b2 ? b1 : b2;
+    w->tmp = ar.take<char>(w->tmp_bytes);
+    return GSDFT_OK;
+}
+
+// Rows, bitmaps and row offsets; *n_sig = the significant count (synchronises).
+int spatial_scan(int64_t M, const double* quat, const double* log_scale, const double* centers,
+                 double eps, int unique, const SpatialWs& w, hipStream_t s, int64_t* n_sig) {
+    GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.N, s));
+    const double L = fmax(-log(eps), 1e-12);
+    k_sp_prep<<<blocks_for(M, 256), 256, 0, s>>>(M, quat, log_scale, L, w.b);
+    k_sp_bbox<<<1, 1024, 0, s>>>(M, centers, w.box);
+    k_sp_morton<<<blocks_for(M, 256), 256, 0, s>>>(M, centers, w.box, w.key_in, w.idx_in);
+    GSDFT_HIP(hipGetLastError());
+    size_t tb = w.tmp_bytes;
+    GSDFT_HIP(hipcub::DeviceRadixSort::SortPairs(w.tmp, tb, w.key_in, w.key_out, w.idx_in,
+                                                 w.perm, (int)M, 0, 30, s));
+    k_sp_blocks<<<blocks_for(M, 256), 256, 0, s>>>(M, w.perm, centers, w.b, w.member, w.blk);
+    GSDFT_HIP(hipGetLastError());
+    const SpGeom g{M, (M + kSpBlock - 1) / kSpBlock, sp_words(M), unique ? 1 : 0, eps};
+    k_sp_rows<<<(unsigned)M, 256, (size_t)g.words * 4, s>>>(g, w.A6, centers, w.N, w.b, w.perm,
+                                                            w.member, w.blk, w.bitmap, w.counts);
+    GSDFT_HIP(hipGetLastError());
+    tb = w.tmp_bytes;
+    GSDFT_HIP(hipcub::DeviceScan::ExclusiveSum(w.tmp, tb, w.counts, w.offsets, (int)M, s));
+    int64_t last_off = 0;
+    int32_t last_cnt = 0;
+    GSDFT_TRY(read_back(&last_off, w.offsets + (M - 1), sizeof(int64_t), s, "spatial: offsets"));
+    GSDFT_TRY(read_back(&last_cnt, w.counts + (M - 1), sizeof(int32_t), s, "spatial: counts"));
+    *n_sig = last_off + last_cnt;
+    return GSDFT_OK;
+}
+
 }  // namespace
 
 int launch_chart(int64_t M, const double* quat, const double* log_scale, double* A6, double* N,
@@ -453,6 +786,45 @@ extern "C" int gsdft_pair_index(int64_t M, int64_t n, const int32_t* pi, const i
                                                      bits, s));
     }
     k_lower_bound<<<blocks_for(M + 1, 256), 256, 0, s>>>(M, n, keys, col_ptr);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_screen_spatial_workspace_size(int64_t M, size_t* bytes) {
+    if (M < 0 || !bytes) return fail(GSDFT_ERR_ARG, "screen_spatial_workspace_size: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    SpatialWs w;
+    GSDFT_TRY(layout_spatial(ar, M, &w));
+    *bytes = ar.need();
+    return GSDFT_OK;
+}
+
+extern "C" int gsdft_screen_spatial(int64_t M, const double* quat, const double* log_scale,
+                                    const double* centers, double eps, int unique, int64_t pad_to,
+                                    int32_t* pi, int32_t* pj, double* weight, void* workspace,
+                                    size_t workspace_bytes, int64_t* n_sig, void* stream) {
+    if (M <= 0 || M > kSpMaxM || !(eps >= 0.0) || !n_sig || !quat || !log_scale || !centers ||
+        (pad_to > 0 && (!pi || !pj || !weight)))
+        return fail(GSDFT_ERR_ARG, "gsdft_screen_spatial: bad arguments (needs 0 < M <= %lld and "
+                    "eps >= 0)", (long long)kSpMaxM);
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    SpatialWs w;
+    GSDFT_TRY(layout_spatial(ar, M, &w));
+    if (!w.tmp) return fail(GSDFT_ERR_WORKSPACE, "gsdft_screen_spatial: workspace too small");
+    ProfileScope prof(kProfScreen, s);
+    GSDFT_TRY(spatial_scan(M, quat, log_scale, centers, eps, unique, w, s, n_sig));
+    if (pad_to < 0) return GSDFT_OK;
+    const int64_t ns = *n_sig;
+    if (ns > pad_to)
+        return fail(GSDFT_ERR_FALLBACK, "gsdft_screen_spatial: %lld significant pairs exceed the "
+                    "pad (%lld); the keep-largest list comes from gsdft_screen_build",
+                    (long long)ns, (long long)pad_to);
+    const SpGeom g{M, (M + kSpBlock - 1) / kSpBlock, sp_words(M), unique ? 1 : 0, eps};
+    if (ns > 0)
+        k_sp_emit<<<(unsigned)((M + 3) / 4), 256, 0, s>>>(g, w.bitmap, w.offsets, pi, pj, weight);
+    if (pad_to > ns)
+        k_fill_tail<<<blocks_for(pad_to - ns, 256), 256, 0, s>>>(ns, pad_to, pi, pj, weight);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }

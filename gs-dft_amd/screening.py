@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
+import os
 
 import torch
 
@@ -46,9 +47,45 @@ def pair_weight(valid: torch.Tensor, dtype=torch.float64) -> torch.Tensor:
     return valid.to(dtype)
 
 
-def count_significant(splats, eps: float, unique: bool = False) -> int:
-    """Number of pairs with |S_ij| > eps (gs_dft/screening/pairs.py:103-118); one host sync."""
+SPATIAL_MAX_M = 262144
+SPATIAL_AUTO_M = 4096
+
+
+def use_spatial(M: int, eps: float) -> bool:
+    """Whether screening takes the spatial candidate path (gs_dft/screening/pairs.py:167-222,
+    284-298). Its list is bit-identical to the dense scan's, so the choice only moves time:
+    ``DFTAX_PAIR_SPATIAL=1`` forces it and ``=0`` forbids it, as the reference's switch does;
+    unset, it is taken from M = 4096 splats up, where it is the faster build. eps < 0 (every pair)
+    and M above 262144 always scan densely."""
+    if eps < 0.0 or M > SPATIAL_MAX_M:
+        return False
+    flag = os.environ.get("DFTAX_PAIR_SPATIAL")
+    if flag is not None and flag.strip() in ("0", "1"):
+        return flag.strip() == "1"
+    return M >= SPATIAL_AUTO_M
+
+
+def _spatial_call(splats, eps: float, unique: bool, pad_to: int, outs=(None, None, None)):
+    """gsdft_screen_spatial: (status, n_sig); pad_to < 0 only counts."""
     M = splats.n_basis
+    q, l, c = _splat_args(splats)
+    L = _lib.lib()
+    ws = _lib.workspace(_lib.size_query(L.gsdft_screen_spatial_workspace_size, M), q.device)
+    n = ctypes.c_int64(0)
+    rc = L.gsdft_screen_spatial(M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), float(eps), int(unique),
+                                int(pad_to), *(_lib.ptr(t) for t in outs), _lib.ptr(ws),
+                                ws.numel(), ctypes.byref(n), _lib.stream())
+    return rc, int(n.value)
+
+
+def count_significant(splats, eps: float, unique: bool = False, spatial: bool | None = None) -> int:
+    """Number of pairs with |S_ij| > eps (gs_dft/screening/pairs.py:103-118); one host sync.
+    ``spatial`` None follows ``use_spatial``."""
+    M = splats.n_basis
+    if (use_spatial(M, eps) if spatial is None else (spatial and eps >= 0.0)):
+        rc, n = _spatial_call(splats, eps, unique, -1)
+        _lib.check(rc, "gsdft_screen_spatial")
+        return n
     q, l, c = _splat_args(splats)
     L = _lib.lib()
     ws = _lib.workspace(_lib.size_query(L.gsdft_screen_workspace_size, M, int(unique), 0), q.device)
@@ -60,11 +97,13 @@ def count_significant(splats, eps: float, unique: bool = False) -> int:
 
 
 def neighbor_pairs(splats, eps: float = 1e-5, pad_to: int | None = None, row_chunk: int = 256,
-                   unique: bool = False):
+                   unique: bool = False, spatial: bool | None = None):
     """``(pi, pj, valid)`` of the significant pairs (gs_dft/screening/pairs.py:225-315).
 
     ``row_chunk`` only set the reference's strip residency; the GPU build tiles the candidate
-    space itself, so the argument is accepted and has no effect on the result."""
+    space itself, so the argument is accepted and has no effect on the result. ``spatial`` (None:
+    ``use_spatial``) builds from the spatial candidate superset; a list that overflows its pad
+    falls back to the dense build and its keep-largest rule, as the reference's does."""
     del row_chunk
     if not _has_splat_interface(splats):
         raise NotImplementedError(
@@ -74,8 +113,9 @@ def neighbor_pairs(splats, eps: float = 1e-5, pad_to: int | None = None, row_chu
     q, l, c = _splat_args(splats)
     dev = q.device
     n_all = M * (M + 1) // 2 if unique else M * M
+    sp = use_spatial(M, eps) if spatial is None else (bool(spatial) and eps >= 0.0)
     if pad_to is None:
-        pad_to = n_all if eps < 0.0 else count_significant(splats, eps, unique)
+        pad_to = n_all if eps < 0.0 else count_significant(splats, eps, unique, spatial=sp)
         if pad_to == 0:
             z = torch.zeros(0, dtype=torch.int32, device=dev)
             return z, z, _pair_weights(z, z, unique)
@@ -83,6 +123,14 @@ def neighbor_pairs(splats, eps: float = 1e-5, pad_to: int | None = None, row_chu
     pi = torch.empty(pad_to, dtype=torch.int32, device=dev)
     pj = torch.empty(pad_to, dtype=torch.int32, device=dev)
     w = torch.empty(pad_to, dtype=torch.float64, device=dev)
+    if sp:
+        rc, n_sp = _spatial_call(splats, eps, unique, pad_to, (pi, pj, w))
+        if rc == _lib.GSDFT_OK:
+            return pi, pj, (w if unique else (w != 0.0))
+        if rc != _lib.GSDFT_ERR_FALLBACK:
+            _lib.check(rc, "gsdft_screen_spatial")
+        print(f"  [screening] spatial path overflowed (sig={n_sp}, pad={pad_to}); using the "
+              f"dense scan", flush=True)
     L = _lib.lib()
     keep_cap = 0
     n_sig = ctypes.c_int64(0)

@@ -195,6 +195,21 @@ def make_system(index: int, *, eps: float = 1e-7) -> System:
                   C=C, occ=np.ones(k), eps=eps, charges=_CHARGES[index]())
 
 
+def make_globule2100(k: int = 16, eps: float = 1e-7) -> System:
+    """A screening-scale shape beyond the benchmark systems: a 2100-atom C/H/O globule (600 C,
+    1200 H, 300 O) at 0.9 g/cm^3 with M = 60000 splats (seed 5), the per-GPU splat count of the
+    reference's largest size-ladder runs. Only its pair list is built at this size, so C has a
+    few columns."""
+    rng = np.random.Generator(np.random.PCG64(5))
+    atoms = globule_atoms({"C": 600, "H": 1200, "O": 300}, rng)
+    M = 60000
+    quat, log_scale, centers = _splats(atoms, M, rng)
+    C = rng.normal(size=(M, k)) / math.sqrt(k)
+    return System(name="globule2100", atoms=atoms, quat=quat, log_scale=log_scale,
+                  centers=centers, C=C, occ=np.ones(k), eps=eps,
+                  charges=np.array([6.0] * 600 + [1.0] * 1200 + [8.0] * 300))
+
+
 def make_small(M: int, k: int, n_atoms: int = 4, seed: int = 0, spread: float = 2.5,
                width=(0.3, 3.0), n_scales: int = 2) -> System:
     """A small random system for parity tests: ``n_atoms`` random atoms in a cube of half-side

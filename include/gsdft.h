@@ -30,6 +30,7 @@ extern "C" {
 #define GSDFT_ERR_HIP 4          /* HIP runtime error                                           */
 #define GSDFT_ERR_LIB 5          /* rocBLAS / rocSOLVER / hipCUB error                          */
 #define GSDFT_ERR_WORKSPACE 6    /* workspace too small; the query names the size               */
+#define GSDFT_ERR_FALLBACK 7     /* spatial screening: the list overflows its pad (use the dense build) */
 
 int gsdft_abi_version(void);
 const char* gsdft_last_error(void);
@@ -66,6 +67,22 @@ int gsdft_screen_build(int64_t M, const double* quat, const double* log_scale,
                        const double* centers, double eps, int unique, int64_t pad_to,
                        int32_t* pi, int32_t* pj, double* weight, void* workspace,
                        size_t workspace_bytes, int64_t* n_sig, void* stream);
+
+/* Spatial screening: the same list as gsdft_screen_build when it fits the pad, built from a
+ * candidate superset instead of every (i, j). A pair is a candidate when
+ * |mu_i - mu_j|^2 < b_i + b_j, b_i = 1.0625 (-ln eps) / lmin_i with lmin_i a lower bound of the
+ * smallest eigenvalue of A_i; every significant pair satisfies this (|S_ij| <= exp(-|d|^2 /
+ * (1/lmin_i + 1/lmin_j))), so the result is bit-identical to the dense scan. pad_to < 0 only
+ * counts (*n_sig). When n_sig > pad_to nothing is written and the call returns GSDFT_ERR_FALLBACK
+ * with *n_sig set: the keep-largest list comes from gsdft_screen_build, as the reference falls
+ * back to its dense strips. Needs eps >= 0 and M <= 262144 (one row's bitmap in LDS).
+ * Synchronises the stream. Replaces _spatial_candidates and _scan_candidate_indices,
+ * gs_dft/screening/pairs.py:167-222,284-298. */
+int gsdft_screen_spatial_workspace_size(int64_t M, size_t* bytes);
+int gsdft_screen_spatial(int64_t M, const double* quat, const double* log_scale,
+                         const double* centers, double eps, int unique, int64_t pad_to,
+                         int32_t* pi, int32_t* pj, double* weight, void* workspace,
+                         size_t workspace_bytes, int64_t* n_sig, void* stream);
 
 /* CSR views of the first n list entries for the atomics-free per-splat reductions of the
  * backward pass: row_ptr/row_perm group entries by pi, col_ptr/col_perm by pj, each group in list

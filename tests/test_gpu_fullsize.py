@@ -43,14 +43,29 @@ def _splat(g, s):
 
 # ----------------------------------------------------------------------------- pair list
 
-@pytest.mark.parametrize("system,unique", [(4, True), (4, False), (5, True)])
-def test_pair_list_bit_exact_globules(g, wl, orc, cuda, system, unique):
+_ORACLE_LISTS = {}
+
+
+def _oracle_list(orc, s, unique):
+    key = (s.name, s.eps, unique)
+    if key not in _ORACLE_LISTS:
+        _ORACLE_LISTS[key] = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, s.eps, None,
+                                                unique)
+    return _ORACLE_LISTS[key]
+
+
+@pytest.mark.parametrize("system,unique,spatial", [(4, True, False), (4, True, True),
+                                                   (4, False, True), (5, True, False),
+                                                   (5, True, True)])
+def test_pair_list_bit_exact_globules(g, wl, orc, cuda, system, unique, spatial):
     """The 300-atom (7.2e7 / 1.4e8 candidates) and 700-atom (2.0e8 candidates) globules at
-    eps = 1e-7: the GPU list equals the oracle's element for element."""
+    eps = 1e-7: the GPU list, from the dense scan and from the spatial candidates, equals the
+    oracle's element for element."""
     s = wl.make_system(system)
-    print(f"[pairs] system {system} M={s.M} eps={s.eps} unique={unique}", flush=True)
-    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=s.eps, unique=unique)
-    ri, rj, rw, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, s.eps, None, unique)
+    print(f"[pairs] system {system} M={s.M} eps={s.eps} unique={unique} spatial={spatial}",
+          flush=True)
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=s.eps, unique=unique, spatial=spatial)
+    ri, rj, rw, n_sig = _oracle_list(orc, s, unique)
     assert len(ri) == n_sig == pi.shape[0]
     assert np.array_equal(_np(pi), ri) and np.array_equal(_np(pj), rj)
     if unique:
@@ -58,6 +73,19 @@ def test_pair_list_bit_exact_globules(g, wl, orc, cuda, system, unique):
     else:
         assert bool(v.all())
     print(f"[pairs] system {system}: {len(ri)} pairs bit-exact", flush=True)
+
+
+def test_spatial_equals_dense_at_60k_splats(g, wl, cuda):
+    """A 2100-atom globule with M = 60000 splats (1.8e9 unique candidates, beyond the oracle's
+    reach in a test): the spatial build equals the dense scan bit for bit, and both counts
+    agree."""
+    s = wl.make_globule2100()
+    basis = _splat(g, s)
+    print(f"[pairs] {s.name} M={s.M} eps={s.eps}", flush=True)
+    a = g.neighbor_pairs(basis, eps=s.eps, unique=True, spatial=True)
+    b = g.neighbor_pairs(basis, eps=s.eps, unique=True, spatial=False)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    print(f"[pairs] {s.name}: {a[0].shape[0]} unique pairs, spatial == dense", flush=True)
 
 
 @pytest.mark.parametrize("system,eps", [(3, 1e-5), (3, 1e-7), (3, 1e-9), (4, 1e-7), (5, 1e-7)])

@@ -67,8 +67,9 @@ def test_overlap_matches_oracle_to_conditioning(g, wl, orc, cuda):
 
 # ----------------------------------------------------------------------------- pair list
 
-def _check_list(g, s, orc, eps, unique, pad_to=None):
-    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=eps, pad_to=pad_to, unique=unique)
+def _check_list(g, s, orc, eps, unique, pad_to=None, spatial=False):
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=eps, pad_to=pad_to, unique=unique,
+                                 spatial=spatial)
     ri, rj, rw, n_sig = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, eps, pad_to, unique)
     assert np.array_equal(_np(pi), ri) and np.array_equal(_np(pj), rj)
     w = _np(v)
@@ -79,48 +80,75 @@ def _check_list(g, s, orc, eps, unique, pad_to=None):
     return len(ri), n_sig
 
 
+@pytest.mark.parametrize("spatial", [False, True])
 @pytest.mark.parametrize("unique", [False, True])
 @pytest.mark.parametrize("eps", [1e-5, 1e-7, 1e-9])
 @pytest.mark.parametrize("which", [0, 1, 2])
-def test_pair_list_bit_exact_small(g, wl, orc, cuda, which, eps, unique):
+def test_pair_list_bit_exact_small(g, wl, orc, cuda, which, eps, unique, spatial):
     s = _small(wl, SMALL[which])
-    n, n_sig = _check_list(g, s, orc, eps, unique)
-    assert n == n_sig == g.count_significant(_splat(g, s), eps, unique)
+    n, n_sig = _check_list(g, s, orc, eps, unique, spatial=spatial)
+    assert n == n_sig == g.count_significant(_splat(g, s), eps, unique, spatial=spatial)
 
 
+@pytest.mark.parametrize("spatial", [False, True])
 @pytest.mark.parametrize("system", [1, 2, 3])
 @pytest.mark.parametrize("eps", [1e-5, 1e-7, 1e-9])
-def test_pair_list_bit_exact_benchmark_systems(g, wl, orc, cuda, system, eps):
+def test_pair_list_bit_exact_benchmark_systems(g, wl, orc, cuda, system, eps, spatial):
     s = wl.make_system(system)
-    print(f"[pairs] system {system} M={s.M} eps={eps}", flush=True)
-    n, _ = _check_list(g, s, orc, eps, True)
+    print(f"[pairs] system {system} M={s.M} eps={eps} spatial={spatial}", flush=True)
+    n, _ = _check_list(g, s, orc, eps, True, spatial=spatial)
     if system < 3:
-        _check_list(g, s, orc, eps, False)
+        _check_list(g, s, orc, eps, False, spatial=spatial)
     print(f"[pairs] system {system}: {n} unique pairs bit-exact", flush=True)
 
 
-def test_pair_list_padding_full_and_overflow(g, wl, orc, cuda):
-    """gs-dft tests/unit/test_device_pairs.py:62,76,91,146 and test_pair_tricks.py:57,260."""
+def test_spatial_screening_on_degenerate_charts(g, wl, orc, cuda):
+    """Splats whose chart bound degenerates: quaternions of norm 1e-9 and 0 (the chart then
+    rotates by a non-unit quaternion, so the eigenvalue bound widens or gives up and the splat
+    is a candidate for every pair), coincident centres and near-isotropic and needle-like widths:
+    the spatial list still equals the oracle's."""
+    s = _small(wl, SMALL[2])
+    quat = s.quat.copy()
+    quat[::17] *= 1e-9
+    quat[5] = 0.0
+    centers = s.centers.copy()
+    centers[40] = centers[41]
+    ls = s.log_scale.copy()
+    ls[7] = [4.0, -3.5, 0.0]
+    s2 = wl.System(name="degenerate", atoms=s.atoms, quat=quat, log_scale=ls, centers=centers,
+                   C=s.C, occ=s.occ)
+    for eps in (1e-3, 1e-7, 1e-11):
+        for unique in (False, True):
+            _check_list(g, s2, orc, eps, unique, spatial=True)
+
+
+@pytest.mark.parametrize("spatial", [False, True])
+def test_pair_list_padding_full_and_overflow(g, wl, orc, cuda, spatial):
+    """gs-dft tests/unit/test_device_pairs.py:62,76,91,146 and test_pair_tricks.py:57,260; the
+    spatial build falls back to the dense keep-largest rule when the list overflows its pad
+    (pairs.py:290-298)."""
     s = _small(wl, SMALL[1])
     M = s.M
     for unique in (False, True):
-        n, _ = _check_list(g, s, orc, 1e-7, unique)
-        _check_list(g, s, orc, 1e-7, unique, pad_to=n + 37)
-        _check_list(g, s, orc, 1e-7, unique, pad_to=M * M + 500)
-        _check_list(g, s, orc, 1e-7, unique, pad_to=n // 2 + 1)          # keep-largest
+        n, _ = _check_list(g, s, orc, 1e-7, unique, spatial=spatial)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=n + 37, spatial=spatial)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=M * M + 500, spatial=spatial)
+        _check_list(g, s, orc, 1e-7, unique, pad_to=n // 2 + 1, spatial=spatial)  # keep-largest
         with pytest.raises(ValueError, match="exceed"):
-            g.neighbor_pairs(_splat(g, s), eps=1e-7, pad_to=n // 3, unique=unique)
+            g.neighbor_pairs(_splat(g, s), eps=1e-7, pad_to=n // 3, unique=unique,
+                             spatial=spatial)
     for pad in (None, M * M, M * M + 313):
         _check_list(g, s, orc, -1.0, False, pad_to=pad)
     _check_list(g, s, orc, -1.0, True)
     _check_list(g, s, orc, -1.0, False, pad_to=M * M // 2)                # eps<0, pad < M^2
 
 
-def test_empty_list(g, wl, cuda):
+@pytest.mark.parametrize("spatial", [False, True])
+def test_empty_list(g, wl, cuda, spatial):
     s = wl.make_small(8, 2, n_atoms=8, spread=200.0, seed=4, width=(0.3, 0.31))
-    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=0.5, unique=False)
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=0.5, unique=False, spatial=spatial)
     assert pi.shape[0] == 8 and bool(v.all())              # only the diagonal (S_ii = 1)
-    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=2.0)
+    pi, pj, v = g.neighbor_pairs(_splat(g, s), eps=2.0, spatial=spatial)
     assert pi.shape[0] == 0
 
 
