@@ -56,6 +56,8 @@ SIGNATURES = {
     "gsdft_gamma_workspace_size": [_i64, _i64, _i64, _i64, _psz],
     "gsdft_gamma": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
                     _vp, _vp, _sz, _vp],
+    "gsdft_gamma_noalloc": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp,
+                            _vp, _vp, _vp, _vp],
     "gsdft_gamma_vjp_workspace_size": [_i64, _i64, _i64, _i64, _psz],
     "gsdft_gamma_vjp": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp,
                         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,

@@ -2116,15 +2116,16 @@ extern "C" int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, i
     return GSDFT_OK;
 }
 
-extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scale,
-                           const double* centers, int64_t k, const double* C, const double* occ,
-                           int64_t N, const double* log_alpha, const double* aux_centers,
-                           int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
-                           double* gamma, void* workspace, size_t workspace_bytes, void* stream) {
-    if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
-        return fail(GSDFT_ERR_ARG, "gsdft_gamma: bad arguments");
-    hipStream_t s = (hipStream_t)stream;
-    Arena ar{(char*)workspace, workspace_bytes, 0};
+namespace {
+
+// gsdft_gamma's body over a workspace of `bytes` bytes; `profile` records the kernel timer
+// (HIP events, created on demand) and the node counter.
+int gamma_run(int64_t M, const double* quat, const double* log_scale, const double* centers,
+              int64_t k, const double* C, const double* occ, int64_t N, const double* log_alpha,
+              const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
+              const double* weight, double* gamma, void* workspace, size_t bytes, hipStream_t s,
+              bool profile) {
+    Arena ar{(char*)workspace, bytes, 0};
     GammaWs w;
     GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
     if (!w.partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_gamma: workspace too small");
@@ -2147,14 +2148,75 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
     const int64_t blocks = groups * ((N + kFwdRecs - 1) / kFwdRecs);
     if (blocks > INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_gamma: n x N_aux too large");
     const dim3 grid((unsigned)blocks);
-    profile_begin(kProfGammaFwd, s);
+    if (profile) profile_begin(kProfGammaFwd, s);
     k_gamma_fwd_pairs<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, w.partial,
-                                           profile_work_counter(kProfGammaFwd));
-    profile_end(kProfGammaFwd, s);
+                                           profile ? profile_work_counter(kProfGammaFwd)
+                                                   : nullptr);
+    if (profile) profile_end(kProfGammaFwd, s);
     GSDFT_HIP(hipGetLastError());
     k_slot_sum<<<blocks_for(N, 256), 256, 0, s>>>(N, G, groups, w.partial, gamma);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
+}
+
+// Static scratch of gsdft_gamma_noalloc: one copy per device, held while the process runs. Host
+// code never names it in a launch or copy: its device address comes from hipGetSymbolAddress, once
+// per device, with that device current.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;      // device address of `scratch`, by device id
+
+int scratch_address(void** out) {
+    int dev = 0;
+    GSDFT_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(GSDFT_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GSDFT_OK;
+}
+
+}  // namespace
+
+extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scale,
+                           const double* centers, int64_t k, const double* C, const double* occ,
+                           int64_t N, const double* log_alpha, const double* aux_centers,
+                           int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
+                           double* gamma, void* workspace, size_t workspace_bytes, void* stream) {
+    if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma: bad arguments");
+    return gamma_run(M, quat, log_scale, centers, k, C, occ, N, log_alpha, aux_centers, n, pi, pj,
+                     weight, gamma, workspace, workspace_bytes, (hipStream_t)stream, true);
+}
+
+extern "C" int gsdft_gamma_noalloc(int64_t M, const double* quat, const double* log_scale,
+                                   const double* centers, int64_t k, const double* C,
+                                   const double* occ, int64_t N, const double* log_alpha,
+                                   const double* aux_centers, int64_t n, const int32_t* pi,
+                                   const int32_t* pj, const double* weight, double* gamma,
+                                   void* stream) {
+    if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma_noalloc: bad arguments");
+    Arena ar{nullptr, 0, 0};
+    GammaWs w;
+    GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
+    if (ar.need() > kScratchBytes)
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma_noalloc: M = %lld, N_aux = %lld, n = %lld need "
+                    "%zu bytes of scratch; the static scratch holds %zu (use gsdft_gamma with a "
+                    "workspace)", (long long)M, (long long)N, (long long)n, ar.need(),
+                    kScratchBytes);
+    void* p = nullptr;
+    GSDFT_TRY(scratch_address(&p));
+    return gamma_run(M, quat, log_scale, centers, k, C, occ, N, log_alpha, aux_centers, n, pi, pj,
+                     weight, gamma, p, kScratchBytes, (hipStream_t)stream, false);
 }
 
 extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,

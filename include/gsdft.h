@@ -142,6 +142,21 @@ int gsdft_gamma(int64_t M, const double* quat, const double* log_scale, const do
                 const int32_t* pi, const int32_t* pj, const double* weight, double* gamma,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* gsdft_gamma without a workspace and without allocating: the same kernels, with their scratch in
+ * a static 64 MiB device array inside the library (one per GPU, held until the process ends; its
+ * address is looked up once per device). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Sizes whose gsdft_gamma workspace exceeds 64 MiB (gsdft_gamma_workspace_size) are
+ * refused with GSDFT_ERR_ARG before any launch: the water octamer (M = 600, N_aux = 2,400,
+ * n = 166,915 pairs, 49.8 MiB) fits, C20H42 (n = 590,298, 179 MiB) does not.
+ * Every call on one GPU shares that GPU's scratch and leaves its contents behind, so calls that
+ * overlap on one GPU (several streams or host threads at once) race; serialise them. */
+int gsdft_gamma_noalloc(int64_t M, const double* quat, const double* log_scale,
+                        const double* centers, int64_t k, const double* C, const double* occ,
+                        int64_t N, const double* log_alpha, const double* aux_centers, int64_t n,
+                        const int32_t* pi, const int32_t* pj, const double* weight, double* gamma,
+                        void* stream);
+
 /* Reverse mode of gsdft_gamma for the cotangent dgamma (N), scaled by the device scalar
  * *dgamma_scale when non-null: J (n) = sum_P dgamma_P (P|a) (0 on zero-weight entries), and the
  * gradients w.r.t. quat, log_scale, centers (M,4/3/3) and C (M,k), aux held constant. Needs the
