@@ -21,7 +21,7 @@ ROCM = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("GSDFT_ARCH", "gfx950")
 
 SOURCES = ["abi.hip", "screen.hip", "dfj.hip", "solve.hip", "order.hip", "grid.hip",
-           "exchange.hip"]
+           "exchange.hip", "gemm.hip"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

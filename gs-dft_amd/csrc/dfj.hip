@@ -1827,9 +1827,8 @@ extern "C" int gsdft_product_aux_pairs(int64_t M, const double* quat, const doub
     return GSDFT_OK;
 }
 
-// Blocked Cholesky: panels of kCholNb rows, trailing updates in column chunks of kCholW.
+// Blocked Cholesky: panels of kCholNb rows.
 constexpr int64_t kCholNb = 2048;
-constexpr int64_t kCholW = 2048;
 
 extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
     if (N < 0 || !bytes) return fail(GSDFT_ERR_ARG, "metric_workspace_size: bad arguments");
@@ -1979,41 +1978,45 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
 
 // P <- U^-T P for the kb x kb upper factor U at Akk and the kb x T panel P (both column-major,
 // leading dimension N), by blocked substitution: each 128-row block is solved by k_panel_subst and
-// applied to the rows below it by an FP64 GEMM. Backward stable, unlike a solve through explicit
-// inverses of the diagonal blocks, whose error grows with their condition number.
-static int panel_solve(rocblas_handle h, hipStream_t s, int64_t N, const double* Akk, int64_t kb,
-                       double* P, int64_t T) {
-    const double one = 1.0, minus_one = -1.0;
+// applied to the rows below it by an FP64 MFMA product. Backward stable, unlike a solve through
+// explicit inverses of the diagonal blocks, whose error grows with their condition number.
+static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, double* P,
+                       int64_t T) {
     for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
         const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
         k_panel_subst<<<(unsigned)((T + 4 * kSubstCols - 1) / (4 * kSubstCols)), 256, 0, s>>>(
             N, Akk + i0 * N + i0, ib, P + i0, T);
         GSDFT_HIP(hipGetLastError());
-        if (i0 + ib < kb) {
-            const rocblas_status st = rocblas_dgemm_64(
-                h, rocblas_operation_transpose, rocblas_operation_none, kb - i0 - ib, T, ib,
-                &minus_one, Akk + (i0 + ib) * N + i0, N, P + i0, N, &one, P + i0 + ib, N);
-            if (st != rocblas_status_success)
-                return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
-        }
+        // P(i0 + ib + m, c) -= sum_r U(i0 + r, i0 + ib + m) P(i0 + r, c)
+        if (i0 + ib < kb)
+            GSDFT_TRY(launch_gemm_tn_sub(kb - i0 - ib, T, ib, Akk + (i0 + ib) * N + i0, N,
+                                         P + i0, N, P + i0 + ib, N, false, s));
     }
     return GSDFT_OK;
 }
 
-// C (upper triangle, T x T at C, leading dimension N) -= P^T P for the kb x T panel P, as FP64
-// GEMMs over column chunks of width chunk, each chunk updating rows 0 .. its last column (the
-// chunk's own sub-diagonal part is computed too and never read).
-static int trailing_update(rocblas_handle h, int64_t N, const double* P, int64_t kb, double* C,
-                           int64_t T, int64_t chunk) {
-    const double one = 1.0, minus_one = -1.0;
-    for (int64_t c0 = 0; c0 < T; c0 += chunk) {
-        const int64_t w = std::min(chunk, T - c0);
-        const rocblas_status st = rocblas_dgemm_64(h, rocblas_operation_transpose,
-                                                   rocblas_operation_none, c0 + w, w, kb,
-                                                   &minus_one, P, N, P + c0 * N, N, &one,
-                                                   C + c0 * N, N);
-        if (st != rocblas_status_success)
-            return fail(GSDFT_ERR_LIB, "rocblas_dgemm failed (status %d)", (int)st);
+// C (T x T at C, leading dimension N) -= P^T P for the kb x T panel P, on the tiles on or above
+// the diagonal (the sub-diagonal half of the diagonal tiles is formed too and never read).
+static int trailing_update(hipStream_t s, int64_t N, const double* P, int64_t kb, double* C,
+                           int64_t T) {
+    return launch_gemm_tn_sub(T, T, kb, P, N, P, N, C, N, true, s);
+}
+
+// The diagonal block [k0, k0 + kb) of the column-major view: 128-row blocks factored by k_potf2,
+// each block's panel solved and its trailing part of the block updated.
+static int factor_diag_block(hipStream_t s, int64_t N, double* A, int64_t k0, int64_t kb,
+                             int64_t* info) {
+    double* Akk = A + k0 * N + k0;
+    for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
+        const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
+        double* Aii = Akk + i0 * N + i0;
+        k_potf2<<<1, kPotfThreads, 0, s>>>(N, Aii, ib, k0 + i0, info);
+        GSDFT_HIP(hipGetLastError());
+        const int64_t Ti = kb - i0 - ib;
+        if (Ti == 0) break;
+        double* Pi = Aii + (int64_t)ib * N;
+        GSDFT_TRY(panel_solve(s, N, Aii, ib, Pi, Ti));
+        GSDFT_TRY(trailing_update(s, N, Pi, ib, Pi + ib, Ti));
     }
     return GSDFT_OK;
 }
@@ -2021,31 +2024,20 @@ static int trailing_update(rocblas_handle h, int64_t N, const double* P, int64_t
 // Right-looking blocked upper Cholesky of the column-major view A (= V, symmetric), A = U^T U, on
 // two levels with the same three steps: for each diagonal block, factor it, solve the panel to its
 // right (P = U_kk^-T A_k,rest) and update the trailing upper triangle (A_rest -= P^T P). The outer
-// level uses kCholNb-row panels (the trailing updates are large FP64 GEMMs); each kCholNb diagonal
-// block is factored the same way with 128-row blocks, whose factorisation is k_potf2. *info
-// receives the first failing leading minor (0 if none).
-static int cholesky_blocked(rocblas_handle h, hipStream_t s, int64_t N, double* A, int64_t* info) {
+// level uses kCholNb-row panels; each kCholNb diagonal block is factored the same way with 128-row
+// blocks, whose factorisation is k_potf2. Every update is an FP64 MFMA product. *info receives the
+// first failing leading minor (0 if none).
+static int cholesky_blocked(hipStream_t s, int64_t N, double* A, int64_t* info) {
     k_info_reset<<<1, 1, 0, s>>>(info);
     GSDFT_HIP(hipGetLastError());
     for (int64_t k0 = 0; k0 < N; k0 += kCholNb) {
         const int64_t kb = std::min(kCholNb, N - k0);
-        double* Akk = A + k0 * N + k0;
-        for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
-            const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
-            double* Aii = Akk + i0 * N + i0;
-            k_potf2<<<1, kPotfThreads, 0, s>>>(N, Aii, ib, k0 + i0, info);
-            GSDFT_HIP(hipGetLastError());
-            const int64_t Ti = kb - i0 - ib;
-            if (Ti == 0) break;
-            double* Pi = Aii + (int64_t)ib * N;
-            GSDFT_TRY(panel_solve(h, s, N, Aii, ib, Pi, Ti));
-            GSDFT_TRY(trailing_update(h, N, Pi, ib, Pi + ib, Ti, Ti));
-        }
+        GSDFT_TRY(factor_diag_block(s, N, A, k0, kb, info));
         const int64_t T = N - k0 - kb;
         if (T == 0) break;
-        double* P = Akk + kb * N;
-        GSDFT_TRY(panel_solve(h, s, N, Akk, kb, P, T));
-        GSDFT_TRY(trailing_update(h, N, P, kb, P + kb, T, kCholW));
+        double* P = A + (k0 + kb) * N + k0;
+        GSDFT_TRY(panel_solve(s, N, A + k0 * N + k0, kb, P, T));
+        GSDFT_TRY(trailing_update(s, N, P, kb, P + kb, T));
     }
     return GSDFT_OK;
 }
@@ -2059,13 +2051,11 @@ extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t work
     ar.take<double>(2 * N + 2);
     int64_t* info = ar.take<int64_t>(2);
     if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_cholesky: workspace too small");
-    rocblas_handle h;
-    GSDFT_TRY(blas_handle(s, &h));
-    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle. ILP64 GEMMs:
-    // N * N exceeds the int32 range of the rocblas_int interfaces from N = 46341.
+    // Row-major lower L is column-major upper U = L^T, so factor the upper triangle (64-bit
+    // offsets throughout: N * N exceeds the int32 range from N = 46341).
     {
         ProfileScope prof(kProfCholesky, s);
-        GSDFT_TRY(cholesky_blocked(h, s, N, V, info));
+        GSDFT_TRY(cholesky_blocked(s, N, V, info));
     }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     k_zero_upper<<<grid, 256, 0, s>>>(N, V);

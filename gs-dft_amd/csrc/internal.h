@@ -65,6 +65,13 @@ enum ProfileId { kProfGammaFwd = 0, kProfGammaBwd = 1, kProfScreen = 2, kProfMet
                  kProfExchTrsm = 12, kProfExchGemm = 13, kProfExchSparse = 14,
                  kProfCount = 15 };
 
+// gemm.hip: C(m, n) -= sum_k A[m lda + k] B[n ldb + k] for m < Mr, n < Nc (C column-major,
+// C(m, n) at C[n ldc + m]) on FP64 MFMA; with `upper` (Mr == Nc) only the 128 x 128 tiles on or
+// above the diagonal are formed (the diagonal tiles in full).
+int launch_gemm_tn_sub(int64_t Mr, int64_t Nc, int64_t K, const double* A, int64_t lda,
+                       const double* B, int64_t ldb, double* C, int64_t ldc, bool upper,
+                       hipStream_t s);
+
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
 

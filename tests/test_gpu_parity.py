@@ -226,12 +226,12 @@ def test_cholesky_and_solve(g, wl, orc, cuda):
     assert abs(E - En) < 1e-10 * abs(En)
 
 
-@pytest.mark.parametrize("N", [1, 1000, 1024, 2500, 3137])
+@pytest.mark.parametrize("N", [1, 100, 1000, 1024, 2500, 3137, 4500])
 def test_blocked_cholesky_matches_lapack(g, cuda, N):
-    """The blocked factorisation (1024-row panels, 128-row substitution blocks, partial last
-    panel and block, panel widths not a multiple of 64) against LAPACK on a well-conditioned SPD
-    matrix; the strict upper triangle is zeroed. A matrix made indefinite inside a later panel
-    reports the failing leading minor of the whole matrix."""
+    """The blocked factorisation (2048-row panels, 128-row substitution blocks, FP64 MFMA
+    updates in 128 x 128 tiles; partial last panel, block and tiles, widths not a multiple of 16)
+    against LAPACK on a well-conditioned SPD matrix; the strict upper triangle is zeroed. A matrix
+    made indefinite inside a later panel reports the failing leading minor of the whole matrix."""
     from gs_dft_amd import _lib
     rng = np.random.default_rng(N)
     A = rng.normal(size=(N, N)) / np.sqrt(N)
