@@ -2,14 +2,16 @@
 //   L y = gamma (forward), L^T d = y (backward)  -- gs_dft/coulomb/ri.py:479's cho_solve.
 //
 // Single right-hand side, so the solves are HBM-bound: each reads the lower triangle once
-// (N^2/2 doubles). Blocked by 128 columns. For every block one workgroup stages the block's
-// strictly lower part in LDS (1024 threads, all loads in flight at once) and one wave solves it:
-// lane l holds rows l and l + 64, each solved value is broadcast from its owner lane with readlane
-// (no barrier in the 128-step chain), and the diagonal enters as a reciprocal. A wide kernel then
-// applies the block to every remaining row (forward: 16 lanes per row, 8 products per lane in
-// column order, fixed 16-lane butterfly) or column (backward: 64 columns x 4 groups of 32 rows per
-// workgroup, each group in row order, the four partial sums added in group order). Every output element is updated by
-// the same sequence of kernels in the same order, so results are deterministic.
+// (N^2/2 doubles). Blocked by 128 columns, one launch per block and direction (k_trsv_fwd_step,
+// k_trsv_bwd_step): the launch applies the solved block to every remaining row (forward: 16 lanes
+// per row, 8 products per lane in column order, fixed 16-lane butterfly) or column (backward: one
+// lane per column, row groups summed in order, group partials added in group order), and its
+// workgroup 0 applies it to the neighbouring block and then solves that block: the block is staged
+// in LDS and wave 0 runs the substitution (lane l holds rows l and 64 + l, each solved value is
+// broadcast from its owner lane with readlane, no barrier in the 128-step chain, the diagonal
+// enters as a reciprocal). The first block (forward) and the last (backward) are solved alone by
+// k_trsv_diag. Every output element is updated by the same sequence of kernels in the same order,
+// so results are deterministic.
 #include "common.h"
 #include "internal.h"
 
@@ -20,38 +22,40 @@ namespace {
 constexpr int kNb = 128;        // block size
 constexpr int kLd = kNb + 1;    // padded LDS row
 
-// Solve the diagonal block rows [j0, j0 + nb) in place in x: forward L_jj y = x, or backward
-// L_jj^T d = x. Launched with 1024 threads: all stage the block (16 loads in flight per thread),
-// wave 0 solves. The sweep always runs all 128 steps: rows and columns past nb hold zeros in LDS
-// and a zero reciprocal, so they neither change nor receive anything.
-constexpr int kDiagThreads = 1024;
-constexpr int kDiagLoads = kNb * kNb / kDiagThreads;
+// Every kernel here runs 1024 threads per workgroup: the 128 x 128 diagonal block is staged in LDS
+// (132 KB, one workgroup per CU) by all threads, 16 elements each, and solved by wave 0.
+constexpr int kThreads = 1024;
+constexpr int kTriLoads = kNb * kNb / kThreads;
 
-template <bool kFwd>
-__global__ __launch_bounds__(kDiagThreads) void k_trsv_diag(int64_t N, const double* __restrict__ L,
-                                                            double* __restrict__ x, int64_t j0,
-                                                            int nb) {
-    __shared__ double Ls[kNb * kLd];
-    double v[kDiagLoads];
+// Strictly lower part of the diagonal block at (r0, r0), rows < nb valid, zeros elsewhere: element
+// e = threadIdx.x + 1024 q is (e / 128, e % 128). Loaded into registers first so that the caller
+// can issue its other loads before any of them is needed.
+__device__ __forceinline__ void load_triangle(int64_t N, const double* __restrict__ L, int64_t r0,
+                                              int nb, double (&v)[kTriLoads]) {
 #pragma unroll
-    for (int q = 0; q < kDiagLoads; ++q) {
-        const int e = threadIdx.x + q * kDiagThreads;
+    for (int q = 0; q < kTriLoads; ++q) {
+        const int e = threadIdx.x + q * kThreads;
         const int r = e >> 7, c = e & (kNb - 1);
-        v[q] = (r < nb && c < r) ? L[(j0 + r) * N + j0 + c] : 0.0;
+        v[q] = (r < nb && c < r) ? L[(r0 + r) * N + r0 + c] : 0.0;
     }
+}
+
+__device__ __forceinline__ void store_triangle(const double (&v)[kTriLoads],
+                                               double* __restrict__ Ls) {
 #pragma unroll
-    for (int q = 0; q < kDiagLoads; ++q) {
-        const int e = threadIdx.x + q * kDiagThreads;
+    for (int q = 0; q < kTriLoads; ++q) {
+        const int e = threadIdx.x + q * kThreads;
         Ls[(e >> 7) * kLd + (e & (kNb - 1))] = v[q];
     }
-    __syncthreads();
-    if (threadIdx.x >= 64) return;
+}
+
+// Wave 0: substitution through the staged block. Lane l holds rows l (acc0) and 64 + l (acc1) with
+// reciprocal diagonals rd0, rd1 (0 past the block's size, so those rows neither change nor
+// contribute); on return acc * rd is the solution. Forward L_jj y = x; backward L_jj^T d = x.
+template <bool kFwd>
+__device__ __forceinline__ void solve_block(const double* __restrict__ Ls, double rd0, double rd1,
+                                            double& acc0, double& acc1) {
     const int l = threadIdx.x;
-    const bool h0 = l < nb, h1 = l + 64 < nb;
-    const double rd0 = h0 ? 1.0 / L[(j0 + l) * N + j0 + l] : 0.0;
-    const double rd1 = h1 ? 1.0 / L[(j0 + 64 + l) * N + j0 + 64 + l] : 0.0;
-    double acc0 = h0 ? x[j0 + l] : 0.0;
-    double acc1 = h1 ? x[j0 + 64 + l] : 0.0;
     if constexpr (kFwd) {
         // rows r > c take -L[r][c] y_c; Ls is zero on and above the diagonal
 #pragma unroll 16
@@ -79,43 +83,85 @@ __global__ __launch_bounds__(kDiagThreads) void k_trsv_diag(int64_t N, const dou
             acc0 = __builtin_fma(-Ls[c * kLd + l], d, acc0);
         }
     }
+}
+
+// Solve the diagonal block rows [j0, j0 + nb) in place in x: forward L_jj y = x, or backward
+// L_jj^T d = x.
+template <bool kFwd>
+__global__ __launch_bounds__(kThreads) void k_trsv_diag(int64_t N, const double* __restrict__ L,
+                                                        double* __restrict__ x, int64_t j0,
+                                                        int nb) {
+    __shared__ double Ls[kNb * kLd];
+    double v[kTriLoads];
+    load_triangle(N, L, j0, nb, v);
+    const int l = threadIdx.x;
+    const bool h0 = l < nb, h1 = l + 64 < nb;
+    double dg0 = 1.0, dg1 = 1.0, acc0 = 0.0, acc1 = 0.0;
+    if (l < 64) {
+        if (h0) dg0 = L[(j0 + l) * N + j0 + l], acc0 = x[j0 + l];
+        if (h1) dg1 = L[(j0 + 64 + l) * N + j0 + 64 + l], acc1 = x[j0 + 64 + l];
+    }
+    store_triangle(v, Ls);
+    __syncthreads();
+    if (l >= 64) return;
+    const double rd0 = h0 ? 1.0 / dg0 : 0.0, rd1 = h1 ? 1.0 / dg1 : 0.0;
+    solve_block<kFwd>(Ls, rd0, rd1, acc0, acc1);
     if (h0) x[j0 + l] = acc0 * rd0;
     if (h1) x[j0 + 64 + l] = acc1 * rd1;
 }
 
-constexpr int kFwdLanes = 16;                      // lanes per row in the forward update
-constexpr int kFwdRowsPerGroup = 256 / kFwdLanes;   // rows per workgroup per iteration
+// Forward update of row i by the solved block at j0: 16 lanes per row, each holding the products of
+// 8 columns (c = 2 (lane % 16) + 32 q + {0, 1}, q = 0..3, 16-byte loads, so every load instruction
+// reads whole 256-byte row segments); the 8 products are added in order, then a 4-step butterfly
+// over the 16 lanes. With kPair (N even, L 16-byte aligned) every pair of columns loads as one
+// double2.
+constexpr int kFwdLanes = 16;
 
-// Forward: x_i -= sum_c L[i][j0+c] y_c for every row i >= j0 + 128 (the block is full: only the
-// last block can be partial, and no row lies below it). 16 lanes per row, each holding the
-// products of 8 columns (c = 2 (lane % 16) + 32 q + {0, 1}, q = 0..3, 16-byte loads, so every load
-// instruction reads whole 256-byte row segments); the 8 products are added in order, then a
-// 4-step butterfly over the 16 lanes.
-// kPair: N even and L 16-byte aligned, so every pair of columns loads as one double2.
+// Backward update of column k by the solved block at j0: one lane per column and kBwdGroups row
+// groups, each summing its rows in order; the group partials are added in group order.
+constexpr int kBwdGroups = 4;
+constexpr int kBwdRows = kNb / kBwdGroups;
+
+// ------------------------------------------------------------------ fused steps
+// One launch per block and direction. Workgroups 1.. apply the solved block to every row (forward)
+// or column (backward) past the neighbouring block; workgroup 0 applies it to the neighbouring
+// block and solves that block, so that the next launch finds it solved. Workgroup 0 issues all of
+// its loads (the 128 x 128 coupling tile, the neighbouring block's triangle and diagonal, its x)
+// before it uses any of them: its path is one memory round trip and the 128-step substitution,
+// under the streaming of the other workgroups.
+
+// Forward step for the solved block at j0 (full): rows i >= j1 + 128 (workgroups 1.., 128 rows
+// per workgroup and iteration, two per 16-lane group) and the next block's rows [j1, j1 + nb1),
+// j1 = j0 + 128 (workgroup 0, which then solves that block), take x_i -= sum_c L[i][j0 + c] y_c.
 template <bool kPair>
-__global__ __launch_bounds__(256) void k_trsv_upd_fwd(int64_t N, const double* __restrict__ L,
-                                                      double* __restrict__ x, int64_t j0) {
+__global__ __launch_bounds__(kThreads) void k_trsv_fwd_step(int64_t N, const double* __restrict__ L,
+                                                            double* __restrict__ x, int64_t j0,
+                                                            int nb1) {
+    __shared__ double Ls[kNb * kLd];
+    __shared__ double xs[kNb];
     const int sub = threadIdx.x & (kFwdLanes - 1);
+    const int rsub = threadIdx.x >> 4;                 // 0 .. 63
     double y[8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         y[2 * q] = x[j0 + 2 * sub + 32 * q];
         y[2 * q + 1] = x[j0 + 2 * sub + 32 * q + 1];
     }
-    const int64_t first = j0 + kNb;
-    for (int64_t i = first + (int64_t)blockIdx.x * kFwdRowsPerGroup + (threadIdx.x >> 4); i < N;
-         i += (int64_t)gridDim.x * kFwdRowsPerGroup) {
+    auto load_row = [&](bool live, int64_t i, double2 (&v)[4]) {
         const double* row = L + i * N + j0 + 2 * sub;
-        double2 v[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            if constexpr (kPair) {
+            if (!live) {
+                v[q] = make_double2(0.0, 0.0);
+            } else if constexpr (kPair) {
                 v[q] = *reinterpret_cast<const double2*>(row + 32 * q);
             } else {
                 v[q].x = row[32 * q];
                 v[q].y = row[32 * q + 1];
             }
         }
+    };
+    auto dot_row = [&](const double2 (&v)[4]) {
         double p = v[0].x * y[0];
         p = __builtin_fma(v[0].y, y[1], p);
 #pragma unroll
@@ -125,41 +171,130 @@ __global__ __launch_bounds__(256) void k_trsv_upd_fwd(int64_t N, const double* _
         }
 #pragma unroll
         for (int off = kFwdLanes / 2; off > 0; off >>= 1) p += __shfl_xor(p, off, kFwdLanes);
-        if (sub == 0) x[i] -= p;
+        return p;
+    };
+    const int64_t j1 = j0 + kNb;
+    if (blockIdx.x == 0) {
+        const int ra = rsub, rb = rsub + 64;
+        double2 va[4], vb[4];
+        load_row(ra < nb1, j1 + ra, va);
+        load_row(rb < nb1, j1 + rb, vb);
+        double tri[kTriLoads];
+        load_triangle(N, L, j1, nb1, tri);
+        double xa = 0.0, xb = 0.0;
+        if (sub == 0) {
+            if (ra < nb1) xa = x[j1 + ra];
+            if (rb < nb1) xb = x[j1 + rb];
+        }
+        const int l = threadIdx.x;
+        const bool h0 = l < nb1, h1 = l + 64 < nb1;
+        double dg0 = 1.0, dg1 = 1.0;
+        if (l < 64) {
+            if (h0) dg0 = L[(j1 + l) * N + j1 + l];
+            if (h1) dg1 = L[(j1 + 64 + l) * N + j1 + 64 + l];
+        }
+        store_triangle(tri, Ls);
+        const double pa = dot_row(va), pb = dot_row(vb);
+        if (sub == 0) {
+            xs[ra] = ra < nb1 ? xa - pa : 0.0;
+            xs[rb] = rb < nb1 ? xb - pb : 0.0;
+        }
+        __syncthreads();
+        if (l >= 64) return;
+        const double rd0 = h0 ? 1.0 / dg0 : 0.0, rd1 = h1 ? 1.0 / dg1 : 0.0;
+        double acc0 = xs[l], acc1 = xs[64 + l];
+        solve_block<true>(Ls, rd0, rd1, acc0, acc1);
+        if (h0) x[j1 + l] = acc0 * rd0;
+        if (h1) x[j1 + 64 + l] = acc1 * rd1;
+        return;
+    }
+    for (int64_t i0 = j1 + kNb + (int64_t)(blockIdx.x - 1) * kNb; i0 < N;
+         i0 += (int64_t)(gridDim.x - 1) * kNb) {
+        const int64_t ia = i0 + rsub, ib = ia + 64;
+        double2 va[4], vb[4];
+        load_row(ia < N, ia, va);
+        load_row(ib < N, ib, vb);
+        const double pa = dot_row(va), pb = dot_row(vb);
+        if (sub == 0) {
+            if (ia < N) x[ia] -= pa;
+            if (ib < N) x[ib] -= pb;
+        }
     }
 }
 
-constexpr int kBwdCols = 64;            // columns per workgroup of the backward update
-constexpr int kBwdGroups = 4;           // row groups (one wave each)
-constexpr int kBwdRows = kNb / kBwdGroups;
-
-// Backward: x_k -= sum_r L[j0+r][k] d_r for every column k < j0. Wave g sums rows
-// [g kBwdRows, (g + 1) kBwdRows) of the block for 64 consecutive columns; the four partials are
+// Backward step for the solved block at j0 (nb rows): columns k < jm = j0 - 128 (workgroups 1..,
+// 256 columns each, 4 groups of 32 rows) and the previous block's columns [jm, j0) (workgroup 0,
+// 128 columns x 8 groups of 16 rows, which then solves that block) take
+// x_k -= sum_r L[j0 + r][k] d_r; each group sums its rows in order and the group partials are
 // added in group order.
-__global__ __launch_bounds__(256) void k_trsv_upd_bwd(int64_t N, const double* __restrict__ L,
-                                                      double* __restrict__ x, int64_t j0,
-                                                      int nb) {
+constexpr int kBulkCols = 256;
+__global__ __launch_bounds__(kThreads) void k_trsv_bwd_step(int64_t N, const double* __restrict__ L,
+                                                            double* __restrict__ x, int64_t j0,
+                                                            int nb) {
+    __shared__ double Ls[kNb * kLd];
     __shared__ double ds[kNb];
-    __shared__ double part[kBwdGroups][kBwdCols];
-    if (threadIdx.x < kNb) ds[threadIdx.x] = threadIdx.x < nb ? x[j0 + threadIdx.x] : 0.0;
+    __shared__ double xs[kNb];
+    __shared__ double part[kThreads];
+    const int t = threadIdx.x;
+    const int64_t jm = j0 - kNb;
+    if (blockIdx.x == 0) {
+        const int c = t & (kNb - 1), g = t >> 7;       // 8 groups of 16 rows
+        double col[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            col[r] = g * 16 + r < nb ? L[(j0 + g * 16 + r) * N + jm + c] : 0.0;
+        double tri[kTriLoads];
+        load_triangle(N, L, jm, kNb, tri);
+        double xv = 0.0, dg0 = 1.0, dg1 = 1.0;
+        if (t < kNb) {
+            xv = x[jm + t];
+            ds[t] = t < nb ? x[j0 + t] : 0.0;
+        }
+        if (t < 64) {
+            dg0 = L[(jm + t) * N + jm + t];
+            dg1 = L[(jm + 64 + t) * N + jm + 64 + t];
+        }
+        store_triangle(tri, Ls);
+        __syncthreads();
+        double p = col[0] * ds[g * 16];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) p = __builtin_fma(col[r], ds[g * 16 + r], p);
+        part[g * kNb + c] = p;
+        __syncthreads();
+        if (t < kNb) {
+            double s = part[t];
+#pragma unroll
+            for (int q = 1; q < kThreads / kNb; ++q) s += part[q * kNb + t];
+            xs[t] = xv - s;
+        }
+        __syncthreads();
+        if (t >= 64) return;
+        const double rd0 = 1.0 / dg0, rd1 = 1.0 / dg1;
+        double acc0 = xs[t], acc1 = xs[64 + t];
+        solve_block<false>(Ls, rd0, rd1, acc0, acc1);
+        x[jm + t] = acc0 * rd0;
+        x[jm + 64 + t] = acc1 * rd1;
+        return;
+    }
+    if (t < kNb) ds[t] = t < nb ? x[j0 + t] : 0.0;
     __syncthreads();
-    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int64_t k = blockIdx.x * (int64_t)kBwdCols + lane;
-    const bool live = k < j0;
+    const int lane = t & (kBulkCols - 1), g = t >> 8;  // 4 groups of 32 rows
+    const int64_t k = (int64_t)(blockIdx.x - 1) * kBulkCols + lane;
+    const bool live = k < jm;
     double acc = 0.0;
     if (live) {
         const int r0 = g * kBwdRows;
         const int r1 = r0 + kBwdRows < nb ? r0 + kBwdRows : nb;
-        const double* col = L + j0 * N + k;
+        const double* colp = L + j0 * N + k;
 #pragma unroll 8
-        for (int r = r0; r < r1; ++r) acc = __builtin_fma(col[(int64_t)r * N], ds[r], acc);
+        for (int r = r0; r < r1; ++r) acc = __builtin_fma(colp[(int64_t)r * N], ds[r], acc);
     }
-    part[g][lane] = acc;
+    part[g * kBulkCols + lane] = acc;
     __syncthreads();
     if (g == 0 && live) {
-        double s = part[0][lane];
+        double s = part[lane];
 #pragma unroll
-        for (int q = 1; q < kBwdGroups; ++q) s += part[q][lane];
+        for (int q = 1; q < kBwdGroups; ++q) s += part[q * kBulkCols + lane];
         x[k] -= s;
     }
 }
@@ -169,24 +304,26 @@ inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) /
 }  // namespace
 
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s) {
-    for (int64_t j0 = 0; j0 < N; j0 += kNb) {
-        const int nb = (int)((N - j0) < kNb ? (N - j0) : kNb);
-        k_trsv_diag<true><<<1, kDiagThreads, 0, s>>>(N, L, x, j0, nb);
-        const int64_t rows = N - j0 - nb;
-        if (rows > 0) {
-            const int64_t blocks = (rows + kFwdRowsPerGroup - 1) / kFwdRowsPerGroup;
-            const unsigned grid = (unsigned)(blocks < 8192 ? blocks : 8192);
-            if (N % 2 == 0 && reinterpret_cast<uintptr_t>(L) % 16 == 0)
-                k_trsv_upd_fwd<true><<<grid, 256, 0, s>>>(N, L, x, j0);
-            else
-                k_trsv_upd_fwd<false><<<grid, 256, 0, s>>>(N, L, x, j0);
-        }
+    const bool pair = N % 2 == 0 && reinterpret_cast<uintptr_t>(L) % 16 == 0;
+    // forward: the first block alone, then one fused step per block
+    k_trsv_diag<true><<<1, kThreads, 0, s>>>(N, L, x, 0, (int)(N < kNb ? N : kNb));
+    for (int64_t j0 = 0; j0 + kNb < N; j0 += kNb) {
+        const int nb1 = (int)((N - j0 - kNb) < kNb ? (N - j0 - kNb) : kNb);
+        const int64_t rows = N - j0 - 2 * kNb;                 // bulk rows past the next block
+        int64_t blocks = rows > 0 ? (rows + kNb - 1) / kNb : 0;
+        if (blocks > 4096) blocks = 4096;
+        if (pair)
+            k_trsv_fwd_step<true><<<(unsigned)(1 + blocks), kThreads, 0, s>>>(N, L, x, j0, nb1);
+        else
+            k_trsv_fwd_step<false><<<(unsigned)(1 + blocks), kThreads, 0, s>>>(N, L, x, j0, nb1);
     }
+    // backward: the last block alone, then one fused step per block
     const int64_t last = ((N - 1) / kNb) * kNb;
-    for (int64_t j0 = last; j0 >= 0; j0 -= kNb) {
+    k_trsv_diag<false><<<1, kThreads, 0, s>>>(N, L, x, last, (int)(N - last));
+    for (int64_t j0 = last; j0 > 0; j0 -= kNb) {
         const int nb = (int)((N - j0) < kNb ? (N - j0) : kNb);
-        k_trsv_diag<false><<<1, kDiagThreads, 0, s>>>(N, L, x, j0, nb);
-        if (j0 > 0) k_trsv_upd_bwd<<<blocks_for(j0, kBwdCols), 256, 0, s>>>(N, L, x, j0, nb);
+        const int64_t cols = j0 - kNb;                         // bulk columns before the block
+        k_trsv_bwd_step<<<1 + blocks_for(cols, kBulkCols), kThreads, 0, s>>>(N, L, x, j0, nb);
     }
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;

@@ -256,11 +256,15 @@ def test_blocked_cholesky_matches_lapack(g, cuda, N):
                                          _lib.stream()), "chol")
 
 
-@pytest.mark.parametrize("N", [1, 64, 127, 128, 300, 1000, 2561])
-def test_blocked_solves_match_lapack(g, cuda, N):
-    """The blocked substitutions (128-column blocks, partial last block) against LAPACK's
-    triangular solves with the same factor: d = L^-T L^-1 gamma and E = gamma.d / 2, for a
-    well-conditioned factor (cond(L) ~ 1e2), so the two agree to a few ulp times cond."""
+@pytest.mark.parametrize("N,offset", [(1, 0), (64, 0), (127, 0), (128, 0), (129, 0), (192, 0),
+                                      (193, 0), (256, 0), (257, 0), (300, 0), (1000, 0),
+                                      (1000, 1), (2561, 0), (4096, 0)])
+def test_blocked_solves_match_lapack(g, cuda, N, offset):
+    """The blocked substitutions (128-column blocks; each step also solves the next block in two
+    64-row halves: next block of 1, 64 or 65 rows, partial last block, no rows past the next
+    block) against LAPACK's triangular solves with the same factor: d = L^-T L^-1 gamma and
+    E = gamma.d / 2, for a well-conditioned factor (cond(L) ~ 1e2), so the two agree to a few ulp
+    times cond. offset = 1 places the factor 8 bytes past a 16-byte boundary (no paired loads)."""
     from scipy.linalg import solve_triangular
     from gs_dft_amd import ri as _ri
     rng = np.random.default_rng(N)
@@ -270,8 +274,12 @@ def test_blocked_solves_match_lapack(g, cuda, N):
     gam = rng.normal(size=N)
     y = solve_triangular(Ln, gam, lower=True)
     dn = solve_triangular(Ln.T, y, lower=False)
-    print(f"[solve] N={N}", flush=True)
-    d, E = _ri._cho_solve(torch.tensor(Ln, device="cuda"), torch.tensor(gam, device="cuda"), True)
+    print(f"[solve] N={N} offset={offset}", flush=True)
+    buf = torch.empty(N * N + offset, dtype=torch.float64, device="cuda")
+    Ld = buf[offset:].view(N, N)
+    Ld.copy_(torch.tensor(Ln))
+    assert Ld.data_ptr() % 16 == 8 * offset
+    d, E = _ri._cho_solve(Ld, torch.tensor(gam, device="cuda"), True)
     err = rel_max(_np(d), dn)
     print(f"[solve] N={N} d rel-to-max {err:.2e}")
     assert err < 1e-12
