@@ -219,18 +219,30 @@ def main() -> int:
         d = np.random.default_rng(0).normal(size=N)
         rng = np.random.default_rng(1)
 
-        def run(m):
+        def run(m, chunk=None):
+            # A seeded random sample of m list entries against all aux functions, timed in
+            # chunks of at most `chunk` entries (one progress line per chunk).
             sel = np.sort(rng.choice(n, size=min(m, n), replace=False))
-            t = time.perf_counter()
-            orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sel], pj[sel], w[sel])
-            orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sel], pj[sel],
-                          w[sel], d)
-            return time.perf_counter() - t, len(sel)
+            chunk = len(sel) if chunk is None else max(1, chunk)
+            total = 0.0
+            for c0 in range(0, len(sel), chunk):
+                sc = sel[c0:c0 + chunk]
+                t = time.perf_counter()
+                orc.gamma(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sc], pj[sc],
+                          w[sc])
+                orc.gamma_vjp(s.quat, s.log_scale, s.centers, s.C, s.occ, la, ac, pi[sc], pj[sc],
+                              w[sc], d)
+                total += time.perf_counter() - t
+                if chunk < len(sel):
+                    log(f"cpu baseline: {min(c0 + chunk, len(sel))} of {len(sel)} sampled pairs, "
+                        f"{total:.1f} s")
+            return total, len(sel)
 
         probe = max(1, min(n, int(2e6 // N) + 1))
         t_probe, m_probe = run(probe)
         m = max(1, min(n, int(m_probe * args.cpu_seconds / max(t_probe, 1e-6))))
-        t_cpu, m_cpu = run(m) if m > m_probe else (t_probe, m_probe)
+        per_chunk = max(m_probe, int(m_probe * 20.0 / max(t_probe, 1e-6)))   # ~20 s per chunk
+        t_cpu, m_cpu = run(m, per_chunk) if m > m_probe else (t_probe, m_probe)
         per_pair = t_cpu / m_cpu
         cpu_step_ms = per_pair * n * 1e3
         cpu = {"value": cpu_step_ms, "unit": "ms per fwd+bwd step (three-centre gamma + reverse, "
