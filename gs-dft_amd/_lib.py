@@ -50,7 +50,7 @@ SIGNATURES = {
     "gsdft_product_aux_pairs": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _pd, _int, _vp, _vp,
                                 _vp, _sz, _vp],
     "gsdft_metric_workspace_size": [_i64, _psz],
-    "gsdft_aux_metric": [_i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp],
+    "gsdft_aux_metric": [_i64, _vp, _vp, _dbl, _dbl, _vp, _vp, _sz, _vp],
     "gsdft_cholesky": [_i64, _vp, _vp, _sz, _vp],
     "gsdft_cho_solve": [_i64, _vp, _vp, _vp, _vp, _vp],
     "gsdft_gamma_workspace_size": [_i64, _i64, _i64, _i64, _psz],
@@ -74,8 +74,8 @@ SIGNATURES = {
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_exchange_workspace_size": [_i64, _i64, _i64, _i64, _int, _int, _i64, _int, _psz],
     "gsdft_exchange": [_i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
-                       _vp, _vp, _vp, _vp, _int, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
-                       _vp],
+                       _vp, _vp, _vp, _vp, _int, _i64, _int, _dbl, _vp, _vp, _vp, _vp, _vp, _vp,
+                       _sz, _vp],
     "gsdft_grid_density_workspace_size": [_i64, _i64, _i64, _int, _int, _psz],
     "gsdft_grid_density": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp, _vp,
                            _vp, _vp, _sz, _vp],

@@ -42,6 +42,17 @@ __host__ __device__ constexpr double quad_w(int i) {
     return w[i];
 }
 
+// A quadrature table of the node integral 1/r = (2/sqrt(pi)) int_0^inf e^(-t^2 r^2) dt, passed to
+// kernels by value: the 20-node half-line rule above, or, for the long-range kernel
+// erf(omega r)/r = (2/sqrt(pi)) int_0^omega e^(-t^2 r^2) dt, Gauss-Legendre with kLrNodes nodes on
+// [0, omega] (gs_dft/integrals/dense.py:56-76 as used by gs_dft/coulomb/ri.py:231-235).
+constexpr int kLrNodes = 12;
+struct NodeTable {
+    double t[kNodes];
+    double w[kNodes];
+    int n;
+};
+
 // ------------------------------------------------------------------ fast FP64 transcendentals
 // e^x by Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2, and the degree-12 Taylor polynomial of
 // e^r in Horner form (truncation < 2e-16 relative), rescaled by ldexp. ln2 is split into the

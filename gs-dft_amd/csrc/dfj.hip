@@ -26,6 +26,7 @@
 #include <rocsolver/rocsolver.h>
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -105,6 +106,55 @@ __global__ void k_product_aux_pairs(int64_t n, const int32_t* __restrict__ pi,
     }
 }
 
+}  // namespace
+
+NodeTable coulomb_table() {
+    NodeTable tb{};
+    for (int i = 0; i < kNodes; ++i) {
+        tb.t[i] = quad_t(i);
+        tb.w[i] = quad_w(i);
+    }
+    tb.n = kNodes;
+    return tb;
+}
+
+// Gauss-Legendre on [0, omega] (gs_dft/integrals/dense.py:56-76): the roots x_i of P_12 in
+// ascending order by Newton's method on the three-term recurrence, weights 2 / ((1 - x^2) P'(x)^2),
+// then t = omega (x + 1) / 2 and w = omega w_x / 2.
+NodeTable long_range_table(double omega) {
+    NodeTable tb{};
+    const int n = kLrNodes;
+    for (int i = 0; i < n; ++i) {
+        double x = -std::cos(kPi * (i + 0.75) / (n + 0.5));
+        double dp = 1.0;
+        for (int it = 0; it < 100; ++it) {
+            double p0 = 1.0, p1 = x;
+            for (int k = 2; k <= n; ++k) {
+                const double p2 = ((2.0 * k - 1.0) * x * p1 - (k - 1.0) * p0) / k;
+                p0 = p1;
+                p1 = p2;
+            }
+            dp = n * (x * p1 - p0) / (x * x - 1.0);
+            const double dx = p1 / dp;
+            x -= dx;
+            if (std::fabs(dx) < 1e-17) break;
+        }
+        double p0 = 1.0, p1 = x;
+        for (int k = 2; k <= n; ++k) {
+            const double p2 = ((2.0 * k - 1.0) * x * p1 - (k - 1.0) * p0) / k;
+            p0 = p1;
+            p1 = p2;
+        }
+        dp = n * (x * p1 - p0) / (x * x - 1.0);
+        tb.t[i] = 0.5 * omega * (x + 1.0);
+        tb.w[i] = 0.5 * omega * (2.0 / ((1.0 - x * x) * dp * dp));
+    }
+    tb.n = n;
+    return tb;
+}
+
+namespace {
+
 // gs_dft/basis/isotropic.py:30-39: beta = e^log_alpha, KN = (2 beta / pi)^(3/4).
 __global__ void k_aux_prep(int64_t N, const double* __restrict__ log_alpha,
                            double* __restrict__ beta, double* __restrict__ kn) {
@@ -120,12 +170,14 @@ __device__ __forceinline__ double boys0(double T) {
     return 0.5 * sqrt(kPi / T) * erf(sqrt(T));
 }
 
-// gs_dft/coulomb/ri.py:63-76 (omega=None) + shift_diag. One thread per element; a block covers
-// 4 rows x 64 columns so each wave writes 64 consecutive doubles of one row.
+// gs_dft/coulomb/ri.py:63-76 + shift_diag: F0 = boys0(rho R^2) for 1/r, or, for the long-range
+// kernel erf(omega r)/r (omega > 0), sqrt(z) boys0(z rho R^2) with z = omega^2 / (omega^2 + rho).
+// One thread per element; a block covers 4 rows x 64 columns so each wave writes 64 consecutive
+// doubles of one row.
 __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restrict__ beta,
                                                 const double* __restrict__ kn,
                                                 const double* __restrict__ R, double lam,
-                                                double* __restrict__ V) {
+                                                double omega, double* __restrict__ V) {
     const int64_t q = blockIdx.x * 64 + (threadIdx.x & 63);
     const int64_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (p >= N || q >= N) return;
@@ -137,7 +189,14 @@ __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restr
     const double PQ2 = dx * dx + dy * dy + dz * dz;
     const double rho = gab / gsum;
     const double T = rho * PQ2;
-    const double coul = kTwoPi25 / (gab * sqrt(gsum)) * boys0(T);
+    double F0;
+    if (omega != 0.0) {
+        const double z = (omega * omega) / (omega * omega + rho);
+        F0 = sqrt(z) * boys0(z * T);
+    } else {
+        F0 = boys0(T);
+    }
+    const double coul = kTwoPi25 / (gab * sqrt(gsum)) * F0;
     double v = (kn[p] * kn[q]) * coul;
     if (p == q) v += lam;
     V[p * N + q] = v;
@@ -279,14 +338,17 @@ __global__ void k_pair_rec(int64_t n, const int32_t* __restrict__ pi,
     r[15] = 0.0;
 }
 
-// Node constants of one aux exponent b: s_t = t^2 b / (b + t^2), wp_t = w_t (b + t^2)^(-3/2).
-__device__ __forceinline__ void node_consts(double b, double s[kNodes], double wp[kNodes]) {
+// Node constants of one aux exponent b for the first tb.n nodes of the table:
+// s_t = t^2 b / (b + t^2), wp_t = w_t (b + t^2)^(-3/2).
+__device__ __forceinline__ void node_consts(double b, const NodeTable& tb, double s[kNodes],
+                                            double wp[kNodes]) {
 #pragma unroll
     for (int t = 0; t < kNodes; ++t) {
-        const double t2 = quad_t(t) * quad_t(t);
+        if (t >= tb.n) break;
+        const double t2 = tb.t[t] * tb.t[t];
         const double a = b + t2;
         s[t] = t2 * b / a;
-        wp[t] = quad_w(t) / (a * sqrt(a));
+        wp[t] = tb.w[t] / (a * sqrt(a));
     }
 }
 
@@ -305,8 +367,9 @@ __device__ __forceinline__ void node_consts(double b, double s[kNodes], double w
 constexpr double kSkipZ = 36.0;
 constexpr int kFirstSkip = 5;
 
+template <int kN = kNodes>
 __host__ __device__ constexpr bool screen_after(int t) {
-    return t >= kFirstSkip && t + 1 < kNodes;
+    return t >= kFirstSkip && t + 1 < kN;
 }
 
 // Lanes past the end of the work hold a centre kFarAway Bohr off (z ~ 1e40 at every node from
@@ -338,16 +401,16 @@ __device__ __forceinline__ void put_node_consts(double* o, int t, double s, doub
     o[8 + 3 * kNodes + t] = 1.0 / s;
 }
 
-// body(std::integral_constant<int, t>) for t = 0, 1, ..., kNodes - 1 until it returns true: a
-// fully unrolled node loop with early exits (node tables stay in registers). Returns the number
-// of nodes evaluated (wave-uniform).
-template <int T, class Body>
+// body(std::integral_constant<int, t>) for t = 0, 1, ..., kN - 1 until it returns true: a fully
+// unrolled node loop with early exits (node tables stay in registers). Returns the number of
+// nodes evaluated (wave-uniform).
+template <int T, int kN = kNodes, class Body>
 __device__ __forceinline__ uint32_t node_loop(Body& body) {
-    if constexpr (T < kNodes) {
+    if constexpr (T < kN) {
         if (body(std::integral_constant<int, T>{})) return T + 1;
-        return node_loop<T + 1>(body);
+        return node_loop<T + 1, kN>(body);
     } else {
-        return kNodes;
+        return kN;
     }
 }
 
@@ -520,13 +583,13 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
                                const double* __restrict__ dgamma,
-                               const double* __restrict__ dscale, int fold,
+                               const double* __restrict__ dscale, int fold, NodeTable tb,
                                double* __restrict__ out) {
     const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (p >= N) return;
     const double b = beta[p];
     double s[kNodes], wp[kNodes];
-    node_consts(b, s, wp);
+    node_consts(b, tb, s, wp);
     const int64_t slot = aux_slot(p, N, G);
     double* o = out + kAuxRec * slot;
     o[0] = R[3 * p]; o[1] = R[3 * p + 1]; o[2] = R[3 * p + 2];
@@ -542,7 +605,16 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
                       __builtin_bit_cast(uint64_t, R[3 * p + 2]));
     }
     o[4] = b; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
-    for (int t = 0; t < kNodes; ++t) put_node_consts(o, t, s[t], wp[t], fold ? u : 1.0);
+    for (int t = 0; t < kNodes; ++t) {
+        if (t < tb.n) {
+            put_node_consts(o, t, s[t], wp[t], fold ? u : 1.0);
+        } else {            // slots past the table: never read by a kernel of tb.n nodes
+            o[8 + t] = 0.0;
+            o[8 + kNodes + t] = 0.0;
+            o[8 + 2 * kNodes + t] = 0.0;
+            o[8 + 3 * kNodes + t] = 0.0;
+        }
+    }
 }
 
 // One lane per pair slot; accumulates over a slab of aux records (u = dgamma_P KN_P)
@@ -567,7 +639,7 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // later).
 constexpr int kAtomChunk = 64;
 
-template <bool kLaneU, bool kAtomF = false, bool kFold = false>
+template <bool kLaneU, bool kAtomF = false, bool kFold = false, int kN = kNodes>
 __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
@@ -675,9 +747,9 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             gs1 += G;
             gs2 = __builtin_fma(G, st, gs2);
             gs3 = __builtin_fma(G, s2, gs3);
-            return screen_after(t) && wave_all_beyond_h(v.zh);
+            return screen_after<kN>(t) && wave_all_beyond_h(v.zh);
         };
-        nodes += node_loop<0>(node);
+        nodes += node_loop<0, kN>(node);
         if constexpr (kFold) continue;
         F = (q0 == q0) ? F : q0;                 // a NaN centre propagates
         jt = __builtin_fma(u, F, jt);
@@ -1440,7 +1512,7 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
 // Bt[perm[slot] * ldb + 16 y ...] (16-byte stores when kPair: ldb even, Bt 16-byte aligned).
 constexpr int kBlockRecs = 16;
 
-template <bool kPair>
+template <bool kPair, int kN>
 __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
                                                           const double* __restrict__ rec,
                                                           const int32_t* __restrict__ perm,
@@ -1485,9 +1557,9 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeArgH v = node_arg_h(Pr, Qn);
             F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
-            return screen_after(t) && wave_all_beyond_h(v.arg);
+            return screen_after<kN>(t) && wave_all_beyond_h(v.arg);
         };
-        nodes += node_loop<0>(node);
+        nodes += node_loop<0, kN>(node);
         val[j][threadIdx.x] = (F * cf) * x[3];
     }
     count_work(work, live, nodes);
@@ -1700,7 +1772,7 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     GSDFT_HIP(hipGetLastError());
     const int64_t G = (N % M == 0) ? N / M : 1;
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, 0, w.aux);
+                                                      nullptr, 0, w.table, w.aux);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
@@ -1721,14 +1793,27 @@ int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)gy);
     const bool pair = ldb % 2 == 0 && reinterpret_cast<uintptr_t>(Bt) % 16 == 0;
     profile_begin(kProfExchBlock, s);
-    if (pair)
-        k_exch_block_pairs<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, w.pair_order.perm, W,
-                                                      w.aux + kAuxRec * q0, ldb, Bt,
-                                                      profile_work_counter(kProfExchBlock));
-    else
-        k_exch_block_pairs<false><<<grid, 256, 0, s>>>(n, w.rec_sorted, w.pair_order.perm, W,
-                                                       w.aux + kAuxRec * q0, ldb, Bt,
-                                                       profile_work_counter(kProfExchBlock));
+    unsigned long long* work = profile_work_counter(kProfExchBlock);
+    const double* aux = w.aux + kAuxRec * q0;
+    if (w.table.n == kLrNodes) {
+        if (pair)
+            k_exch_block_pairs<true, kLrNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
+                                                                    w.pair_order.perm, W, aux, ldb,
+                                                                    Bt, work);
+        else
+            k_exch_block_pairs<false, kLrNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
+                                                                     w.pair_order.perm, W, aux,
+                                                                     ldb, Bt, work);
+    } else {
+        if (pair)
+            k_exch_block_pairs<true, kNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
+                                                                  w.pair_order.perm, W, aux, ldb,
+                                                                  Bt, work);
+        else
+            k_exch_block_pairs<false, kNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
+                                                                   w.pair_order.perm, W, aux, ldb,
+                                                                   Bt, work);
+    }
     profile_end(kProfExchBlock, s);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -1740,9 +1825,15 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* T
     const Split sp = bwd_split(W, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfExchBwd, s);
-    k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab,
-                                           w.part, profile_work_counter(kProfExchBwd), Tbar, ldt,
-                                           nullptr);
+    if (w.table.n == kLrNodes)
+        k_gamma_bwd<true, false, false, kLrNodes><<<grid, 256, 0, s>>>(
+            n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab, w.part,
+            profile_work_counter(kProfExchBwd), Tbar, ldt, nullptr);
+    else
+        k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0,
+                                               sp.per_slab, w.part,
+                                               profile_work_counter(kProfExchBwd), Tbar, ldt,
+                                               nullptr);
     profile_end(kProfExchBwd, s);
     GSDFT_HIP(hipGetLastError());
     k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);
@@ -1840,10 +1931,12 @@ extern "C" int gsdft_metric_workspace_size(int64_t N, size_t* bytes) {
 }
 
 extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double* aux_centers,
-                                double lam, double* V, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+                                double lam, double omega, double* V, void* workspace,
+                                size_t workspace_bytes, void* stream) {
     if (N <= 0 || !log_alpha || !aux_centers || !V)
         return fail(GSDFT_ERR_ARG, "gsdft_aux_metric: bad arguments");
+    if (!(omega >= 0.0) || std::isinf(omega))
+        return fail(GSDFT_ERR_ARG, "gsdft_aux_metric: omega must be finite and >= 0");
     if ((N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_aux_metric: N too large");
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
@@ -1852,7 +1945,7 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     profile_begin(kProfMetric, s);
-    k_metric<<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, V);
+    k_metric<<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, V);
     profile_end(kProfMetric, s);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -2128,7 +2221,7 @@ int gamma_run(int64_t M, const double* quat, const double* log_scale, const doub
                              weight, w, s));
     const int64_t G = (N % M == 0) ? N / M : 1;          // scales per centre of a product aux
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, 0, w.aux);
+                                                      nullptr, 0, coulomb_table(), w.aux);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
@@ -2232,7 +2325,8 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     if (n > 0) {
         const int64_t G = (N % M == 0) ? N / M : 1;      // scales per centre of a product aux
         k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers,
-                                                          dgamma, dgamma_scale, 1, w.aux);
+                                                          dgamma, dgamma_scale, 1, coulomb_table(),
+                                                          w.aux);
         GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
         k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
                                                                 w.rec_sorted);

@@ -26,6 +26,8 @@
 
 #include <algorithm>
 
+#include <cmath>
+
 #include "common.h"
 #include "internal.h"
 
@@ -468,8 +470,8 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
                               const double* weight, const int32_t* row_ptr,
                               const int32_t* row_perm, const int32_t* col_ptr,
                               const int32_t* col_perm, int symmetric, int64_t aux_chunk,
-                              int recompute, double* energy, double* dquat, double* dlog_scale,
-                              double* dcenters, double* dC, void* workspace,
+                              int recompute, double omega, double* energy, double* dquat,
+                              double* dlog_scale, double* dcenters, double* dC, void* workspace,
                               size_t workspace_bytes, void* stream) {
     const bool grads = dquat != nullptr;
     if (M <= 0 || k <= 0 || N <= 0 || n < 0 || aux_chunk < 0 || !quat || !log_scale ||
@@ -477,6 +479,8 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         (n > 0 && (!pi || !pj || !row_perm)) ||
         (grads && (!dlog_scale || !dcenters || !dC || !col_ptr || (n > 0 && !col_perm))))
         return fail(GSDFT_ERR_ARG, "gsdft_exchange: bad arguments");
+    if (!(omega >= 0.0) || std::isinf(omega))
+        return fail(GSDFT_ERR_ARG, "gsdft_exchange: omega must be finite and >= 0");
     hipStream_t s = (hipStream_t)stream;
     const bool sym = symmetric != 0;
     const int64_t Pc = exch_chunk(M, k, N, n, sym, grads, aux_chunk);
@@ -484,6 +488,7 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     ExchWs w;
     GSDFT_TRY(layout_exchange(ar, M, k, N, n, sym, grads, recompute != 0, Pc, &w));
     if (!w.red) return fail(GSDFT_ERR_WORKSPACE, "gsdft_exchange: workspace too small");
+    w.tc.table = omega > 0.0 ? long_range_table(omega) : coulomb_table();
     GSDFT_TRY(exch_tc_prologue(M, quat, log_scale, centers, N, log_alpha, aux_centers, n, pi, pj,
                                weight, grads, w.tc, s));
     if (n == 0) {                       // D = 0: E_K = 0 and every gradient vanishes

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "../../include/gsdft.h"
+#include "common.h"
 
 namespace gsdft {
 
@@ -98,7 +99,11 @@ struct ExchTcWs {
     double *rec_sorted, *aux, *part, *acc, *J, *contrib;
     int32_t* inv_perm;
     PairOrderWs pair_order;
+    NodeTable table;        // the kernel's node rule (set after exch_tc_layout)
 };
+// The node rule of the 1/r kernel and of the long-range erf(omega r)/r kernel (omega > 0).
+NodeTable coulomb_table();
+NodeTable long_range_table(double omega);
 int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
                    ExchTcWs* w);
 int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,

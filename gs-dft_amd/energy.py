@@ -56,8 +56,9 @@ def train_pad_to(screen: Pairlist, n0: int, n_devices: int = 1) -> int:
 class SplatDFJ:
     """The two-electron energy of a splat model through ``coulomb=df()`` (or ``exact()``) and
     ``screen=pairlist(...)``: E_J, plus hf_coeff * E_K for a hybrid ``xc`` (an object with
-    ``exact_exchange_fraction`` or ``hf_coeff``; gs_dft/ks/energy.py:400-410 adds the same
-    term to the total)."""
+    ``exact_exchange_fraction`` or ``hf_coeff``) and hf_coeff_lr * E_K[erf(omega r)/r] for a
+    range-separated one (``hf_coeff_lr``, ``omega``); gs_dft/ks/energy.py:400-410 adds the same
+    terms to the total."""
 
     def __init__(self, *, coulomb: DFSpec | ExactSpec | None = None,
                  screen: Pairlist | None = None, xc=None, mesh=None):
@@ -72,6 +73,8 @@ class SplatDFJ:
         self.screen = screen
         self.coulomb = _make_coulomb(spec, screened=True,
                                      a_x=hf_coeff(xc) if xc is not None else 0.0,
+                                     a_x_lr=float(getattr(xc, "hf_coeff_lr", 0.0) or 0.0),
+                                     omega=float(getattr(xc, "omega", 0.0) or 0.0),
                                      skip_pad=bool(screen.skip_pad))
         if screen.unique and self.coulomb.hf_coeff != 0.0:
             raise ValueError("pairlist(unique=True) is PBE-class only: the screened RI-K "
@@ -88,7 +91,8 @@ class SplatDFJ:
             if state.aux is None:
                 raise ValueError("coulomb=df() needs the frozen product aux: "
                                  "pass the refresh state -- see refresh(ks, basis).")
-            if self.coulomb.hf_coeff != 0.0 and state.aux_K is None:
+            if ((self.coulomb.hf_coeff != 0.0 or self.coulomb.hf_coeff_lr != 0.0)
+                    and state.aux_K is None):
                 raise ValueError("hybrid df() needs the K-aux: pass the refresh state "
                                  "(state.aux_K) -- see refresh(ks, basis).")
 
@@ -96,9 +100,13 @@ class SplatDFJ:
         state = SplatState() if state is None else state
         self._check_state(state)
         e_j, e_k = self.coulomb.energy(model.basis, model.C, None, model.occupations, state)
+        e = e_j
         if self.coulomb.hf_coeff != 0.0:
-            return e_j + self.coulomb.hf_coeff * e_k
-        return e_j
+            e = e + self.coulomb.hf_coeff * e_k
+        if self.coulomb.hf_coeff_lr != 0.0:     # gs_dft/ks/energy.py:330,406-408
+            e = e + self.coulomb.hf_coeff_lr * self.coulomb.energy_lr(
+                model.basis, model.C, None, model.occupations, state)
+        return e
 
 
 def refresh(ks, basis: Splat, *, pad_to: int | None = None,
@@ -123,7 +131,7 @@ def refresh(ks, basis: Splat, *, pad_to: int | None = None,
     if isinstance(coul, ScreenedProductDFCoulomb) or type(coul).__name__ in (
             "ScreenedProductDFCoulomb", "ProductDFCoulomb"):
         aux = init_product_aux(basis, scales=coul.scales, diagonal_only=coul.diagonal)
-        if getattr(coul, "hf_coeff", 0.0) != 0.0:
+        if getattr(coul, "hf_coeff", 0.0) != 0.0 or getattr(coul, "hf_coeff_lr", 0.0) != 0.0:
             aux_K = aux
         cholV = _cdf.aux_cholesky(aux, coul.lam)
     return SplatState(pairs=pairs, aux=aux, aux_K=aux_K, cholV=cholV, pair_index=index)

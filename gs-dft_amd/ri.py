@@ -18,19 +18,27 @@ from .screening import PairIndex, build_pair_index, live_length
 
 # ------------------------------------------------------------------------------------ metric
 
+def _omega(omega) -> float:
+    """The reference's ``omega`` argument as the library's: None / 0 select the 1/r kernel, a
+    positive value the long-range kernel erf(omega r)/r."""
+    w = 0.0 if not omega else float(omega)
+    if not (w >= 0.0) or w == float("inf"):
+        raise ValueError(f"omega must be a finite number >= 0 (or None), got {omega!r}")
+    return w
+
+
 def aux_metric(aux: IsotropicSplat, omega=None, *, lam: float = 0.0) -> torch.Tensor:
-    """V_PQ = (P|Q) (gs_dft/coulomb/ri.py:267-275); ``lam`` is added to the diagonal in the same
-    kernel (the reference's ``shift_diag``)."""
-    if omega:
-        raise NotImplementedError("aux_metric(omega=...): the range-separated (erf) metric of "
-                                  "long-range exchange is not implemented")
+    """V_PQ = (P|Q) (gs_dft/coulomb/ri.py:267-275), with the kernel erf(omega r)/r when ``omega``
+    is given (ri.py:70-72); ``lam`` is added to the diagonal in the same kernel (the reference's
+    ``shift_diag``)."""
+    w = _omega(omega)
     N = aux.n_basis
     dev = aux.log_alpha.device
     V = torch.empty((N, N), dtype=torch.float64, device=dev)
     L = _lib.lib()
     ws = _lib.workspace(_lib.size_query(L.gsdft_metric_workspace_size, N), dev)
     _lib.check(L.gsdft_aux_metric(N, _lib.ptr(aux.log_alpha), _lib.ptr(aux.centers), float(lam),
-                                  _lib.ptr(V), _lib.ptr(ws), ws.numel(), _lib.stream()),
+                                  w, _lib.ptr(V), _lib.ptr(ws), ws.numel(), _lib.stream()),
                "gsdft_aux_metric")
     return V
 
@@ -43,8 +51,8 @@ def shift_diag(V: torch.Tensor, lam: float) -> torch.Tensor:
 
 
 def aux_cholesky(aux: IsotropicSplat, lam: float, omega=None) -> torch.Tensor:
-    """Lower Cholesky factor of V + lam I (gs_dft/coulomb/ri.py:253-264), factored in place in
-    the metric's own buffer."""
+    """Lower Cholesky factor of V + lam I (gs_dft/coulomb/ri.py:253-264), V the metric of the
+    kernel ``omega`` selects, factored in place in the metric's own buffer."""
     V = aux_metric(aux, omega, lam=lam)
     N = V.shape[0]
     Lb = _lib.lib()
@@ -256,7 +264,7 @@ def _list_symmetric(M: int, pi: torch.Tensor, pj: torch.Tensor, w: torch.Tensor,
 
 class _ExchangeInputs:
     def __init__(self, splats: Splat, C_occ, aux: IsotropicSplat, pi, pj, valid, L, index,
-                 aux_chunk: int, recompute: bool):
+                 aux_chunk: int, recompute: bool, omega: float = 0.0):
         dev = _lib.device()
         self.M = splats.n_basis
         self.quat, self.log_scale, self.centers = splats.quat, splats.log_scale, splats.centers
@@ -292,6 +300,7 @@ class _ExchangeInputs:
         self.symmetric = _list_symmetric(self.M, self.pi, self.pj, self.w, self.n)
         self.aux_chunk = int(aux_chunk)
         self.recompute = int(bool(recompute))
+        self.omega = float(omega)
 
 
 def _exchange(x: _ExchangeInputs, grads: bool):
@@ -312,7 +321,8 @@ def _exchange(x: _ExchangeInputs, grads: bool):
                                  _lib.ptr(x.L), x.n, _lib.ptr(x.pi), _lib.ptr(x.pj),
                                  _lib.ptr(x.w), _lib.ptr(idx.row_ptr), _lib.ptr(idx.row_perm),
                                  _lib.ptr(idx.col_ptr), _lib.ptr(idx.col_perm),
-                                 int(x.symmetric), x.aux_chunk, x.recompute, _lib.ptr(E),
+                                 int(x.symmetric), x.aux_chunk, x.recompute, x.omega,
+                                 _lib.ptr(E),
                                  *[_lib.ptr(t) for t in out], _lib.ptr(ws), ws.numel(),
                                  _lib.stream()), "df_exchange_energy_screened")
     return (E, *out)
@@ -351,12 +361,12 @@ def df_exchange_energy_screened(splats: Splat, C_occ, aux: IsotropicSplat, pi, p
     reference's memory and do not change its value; ``aux_chunk`` (aux functions per pass,
     0 = automatic) and ``recompute`` (recompute the forward's (M, N, k) products in the reverse
     instead of keeping them) are this library's memory knobs, likewise without effect on the
-    value. ``cholV`` = the Cholesky factor of V + lam I for this ``aux`` (built here when
-    absent)."""
+    value. ``omega`` (> 0) evaluates the long-range exchange E_K[erf(omega r)/r] of range-separated
+    hybrids (ri.py:534-544 with omega): the three-centre integrals take the 12-node rule on
+    [0, omega] and the metric the erf kernel. ``cholV`` = the Cholesky factor of V + lam I for
+    this ``aux`` and this ``omega`` (built here when absent)."""
     del chunk, occ_chunk
-    if omega:
-        raise NotImplementedError("df_exchange_energy_screened(omega=...): the range-separated "
-                                  "(long-range erf) exchange is not implemented")
-    L = aux_cholesky(aux, lam) if cholV is None else cholV
-    x = _ExchangeInputs(splats, C_occ, aux, pi, pj, valid, L, index, aux_chunk, recompute)
+    w = _omega(omega)
+    L = aux_cholesky(aux, lam, w) if cholV is None else cholV
+    x = _ExchangeInputs(splats, C_occ, aux, pi, pj, valid, L, index, aux_chunk, recompute, w)
     return _ExchangeFn.apply(x.quat, x.log_scale, x.centers, x.C, x)

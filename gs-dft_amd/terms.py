@@ -88,7 +88,8 @@ class CoulombTerm(abc.ABC):
 class ScreenedProductDFCoulomb(CoulombTerm):
     """Frozen pair-product RI-J / RI-K over the significant pairs (gs_dft/ks/terms.py:236-264).
     E_K (unscaled) is evaluated when ``hf_coeff`` != 0, on the K-aux ``state.aux_K``; the
-    long-range (erf) exchange of range-separated hybrids is not implemented."""
+    long-range exchange E_K[erf(omega r)/r] of range-separated hybrids when ``hf_coeff_lr`` != 0
+    (``energy_lr``)."""
 
     hf_coeff: float = 0.0
     hf_coeff_lr: float = 0.0
@@ -116,10 +117,14 @@ class ScreenedProductDFCoulomb(CoulombTerm):
         return e_j, e_k
 
     def energy_lr(self, basis, C_orth, P, occ, state):
+        """Unscaled E_K[erf(omega r)/r] on ``state.aux_K`` (gs_dft/ks/terms.py:258-264); the erf
+        metric's factor is formed here, as the reference forms its metric inside the call."""
         if self.hf_coeff_lr == 0.0:
             return torch.zeros((), dtype=torch.float64, device=C_orth.device)
-        raise NotImplementedError("the long-range (erf) screened exchange of range-separated "
-                                  "hybrids (gs_dft/ks/terms.py:258-264) is not implemented")
+        pi, pj, valid = state.pairs
+        return _cdf.df_exchange_energy_screened(
+            basis, C_orth, state.aux_K, pi, pj, lam=self.lam, chunk=self.chunk, valid=valid,
+            omega=self.omega, index=getattr(state, "pair_index", None))
 
 
 @dataclass(frozen=True)
@@ -152,9 +157,6 @@ def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
         if not screened:
             raise NotImplementedError("dense (unscreened) DF is not part of this library; pass "
                                       "screen=pairlist(eps=-1.0) for the full pair list")
-        if a_x_lr != 0.0:
-            raise NotImplementedError("range-separated hybrids (hf_coeff_lr != 0) need the "
-                                      "long-range erf exchange, which is not implemented")
         return ScreenedProductDFCoulomb(hf_coeff=a_x, hf_coeff_lr=a_x_lr, omega=omega,
                                         lam=spec.lam, chunk=spec.chunk, scales=spec.scales,
                                         diagonal=spec.diagonal, skip_pad=bool(skip_pad))

@@ -117,10 +117,13 @@ int gsdft_product_aux_pairs(int64_t M, const double* quat, const double* log_sca
 /* Workspace for gsdft_aux_metric and gsdft_cholesky. */
 int gsdft_metric_workspace_size(int64_t N, size_t* bytes);
 
-/* V_PQ = (P|Q) with lam added to the diagonal. Replaces aux_metric / coulomb_block /
- * _coulomb_rows (+ shift_diag), gs_dft/coulomb/ri.py:63-123,243-250,267-275. */
+/* V_PQ = (P|Q) with lam added to the diagonal: the 1/r kernel for omega = 0, the long-range
+ * kernel erf(omega r)/r for omega > 0 (ri.py:70-72); omega < 0, NaN or inf is refused. Replaces
+ * aux_metric / coulomb_block / _coulomb_rows (+ shift_diag),
+ * gs_dft/coulomb/ri.py:63-123,243-250,267-275. */
 int gsdft_aux_metric(int64_t N, const double* log_alpha, const double* aux_centers, double lam,
-                     double* V, void* workspace, size_t workspace_bytes, void* stream);
+                     double omega, double* V, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* In-place lower Cholesky of V (row-major), strict upper triangle zeroed. Synchronises the stream
  * to read the factorisation status. Replaces _chol_donated / aux_cholesky,
@@ -263,8 +266,12 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
  * functions per pass (0: the library's choice; the result does not depend on it beyond
  * round-off). With gradients the forward keeps its (M, N, k) products for the reverse when they
  * fit in 32 GiB; recompute = 1 forgoes that and recomputes them (less memory, more time), the
- * role the reference's occ_chunk knob plays for its memory. Writes energy (one device double);
- * with non-null dquat also dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
+ * role the reference's occ_chunk knob plays for its memory. omega = 0 is exchange with 1/r;
+ * omega > 0 is the long-range exchange E_K[erf(omega r)/r] of range-separated hybrids
+ * (gs_dft/ks/terms.py:258-264): the three-centre integrals then use the 12-node Gauss-Legendre rule
+ * on [0, omega] (ri.py:231-235) and chol must factor the erf metric (gsdft_aux_metric with the
+ * same omega). Writes energy (one device double); with non-null dquat also
+ * dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
 int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, int symmetric,
                                   int grads, int64_t aux_chunk, int recompute, size_t* bytes);
 int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const double* centers,
@@ -272,8 +279,8 @@ int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const
                    const double* aux_centers, const double* chol, int64_t n, const int32_t* pi,
                    const int32_t* pj, const double* weight, const int32_t* row_ptr,
                    const int32_t* row_perm, const int32_t* col_ptr, const int32_t* col_perm,
-                   int symmetric, int64_t aux_chunk, int recompute, double* energy,
-                   double* dquat,
+                   int symmetric, int64_t aux_chunk, int recompute, double omega,
+                   double* energy, double* dquat,
                    double* dlog_scale, double* dcenters, double* dC, void* workspace,
                    size_t workspace_bytes, void* stream);
 

@@ -473,21 +473,29 @@ double orc_boys0(double T) {
 }
 
 /* gs_dft/coulomb/ri.py:63-76 (omega=None) for one (row, col) element. */
+/* gs_dft/coulomb/ri.py:63-76: 1/r for omega = 0; erf(omega r)/r otherwise (ri.py:70-72:
+ * z = omega^2 / (omega^2 + rho), F0 = sqrt(z) boys0(z T)). */
 static double metric_one(double g1, const double* P1, double KN1, double g2, const double* P2,
-                         double KN2) {
+                         double KN2, double omega) {
     double gab = g1 * g2;
     double gsum = g1 + g2;
     double dx = P1[0] - P2[0], dy = P1[1] - P2[1], dz = P1[2] - P2[2];
     double PQ2 = dx * dx + dy * dy + dz * dz;
     double rho = gab / gsum;
     double T = rho * PQ2;
-    double F0 = orc_boys0(T);
+    double F0;
+    if (omega != 0.0) {
+        double z = (omega * omega) / (omega * omega + rho);
+        F0 = sqrt(z) * orc_boys0(z * T);
+    } else {
+        F0 = orc_boys0(T);
+    }
     double coul = (2.0 * pow(M_PI, 2.5)) / (gab * sqrt(gsum)) * F0;
     return (KN1 * KN2) * coul;
 }
 
 void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, double lam,
-                    double* V) {
+                    double omega, double* V) {
     double* beta = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
     double* KN = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
     for (int64_t p = 0; p < N; ++p) {          /* gs_dft/basis/isotropic.py:30-39 */
@@ -497,7 +505,8 @@ void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, d
 #pragma omp parallel for schedule(static)
     for (int64_t p = 0; p < N; ++p)
         for (int64_t q = 0; q < N; ++q)
-            V[p * N + q] = metric_one(beta[p], centers + 3 * p, KN[p], beta[q], centers + 3 * q, KN[q]);
+            V[p * N + q] = metric_one(beta[p], centers + 3 * p, KN[p], beta[q], centers + 3 * q,
+                                      KN[q], omega);
     if (lam != 0.0)
         for (int64_t p = 0; p < N; ++p) V[p * N + p] += lam;   /* ri.py:243-250 */
     free(beta);

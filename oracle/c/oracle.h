@@ -77,9 +77,10 @@ void orc_product_aux_pairs(int64_t M, const double* quat, const double* log_scal
                            const int32_t* pj, const double* valid, const double* scales,
                            int n_scales, double* log_alpha, double* aux_centers);
 
-/* gs_dft/coulomb/ri.py:63-76,267-275 (+ shift_diag :243-250 when lam != 0) -- metric V (N,N). */
+/* gs_dft/coulomb/ri.py:63-76,267-275 (+ shift_diag :243-250 when lam != 0) -- metric V (N,N);
+ * omega != 0 selects the kernel erf(omega r)/r (ri.py:70-72). */
 void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, double lam,
-                    double* V);
+                    double omega, double* V);
 
 /* Boys F0 used by the metric: 0.5*sqrt(pi/T)*erf(sqrt(T)), series below 1e-12. */
 double orc_boys0(double T);

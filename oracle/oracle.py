@@ -5,6 +5,7 @@ The shipped package never imports this module.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import pathlib
@@ -69,6 +70,34 @@ def reference_quad_table(n: int = 20):
     t = np.ascontiguousarray(s / (1.0 - s), dtype=np.float64)
     w = np.ascontiguousarray((wl / 2.0) * (1.0 / (1.0 - s) ** 2), dtype=np.float64)
     return t, w
+
+
+def lr_quad_table(omega: float, n: int = 12):
+    """gs_dft/integrals/dense.py:56-76 (_gauss_legendre_segment, as ri.py:231-235 calls it):
+    numpy leggauss(n) mapped to [0, omega], the rule of the long-range kernel erf(omega r)/r."""
+    x, wl = np.polynomial.legendre.leggauss(n)
+    t = np.ascontiguousarray(0.5 * float(omega) * (x + 1.0), dtype=np.float64)
+    w = np.ascontiguousarray(0.5 * float(omega) * wl, dtype=np.float64)
+    return t, w
+
+
+@contextlib.contextmanager
+def node_rule(t, w):
+    """Every three-centre routine integrates with the rule (t, w) (at most 20 nodes) inside the
+    block: the table is padded with zero-weight nodes at t = 0, which add exactly 0 to every node
+    sum and its derivatives; the reference's 20-node table is restored on exit."""
+    t, w = np.asarray(t, dtype=np.float64), np.asarray(w, dtype=np.float64)
+    if t.shape != w.shape or t.ndim != 1 or len(t) > 20:
+        raise ValueError("node_rule: t and w must be 1-D of the same length <= 20")
+    tp, wp = np.zeros(20), np.zeros(20)
+    tp[:len(t)], wp[:len(w)] = t, w
+    L = lib()
+    L.orc_set_quad_table(_d(tp), _d(wp))
+    try:
+        yield
+    finally:
+        tr, wr = reference_quad_table(20)
+        L.orc_set_quad_table(_d(tr), _d(wr))
 
 
 def num_threads() -> int:
@@ -204,11 +233,13 @@ def boys0(T: float) -> float:
     return float(lib().orc_boys0(float(T)))
 
 
-def aux_metric(log_alpha, centers, lam=0.0):
+def aux_metric(log_alpha, centers, lam=0.0, omega=0.0):
+    """gs_dft/coulomb/ri.py:63-76,267-275 (+ shift_diag); omega != 0: the erf(omega r)/r metric."""
     la, cen = _f64(log_alpha), _f64(centers)
     N = la.shape[0]
     V = np.empty((N, N))
-    lib().orc_aux_metric(_i64(N), _d(la), _d(cen), ctypes.c_double(lam), _d(V))
+    lib().orc_aux_metric(_i64(N), _d(la), _d(cen), ctypes.c_double(lam), ctypes.c_double(omega),
+                         _d(V))
     return V
 
 
@@ -330,18 +361,25 @@ def exact_coulomb(quat, log_scale, centers, C, occ, pi, pj, weight):
     return float(E), J
 
 
-def exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers, pi, pj, valid, lam):
+def exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers, pi, pj, valid, lam,
+                    omega=0.0):
     """Screened RI-K energy following gs_dft/coulomb/ri.py:497-544:
     D[P,o,o'] = sum over the valid listed pairs (i, k) of C_io C_ko' (P|ik) (``valid`` read as a
     mask, ri.py:529), M = sum_oo' D[P,o,o'] D[Q,o,o'] (ri.py:532), and
-    E_K = -tr(solve(V + lam I, M)) with a dense solve (ri.py:544). Returns (E_K, D)."""
+    E_K = -tr(solve(V + lam I, M)) with a dense solve (ri.py:544). omega != 0: the long-range
+    exchange, (P|ik) with the rule lr_quad_table(omega) (ri.py:149,231-235) and V the erf metric
+    (ri.py:543). Returns (E_K, D)."""
     C = _f64(C)
     pi_, pj_ = np.asarray(pi, dtype=np.int64), np.asarray(pj, dtype=np.int64)
-    B = three_center_block(quat, log_scale, centers, log_alpha, aux_centers, pi, pj)
+    if omega:
+        with node_rule(*lr_quad_table(omega)):
+            B = three_center_block(quat, log_scale, centers, log_alpha, aux_centers, pi, pj)
+    else:
+        B = three_center_block(quat, log_scale, centers, log_alpha, aux_centers, pi, pj)
     m = (np.asarray(valid) != 0).astype(np.float64)
     D = np.einsum("Ap,po,pq->Aoq", B, C[pi_] * m[:, None], C[pj_], optimize=True)
     Mmat = np.einsum("Aoq,Boq->AB", D, D, optimize=True)
-    V = aux_metric(log_alpha, aux_centers, lam)
+    V = aux_metric(log_alpha, aux_centers, lam, omega)
     return -float(np.trace(np.linalg.solve(V, Mmat))), D
 
 

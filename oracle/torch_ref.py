@@ -121,14 +121,18 @@ def boys0(T):
     return torch.where(T < 1e-12, 1.0 - T / 3.0, big)
 
 
-def coulomb_block(g1, P1, KN1, g2, P2, KN2):
-    """gs_dft/coulomb/ri.py:63-76 (omega=None)"""
+def coulomb_block(g1, P1, KN1, g2, P2, KN2, omega=None):
+    """gs_dft/coulomb/ri.py:63-76"""
     gab = g1[:, None] * g2[None, :]
     gsum = g1[:, None] + g2[None, :]
     PQ2 = torch.sum((P1[:, None, :] - P2[None, :, :]) ** 2, dim=-1)
     rho = gab / gsum
     T = rho * PQ2
-    F0 = boys0(T)
+    if omega:
+        z = (omega ** 2) / (omega ** 2 + rho)
+        F0 = torch.sqrt(z) * boys0(z * T)
+    else:
+        F0 = boys0(T)
     coulomb = 2.0 * PI ** 2.5 / (gab * torch.sqrt(gsum)) * F0
     return (KN1[:, None] * KN2[None, :]) * coulomb
 
@@ -139,9 +143,10 @@ def aux_quantities(log_alpha, centers):
     return beta, centers, (2.0 * beta / PI) ** 0.75
 
 
-def aux_metric(log_alpha, centers):
+def aux_metric(log_alpha, centers, omega=None):
+    """gs_dft/coulomb/ri.py:267-275"""
     b, R, n = aux_quantities(log_alpha, centers)
-    return coulomb_block(b, R, n, b, R, n)
+    return coulomb_block(b, R, n, b, R, n, omega)
 
 
 def isobra_nodes(beta, dp2, Lam, table=None):
@@ -190,10 +195,12 @@ def gamma_screened(quat, log_scale, centers, C, occ, log_alpha, aux_centers, pi,
 
 
 def screened_exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers, pi, pj, valid,
-                             lam, chunk=2048, occ_chunk=16, table=None):
+                             lam, chunk=2048, occ_chunk=16, table=None, omega=None):
     """gs_dft/coulomb/ri.py:497-544 as written: per occupied chunk, the pair stream builds
     D[:, chunk, :] (ri.py:524-531) and M += D D^T (ri.py:532); E_K = -tr(solve(V + lam I, M)).
-    ``table`` replaces the 20-node rule of the three-centre block (for limit checks)."""
+    ``table`` replaces the 20-node rule of the three-centre block (for limit checks); ``omega``
+    selects the erf metric (ri.py:543) -- the long-range exchange passes the segment rule on
+    [0, omega] as ``table`` together with it."""
     A, N = splat_A(quat, log_scale), splat_norm(log_scale)
     aux_q = aux_quantities(log_alpha, aux_centers)
     Na, n_occ, n = log_alpha.shape[0], C.shape[1], pi.shape[0]
@@ -208,7 +215,7 @@ def screened_exchange_energy(quat, log_scale, centers, C, log_alpha, aux_centers
             Ci = torch.where(cv[:, None], C[ci][:, o0:o1], torch.zeros((), dtype=torch.float64))
             D = D + torch.einsum("Ap,po,pq->Aoq", block, Ci, C[cj])
         Mmat = Mmat + torch.einsum("Aoq,Boq->AB", D, D)
-    V = aux_metric(log_alpha, aux_centers)
+    V = aux_metric(log_alpha, aux_centers, omega)
     Vs = V + lam * torch.eye(Na, dtype=torch.float64)
     return -torch.trace(torch.linalg.solve(Vs, Mmat))
 

@@ -74,6 +74,113 @@ def test_exchange_matches_oracle_and_autograd(g, wl, orc, tr, cuda, masked, k, a
         assert e < REL_G
 
 
+def _lr_tolerance(cond):
+    """Relative bound on E_K[erf(omega r)/r] between two correct evaluations: the erf metric is
+    ill-conditioned (cond(V + lam I) ~ 1e9 at lam = 1e-8), and E_K inherits ~cond x eps from
+    round-off in V and M (the oracle and the torch literal differ by 1.6e-17 to 8.6e-17 x cond)."""
+    return max(1e-12, 1e-15 * cond)
+
+
+def test_long_range_metric_matches_oracle(g, wl, orc, cuda):
+    """The erf(omega r)/r metric (gs_dft/coulomb/ri.py:70-72) on the water octamer's product aux
+    against the oracle; omega < 0 is refused."""
+    s = wl.make_system(2)
+    aux = g.init_product_aux(_basis(g, s, grad=False), scales=s.scales)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    for om in (0.11, 0.3):
+        V = _np(g.aux_metric(aux, om, lam=1e-8))
+        Vo = orc.aux_metric(la, ac, 1e-8, om)
+        err = np.max(np.abs(V - Vo) / np.abs(Vo))
+        print(f"[exchange] erf metric omega={om} N={len(la)} rel {err:.2e}")
+        assert err < 1e-13
+        assert np.array_equal(V, V.T)
+    with pytest.raises(ValueError, match="omega"):
+        g.aux_metric(aux, -0.3)
+
+
+@pytest.mark.parametrize("om,lam,masked", [(0.3, 1e-2, False), (0.3, 1e-8, True),
+                                           (0.11, 1e-2, True), (0.11, 1e-8, False)])
+def test_long_range_exchange_matches_oracle_and_autograd(g, wl, orc, tr, cuda, om, lam, masked):
+    """E_K[erf(omega r)/r] of range-separated hybrids (ri.py:534-544 with omega; the 12-node rule
+    on [0, omega], ri.py:231-235) against the oracle and the gradients against autograd of the
+    torch literal under the same rule; the bars scale with cond(V_omega + lam I), which at
+    lam = 1e-2 keeps them at the 1e-10 / 1e-9 of the 1/r exchange."""
+    k = 4
+    s = wl.make_small(30, k, n_atoms=3, seed=31)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    w = w.astype(np.float64)
+    if masked:
+        w = w * (np.random.default_rng(7).uniform(size=w.shape) > 0.15)
+    cond = np.linalg.cond(orc.aux_metric(la, ac, lam, om))
+    tol_e = _lr_tolerance(cond)
+    tol_g = max(REL_G, 1e-14 * cond)
+    print(f"[exchange-lr] M={s.M} k={k} N={len(la)} n={len(pi)} omega={om} lam={lam} "
+          f"masked={masked} cond {cond:.2e}", flush=True)
+    basis, C = _basis(g, s), _cu(s.C, True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    E = g.df_exchange_energy_screened(basis, C, aux, torch.tensor(pi, device="cuda"),
+                                      torch.tensor(pj, device="cuda"), lam=lam,
+                                      valid=torch.tensor(w, device="cuda"), omega=om)
+    Eo, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, w, lam,
+                                omega=om)
+    err = abs(E.item() - Eo) / abs(Eo)
+    print(f"[exchange-lr] E_K {E.item():.15e} oracle {Eo:.15e} rel {err:.2e} (bar {tol_e:.1e})")
+    assert err < tol_e
+    E.backward()
+    t, wq = orc.lr_quad_table(om)
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*leaves, _t(la), _t(ac), _idx(pi), _idx(pj), _t(w), lam,
+                                     table=([float(v) for v in t], [float(v) for v in wq]),
+                                     omega=om)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"),
+                          (basis.quat, basis.log_scale, basis.centers, C), leaves):
+        e = rel_max(_np(a.grad), b.grad.numpy())
+        print(f"[exchange-lr] d{name} rel-to-max {e:.2e} (bar {tol_g:.1e})")
+        assert e < tol_g
+
+
+def test_long_range_plugin_energy(g, wl, cuda):
+    """SplatDFJ with a range-separated xc (hf_coeff, hf_coeff_lr, omega) evaluates
+    E_J + a E_K + b E_K[erf(omega r)/r] (gs_dft/ks/terms.py:258-264, gs_dft/ks/energy.py:330,
+    406-408); a purely long-range xc (hf_coeff = 0) still gets its K-aux from refresh."""
+
+    class RangeSeparated:
+        hf_coeff = 0.19
+        hf_coeff_lr = 0.46
+        omega = 0.33
+
+    class LongRangeOnly:
+        hf_coeff = 0.0
+        hf_coeff_lr = 1.0
+        omega = 0.4
+
+    s = wl.make_small(40, 5, n_atoms=4, seed=9)
+    basis, C = _basis(g, s), _cu(s.C, True)
+    occ = torch.tensor(s.occ, device="cuda")
+    for xc in (RangeSeparated(), LongRangeOnly()):
+        ks = g.SplatDFJ(coulomb=g.df(scales=s.scales), screen=g.pairlist(1e-7), xc=xc)
+        state = g.refresh(ks, basis)
+        assert state.aux_K is state.aux
+        model = g.SplatModel(basis=basis, C=C, occupations=occ)
+        E = ks(model, state)
+        pi, pj, valid = state.pairs
+        with torch.no_grad():
+            EJ = g.df_coulomb_energy_screened(basis, C, occ, state.aux, pi, pj, valid=valid,
+                                              cholV=state.cholV)
+            EK = g.df_exchange_energy_screened(basis, C, state.aux, pi, pj, valid=valid)
+            ELR = g.df_exchange_energy_screened(basis, C, state.aux, pi, pj, valid=valid,
+                                                omega=xc.omega)
+        ref = EJ.item() + xc.hf_coeff * EK.item() + xc.hf_coeff_lr * ELR.item()
+        print(f"[exchange-lr] plugin E {E.item():.15e} = E_J {EJ.item():.6e} + "
+              f"{xc.hf_coeff} E_K {EK.item():.6e} + {xc.hf_coeff_lr} E_K^lr {ELR.item():.6e}")
+        assert abs(E.item() - ref) < 1e-12 * abs(E.item())
+        C.grad = None
+        E.backward()
+        assert torch.isfinite(C.grad).all() and torch.isfinite(basis.centers.grad).all()
+
+
 def test_exchange_plugin_hybrid_and_state(g, wl, cuda):
     """SplatDFJ with a hybrid xc evaluates E_J + a_x E_K through refresh's K-aux and factor
     (gs_dft/ks/terms.py:245-256, gs_dft/ks/energy.py:400-410, 454-473)."""

@@ -20,8 +20,9 @@ def test_pairlist_defaults(g):
 
 def test_make_coulomb_resolves_the_screened_strategies(g):
     """gs_dft/ks/terms.py:273-301: df() and exact() with a screen resolve to their screened terms
-    (exact() with the reference's default chunk 128), df() with a hybrid carries its a_x; the
-    dense strategies, hybrids on the exact path and range-separated exchange raise."""
+    (exact() with the reference's default chunk 128), df() with a hybrid carries its a_x and a
+    range-separated one its a_x_lr and omega; the dense strategies and hybrids on the exact path
+    raise."""
     from gs_dft_amd.terms import _make_coulomb
     t = _make_coulomb(g.df(lam=1e-6), screened=True, skip_pad=True)
     assert isinstance(t, g.ScreenedProductDFCoulomb) and t.lam == 1e-6 and t.skip_pad
@@ -38,15 +39,16 @@ def test_make_coulomb_resolves_the_screened_strategies(g):
         _make_coulomb(g.exact(), screened=True, a_x_lr=0.5)
     hyb = _make_coulomb(g.df(), screened=True, a_x=0.25)
     assert isinstance(hyb, g.ScreenedProductDFCoulomb) and hyb.hf_coeff == 0.25
-    with pytest.raises(NotImplementedError):
-        _make_coulomb(g.df(), screened=True, a_x=0.25, a_x_lr=0.5)
+    rsh = _make_coulomb(g.df(), screened=True, a_x=0.25, a_x_lr=0.5, omega=0.3)
+    assert (rsh.hf_coeff, rsh.hf_coeff_lr, rsh.omega) == (0.25, 0.5, 0.3)
     with pytest.raises(TypeError):
         _make_coulomb("df", screened=True)
 
 
 def test_hybrid_checks_mirror_the_reference(g):
     """gs_dft/ks/energy.py:240-241 (unique lists are PBE-class only), 283-285 (hybrid df() needs
-    state.aux_K); the omega (long-range) exchange is not implemented and says so."""
+    state.aux_K, here also for a purely long-range xc); a negative or infinite omega is refused
+    before any device work."""
 
     class Hybrid:
         exact_exchange_fraction = 0.25
@@ -57,8 +59,18 @@ def test_hybrid_checks_mirror_the_reference(g):
     assert ks.coulomb.hf_coeff == 0.25 and g.hf_coeff(Hybrid()) == 0.25
     with pytest.raises(ValueError, match="aux_K"):
         ks._check_state(g.SplatState(pairs=(1, 2, 3), aux=object()))
-    with pytest.raises(NotImplementedError, match="range-separated"):
-        g.df_exchange_energy_screened(None, None, None, None, None, omega=0.3)
+
+    class LongRange:
+        hf_coeff_lr = 1.0
+        omega = 0.4
+
+    lr = g.SplatDFJ(coulomb=g.df(), screen=g.pairlist(), xc=LongRange())
+    assert (lr.coulomb.hf_coeff, lr.coulomb.hf_coeff_lr, lr.coulomb.omega) == (0.0, 1.0, 0.4)
+    with pytest.raises(ValueError, match="aux_K"):
+        lr._check_state(g.SplatState(pairs=(1, 2, 3), aux=object()))
+    for bad in (-0.3, float("inf"), float("nan")):
+        with pytest.raises(ValueError, match="omega"):
+            g.df_exchange_energy_screened(None, None, None, None, None, omega=bad)
 
 
 def test_train_pad_rule(g):
