@@ -71,6 +71,9 @@ def main() -> int:
                          "configuration is also quoted at 1e-5 and 1e-9")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
+    ap.add_argument("--cpu-sample-frac", type=float, default=0.0,
+                    help="DF-J term: sample this fraction of the pair list for the CPU baseline "
+                         "instead of sizing the sample by --cpu-seconds")
     ap.add_argument("--term", choices=("dfj", "nuclear", "exact", "grid", "exchange", "screen"),
                     default="dfj",
                     help="dfj: the screened DF-J step (the headline); nuclear: the screened "
@@ -241,6 +244,8 @@ def main() -> int:
         probe = max(1, min(n, int(2e6 // N) + 1))
         t_probe, m_probe = run(probe)
         m = max(1, min(n, int(m_probe * args.cpu_seconds / max(t_probe, 1e-6))))
+        if args.cpu_sample_frac > 0:
+            m = max(1, min(n, int(round(args.cpu_sample_frac * n))))
         per_chunk = max(m_probe, int(m_probe * 20.0 / max(t_probe, 1e-6)))   # ~20 s per chunk
         t_cpu, m_cpu = run(m, per_chunk) if m > m_probe else (t_probe, m_probe)
         per_pair = t_cpu / m_cpu
