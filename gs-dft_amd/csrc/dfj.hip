@@ -390,15 +390,22 @@ __device__ __forceinline__ bool new_centre(const double* __restrict__ x) {
 
 // Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / 24, s_t^2
 // and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes;
-// `scale` multiplies the weight (the record's u, for the reverse pass that folds it in).
+// `scale` multiplies the weight (the record's u, for the reverse pass that folds it in). Stored
+// node-major from offset 8 (node t at 8 + 4 t): the four values a node reads are one 32-byte run,
+// a single scalar load, and two nodes share a cache line.
 constexpr double kExpMinusHalf = 0x1.368b2fc6f960ap-1;     // e^(-1/2), correctly rounded
+
+__host__ __device__ constexpr int rec_s(int t) { return 8 + 4 * t; }
+__host__ __device__ constexpr int rec_wh(int t) { return 8 + 4 * t + 1; }
+__host__ __device__ constexpr int rec_s2(int t) { return 8 + 4 * t + 2; }
+__host__ __device__ constexpr int rec_is(int t) { return 8 + 4 * t + 3; }
 
 __device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp,
                                                 double scale = 1.0) {
-    o[8 + t] = s;
-    o[8 + kNodes + t] = wp / sqrt(s) * (kExpMinusHalf / 24.0) * scale;
-    o[8 + 2 * kNodes + t] = s * s;
-    o[8 + 3 * kNodes + t] = 1.0 / s;
+    o[rec_s(t)] = s;
+    o[rec_wh(t)] = wp / sqrt(s) * (kExpMinusHalf / 24.0) * scale;
+    o[rec_s2(t)] = s * s;
+    o[rec_is(t)] = 1.0 / s;
 }
 
 // body(std::integral_constant<int, t>) for t = 0, 1, ..., kN - 1 until it returns true: a fully
@@ -480,13 +487,23 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 cf = (q0d == q0d) ? coef : q0d;      // a NaN centre propagates
             }
             double F = 0.0;
+            // each node's constants are read one node ahead, so their scalar load overlaps the
+            // previous node's arithmetic
+            double n_s = x[rec_s(0)], n_wh = x[rec_wh(0)], n_is = x[rec_is(0)];
             auto node = [&](auto tc) {
                 constexpr int t = decltype(tc)::value;
-                const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
+                const double st = n_s, wh = n_wh, is = n_is;
+                if constexpr (t + 1 < kNodes) {
+                    n_s = x[rec_s(t + 1)];
+                    n_wh = x[rec_wh(t + 1)];
+                    n_is = x[rec_is(t + 1)];
+                }
                 const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
                 const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
                 const NodeArgH v = node_arg_h(Pr, Qn);
-                F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+                F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+                // keep the next node's loads ahead of the early exit (not sunk past it)
+                if constexpr (t + 1 < kNodes) asm volatile("" ::"s"(n_s), "s"(n_wh), "s"(n_is));
                 return screen_after(t) && wave_all_beyond_h(v.arg);
             };
             lane_nodes += lanes * node_loop<0>(node);
@@ -572,8 +589,8 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 }
 
 
-// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | s_t | wh_t | s_t^2 |
-// 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored centre-grouped: with G = N / M exponent scales (the
+// Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | per node t: s_t, wh_t,
+// s_t^2, 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored centre-grouped: with G = N / M exponent scales (the
 // product aux is scale-major, P = s M + m, every scale of splat m at one centre), the record of P
 // sits at slot m G + s, so the scales sharing a centre are consecutive; otherwise (N not a
 // multiple of M) in aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
@@ -609,10 +626,10 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
         if (t < tb.n) {
             put_node_consts(o, t, s[t], wp[t], fold ? u : 1.0);
         } else {            // slots past the table: never read by a kernel of tb.n nodes
-            o[8 + t] = 0.0;
-            o[8 + kNodes + t] = 0.0;
-            o[8 + 2 * kNodes + t] = 0.0;
-            o[8 + 3 * kNodes + t] = 0.0;
+            o[rec_s(t)] = 0.0;
+            o[rec_wh(t)] = 0.0;
+            o[rec_s2(t)] = 0.0;
+            o[rec_is(t)] = 0.0;
         }
     }
 }
@@ -730,10 +747,18 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         if constexpr (!kFold) {
             F = 0; dP0 = 0; dP1 = 0; dP2 = 0; gs1 = 0; gs2 = 0; gs3 = 0;
         }
+        // each node's constants are read one node ahead, so their scalar load overlaps the
+        // previous node's arithmetic
+        double n_s = x[rec_s(0)], n_wh = x[rec_wh(0)], n_s2 = x[rec_s2(0)], n_is = x[rec_is(0)];
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[8 + t], wh = x[8 + kNodes + t], s2 = x[8 + 2 * kNodes + t],
-                         is = x[8 + 3 * kNodes + t];
+            const double st = n_s, wh = n_wh, s2 = n_s2, is = n_is;
+            if constexpr (t + 1 < kN) {
+                n_s = x[rec_s(t + 1)];
+                n_wh = x[rec_wh(t + 1)];
+                n_s2 = x[rec_s2(t + 1)];
+                n_is = x[rec_is(t + 1)];
+            }
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeValH v = node_val_h(Pr, Qn);
@@ -747,6 +772,9 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             gs1 += G;
             gs2 = __builtin_fma(G, st, gs2);
             gs3 = __builtin_fma(G, s2, gs3);
+            // keep the next node's loads ahead of the early exit (not sunk past it)
+            if constexpr (t + 1 < kN)
+                asm volatile("" ::"s"(n_s), "s"(n_wh), "s"(n_s2), "s"(n_is));
             return screen_after<kN>(t) && wave_all_beyond_h(v.zh);
         };
         nodes += node_loop<0, kN>(node);
@@ -1552,11 +1580,11 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
         double F = 0.0;
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[8 + t], is = x[8 + 3 * kNodes + t];
+            const double st = x[rec_s(t)], is = x[rec_is(t)];
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeArgH v = node_arg_h(Pr, Qn);
-            F = __builtin_fma(x[8 + kNodes + t] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            F = __builtin_fma(x[rec_wh(t)] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
             return screen_after<kN>(t) && wave_all_beyond_h(v.arg);
         };
         nodes += node_loop<0, kN>(node);
