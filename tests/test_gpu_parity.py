@@ -258,18 +258,27 @@ def test_blocked_cholesky_matches_lapack(g, cuda, N):
 
 @pytest.mark.parametrize("N,offset", [(1, 0), (64, 0), (127, 0), (128, 0), (129, 0), (192, 0),
                                       (193, 0), (256, 0), (257, 0), (300, 0), (1000, 0),
-                                      (1000, 1), (2561, 0), (4096, 0)])
+                                      (1000, 1), (2561, 0), (4096, 0), (8193, 0)])
 def test_blocked_solves_match_lapack(g, cuda, N, offset):
-    """The blocked substitutions (128-column blocks; each step also solves the next block in two
-    64-row halves: next block of 1, 64 or 65 rows, partial last block, no rows past the next
-    block) against LAPACK's triangular solves with the same factor: d = L^-T L^-1 gamma and
-    E = gamma.d / 2, for a well-conditioned factor (cond(L) ~ 1e2), so the two agree to a few ulp
-    times cond. offset = 1 places the factor 8 bytes past a 16-byte boundary (no paired loads)."""
+    """The blocked substitutions (128-column blocks, one launch per block, each also solving the
+    next block: next blocks of 1, 64 or 65 rows, partial last block of 1 row at 8193, steps with no
+    rows past the next block) against LAPACK's triangular solves with the same factor:
+    d = L^-T L^-1 gamma and E = gamma.d / 2, for a well-conditioned factor (cond(L) ~ 1e2), so the
+    two agree to a few ulp times cond. offset = 1 places the factor 8 bytes past a 16-byte
+    boundary (no paired loads)."""
     from scipy.linalg import solve_triangular
     from gs_dft_amd import ri as _ri
     rng = np.random.default_rng(N)
-    A = rng.normal(size=(N, N)) / np.sqrt(N)
-    Ln = np.linalg.cholesky(A @ A.T + np.eye(N))
+    if N <= 4096:
+        A = rng.normal(size=(N, N)) / np.sqrt(N)
+        Ln = np.linalg.cholesky(A @ A.T + np.eye(N))
+    else:                                   # a unit-diagonal factor with small random entries
+        Ln = rng.uniform(-1.0, 1.0, size=(N, N))
+        for i0 in range(0, N, 1024):        # in place, by row blocks
+            blk = Ln[i0:i0 + 1024]
+            blk *= 0.5 / N
+            blk[:] = np.tril(blk, i0 - 1)
+        Ln[np.diag_indices(N)] = 1.0
     Ln[np.diag_indices(N)] *= rng.uniform(0.5, 2.0, size=N)
     gam = rng.normal(size=N)
     y = solve_triangular(Ln, gam, lower=True)
@@ -277,7 +286,7 @@ def test_blocked_solves_match_lapack(g, cuda, N, offset):
     print(f"[solve] N={N} offset={offset}", flush=True)
     buf = torch.empty(N * N + offset, dtype=torch.float64, device="cuda")
     Ld = buf[offset:].view(N, N)
-    Ld.copy_(torch.tensor(Ln))
+    Ld.copy_(torch.from_numpy(Ln))
     assert Ld.data_ptr() % 16 == 8 * offset
     d, E = _ri._cho_solve(Ld, torch.tensor(gam, device="cuda"), True)
     err = rel_max(_np(d), dn)
