@@ -1639,6 +1639,30 @@ Split bwd_split(int64_t N, int64_t n) {
     return Split{(N + per - 1) / (per > 0 ? per : 1), per > 0 ? per : 1};
 }
 
+// The DF-J reverse: besides enough slabs to fill the device (bwd_split), the aux records are cut
+// into slabs of at most kL2Records records (2.9 MB) so that the workgroups running together walk
+// one slab, which then stays in the XCD's 4 MB L2 instead of coming from the MALL once per
+// workgroup, as long as the slabs' partial moments (kAcc x n doubles each) fit in kSlabBudget.
+// At globule700 (80,000 records, 11.2 M pairs) that is 20 slabs and 44.6 GB of partial moments:
+// the reverse takes 8.49 instead of 9.05 s. The result depends on the split only through the
+// order in which the slabs' moments are added (fixed for given N and n).
+constexpr int64_t kL2Records = 4096;
+constexpr double kSlabBudget = 48.0 * (1ull << 30);
+
+Split bwd_split_records(int64_t N, int64_t n) {
+    Split sp = bwd_split(N, n);
+    const int64_t want = (N + kL2Records - 1) / kL2Records;
+    if (N <= 0 || sp.slabs >= want) return sp;
+    const double per_slab_bytes = 8.0 * kAcc * (double)(n > 0 ? n : 1);
+    int64_t slabs = want;
+    const int64_t cap = (int64_t)(kSlabBudget / per_slab_bytes);
+    if (slabs > cap) slabs = cap;
+    if (slabs > 65535) slabs = 65535;
+    if (slabs <= sp.slabs || slabs < 1) return sp;
+    const int64_t per = (N + slabs - 1) / slabs;
+    return Split{(N + per - 1) / per, per};
+}
+
 struct GammaWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec, *partial;
     double *aux, *acc, *contrib, *rec_sorted;
@@ -1660,7 +1684,8 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
         GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
         w->partial = ar.take<double>(groups * N + 1);
     } else {
-        const Split sp = bwd_split(N, n);
+        // at least as many slabs as bwd_split's, which the nuclear pass launches with
+        const Split sp = bwd_split_records(N, n);
         w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
         w->acc = ar.take<double>(sp.slabs * kAcc * n + 1);
         w->rec_sorted = ar.take<double>(kRec * n + kRec);
@@ -2358,7 +2383,7 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
         k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
                                                                 w.rec_sorted);
-        const Split sp = bwd_split(N, n);
+        const Split sp = bwd_split_records(N, n);
         dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
         profile_begin(kProfGammaBwd, s);
         k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
