@@ -287,11 +287,12 @@ def main() -> int:
                      "fp64_counters": counter_record(s.name, dom[1]),
                      "note": "FP64 compute bound on the vector ALUs (VALU; MI355X FP64 vector "
                              "peak 78.6 TFLOP/s, no MFMA: the work is elementwise). frac is "
-                             "algorithmic: it credits every integral with all 20 nodes, so the "
-                             "nodes the screen skips count as done; executed_* count only the "
-                             "nodes evaluated; fp64_counters holds the hardware FP64 VALU "
-                             "instruction rate of the same kernel at this workload from the "
-                             "rocprofv3 counter runs in profiles/"},
+                             "algorithmic (the per-integral figure at all 20 nodes): it credits "
+                             "the nodes the screen skips as done, so it can exceed 1 once the "
+                             "screen skips more than the kernel loses to the peak; executed_* "
+                             "count only the nodes evaluated; fp64_counters holds the hardware "
+                             "FP64 VALU instruction rate of the same kernel at this workload "
+                             "from the rocprofv3 counter runs in profiles/"},
         "kernels": {"three_centre_fwd_ms": fwd_ms, "three_centre_bwd_ms": bwd_ms,
                     "fwd_frac_fp64": fwd_tf / PEAK_FP64, "bwd_frac_fp64": bwd_tf / PEAK_FP64,
                     "fwd_executed_frac_fp64": fwd_exec_tf / PEAK_FP64,
