@@ -165,7 +165,10 @@ int gsdft_gamma_noalloc(int64_t M, const double* quat, const double* log_scale,
  * gradients w.r.t. quat, log_scale, centers (M,4/3/3) and C (M,k), aux held constant. Needs the
  * pair index of the same n entries. Replaces JAX's reverse pass through
  * gs_dft/coulomb/ri.py:436-469, :190-222, gs_dft/coulomb/stream.py:203-215 and
- * gs_dft/basis/spectral.py:33-40,72-82 (gs_dft/ks/train.py:367-373 holds the aux constant). */
+ * gs_dft/basis/spectral.py:33-40,72-82 (gs_dft/ks/train.py:367-373 holds the aux constant).
+ * The workspace holds 200 bytes per pair for each slab of at most 4096 aux functions the pass is
+ * cut into (up to 48 GiB in all: 44.6 GB for 11.2 M pairs and 80,000 aux functions), so that each
+ * slab's records stay in one XCD's L2 while the workgroups running together walk it. */
 int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, size_t* bytes);
 int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,
                     const double* centers, int64_t k, const double* C, const double* occ,
