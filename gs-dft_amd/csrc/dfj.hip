@@ -1578,13 +1578,23 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             cf = (q0d == q0d) ? coef : q0d;          // a NaN centre propagates
         }
         double F = 0.0;
+        // each node's constants are read one node ahead, so their scalar load overlaps the
+        // previous node's arithmetic
+        double n_s = x[rec_s(0)], n_wh = x[rec_wh(0)], n_is = x[rec_is(0)];
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
-            const double st = x[rec_s(t)], is = x[rec_is(t)];
+            const double st = n_s, wh = n_wh, is = n_is;
+            if constexpr (t + 1 < kN) {
+                n_s = x[rec_s(t + 1)];
+                n_wh = x[rec_wh(t + 1)];
+                n_is = x[rec_is(t + 1)];
+            }
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeArgH v = node_arg_h(Pr, Qn);
-            F = __builtin_fma(x[rec_wh(t)] * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            // keep the next node's loads ahead of the early exit (not sunk past it)
+            if constexpr (t + 1 < kN) asm volatile("" ::"s"(n_s), "s"(n_wh), "s"(n_is));
             return screen_after<kN>(t) && wave_all_beyond_h(v.arg);
         };
         nodes += node_loop<0, kN>(node);
