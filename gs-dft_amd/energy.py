@@ -37,7 +37,10 @@ class SplatState:
     """Refresh products for the current splats (gs_dft/ks/energy.py:121-139).
 
     ``pair_index`` is this library's addition: the CSR views of ``pairs`` the reverse pass uses.
-    ``refresh`` fills it; when it is None it is built on first use."""
+    ``refresh`` fills it; when it is None it is built on first use. ``cholV_lr`` is the other
+    addition: for a range-separated xc, the Cholesky factor of the erf(omega r)/r metric of
+    ``aux_K`` (+ lam I), formed once per refresh like ``cholV`` instead of once per step (the
+    reference forms that metric inside every long-range exchange call, ri.py:543)."""
 
     pairs: tuple | None = None
     aux: object | None = None
@@ -45,6 +48,7 @@ class SplatState:
     cholV: torch.Tensor | None = None
     cells: tuple | None = None
     pair_index: _scr.PairIndex | None = None
+    cholV_lr: torch.Tensor | None = None
 
 
 def train_pad_to(screen: Pairlist, n0: int, n_devices: int = 1) -> int:
@@ -126,7 +130,7 @@ def refresh(ks, basis: Splat, *, pad_to: int | None = None,
         pairs = _scr.neighbor_pairs(basis, eps=ks.screen.eps, pad_to=pad_to,
                                     unique=ks.screen.unique)
         index = _scr.build_pair_index(basis.n_basis, *pairs)
-    aux = aux_K = cholV = None
+    aux = aux_K = cholV = cholV_lr = None
     coul = ks.coulomb
     if isinstance(coul, ScreenedProductDFCoulomb) or type(coul).__name__ in (
             "ScreenedProductDFCoulomb", "ProductDFCoulomb"):
@@ -134,4 +138,7 @@ def refresh(ks, basis: Splat, *, pad_to: int | None = None,
         if getattr(coul, "hf_coeff", 0.0) != 0.0 or getattr(coul, "hf_coeff_lr", 0.0) != 0.0:
             aux_K = aux
         cholV = _cdf.aux_cholesky(aux, coul.lam)
-    return SplatState(pairs=pairs, aux=aux, aux_K=aux_K, cholV=cholV, pair_index=index)
+        if getattr(coul, "hf_coeff_lr", 0.0) != 0.0:
+            cholV_lr = _cdf.aux_cholesky(aux_K, coul.lam, coul.omega)
+    return SplatState(pairs=pairs, aux=aux, aux_K=aux_K, cholV=cholV, pair_index=index,
+                      cholV_lr=cholV_lr)

@@ -117,14 +117,16 @@ class ScreenedProductDFCoulomb(CoulombTerm):
         return e_j, e_k
 
     def energy_lr(self, basis, C_orth, P, occ, state):
-        """Unscaled E_K[erf(omega r)/r] on ``state.aux_K`` (gs_dft/ks/terms.py:258-264); the erf
-        metric's factor is formed here, as the reference forms its metric inside the call."""
+        """Unscaled E_K[erf(omega r)/r] on ``state.aux_K`` (gs_dft/ks/terms.py:258-264), with the
+        erf metric's factor from ``state.cholV_lr`` (refresh forms it) or, without one, formed
+        here as the reference forms its metric inside the call."""
         if self.hf_coeff_lr == 0.0:
             return torch.zeros((), dtype=torch.float64, device=C_orth.device)
         pi, pj, valid = state.pairs
         return _cdf.df_exchange_energy_screened(
             basis, C_orth, state.aux_K, pi, pj, lam=self.lam, chunk=self.chunk, valid=valid,
-            omega=self.omega, index=getattr(state, "pair_index", None))
+            omega=self.omega, cholV=getattr(state, "cholV_lr", None),
+            index=getattr(state, "pair_index", None))
 
 
 @dataclass(frozen=True)

@@ -162,7 +162,7 @@ def test_long_range_plugin_energy(g, wl, cuda):
     for xc in (RangeSeparated(), LongRangeOnly()):
         ks = g.SplatDFJ(coulomb=g.df(scales=s.scales), screen=g.pairlist(1e-7), xc=xc)
         state = g.refresh(ks, basis)
-        assert state.aux_K is state.aux
+        assert state.aux_K is state.aux and state.cholV_lr is not None
         model = g.SplatModel(basis=basis, C=C, occupations=occ)
         E = ks(model, state)
         pi, pj, valid = state.pairs
@@ -176,6 +176,10 @@ def test_long_range_plugin_energy(g, wl, cuda):
         print(f"[exchange-lr] plugin E {E.item():.15e} = E_J {EJ.item():.6e} + "
               f"{xc.hf_coeff} E_K {EK.item():.6e} + {xc.hf_coeff_lr} E_K^lr {ELR.item():.6e}")
         assert abs(E.item() - ref) < 1e-12 * abs(E.item())
+        # the refresh's erf factor is the one the call would form itself: same energy bit for bit
+        with torch.no_grad():
+            ELR_state = ks.coulomb.energy_lr(basis, C, None, occ, state)
+        assert ELR_state.item() == ELR.item()
         C.grad = None
         E.backward()
         assert torch.isfinite(C.grad).all() and torch.isfinite(basis.centers.grad).all()
