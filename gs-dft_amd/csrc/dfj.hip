@@ -18,12 +18,12 @@
 //               tables, centre-grouped so the centre terms are shared by the exponent scales);
 //               each lane keeps its partial sums per record in LDS, the block adds them in lane
 //               order, and the per-block partials are summed in fixed order.
-//   reverse  -- one lane per pair slot; the wave walks the aux records the same way; each lane
-//               accumulates its pair's 25 cotangent moments in registers; per-pair results are
-//               mapped to per-splat gradients by wave-per-splat segmented sums over the CSR pair
-//               index.
+//   reverse  -- one lane per pair slot; the wave walks the aux records the same way, over slabs
+//               of records small enough to stay in L2; each lane accumulates its pair's 25
+//               cotangent moments per slab in registers; the slabs' moments are added in slab
+//               order, and per-pair results are mapped to per-splat gradients by wave-per-splat
+//               segmented sums over the CSR pair index.
 #include <rocblas/rocblas.h>
-#include <rocsolver/rocsolver.h>
 
 #include <algorithm>
 #include <cmath>

@@ -28,7 +28,7 @@ extern "C" {
 #define GSDFT_ERR_OVERFLOW 2     /* significant pairs exceed twice the pad (pairs.py:157-161)   */
 #define GSDFT_ERR_NOT_PD 3       /* Cholesky met a non-positive pivot                           */
 #define GSDFT_ERR_HIP 4          /* HIP runtime error                                           */
-#define GSDFT_ERR_LIB 5          /* rocBLAS / rocSOLVER / hipCUB error                          */
+#define GSDFT_ERR_LIB 5          /* rocBLAS / hipCUB error                                      */
 #define GSDFT_ERR_WORKSPACE 6    /* workspace too small; the query names the size               */
 #define GSDFT_ERR_FALLBACK 7     /* spatial screening: the list overflows its pad (use the dense build) */
 
