@@ -70,9 +70,17 @@ inline int64_t padded_cols(int64_t k) { return (k + 15) / 16 * 16; }
 // kp = 16 ceil(k / 16) columns (zeros). Per row i this is the product of the row's block columns
 // (W x deg) and its gathered C rows (deg x kp): grid (rows, ceil(W / (4 kMfAux)), column
 // blocks), 4 waves, each wave a 32 x 16 NT tile of Y_i in 2 NT MFMA accumulators (NT = 6 for the
-// full 96-column blocks, the remainder in one more launch), K = 4
-// pairs per step (A: the Bt entries, one 128-byte row segment per quarter-wave; B: the C row
-// segments of the same 4 pairs), the next step's operands loaded before the current step's MFMAs.
+// full 96-column blocks, the remainder in one more launch), K = 4 pairs per MFMA. The row's pairs
+// go through LDS in stages of kSpPairs: the workgroup loads a stage's 128 block columns and
+// 16 NT-wide C rows once (wave w the pairs w, w + 4, ..., so each pair's indices are wave-uniform
+// scalar loads) into one of two buffers while the MFMAs run on the other.
+constexpr int kSpPairs = 16;
+constexpr int kSpAux = 4 * kMfAux;              // aux columns per workgroup
+// Padded LDS rows: each row starts 128 bytes (mod 256) after the previous one, so the two rows an
+// MFMA operand read takes per half-wave fall in different banks.
+constexpr int kSpLdA = kSpAux + 16;
+__host__ __device__ constexpr int sp_ld_c(int nt) { return 16 * nt + (nt % 2 == 0 ? 16 : 0); }
+
 template <int NT>
 __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t kp, int64_t ldb,
                                                    int64_t obase,
@@ -82,11 +90,14 @@ __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t
                                                    const double* __restrict__ Bt,
                                                    const double* __restrict__ Cp,
                                                    double* __restrict__ Y) {
+    constexpr int kLdC = sp_ld_c(NT);
+    __shared__ double As[2][kSpPairs][kSpLdA];
+    __shared__ double Cs[2][kSpPairs][kLdC];
     const int64_t i = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kq = lane >> 4, c16 = lane & 15;
-    const int64_t lw = (int64_t)blockIdx.y * (4 * kMfAux) + (int64_t)wave * kMfAux;
+    const int64_t lbase = (int64_t)blockIdx.y * kSpAux;
     const int64_t ob = obase + (int64_t)blockIdx.z * (16 * NT);
     v4d acc[2][NT];
 #pragma unroll
@@ -94,34 +105,82 @@ __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t
 #pragma unroll
         for (int to = 0; to < NT; ++to) acc[ta][to] = v4d{0.0, 0.0, 0.0, 0.0};
     const int64_t r0 = ptr[i], r1 = ptr[i + 1];
-    // operands of the K step at rb (the 4 pairs rb .. rb + 3), loaded one step ahead
-    double av[2], bv[NT];
-    auto load = [&](int64_t rb) {
-        const bool has = rb + kq < r1;
-        const int64_t a = perm[has ? rb + kq : r0];
-        const int64_t cr = col[rb + kq];                  // padded past n
-#pragma unroll
-        for (int ta = 0; ta < 2; ++ta) {
-            const int64_t l = lw + ta * 16 + c16;
-            av[ta] = (has && l < W) ? Bt[a * ldb + l] : 0.0;
-        }
-#pragma unroll
-        for (int to = 0; to < NT; ++to) bv[to] = Cp[cr * kp + ob + to * 16 + c16];
+    // Stage at CSR position rs: wave w loads pairs w + 4 j (j < 4) into registers. The pairs'
+    // indices come one stage earlier from one vector load (lane j: perm, lane 4 + j: col; vector
+    // rather than scalar loads, whose counter the LDS reads of the MFMAs share) and are broadcast
+    // with readlane. Every load reads an in-range address (positions past the row clamped to its
+    // last one, columns past W to W - 1, C columns past the block to its last); the values that
+    // stand for nothing are zeroed when the stage is written to LDS, so the loads stay in flight
+    // through the current stage's MFMAs.
+    double sa[4][2], sc[4][2];
+    int64_t staged = 0;                                         // position of the loaded stage
+    const int64_t la0 = min(lbase + lane, W - 1), la1 = min(lbase + 64 + lane, W - 1);
+    const bool in0 = lbase + lane < W, in1 = lbase + 64 + lane < W;
+    const int oc0 = min(lane, 16 * NT - 1), oc1 = min(64 + lane, 16 * NT - 1);
+    int idx = 0;                                                // indices of the next stage
+    auto load_idx = [&](int64_t rs) {
+        const int64_t r = rs + wave + 4 * (lane & 3);
+        const int64_t rc = r < r1 ? r : r1 - 1;
+        if (lane < 8) idx = lane < 4 ? perm[rc] : col[rc];
     };
-    if (r0 < r1) load(r0);
-    for (int64_t rb = r0; rb < r1; rb += 4) {
-        double ac[2], bc[NT];
+    auto load = [&](int64_t rs) {
+        staged = rs;
 #pragma unroll
-        for (int ta = 0; ta < 2; ++ta) ac[ta] = av[ta];
-#pragma unroll
-        for (int to = 0; to < NT; ++to) bc[to] = bv[to];
-        if (rb + 4 < r1) load(rb + 4);
-#pragma unroll
-        for (int to = 0; to < NT; ++to) {
-            acc[0][to] = mfma16x16x4(ac[0], bc[to], acc[0][to]);
-            acc[1][to] = mfma16x16x4(ac[1], bc[to], acc[1][to]);
+        for (int j = 0; j < 4; ++j) {
+            const int64_t a = __builtin_amdgcn_readlane(idx, j);
+            const int64_t c = __builtin_amdgcn_readlane(idx, 4 + j);
+            const double* __restrict__ ba = Bt + a * ldb;
+            const double* __restrict__ cb = Cp + c * kp + ob;
+            sa[j][0] = ba[la0];
+            sa[j][1] = ba[la1];
+            sc[j][0] = cb[oc0];
+            sc[j][1] = cb[oc1];
         }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = wave + 4 * j;
+            const bool has = staged + p < r1;
+            As[buf][p][lane] = has && in0 ? sa[j][0] : 0.0;
+            As[buf][p][64 + lane] = has && in1 ? sa[j][1] : 0.0;
+            if (lane < 16 * NT) Cs[buf][p][lane] = sc[j][0];
+            if (64 + lane < 16 * NT) Cs[buf][p][64 + lane] = sc[j][1];
+        }
+    };
+    if (r0 < r1) {
+        load_idx(r0);
+        load(r0);
+        load_idx(r0 + kSpPairs);
+        store(0);
     }
+    __syncthreads();
+    int buf = 0;
+    for (int64_t rs = r0; rs < r1; rs += kSpPairs) {          // workgroup-uniform
+        const bool more = rs + kSpPairs < r1;
+        if (more) {
+            load(rs + kSpPairs);
+            load_idx(rs + 2 * kSpPairs);
+        }
+#pragma unroll
+        for (int k4 = 0; k4 < kSpPairs / 4; ++k4) {
+            const int p = 4 * k4 + kq;
+            const double a0 = As[buf][p][wave * kMfAux + c16];
+            const double a1 = As[buf][p][wave * kMfAux + 16 + c16];
+            double bc[NT];
+#pragma unroll
+            for (int to = 0; to < NT; ++to) bc[to] = Cs[buf][p][to * 16 + c16];
+#pragma unroll
+            for (int to = 0; to < NT; ++to) {
+                acc[0][to] = mfma16x16x4(a0, bc[to], acc[0][to]);
+                acc[1][to] = mfma16x16x4(a1, bc[to], acc[1][to]);
+            }
+        }
+        if (more) store(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+    const int64_t lw = lbase + (int64_t)wave * kMfAux;
     const int64_t Wk = W * k;
 #pragma unroll
     for (int ta = 0; ta < 2; ++ta)
