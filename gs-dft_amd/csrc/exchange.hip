@@ -268,9 +268,17 @@ __global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t
 // ceil(W / (4 kMfAux))), 4 waves, each wave 32 aux x 16 pairs per MFMA pair tile, K = 4 orbitals
 // per step. Per pass of 4 NS orbitals (NS = kMfK / 4 for the full passes, the remainder in one
 // more launch) the wave holds its Ybar block in registers and walks the row's pair tiles; a pass
-// after the first adds to Tbar (same lane, passes in order), so every sum has a fixed order.
+// after the first adds to Tbar (same lane, passes in order), so every sum has a fixed order. The
+// tiles' C rows go through LDS (loaded once per workgroup, wave w the pairs w + 4 j, into one of
+// two buffers while the MFMAs run on the other); the next tile's column indices and output rows
+// are loaded one tile ahead.
+constexpr int kSdPairs = 16;
+// Padded LDS rows: row p starts 32 bytes (mod 256) after row p - 1, so the 16 rows of four
+// consecutive orbitals an MFMA operand read takes fill the banks twice over without conflicts.
+__host__ __device__ constexpr int sd_ld_c(int ns) { return 4 * ns + (36 - (4 * ns) % 32) % 32; }
+
 template <int NS>
-__global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_t kp, int64_t ldt,
+__global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int64_t kp, int64_t ldt,
                                                     int64_t oc_begin, int64_t oc_end, int first,
                                                     const int32_t* __restrict__ ptr,
                                                     const int32_t* __restrict__ perm,
@@ -279,14 +287,22 @@ __global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_
                                                     const double* __restrict__ Ybar,
                                                     const double* __restrict__ Cp,
                                                     double* __restrict__ Tbar) {
+    constexpr int kW = 4 * NS;                  // orbitals per pass
+    constexpr int kLd = sd_ld_c(NS);
+    __shared__ double Cs[2][kSdPairs][kLd];
     const int64_t i = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kq = lane >> 4, c16 = lane & 15;
     const int64_t lw = (int64_t)blockIdx.y * (4 * kMfAux) + (int64_t)wave * kMfAux;
     const int64_t Wk = W * k;
     const int64_t r0 = ptr[i], r1 = ptr[i + 1];
-    for (int64_t oc = oc_begin; oc < oc_end; oc += 4 * NS) {
+    if (r0 >= r1) return;                       // workgroup-uniform: an empty row writes nothing
+    auto clampr = [&](int64_t r) { return r < r1 ? r : r1 - 1; };
+    // every C load reads an in-range address (positions past the row clamped to its last one,
+    // orbitals past the pass to its last); the products of pairs past the row are never stored
+    const int o0 = min(lane, kW - 1), o1 = min(64 + lane, kW - 1);
+    for (int64_t oc = oc_begin; oc < oc_end; oc += kW) {
         const bool store = first && oc == oc_begin;
         double ya[2][NS];
 #pragma unroll
@@ -298,17 +314,54 @@ __global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_
                 ya[ta][s4] = (l < W && o < k) ? Ybar[i * Wk + l * k + o] : 0.0;
             }
         }
-        for (int64_t rb = r0; rb < r1; rb += 16) {
-            const int64_t cr = col[rb + c16];                 // padded past n
+        int idx = 0;                            // lanes j < 4: col of pair wave + 4 j of a tile
+        double sc[4][2];
+        auto load_idx = [&](int64_t rb) {
+            if (lane < 4) idx = col[clampr(rb + wave + 4 * lane)];
+        };
+        auto load_c = [&](int64_t rb) {
+            (void)rb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t c = __builtin_amdgcn_readlane(idx, j);
+                const double* __restrict__ cb = Cp + c * kp + oc;
+                sc[j][0] = cb[o0];
+                sc[j][1] = cb[o1];
+            }
+        };
+        auto store_c = [&](int buf) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int p = wave + 4 * j;
+                if (lane < kW) Cs[buf][p][lane] = sc[j][0];
+                if (64 + lane < kW) Cs[buf][p][64 + lane] = sc[j][1];
+            }
+        };
+        load_idx(r0);
+        load_c(r0);
+        load_idx(r0 + kSdPairs);
+        int64_t orow = inv[perm[clampr(r0 + c16)]];    // Tbar row of this lane's pair
+        int32_t pnext = perm[clampr(r0 + kSdPairs + c16)];      // its pair in the next tile
+        store_c(0);
+        __syncthreads();
+        int buf = 0;
+        for (int64_t rb = r0; rb < r1; rb += kSdPairs) {       // workgroup-uniform
+            // the next tiles' loads run unconditionally (clamped, so past the last tile they read
+            // the row's last pair and go unused): no branch splits the loop body, and every index
+            // a load needs arrived an iteration earlier
+            load_c(rb + kSdPairs);
+            load_idx(rb + 2 * kSdPairs);
+            const int32_t pn2 = perm[clampr(rb + 2 * kSdPairs + c16)];
             v4d acc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
 #pragma unroll
             for (int s4 = 0; s4 < NS; ++s4) {
-                const double bv = Cp[cr * kp + oc + 4 * s4 + kq];
+                const double bv = Cs[buf][c16][4 * s4 + kq];
                 acc[0] = mfma16x16x4(ya[0][s4], bv, acc[0]);
                 acc[1] = mfma16x16x4(ya[1][s4], bv, acc[1]);
             }
+            const int64_t orow_next = inv[pnext];
             if (rb + c16 < r1) {
-                double* __restrict__ out = Tbar + (int64_t)inv[perm[rb + c16]] * ldt;
+                double* __restrict__ out = Tbar + orow * ldt;
 #pragma unroll
                 for (int ta = 0; ta < 2; ++ta)
 #pragma unroll
@@ -317,6 +370,11 @@ __global__ __launch_bounds__(256) void k_exch_sddmm(int64_t W, int64_t k, int64_
                         if (l < W) out[l] = store ? acc[ta][r] : out[l] + acc[ta][r];
                     }
             }
+            store_c(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+            orow = orow_next;
+            pnext = pn2;
         }
     }
 }
