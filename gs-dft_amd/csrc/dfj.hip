@@ -646,8 +646,9 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // With kFold the record weights already carry u (k_aux_bwd_prep with fold): the node sums then run
 // over all records of a centre and are turned into jt, T1..T3 and C0..C2 once per centre (flush),
 // since every per-record term is linear in u and q0, q1 are the centre's.
-// With kLaneU the cotangent of (P|a) is not separable: u = x[3] * ut[slot * ldu + p] per lane
-// (the exchange's dE/d(P|a), stored slot-major).
+// With kLaneU the cotangent of (P|a) is not separable: lane slot a holds the group g = uperm[a] of
+// list entries sharing one product Gaussian, and u = x[3] * sum over e in [uptr[g], uptr[g + 1])
+// of ut[e * ldu + p] (the exchange's dE/d(P|a) per entry, rows in key order), added in order.
 // With kAtomF the records are nuclei (point charges) and the pass also forms every nucleus' force
 // from the same node sums: per (nucleus p, pair a) the vector 2 KN_a q_a (f0 d + f1 Ah d + f2 Ah^2 d),
 // f0 = -I3 sum g s, f1 = -(I1 sum g s^2 + sum g s^3), f2 = sum g s^2 (dF/dR of
@@ -660,7 +661,8 @@ template <bool kLaneU, bool kAtomF = false, bool kFold = false, int kN = kNodes>
 __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
-    const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part) {
+    const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part,
+    const int32_t* __restrict__ uperm, const int32_t* __restrict__ uptr) {
     __shared__ double tab[256];
     __shared__ double af[kAtomF ? 4 : 1][kAtomF ? kAtomChunk : 1][3];
     // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
@@ -684,6 +686,15 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     double d[3] = {0, 0, 0}, q0 = 0, q1 = 0, X0 = 0, rr = 0;
     double ad[3] = {0, 0, 0}, a2d[3] = {0, 0, 0};      // Ah d, Ah^2 d (kAtomF)
     const double cq2 = kAtomF && live ? 2.0 * r[13] * r[14] : 0.0;
+    int64_t ut0 = 0;                     // kLaneU: the lane's cotangent rows [ut0, ut0 + utn)
+    int utn = 0;
+    if constexpr (kLaneU) {
+        if (live) {
+            const int32_t g = uperm[a];
+            ut0 = uptr[g];
+            utn = uptr[g + 1] - uptr[g];
+        }
+    }
     int64_t chunk0 = blockIdx.y * per_slab;
     double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;      // node sums
     auto flush = [&]() {
@@ -722,7 +733,11 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
         double u = x[3];
-        if constexpr (kLaneU) u *= live ? ut[a * ldu + p] : 0.0;
+        if constexpr (kLaneU) {
+            double us = 0.0;
+            for (int e = 0; e < utn; ++e) us += ut[(ut0 + e) * ldu + p];
+            u *= us;
+        }
         if (p == p0 || new_centre(x)) {          // wave-uniform
             flush();
             const int l = threadIdx.x;
@@ -902,10 +917,11 @@ __device__ void pair_reverse(int64_t n, int64_t a, int64_t i, int64_t j,
 // Per pair: sum the slab moments, map them to dE/dAh, dE/dPa, dE/dKN_a, then through
 // gs_dft/coulomb/stream.py:203-215 to the two splats. Writes J and 20 contributions (SoA):
 //   [0..5] G_i  [6..8] g_mu_i  [9] g_N_i  [10..15] G_j  [16..18] g_mu_j  [19] g_N_j.
-// Slot `slot` holds pair a = perm[slot] (its record and slab moments are stored by slot). pref is
-// the integral's prefactor (2 pi^3/sqrt(pi) for (P|a), 2 pi for the nuclear attraction); a null
-// weight treats every entry as live.
-__global__ void k_pair_finalize(int64_t n, int64_t slabs, double pref,
+// Slot `slot` (of n) holds pair a = perm[slot] (its record and slab moments are stored by slot,
+// stride n); J and contrib are indexed by pair, stride nc. pref is the integral's prefactor
+// (2 pi^3/sqrt(pi) for (P|a), 2 pi for the nuclear attraction); a null weight treats every entry
+// as live.
+__global__ void k_pair_finalize(int64_t n, int64_t nc, int64_t slabs, double pref,
                                 const int32_t* __restrict__ perm,
                                 const int32_t* __restrict__ pi,
                                 const int32_t* __restrict__ pj,
@@ -919,7 +935,7 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, double pref,
     const int64_t a = perm[slot];
     if (weight && weight[a] == 0.0) {
         J[a] = 0.0;
-        for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
+        for (int c = 0; c < 20; ++c) contrib[(int64_t)c * nc + a] = 0.0;
         return;
     }
     double m[kAcc];
@@ -963,7 +979,7 @@ __global__ void k_pair_finalize(int64_t n, int64_t slabs, double pref,
         Gh[k] = scale * ((I1 * Sa[k] + Sb[k]) - (AS[3 * rw + cl] + AS[3 * cl + rw]) + T1 * eye
                          + T2 * (I1 * eye - Ah[k]) + T3 * adj[3 * rw + cl]);
     }
-    pair_reverse(n, a, pi[a], pj[a], A6, mu, Nrm, Gh, gP, gKN, contrib);
+    pair_reverse(nc, a, pi[a], pj[a], A6, mu, Nrm, Gh, gP, gKN, contrib);
 }
 
 // One wave per splat: deterministic segmented sums of the i-side and j-side contributions, then
@@ -1529,10 +1545,11 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
 }
 
 // ------------------------------------------------------------------ exchange three-centre block
-// Bt[perm[slot] * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and the pair of each
-// pair slot, the pair record carrying q_a = w_a: the screened block of RI-K
+// Bt[perm[slot] * ldb + l] = (P|a) for the aux function of slot q0 + l (l < W) and the pair group
+// of each slot (the list entries of one unordered splat pair share one product Gaussian, so one
+// row serves them all), the record carrying q_a = w_a: the screened block of RI-K
 // (gs_dft/coulomb/ri.py:527-531, full_isobra_block), written rather than contracted. One lane per
-// pair slot (the pair order of the reverse, so the 64 pairs of a wave are close in space and width
+// slot (the pair order of the reverse, so the 64 pairs of a wave are close in space and width
 // and the node screen fires for whole waves) and the aux records
 // of slots q0 + l wave-uniform and centre-grouped (d, A d, q0..q2 formed once per centre, x[3] =
 // KN_P): block (x, y) covers the pair slots [256 x, 256 x + 256) and the sixteen aux slots from
@@ -1789,6 +1806,13 @@ int blas_handle(hipStream_t s, rocblas_handle* out) {
 
 // ------------------------------------------------------------------ exchange: three-centre passes
 
+// slot_pair[slot] = rep[perm[slot]].
+__global__ void k_compose(int64_t n, const int32_t* __restrict__ perm,
+                          const int32_t* __restrict__ rep, int32_t* __restrict__ out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t < n) out[t] = rep[perm[t]];
+}
+
 int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
                    ExchTcWs* w) {
     *w = ExchTcWs{};
@@ -1798,21 +1822,29 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
     w->kn = ar.take<double>(N + 1);
     w->q = ar.take<double>(n + 1);
     w->rec = ar.take<double>(kRec * n + kRec);
+    w->rec_grp = ar.take<double>(kRec * n + kRec);
     w->rec_sorted = ar.take<double>(kRec * n + kRec);
     w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
+    w->ent_group = ar.take<int32_t>(n + 1);
+    w->ent_pos = ar.take<int32_t>(n + 1);
+    w->grp_first = ar.take<int32_t>(n + 2);
+    w->grp_rep = ar.take<int32_t>(n + 1);
+    w->slot_pair = ar.take<int32_t>(n + 1);
+    w->head = ar.take<int32_t>(n + 1);
+    w->n_groups_dev = ar.take<int64_t>(1);
+    w->scan_bytes = pair_groups_scan_bytes(n);
+    w->scan_tmp = ar.take<char>(w->scan_bytes + 1);
     GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
     if (grads) {
-        // bwd_split(W, n).slabs for every chunk width W <= Pc stays within min(ceil(target /
-        // groups), (Pc + 15) / 16) (the count before its rounding to whole slabs)
-        const int64_t groups = n > 0 ? (n + 255) / 256 : 1;
-        int64_t slab_bound = (256 * 4 * 4 + groups - 1) / groups;
-        slab_bound = std::min<int64_t>(std::min<int64_t>(slab_bound, (Pc + 15) / 16), 65535);
-        if (slab_bound < 1) slab_bound = 1;
-        w->part = ar.take<double>(slab_bound * kAcc * n + 1);
+        // bwd_split(W, m).slabs x m over every chunk width W <= Pc and group count m <= n: at most
+        // (4096 / ceil(m / 256) + 1) m <= 4096 x 256 + n + 256, and at most the slab cap x n
+        int64_t cap = std::min<int64_t>((Pc + 15) / 16, 65535);
+        if (cap < 1) cap = 1;
+        const int64_t bound = std::min<int64_t>(cap * n, 4096 * 256 + n + 256);
+        w->part = ar.take<double>(kAcc * bound + 1);
         w->acc = ar.take<double>(kAcc * n + 1);
         w->J = ar.take<double>(n + 1);
         w->contrib = ar.take<double>(20 * n + 1);
-        w->inv_perm = ar.take<int32_t>(n + 1);
     }
     return GSDFT_OK;
 }
@@ -1820,7 +1852,10 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
 int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, int64_t N, const double* log_alpha,
                      const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
-                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s) {
+                     const double* weight, bool grads, const ExchTcWs& w, int64_t* n_groups,
+                     hipStream_t s) {
+    (void)grads;
+    *n_groups = 0;
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
     GSDFT_HIP(hipGetLastError());
@@ -1837,18 +1872,28 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
                                                       nullptr, 0, w.table, w.aux);
     GSDFT_HIP(hipGetLastError());
-    GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
-    k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
-                                                            w.rec_sorted);
+    // one record per group (its first entry's), then the groups' slot order
+    GSDFT_TRY(launch_pair_groups(M, n, pi, pj, w.q, w.pair_order, w.head, w.scan_tmp,
+                                 w.scan_bytes, w.ent_group, w.ent_pos, w.grp_first, w.grp_rep,
+                                 w.n_groups_dev, s));
+    int64_t ng = 0;
+    GSDFT_TRY(read_back(&ng, w.n_groups_dev, sizeof(int64_t), s, "exchange: pair groups"));
+    if (ng < 1 || ng > n) return fail(GSDFT_ERR_LIB, "exchange: bad pair group count %lld",
+                                      (long long)ng);
+    k_rec_gather<<<blocks_for(ng * kRec, 256), 256, 0, s>>>(ng, w.grp_rep, w.rec, w.rec_grp);
     GSDFT_HIP(hipGetLastError());
-    if (!grads) return GSDFT_OK;
-    k_inv_perm<<<blocks_for(n, 256), 256, 0, s>>>(n, w.pair_order.perm, w.inv_perm);
+    GSDFT_TRY(launch_pair_order(ng, w.rec_grp, kRec, w.pair_order, s));
+    k_rec_gather<<<blocks_for(ng * kRec, 256), 256, 0, s>>>(ng, w.pair_order.perm, w.rec_grp,
+                                                             w.rec_sorted);
+    k_compose<<<blocks_for(ng, 256), 256, 0, s>>>(ng, w.pair_order.perm, w.grp_rep, w.slot_pair);
     GSDFT_HIP(hipGetLastError());
+    *n_groups = ng;
     return GSDFT_OK;
 }
 
 int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
-                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
+                  int64_t n_groups, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
+    const int64_t n = n_groups;
     if (n <= 0 || W <= 0) return GSDFT_OK;
     (void)M; (void)N; (void)aux_centers;
     const int64_t gy = (W + kBlockRecs - 1) / kBlockRecs;
@@ -1882,8 +1927,9 @@ int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux
     return GSDFT_OK;
 }
 
-int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* Tbar, int64_t ldt,
-                    bool first, const ExchTcWs& w, hipStream_t s) {
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n_groups, const double* Tbar,
+                    int64_t ldt, bool first, const ExchTcWs& w, hipStream_t s) {
+    const int64_t n = n_groups;
     if (n <= 0 || W <= 0) return GSDFT_OK;
     const Split sp = bwd_split(W, n);
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
@@ -1891,12 +1937,13 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* T
     if (w.table.n == kLrNodes)
         k_gamma_bwd<true, false, false, kLrNodes><<<grid, 256, 0, s>>>(
             n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab, w.part,
-            profile_work_counter(kProfExchBwd), Tbar, ldt, nullptr);
+            profile_work_counter(kProfExchBwd), Tbar, ldt, nullptr, w.pair_order.perm,
+            w.grp_first);
     else
         k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0,
                                                sp.per_slab, w.part,
                                                profile_work_counter(kProfExchBwd), Tbar, ldt,
-                                               nullptr);
+                                               nullptr, w.pair_order.perm, w.grp_first);
     profile_end(kProfExchBwd, s);
     GSDFT_HIP(hipGetLastError());
     k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);
@@ -1905,15 +1952,19 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* T
     return GSDFT_OK;
 }
 
-int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+int exch_tc_finish(int64_t M, int64_t n, int64_t n_groups, const int32_t* pi, const int32_t* pj,
                    const double* weight, const double* quat, const double* log_scale,
                    const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
                    const int32_t* col_ptr, const int32_t* col_perm, double* dquat,
                    double* dlog_scale, double* dcenters, const ExchTcWs& w, hipStream_t s) {
     if (n > 0) {
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, kPref3c, w.pair_order.perm, pi,
-                                                           pj, weight, w.A6, centers, w.Nrm,
-                                                           w.rec_sorted, w.acc, w.J, w.contrib);
+        // every entry but its group's first contributes nothing of its own
+        k_fill<<<blocks_for(20 * n, 256), 256, 0, s>>>(20 * n, 0.0, w.contrib);
+        k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 0.0, w.J);
+        GSDFT_HIP(hipGetLastError());
+        k_pair_finalize<<<blocks_for(n_groups, 256), 256, 0, s>>>(
+            n_groups, n, 1, kPref3c, w.slot_pair, pi, pj, weight, w.A6, centers, w.Nrm,
+            w.rec_sorted, w.acc, w.J, w.contrib);
         GSDFT_HIP(hipGetLastError());
     }
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
@@ -2399,10 +2450,10 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
                                                              sp.per_slab, w.acc,
                                                              profile_work_counter(kProfGammaBwd),
-                                                             nullptr, 0, nullptr);
+                                                             nullptr, 0, nullptr, nullptr, nullptr);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPref3c, w.pair_order.perm, pi,
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPref3c, w.pair_order.perm, pi,
                                                            pj, weight, w.A6, centers, w.Nrm,
                                                            w.rec_sorted, w.acc, J, w.contrib);
         GSDFT_HIP(hipGetLastError());
@@ -2487,14 +2538,14 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
         k_gamma_bwd<false, true><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux,
                                                       sp.per_slab, w.g.acc,
                                                       profile_work_counter(kProfNucPairs),
-                                                      nullptr, 0, w.atom_partial);
+                                                      nullptr, 0, w.atom_partial, nullptr, nullptr);
     else
         k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab,
                                                 w.g.acc, profile_work_counter(kProfNucPairs),
-                                                nullptr, 0, nullptr);
+                                                nullptr, 0, nullptr, nullptr, nullptr);
     profile_end(kProfNucPairs, s);
     GSDFT_HIP(hipGetLastError());
-    k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, sp.slabs, kPrefNuc,
+    k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPrefNuc,
                                                        w.g.pair_order.perm, pi, pj, weight,
                                                        w.g.A6, centers, w.g.Nrm, w.g.rec_sorted,
                                                        w.g.acc, V, w.g.contrib);

@@ -8,9 +8,13 @@
 // pair list (every live (i, k, w) has its (k, i, w)) each D_P is symmetric up to round-off and the
 // antisymmetric columns are dropped.
 //
+// The list's entries are grouped by unordered splat pair {i, k}: (i, k) and (k, i) share one
+// product Gaussian, so the three-centre passes run once per group (on a symmetric list half the
+// entries), the block's row of a group serves all its entries, and the reverse takes the sum of
+// their cotangents.
 // Forward, per chunk of W aux functions (centre-grouped slot order):
-//   Bt (n x W)          the screened three-centre block (k_exch_block_pairs, dfj.hip)
-//   Y[i][l][o']         = sum over pairs a of row i of Bt[a][l] C[k_a][o']     (k_exch_spmm, FP64
+//   Bt (groups x W)     the screened three-centre block (k_exch_block_pairs, dfj.hip)
+//   Y[i][l][o']         = sum over pairs a of row i of Bt[g_a][l] C[k_a][o']   (k_exch_spmm, FP64
 //                         MFMA over the row's block columns and gathered C rows)
 //   D_P = C^T Y_P       one FP64 GEMM per chunk: k x (W k) x M
 //   Dt[:, P]            packed columns of D_P                                    (k_exch_pack)
@@ -20,8 +24,9 @@
 //   dC    += Y_P Dbar_P^T + Y'_P Dbar_P      Y'[m][l][o] = sum over pairs a of column m of
 //                                            Bt[a][l] C[i_a][o] (= Y on a symmetric list)
 //   Ybar_P = C Dbar_P,   Tbar[a][l] = Ybar[i_a][l] . C[k_a]            (k_exch_sddmm, FP64 MFMA)
-//   and the three-centre reverse with the per-(P, a) cotangent Tbar (dfj.hip) for the splat
-//   gradients. Every sum runs in a fixed order (no atomics; rocBLAS runs with atomics off).
+//   and the three-centre reverse with the per-(P, group) cotangent, the sum of its entries' Tbar
+//   (dfj.hip), for the splat gradients. Every sum runs in a fixed order (no atomics; rocBLAS runs
+//   with atomics off).
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
@@ -66,8 +71,9 @@ constexpr int kMfK = 96;        // orbitals held in registers per pass of the Tb
 inline int64_t padded_cols(int64_t k) { return (k + 15) / 16 * 16; }
 
 // Y[i][l][o] = sum_{r in [ptr[i], ptr[i+1])} Bt[perm[r] * ldb + l] C[col[r] * k + o] for l < W,
-// o < k (col[r] = the partner splat of CSR position r), with C read from Cp, its rows padded to
-// kp = 16 ceil(k / 16) columns (zeros). Per row i this is the product of the row's block columns
+// o < k (perm[r] = the block row of CSR position r, its pair group; col[r] = its partner splat),
+// with C read from Cp, its rows padded to kp = 16 ceil(k / 16) columns (zeros). Per row i this is
+// the product of the row's block columns
 // (W x deg) and its gathered C rows (deg x kp): grid (rows, ceil(W / (4 kMfAux)), column
 // blocks), 4 waves, each wave a 32 x 16 NT tile of Y_i in 2 NT MFMA accumulators (NT = 6 for the
 // full 96-column blocks, the remainder in one more launch), K = 4 pairs per MFMA. The row's pairs
@@ -421,6 +427,13 @@ __global__ void k_sum_slices(int64_t count, int64_t S, const double* __restrict_
     out[e] = v;
 }
 
+// out[r] = src[idx[r]].
+__global__ void k_gather_i32(int64_t n, const int32_t* __restrict__ idx,
+                             const int32_t* __restrict__ src, int32_t* __restrict__ out) {
+    const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (r < n) out[r] = src[idx[r]];
+}
+
 __global__ void k_fill0(int64_t n, double* __restrict__ out) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i < n) out[i] = 0.0;
@@ -460,6 +473,7 @@ struct ExchWs {
     ExchTcWs tc;
     double *Dt, *Bt, *Y, *Yp, *Ys, *Yps, *Dfull, *Ebar, *part, *red;
     int32_t *row_col, *col_row;       // partner splat per CSR position (rows: pj, columns: pi)
+    int32_t *row_grp, *col_grp;       // pair group (block row) per CSR position
     double* Cp;                       // C with rows padded to padded_cols(k) columns
 };
 
@@ -481,6 +495,8 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
     w->Cp = ar.take<double>(M * padded_cols(k) + 1);
     w->row_col = ar.take<int32_t>(n + kColPad);
     w->col_row = sym ? nullptr : ar.take<int32_t>(n + kColPad);
+    w->row_grp = ar.take<int32_t>(n + 1);
+    w->col_grp = sym ? nullptr : ar.take<int32_t>(n + 1);
     return GSDFT_OK;
 }
 
@@ -606,15 +622,16 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     GSDFT_TRY(layout_exchange(ar, M, k, N, n, sym, grads, recompute != 0, Pc, &w));
     if (!w.red) return fail(GSDFT_ERR_WORKSPACE, "gsdft_exchange: workspace too small");
     w.tc.table = omega > 0.0 ? long_range_table(omega) : coulomb_table();
+    int64_t ng = 0;                     // pair groups: the list's distinct product Gaussians
     GSDFT_TRY(exch_tc_prologue(M, quat, log_scale, centers, N, log_alpha, aux_centers, n, pi, pj,
-                               weight, grads, w.tc, s));
+                               weight, grads, w.tc, &ng, s));
     if (n == 0) {                       // D = 0: E_K = 0 and every gradient vanishes
         k_fill0<<<1, 1, 0, s>>>(1, energy);
         GSDFT_HIP(hipGetLastError());
         if (grads) {
             k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
             GSDFT_HIP(hipGetLastError());
-            GSDFT_TRY(exch_tc_finish(M, 0, pi, pj, weight, quat, log_scale, centers, row_ptr,
+            GSDFT_TRY(exch_tc_finish(M, 0, 0, pi, pj, weight, quat, log_scale, centers, row_ptr,
                                      row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters,
                                      w.tc, s));
         }
@@ -623,10 +640,12 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     rocblas_handle h;
     GSDFT_TRY(blas_handle(s, &h));
     k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, row_perm, pj, w.row_col);
+    k_gather_i32<<<nblk(n, 256), 256, 0, s>>>(n, row_perm, w.tc.ent_group, w.row_grp);
     k_pad_cols<<<nblk(M * padded_cols(k), 256), 256, 0, s>>>(M, k, padded_cols(k), C, w.Cp);
     GSDFT_HIP(hipGetLastError());
     if (!sym) {
         k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, col_perm, pi, w.col_row);
+        k_gather_i32<<<nblk(n, 256), 256, 0, s>>>(n, col_perm, w.tc.ent_group, w.col_grp);
         GSDFT_HIP(hipGetLastError());
     }
     const int64_t G = (N % M == 0) ? N / M : 1;
@@ -638,10 +657,10 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     for (int64_t q0 = 0; q0 < N; q0 += Pc) {
         const int64_t W = std::min(Pc, N - q0);
         double* Yc = store ? w.Ys + M * q0 * k : w.Y;
-        GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
-        GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.Bt, w.Cp, Yc, s));
+        GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, ng, Pc, w.Bt, w.tc, s));
+        GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, Yc, s));
         if (store && !sym)
-            GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, w.col_row, w.Bt, w.Cp,
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp,
                                   w.Yps + M * q0 * k, s));
         profile_begin(kProfExchGemm, s);
         GSDFT_BLAS(rocblas_dgemm_64(h, N_, T_, k, W * k, M, &one, C, k, Yc, W * k, &zero,
@@ -680,10 +699,10 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
             Yc = w.Ys + M * q0 * k;
             Ypc = sym ? nullptr : w.Yps + M * q0 * k;
         } else {
-            GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
-            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.Bt, w.Cp, w.Y, s));
+            GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, ng, Pc, w.Bt, w.tc, s));
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, w.Y, s));
             if (!sym)
-                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, col_perm, w.col_row, w.Bt, w.Cp, w.Yp, s));
+                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp, w.Yp, s));
         }
         profile_begin(kProfExchGemm, s);
         // dC += Y_P Dbar_P^T (+ Y'_P Dbar_P; the same term again on a symmetric list)
@@ -694,12 +713,12 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
                                     W * k));
         profile_end(kProfExchGemm, s);
         // Tbar (slot-major, ld Pc) into the block's buffer
-        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.inv_perm, w.Y, w.Cp,
+        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.ent_pos, w.Y, w.Cp,
                                w.Bt,
                                s));
-        GSDFT_TRY(exch_tc_reverse(N, q0, W, n, w.Bt, Pc, q0 == 0, w.tc, s));
+        GSDFT_TRY(exch_tc_reverse(N, q0, W, ng, w.Bt, Pc, q0 == 0, w.tc, s));
     }
-    GSDFT_TRY(exch_tc_finish(M, n, pi, pj, weight, quat, log_scale, centers, row_ptr, row_perm,
-                             col_ptr, col_perm, dquat, dlog_scale, dcenters, w.tc, s));
+    GSDFT_TRY(exch_tc_finish(M, n, ng, pi, pj, weight, quat, log_scale, centers, row_ptr,
+                             row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters, w.tc, s));
     return GSDFT_OK;
 }

@@ -87,17 +87,35 @@ struct PairOrderWs {
 int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w);
 int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
                       hipStream_t s);
+// order.hip: groups of list entries by unordered splat pair (live entries; each dead entry, q = 0,
+// alone), numbered in key order, through the sort buffers of po (sized for n). Fills ent_group
+// and ent_pos (per entry), grp_first (n_groups + 1) and grp_rep (per group) and the device count
+// *n_groups; head is n ints of scratch, scan_tmp pair_groups_scan_bytes(n) bytes.
+size_t pair_groups_scan_bytes(int64_t n);
+int launch_pair_groups(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                       const double* q, const PairOrderWs& po, int32_t* head, char* scan_tmp,
+                       size_t scan_bytes, int32_t* ent_group, int32_t* ent_pos,
+                       int32_t* grp_first, int32_t* grp_rep, int64_t* n_groups, hipStream_t s);
 
 // dfj.hip: the library's rocBLAS handle for the current device, bound to stream s.
 int blas_handle(hipStream_t s, struct _rocblas_handle** out);
 
 // dfj.hip: the three-centre passes of the screened exchange. Charts, aux quantities and pair
-// records (q_a = w_a) in list order; for the reverse also the slot order of the pairs, its
-// inverse, the aux records (u = KN_P, centre-grouped slots) and the moment accumulators.
+// records (q_a = w_a) in list order. The entries of the list are grouped by their unordered splat
+// pair {i, j} (live entries only; each dead entry is a group of its own): the entries of a group
+// share one product Gaussian and so one (P|a), which the passes form once per group. Groups are
+// numbered in order of their first entry in key order; per entry its group (ent_group) and its
+// position in key order (ent_pos, the row of its cotangent), per group its first key-order
+// position (grp_first, n_groups + 1 entries) and its first entry (grp_rep). The three-centre
+// passes run over the groups in slot order (pair_order.perm: slot -> group); slot_pair maps a
+// slot to its group's first entry.
 struct ExchTcWs {
     double *A6, *Nrm, *beta, *kn, *q, *rec;
-    double *rec_sorted, *aux, *part, *acc, *J, *contrib;
-    int32_t* inv_perm;
+    double *rec_grp, *rec_sorted, *aux, *part, *acc, *J, *contrib;
+    int32_t *ent_group, *ent_pos, *grp_first, *grp_rep, *slot_pair, *head;
+    int64_t* n_groups_dev;
+    char* scan_tmp;
+    size_t scan_bytes;
     PairOrderWs pair_order;
     NodeTable table;        // the kernel's node rule (set after exch_tc_layout)
 };
@@ -106,20 +124,25 @@ NodeTable coulomb_table();
 NodeTable long_range_table(double omega);
 int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
                    ExchTcWs* w);
+// Charts, records, the groups and their slot order; *n_groups receives the group count (read
+// back from the device: the call waits for the stream).
 int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, int64_t N, const double* log_alpha,
                      const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
-                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s);
-// Bt[a * ldb + l] = (P|a) w_a for the aux of slots q0 .. q0 + W - 1 (slot order: the G = N / M
-// scales of one centre consecutive when N is a multiple of M, else aux order).
+                     const double* weight, bool grads, const ExchTcWs& w, int64_t* n_groups,
+                     hipStream_t s);
+// Bt[g * ldb + l] = (P|a) w_g for every group g and the aux of slots q0 .. q0 + W - 1 (slot order:
+// the G = N / M scales of one centre consecutive when N is a multiple of M, else aux order).
 int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
-                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
-// Adds (first: sets) the reverse moments of the aux slots q0 .. q0 + W - 1 with the cotangent
-// Tbar[slot * ldt + l] of (P_l|a_slot).
-int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, const double* Tbar, int64_t ldt,
-                    bool first, const ExchTcWs& w, hipStream_t s);
-// Moments -> per-pair splat contributions -> dquat, dlog_scale, dcenters.
-int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                  int64_t n_groups, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
+// Adds (first: sets) the reverse moments of the aux slots q0 .. q0 + W - 1 with the cotangent of
+// group g's (P|a_l): the sum, in key order, of Tbar[e * ldt + l] over its entries' key-order
+// positions e.
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n_groups, const double* Tbar,
+                    int64_t ldt, bool first, const ExchTcWs& w, hipStream_t s);
+// Moments -> per-group splat contributions (on the group's first entry, zero on the others) ->
+// dquat, dlog_scale, dcenters.
+int exch_tc_finish(int64_t M, int64_t n, int64_t n_groups, const int32_t* pi, const int32_t* pj,
                    const double* weight, const double* quat, const double* log_scale,
                    const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
                    const int32_t* col_ptr, const int32_t* col_perm, double* dquat,

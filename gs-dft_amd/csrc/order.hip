@@ -47,7 +47,83 @@ __global__ void k_pair_keys(int64_t n, const double* __restrict__ rec, int rec_s
     idx[a] = (int32_t)a;
 }
 
+// Group key of list entry p: min(i, j) M + max(i, j) for a live entry (the two orders of a splat
+// pair, and repeats of either, share it), M^2 + p for a dead one (a group of its own).
+__global__ void k_group_keys(int64_t n, int64_t M, const int32_t* __restrict__ pi,
+                             const int32_t* __restrict__ pj, const double* __restrict__ q,
+                             uint64_t* __restrict__ key, int32_t* __restrict__ idx) {
+    const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int64_t i = pi[p], j = pj[p];
+    key[p] = q[p] != 0.0 ? (uint64_t)(min(i, j) * M + max(i, j)) : (uint64_t)(M * M + p);
+    idx[p] = (int32_t)p;
+}
+
+// head[s] = 1 where key order position s starts a group.
+__global__ void k_group_heads(int64_t n, const uint64_t* __restrict__ key,
+                              int32_t* __restrict__ head) {
+    const int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    head[s] = (s == 0 || key[s] != key[s - 1]) ? 1 : 0;
+}
+
+// gid[s]: inclusive count of group starts up to s; ent[s]: the entry at key order position s.
+__global__ void k_group_fill(int64_t n, const int32_t* __restrict__ gid,
+                             const int32_t* __restrict__ head, const int32_t* __restrict__ ent,
+                             int32_t* __restrict__ ent_group, int32_t* __restrict__ ent_pos,
+                             int32_t* __restrict__ grp_first, int32_t* __restrict__ grp_rep,
+                             int64_t* __restrict__ n_groups) {
+    const int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const int32_t g = gid[s] - 1, e = ent[s];
+    ent_group[e] = g;
+    ent_pos[e] = (int32_t)s;
+    if (head[s]) {
+        grp_first[g] = (int32_t)s;
+        grp_rep[g] = e;
+    }
+    if (s == n - 1) {
+        grp_first[g + 1] = (int32_t)n;
+        *n_groups = g + 1;
+    }
+}
+
+inline int bit_length(uint64_t v) { return v == 0 ? 1 : 64 - __builtin_clzll(v); }
+
 }  // namespace
+
+size_t pair_groups_scan_bytes(int64_t n) {
+    size_t b = 0;
+    if (hipcub::DeviceScan::InclusiveSum(nullptr, b, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                         (int)(n > 0 ? n : 1)) != hipSuccess)
+        return 0;
+    return b;
+}
+
+int launch_pair_groups(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
+                       const double* q, const PairOrderWs& po, int32_t* head, char* scan_tmp,
+                       size_t scan_bytes, int32_t* ent_group, int32_t* ent_pos,
+                       int32_t* grp_first, int32_t* grp_rep, int64_t* n_groups, hipStream_t s) {
+    if (n > INT32_MAX) return fail(GSDFT_ERR_ARG, "pair groups: n exceeds the int32 range");
+    if (n <= 0) return GSDFT_OK;
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    k_group_keys<<<blocks, 256, 0, s>>>(n, M, pi, pj, q, po.key_in, po.idx_in);
+    GSDFT_HIP(hipGetLastError());
+    size_t b = po.sort_bytes;
+    const int bits = bit_length((uint64_t)(M * M + n));
+    GSDFT_HIP(hipcub::DeviceRadixSort::SortPairs(po.sort_tmp, b, po.key_in, po.key_out,
+                                                 po.idx_in, po.perm, (int)n, 0, bits, s));
+    k_group_heads<<<blocks, 256, 0, s>>>(n, po.key_out, head);
+    GSDFT_HIP(hipGetLastError());
+    // the group ids go where the unsorted keys were (no longer needed)
+    int32_t* gid = reinterpret_cast<int32_t*>(po.key_in);
+    b = scan_bytes;
+    GSDFT_HIP(hipcub::DeviceScan::InclusiveSum(scan_tmp, b, head, gid, (int)n, s));
+    k_group_fill<<<blocks, 256, 0, s>>>(n, gid, head, po.perm, ent_group, ent_pos, grp_first,
+                                        grp_rep, n_groups);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
+}
 
 int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w) {
     w->key_in = ar.take<uint64_t>(n + 1);
