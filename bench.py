@@ -715,7 +715,12 @@ def run_exchange(args) -> int:
                      "note": "per step, summed over the chunk launches; algorithmic flops: "
                              "N n x 419 (block), N n x 780 (reverse), 4 N n k (Y = T C and "
                              "Tbar), 6 N M k^2 (GEMMs), 2 N^2 K2 (solves); FP64 peak 78.6 "
-                             "(vector and matrix)"},
+                             "(vector and matrix). n counts the ordered list entries, as the "
+                             "reference evaluates them; the three-centre passes run once per "
+                             "unordered splat pair (half of them on a symmetric list) and once "
+                             "per node the screen keeps, so the algorithmic fraction credits "
+                             "both as done and can pass 1; reverse_nodes_evaluated_frac is "
+                             "the executed share of N n x 20 nodes"},
         "kernels": {"trsm_ms_per_step": trsm_ms, "trsm_tflops": trsm_tf / 1e12,
                     "gemm_ms_per_step": gemm_ms, "gemm_tflops": gemm_tf / 1e12,
                     "block_ms_per_step": blk_ms, "reverse_ms_per_step": rev_ms,
