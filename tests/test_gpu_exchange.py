@@ -74,6 +74,50 @@ def test_exchange_matches_oracle_and_autograd(g, wl, orc, tr, cuda, masked, k, a
         assert e < REL_G
 
 
+@pytest.mark.parametrize("aux_chunk", [0, 37])
+def test_exchange_repeated_entries(g, wl, orc, tr, cuda, aux_chunk):
+    """Entries the three-centre passes share: a list whose entries repeat (some (i, k) twice, with
+    and without their (k, i)), a self pair repeated, and dead entries (weight 0) among the live
+    ones -- groups of one, two, three and four entries of one unordered splat pair, against the
+    oracle's and the torch literal's entry-by-entry contraction."""
+    k = 5
+    s = wl.make_small(30, k, n_atoms=3, seed=11)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    w = w.astype(np.float64)
+    rng = np.random.default_rng(4)
+    off = np.flatnonzero(pi != pj)
+    rep = rng.choice(off, size=len(off) // 5, replace=False)      # (i, k) again
+    selfp = np.flatnonzero(pi == pj)[:3]                           # (i, i) again
+    mirror = rep[: len(rep) // 2]                                  # and some (k, i) again
+    pi2 = np.concatenate([pi, pi[rep], pi[selfp], pj[mirror]]).astype(np.int32)
+    pj2 = np.concatenate([pj, pj[rep], pj[selfp], pi[mirror]]).astype(np.int32)
+    w2 = np.concatenate([w, w[rep], w[selfp], w[mirror]])
+    dead = rng.choice(len(w2), size=len(w2) // 10, replace=False)
+    w2[dead] = 0.0
+    print(f"[exchange] repeated entries: n={len(pi2)} (list {len(pi)}, +{len(rep)} repeats, "
+          f"+{len(selfp)} self, +{len(mirror)} mirrors, {len(dead)} dead) aux_chunk={aux_chunk}",
+          flush=True)
+    basis, C = _basis(g, s), _cu(s.C, True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    E = g.df_exchange_energy_screened(basis, C, aux, torch.tensor(pi2, device="cuda"),
+                                      torch.tensor(pj2, device="cuda"), lam=1e-8,
+                                      valid=torch.tensor(w2, device="cuda"), aux_chunk=aux_chunk)
+    Eo, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi2, pj2, w2, 1e-8)
+    err = abs(E.item() - Eo) / abs(Eo)
+    print(f"[exchange] E_K {E.item():.15e} oracle {Eo:.15e} rel {err:.2e}")
+    assert err < REL_E
+    E.backward()
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*leaves, _t(la), _t(ac), _idx(pi2), _idx(pj2), _t(w2), 1e-8)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"),
+                          (basis.quat, basis.log_scale, basis.centers, C), leaves):
+        e = rel_max(_np(a.grad), b.grad.numpy())
+        print(f"[exchange] d{name} rel-to-max {e:.2e}")
+        assert e < REL_G
+
+
 def _lr_tolerance(cond):
     """Relative bound on E_K[erf(omega r)/r] between two correct evaluations: the erf metric is
     ill-conditioned (cond(V + lam I) ~ 1e9 at lam = 1e-8), and E_K inherits ~cond x eps from
