@@ -662,7 +662,10 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
     const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part,
-    const int32_t* __restrict__ uperm, const int32_t* __restrict__ uptr) {
+    const int32_t* __restrict__ uperm, const int32_t* __restrict__ uptr,
+    const int64_t* __restrict__ n_live) {
+    // whole workgroups past the real slots leave at once (workgroup-uniform, before any barrier)
+    if (n_live && (int64_t)blockIdx.x * blockDim.x >= *n_live) return;
     __shared__ double tab[256];
     __shared__ double af[kAtomF ? 4 : 1][kAtomF ? kAtomChunk : 1][3];
     // Each lane's Ah (6) and centre (3), read again at every new aux centre: held in LDS (one
@@ -670,7 +673,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     __shared__ double geo[9][256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = a < n;
+    const bool live = a < (n_live ? *n_live : n);      // n_live: a device count of real slots
     const double* r = rec + kRec * (live ? a : 0);
     const double I1 = r[0], I2 = r[1], I3 = r[2];
 #pragma unroll
@@ -957,9 +960,10 @@ __global__ void k_pair_finalize(int64_t n, int64_t nc, int64_t slabs, double pre
                                 const double* __restrict__ A6, const double* __restrict__ mu,
                                 const double* __restrict__ Nrm, const double* __restrict__ rec,
                                 const double* __restrict__ partial, double* __restrict__ J,
-                                double* __restrict__ contrib) {
+                                double* __restrict__ contrib,
+                                const int64_t* __restrict__ n_live = nullptr) {
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (slot >= n) return;
+    if (slot >= (n_live ? *n_live : n)) return;       // n_live: a device count of real slots
     const int64_t a = perm[slot];
     if (weight && weight[a] == 0.0) {
         J[a] = 0.0;
@@ -1591,13 +1595,16 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
                                                           const int32_t* __restrict__ perm,
                                                           int64_t W, const double* __restrict__ aux,
                                                           int64_t ldb, double* __restrict__ Bt,
-                                                          unsigned long long* __restrict__ work) {
+                                                          unsigned long long* __restrict__ work,
+                                                          const int64_t* __restrict__ n_live) {
+    // whole workgroups past the real slots leave at once (workgroup-uniform, before any barrier)
+    if (n_live && (int64_t)blockIdx.x * blockDim.x >= *n_live) return;
     __shared__ double tab[256];
     __shared__ double val[kBlockRecs][256];
     for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2_frac_lead(i);
     __syncthreads();
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const bool live = slot < n;
+    const bool live = slot < (n_live ? *n_live : n);   // n_live: a device count of real slots
     const double* __restrict__ r = rec + kRec * (live ? slot : 0);
     const double I1 = r[0], I2 = r[1], I3 = r[2];
     const double xx = r[3], yy = r[4], zz = r[5], xy = r[6], xz = r[7], yz = r[8];
@@ -1834,7 +1841,16 @@ int blas_handle(hipStream_t s, rocblas_handle* out) {
 
 // ------------------------------------------------------------------ exchange: three-centre passes
 
-// slot_pair[slot] = rep[perm[slot]].
+// out[g] = rec[perm[g]] for g < *n_live (records past it are left alone).
+__global__ void k_rec_gather_live(int64_t n, const int64_t* __restrict__ n_live,
+                                  const int32_t* __restrict__ perm, const double* __restrict__ rec,
+                                  double* __restrict__ out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= n * kRec || t / kRec >= *n_live) return;
+    out[t] = rec[(int64_t)perm[t / kRec] * kRec + t % kRec];
+}
+
+// slot_pair[slot] = rep[perm[slot]] (slots past the groups get whatever rep holds there: unused).
 __global__ void k_compose(int64_t n, const int32_t* __restrict__ perm,
                           const int32_t* __restrict__ rep, int32_t* __restrict__ out) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -1864,11 +1880,12 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
     w->scan_tmp = ar.take<char>(w->scan_bytes + 1);
     GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
     if (grads) {
-        // bwd_split(W, m).slabs x m over every chunk width W <= Pc and group count m <= n: at most
-        // (4096 / ceil(m / 256) + 1) m <= 4096 x 256 + n + 256, and at most the slab cap x n
+        // bwd_split(W, m).slabs x n (the moments' slot stride is n) over every chunk width
+        // W <= Pc and slab estimate m >= n / 2: at most (4096 / ceil(m / 256) + 1) n <=
+        // 2 x 4096 x 256 + n + 512, and at most the slab cap x n
         int64_t cap = std::min<int64_t>((Pc + 15) / 16, 65535);
         if (cap < 1) cap = 1;
-        const int64_t bound = std::min<int64_t>(cap * n, 4096 * 256 + n + 256);
+        const int64_t bound = std::min<int64_t>(cap * n, 2 * 4096 * 256 + n + 512);
         w->part = ar.take<double>(kAcc * bound + 1);
         w->acc = ar.take<double>(kAcc * n + 1);
         w->J = ar.take<double>(n + 1);
@@ -1880,10 +1897,8 @@ int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool 
 int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, int64_t N, const double* log_alpha,
                      const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
-                     const double* weight, bool grads, const ExchTcWs& w, int64_t* n_groups,
-                     hipStream_t s) {
+                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s) {
     (void)grads;
-    *n_groups = 0;
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, w.beta, w.kn);
     GSDFT_HIP(hipGetLastError());
@@ -1900,28 +1915,25 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
                                                       nullptr, 0, w.table, w.aux);
     GSDFT_HIP(hipGetLastError());
-    // one record per group (its first entry's), then the groups' slot order
+    // one record per group (its first entry's), then the groups' slot order: the group count
+    // stays on the device, the first n_groups_dev slots are the groups and the rest idle
     GSDFT_TRY(launch_pair_groups(M, n, pi, pj, w.q, w.pair_order, w.head, w.scan_tmp,
                                  w.scan_bytes, w.ent_group, w.ent_pos, w.grp_first, w.grp_rep,
                                  w.n_groups_dev, s));
-    int64_t ng = 0;
-    GSDFT_TRY(read_back(&ng, w.n_groups_dev, sizeof(int64_t), s, "exchange: pair groups"));
-    if (ng < 1 || ng > n) return fail(GSDFT_ERR_LIB, "exchange: bad pair group count %lld",
-                                      (long long)ng);
-    k_rec_gather<<<blocks_for(ng * kRec, 256), 256, 0, s>>>(ng, w.grp_rep, w.rec, w.rec_grp);
+    k_rec_gather_live<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.n_groups_dev, w.grp_rep,
+                                                                 w.rec, w.rec_grp);
     GSDFT_HIP(hipGetLastError());
-    GSDFT_TRY(launch_pair_order(ng, w.rec_grp, kRec, w.pair_order, s));
-    k_rec_gather<<<blocks_for(ng * kRec, 256), 256, 0, s>>>(ng, w.pair_order.perm, w.rec_grp,
-                                                             w.rec_sorted);
-    k_compose<<<blocks_for(ng, 256), 256, 0, s>>>(ng, w.pair_order.perm, w.grp_rep, w.slot_pair);
+    GSDFT_TRY(launch_pair_order(n, w.rec_grp, kRec, w.pair_order, s, w.n_groups_dev));
+    k_rec_gather_live<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.n_groups_dev,
+                                                                 w.pair_order.perm, w.rec_grp,
+                                                                 w.rec_sorted);
+    k_compose<<<blocks_for(n, 256), 256, 0, s>>>(n, w.pair_order.perm, w.grp_rep, w.slot_pair);
     GSDFT_HIP(hipGetLastError());
-    *n_groups = ng;
     return GSDFT_OK;
 }
 
 int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
-                  int64_t n_groups, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
-    const int64_t n = n_groups;
+                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s) {
     if (n <= 0 || W <= 0) return GSDFT_OK;
     (void)M; (void)N; (void)aux_centers;
     const int64_t gy = (W + kBlockRecs - 1) / kBlockRecs;
@@ -1935,43 +1947,44 @@ int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux
         if (pair)
             k_exch_block_pairs<true, kLrNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
                                                                     w.pair_order.perm, W, aux, ldb,
-                                                                    Bt, work);
+                                                                    Bt, work, w.n_groups_dev);
         else
             k_exch_block_pairs<false, kLrNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
                                                                      w.pair_order.perm, W, aux,
-                                                                     ldb, Bt, work);
+                                                                     ldb, Bt, work, w.n_groups_dev);
     } else {
         if (pair)
             k_exch_block_pairs<true, kNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
                                                                   w.pair_order.perm, W, aux, ldb,
-                                                                  Bt, work);
+                                                                  Bt, work, w.n_groups_dev);
         else
             k_exch_block_pairs<false, kNodes><<<grid, 256, 0, s>>>(n, w.rec_sorted,
                                                                    w.pair_order.perm, W, aux, ldb,
-                                                                   Bt, work);
+                                                                   Bt, work, w.n_groups_dev);
     }
     profile_end(kProfExchBlock, s);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
 }
 
-int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n_groups, const double* Tbar,
-                    int64_t ldt, bool first, const ExchTcWs& w, hipStream_t s) {
-    const int64_t n = n_groups;
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, int64_t n_est,
+                    const double* Tbar, int64_t ldt, bool first, const ExchTcWs& w,
+                    hipStream_t s) {
     if (n <= 0 || W <= 0) return GSDFT_OK;
-    const Split sp = bwd_split(W, n);
+    const Split sp = bwd_split(W, std::max<int64_t>(1, std::min(n, n_est)));
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
     profile_begin(kProfExchBwd, s);
     if (w.table.n == kLrNodes)
         k_gamma_bwd<true, false, false, kLrNodes><<<grid, 256, 0, s>>>(
             n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab, w.part,
             profile_work_counter(kProfExchBwd), Tbar, ldt, nullptr, w.pair_order.perm,
-            w.grp_first);
+            w.grp_first, w.n_groups_dev);
     else
         k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0,
                                                sp.per_slab, w.part,
                                                profile_work_counter(kProfExchBwd), Tbar, ldt,
-                                               nullptr, w.pair_order.perm, w.grp_first);
+                                               nullptr, w.pair_order.perm, w.grp_first,
+                                               w.n_groups_dev);
     profile_end(kProfExchBwd, s);
     GSDFT_HIP(hipGetLastError());
     k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);
@@ -1980,7 +1993,7 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n_groups, const do
     return GSDFT_OK;
 }
 
-int exch_tc_finish(int64_t M, int64_t n, int64_t n_groups, const int32_t* pi, const int32_t* pj,
+int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
                    const double* weight, const double* quat, const double* log_scale,
                    const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
                    const int32_t* col_ptr, const int32_t* col_perm, double* dquat,
@@ -1990,9 +2003,9 @@ int exch_tc_finish(int64_t M, int64_t n, int64_t n_groups, const int32_t* pi, co
         k_fill<<<blocks_for(20 * n, 256), 256, 0, s>>>(20 * n, 0.0, w.contrib);
         k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 0.0, w.J);
         GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n_groups, 256), 256, 0, s>>>(
-            n_groups, n, 1, kPref3c, w.slot_pair, pi, pj, weight, w.A6, centers, w.Nrm,
-            w.rec_sorted, w.acc, w.J, w.contrib);
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(
+            n, n, 1, kPref3c, w.slot_pair, pi, pj, weight, w.A6, centers, w.Nrm, w.rec_sorted,
+            w.acc, w.J, w.contrib, w.n_groups_dev);
         GSDFT_HIP(hipGetLastError());
     }
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
@@ -2478,7 +2491,7 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
                                                              sp.per_slab, w.acc,
                                                              profile_work_counter(kProfGammaBwd),
-                                                             nullptr, 0, nullptr, nullptr, nullptr);
+                                                             nullptr, 0, nullptr, nullptr, nullptr, nullptr);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
         k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPref3c, w.pair_order.perm, pi,
@@ -2566,11 +2579,11 @@ int external_pass(int64_t M, const double* quat, const double* log_scale, const 
         k_gamma_bwd<false, true><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux,
                                                       sp.per_slab, w.g.acc,
                                                       profile_work_counter(kProfNucPairs),
-                                                      nullptr, 0, w.atom_partial, nullptr, nullptr);
+                                                      nullptr, 0, w.atom_partial, nullptr, nullptr, nullptr);
     else
         k_gamma_bwd<false><<<grid, 256, 0, s>>>(n, w.g.rec_sorted, n_atoms, w.g.aux, sp.per_slab,
                                                 w.g.acc, profile_work_counter(kProfNucPairs),
-                                                nullptr, 0, nullptr, nullptr, nullptr);
+                                                nullptr, 0, nullptr, nullptr, nullptr, nullptr);
     profile_end(kProfNucPairs, s);
     GSDFT_HIP(hipGetLastError());
     k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPrefNuc,

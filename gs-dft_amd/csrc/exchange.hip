@@ -622,16 +622,15 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     GSDFT_TRY(layout_exchange(ar, M, k, N, n, sym, grads, recompute != 0, Pc, &w));
     if (!w.red) return fail(GSDFT_ERR_WORKSPACE, "gsdft_exchange: workspace too small");
     w.tc.table = omega > 0.0 ? long_range_table(omega) : coulomb_table();
-    int64_t ng = 0;                     // pair groups: the list's distinct product Gaussians
     GSDFT_TRY(exch_tc_prologue(M, quat, log_scale, centers, N, log_alpha, aux_centers, n, pi, pj,
-                               weight, grads, w.tc, &ng, s));
+                               weight, grads, w.tc, s));
     if (n == 0) {                       // D = 0: E_K = 0 and every gradient vanishes
         k_fill0<<<1, 1, 0, s>>>(1, energy);
         GSDFT_HIP(hipGetLastError());
         if (grads) {
             k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
             GSDFT_HIP(hipGetLastError());
-            GSDFT_TRY(exch_tc_finish(M, 0, 0, pi, pj, weight, quat, log_scale, centers, row_ptr,
+            GSDFT_TRY(exch_tc_finish(M, 0, pi, pj, weight, quat, log_scale, centers, row_ptr,
                                      row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters,
                                      w.tc, s));
         }
@@ -657,7 +656,7 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     for (int64_t q0 = 0; q0 < N; q0 += Pc) {
         const int64_t W = std::min(Pc, N - q0);
         double* Yc = store ? w.Ys + M * q0 * k : w.Y;
-        GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, ng, Pc, w.Bt, w.tc, s));
+        GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
         GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, Yc, s));
         if (store && !sym)
             GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp,
@@ -699,7 +698,7 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
             Yc = w.Ys + M * q0 * k;
             Ypc = sym ? nullptr : w.Yps + M * q0 * k;
         } else {
-            GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, ng, Pc, w.Bt, w.tc, s));
+            GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
             GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, w.Y, s));
             if (!sym)
                 GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp, w.Yp, s));
@@ -716,9 +715,9 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.ent_pos, w.Y, w.Cp,
                                w.Bt,
                                s));
-        GSDFT_TRY(exch_tc_reverse(N, q0, W, ng, w.Bt, Pc, q0 == 0, w.tc, s));
+        GSDFT_TRY(exch_tc_reverse(N, q0, W, n, sym ? (n + 1) / 2 : n, w.Bt, Pc, q0 == 0, w.tc, s));
     }
-    GSDFT_TRY(exch_tc_finish(M, n, ng, pi, pj, weight, quat, log_scale, centers, row_ptr,
+    GSDFT_TRY(exch_tc_finish(M, n, pi, pj, weight, quat, log_scale, centers, row_ptr,
                              row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters, w.tc, s));
     return GSDFT_OK;
 }

@@ -85,8 +85,10 @@ struct PairOrderWs {
     size_t sort_bytes;
 };
 int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w);
+// With n_live (a device count), only the first *n_live records are real: the rest take the slots
+// after them.
 int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
-                      hipStream_t s);
+                      hipStream_t s, const int64_t* n_live = nullptr);
 // order.hip: groups of list entries by unordered splat pair (live entries; each dead entry, q = 0,
 // alone), numbered in key order, through the sort buffers of po (sized for n). Fills ent_group
 // and ent_pos (per entry), grp_first (n_groups + 1) and grp_rep (per group) and the device count
@@ -124,25 +126,26 @@ NodeTable coulomb_table();
 NodeTable long_range_table(double omega);
 int exch_tc_layout(Arena& ar, int64_t M, int64_t N, int64_t n, int64_t Pc, bool grads,
                    ExchTcWs* w);
-// Charts, records, the groups and their slot order; *n_groups receives the group count (read
-// back from the device: the call waits for the stream).
+// Charts, records, the groups and their slot order. The group count stays on the device
+// (n_groups_dev; nothing is read back): the passes below run over n slots, the first
+// *n_groups_dev of them the groups, the rest idle.
 int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
                      const double* centers, int64_t N, const double* log_alpha,
                      const double* aux_centers, int64_t n, const int32_t* pi, const int32_t* pj,
-                     const double* weight, bool grads, const ExchTcWs& w, int64_t* n_groups,
-                     hipStream_t s);
+                     const double* weight, bool grads, const ExchTcWs& w, hipStream_t s);
 // Bt[g * ldb + l] = (P|a) w_g for every group g and the aux of slots q0 .. q0 + W - 1 (slot order:
 // the G = N / M scales of one centre consecutive when N is a multiple of M, else aux order).
 int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux_centers,
-                  int64_t n_groups, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
+                  int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
 // Adds (first: sets) the reverse moments of the aux slots q0 .. q0 + W - 1 with the cotangent of
 // group g's (P|a_l): the sum, in key order, of Tbar[e * ldt + l] over its entries' key-order
-// positions e.
-int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n_groups, const double* Tbar,
-                    int64_t ldt, bool first, const ExchTcWs& w, hipStream_t s);
+// positions e. n_est (at least n / 2) estimates the group count for the split of the aux slots.
+int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, int64_t n_est,
+                    const double* Tbar, int64_t ldt, bool first, const ExchTcWs& w,
+                    hipStream_t s);
 // Moments -> per-group splat contributions (on the group's first entry, zero on the others) ->
 // dquat, dlog_scale, dcenters.
-int exch_tc_finish(int64_t M, int64_t n, int64_t n_groups, const int32_t* pi, const int32_t* pj,
+int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
                    const double* weight, const double* quat, const double* log_scale,
                    const double* centers, const int32_t* row_ptr, const int32_t* row_perm,
                    const int32_t* col_ptr, const int32_t* col_perm, double* dquat,

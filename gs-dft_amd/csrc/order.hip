@@ -28,11 +28,19 @@ __device__ __forceinline__ uint64_t spread3_10(uint32_t v) {   // 10 bits -> eve
     return x;
 }
 
-// rec: pair records in list order (I1 I2 I3 | Ah | P | ...), stride rec_stride doubles.
-__global__ void k_pair_keys(int64_t n, const double* __restrict__ rec, int rec_stride,
+// rec: pair records in list order (I1 I2 I3 | Ah | P | ...), stride rec_stride doubles. With
+// n_live, records from *n_live on stand for nothing: they take the largest key, so the stable
+// sort puts them after every real one, in index order, and are never read.
+__global__ void k_pair_keys(int64_t n, const int64_t* __restrict__ n_live,
+                            const double* __restrict__ rec, int rec_stride,
                             uint64_t* __restrict__ key, int32_t* __restrict__ idx) {
     const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (a >= n) return;
+    idx[a] = (int32_t)a;
+    if (n_live && a >= *n_live) {
+        key[a] = (1ull << kKeyBits) - 1;
+        return;
+    }
     const double* r = rec + (int64_t)rec_stride * a;
     const double band = __builtin_fmax(__builtin_fmin(
         __builtin_floor(2.0 * log2(r[2] / r[1])) + 32.0, 63.0), 0.0);
@@ -44,7 +52,6 @@ __global__ void k_pair_keys(int64_t n, const double* __restrict__ rec, int rec_s
         code |= spread3_10((uint32_t)c) << d;
     }
     key[a] = ((uint64_t)band << 30) | code;
-    idx[a] = (int32_t)a;
 }
 
 // Group key of list entry p: min(i, j) M + max(i, j) for a live entry (the two orders of a splat
@@ -142,10 +149,10 @@ int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w) {
 }
 
 int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
-                      hipStream_t s) {
+                      hipStream_t s, const int64_t* n_live) {
     if (n > INT32_MAX) return fail(GSDFT_ERR_ARG, "pair order: n exceeds the int32 range");
     if (n <= 0) return GSDFT_OK;
-    k_pair_keys<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(n, rec, rec_stride, w.key_in,
+    k_pair_keys<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(n, n_live, rec, rec_stride, w.key_in,
                                                             w.idx_in);
     GSDFT_HIP(hipGetLastError());
     size_t b = w.sort_bytes;
