@@ -80,7 +80,7 @@ inline int64_t padded_cols(int64_t k) { return (k + 15) / 16 * 16; }
 // go through LDS in stages of kSpPairs: the workgroup loads a stage's 128 block columns and
 // 16 NT-wide C rows once (wave w the pairs w, w + 4, ..., so each pair's indices are wave-uniform
 // scalar loads) into one of two buffers while the MFMAs run on the other.
-constexpr int kSpPairs = 16;
+constexpr int kSpPairs = 8;       // 33 KB of LDS: three workgroups per CU (16: two, 2.5% slower)
 constexpr int kSpAux = 4 * kMfAux;              // aux columns per workgroup
 // Padded LDS rows: each row starts 128 bytes (mod 256) after the previous one, so the two rows an
 // MFMA operand read takes per half-wave fall in different banks.
@@ -111,30 +111,31 @@ __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t
 #pragma unroll
         for (int to = 0; to < NT; ++to) acc[ta][to] = v4d{0.0, 0.0, 0.0, 0.0};
     const int64_t r0 = ptr[i], r1 = ptr[i + 1];
-    // Stage at CSR position rs: wave w loads pairs w + 4 j (j < 4) into registers. The pairs'
-    // indices come one stage earlier from one vector load (lane j: perm, lane 4 + j: col; vector
-    // rather than scalar loads, whose counter the LDS reads of the MFMAs share) and are broadcast
-    // with readlane. Every load reads an in-range address (positions past the row clamped to its
+    // Stage at CSR position rs: wave w loads pairs w + 4 j (j < kSpPairs / 4) into registers. The
+    // pairs' indices come one stage earlier from one vector load (lane j: perm, lane kPw + j: col;
+    // vector rather than scalar loads, whose counter the LDS reads of the MFMAs share) and are
+    // broadcast with readlane. Every load reads an in-range address (positions past the row clamped to its
     // last one, columns past W to W - 1, C columns past the block to its last); the values that
     // stand for nothing are zeroed when the stage is written to LDS, so the loads stay in flight
     // through the current stage's MFMAs.
-    double sa[4][2], sc[4][2];
+    constexpr int kPw = kSpPairs / 4;                           // pairs per wave and stage
+    double sa[kPw][2], sc[kPw][2];
     int64_t staged = 0;                                         // position of the loaded stage
     const int64_t la0 = min(lbase + lane, W - 1), la1 = min(lbase + 64 + lane, W - 1);
     const bool in0 = lbase + lane < W, in1 = lbase + 64 + lane < W;
     const int oc0 = min(lane, 16 * NT - 1), oc1 = min(64 + lane, 16 * NT - 1);
     int idx = 0;                                                // indices of the next stage
     auto load_idx = [&](int64_t rs) {
-        const int64_t r = rs + wave + 4 * (lane & 3);
+        const int64_t r = rs + wave + 4 * (lane % kPw);
         const int64_t rc = r < r1 ? r : r1 - 1;
-        if (lane < 8) idx = lane < 4 ? perm[rc] : col[rc];
+        if (lane < 2 * kPw) idx = lane < kPw ? perm[rc] : col[rc];
     };
     auto load = [&](int64_t rs) {
         staged = rs;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kPw; ++j) {
             const int64_t a = __builtin_amdgcn_readlane(idx, j);
-            const int64_t c = __builtin_amdgcn_readlane(idx, 4 + j);
+            const int64_t c = __builtin_amdgcn_readlane(idx, kPw + j);
             const double* __restrict__ ba = Bt + a * ldb;
             const double* __restrict__ cb = Cp + c * kp + ob;
             sa[j][0] = ba[la0];
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kPw; ++j) {
             const int p = wave + 4 * j;
             const bool has = staged + p < r1;
             As[buf][p][lane] = has && in0 ? sa[j][0] : 0.0;
