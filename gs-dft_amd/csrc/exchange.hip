@@ -73,13 +73,12 @@ inline int64_t padded_cols(int64_t k) { return (k + 15) / 16 * 16; }
 // Y[i][l][o] = sum_{r in [ptr[i], ptr[i+1])} Bt[perm[r] * ldb + l] C[col[r] * k + o] for l < W,
 // o < k (perm[r] = the block row of CSR position r, its pair group; col[r] = its partner splat),
 // with C read from Cp, its rows padded to kp = 16 ceil(k / 16) columns (zeros). Per row i this is
-// the product of the row's block columns
-// (W x deg) and its gathered C rows (deg x kp): grid (rows, ceil(W / (4 kMfAux)), column
-// blocks), 4 waves, each wave a 32 x 16 NT tile of Y_i in 2 NT MFMA accumulators (NT = 6 for the
-// full 96-column blocks, the remainder in one more launch), K = 4 pairs per MFMA. The row's pairs
-// go through LDS in stages of kSpPairs: the workgroup loads a stage's 128 block columns and
-// 16 NT-wide C rows once (wave w the pairs w, w + 4, ..., so each pair's indices are wave-uniform
-// scalar loads) into one of two buffers while the MFMAs run on the other.
+// the product of the row's block columns (W x deg) and its gathered C rows (deg x kp): grid
+// (rows, ceil(W / (4 kMfAux)), column blocks), 4 waves, each wave a 32 x 16 NT tile of Y_i in
+// 2 NT MFMA accumulators (NT = 6 for the full 96-column blocks, the remainder in one more
+// launch), K = 4 pairs per MFMA. The row's pairs go through LDS in stages of kSpPairs: the
+// workgroup loads a stage's 128 block columns and 16 NT-wide C rows once (wave w the pairs
+// w, w + 4, ...) into one of two buffers while the MFMAs run on the other.
 constexpr int kSpPairs = 8;       // 33 KB of LDS: three workgroups per CU (16: two, 2.5% slower)
 constexpr int kSpAux = 4 * kMfAux;              // aux columns per workgroup
 // Padded LDS rows: each row starts 128 bytes (mod 256) after the previous one, so the two rows an
