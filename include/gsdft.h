@@ -273,7 +273,10 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
  * omega > 0 is the long-range exchange E_K[erf(omega r)/r] of range-separated hybrids
  * (gs_dft/ks/terms.py:258-264): the three-centre integrals then use the 12-node Gauss-Legendre rule
  * on [0, omega] (ri.py:231-235) and chol must factor the erf metric (gsdft_aux_metric with the
- * same omega). Writes energy (one device double); with non-null dquat also
+ * same omega). Entries of one unordered splat pair ((i, j) and (j, i), repeats included) share
+ * their product Gaussian, so each (P|a) is formed once per such pair and serves all its entries
+ * (the result equals the entry-by-entry sum to round-off). The call never waits on the host
+ * (the stream's work is only queued). Writes energy (one device double); with non-null dquat also
  * dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
 int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, int symmetric,
                                   int grads, int64_t aux_chunk, int recompute, size_t* bytes);
