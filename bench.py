@@ -155,7 +155,9 @@ def main() -> int:
     metric_ms = _lib.profile_read(_lib.PROF_METRIC, reset=True)[0]
     chol_ms = _lib.profile_read(_lib.PROF_CHOLESKY, reset=True)[0]
     log(f"refresh: n_pairs={n} pad={pad_to} total {t_refresh * 1e3:.1f} ms "
-        f"(screen kernels {screen_ms:.1f} ms, metric {metric_ms:.1f} ms, cholesky {chol_ms:.1f} ms)")
+        f"(screening call {screen_ms:.1f} ms between its events, the first call's code loading "
+        f"and count read-back included -- bench.py --term screen times the kernels; metric "
+        f"{metric_ms:.1f} ms, cholesky {chol_ms:.1f} ms)")
 
     # ------------------------------------------------------------------ step
     def step():
