@@ -118,6 +118,42 @@ def test_exchange_repeated_entries(g, wl, orc, tr, cuda, aux_chunk):
         assert e < REL_G
 
 
+@pytest.mark.parametrize("case", ["one_self_pair", "self_pairs_only", "one_pair_both_ways"])
+def test_exchange_tiny_lists(g, wl, orc, tr, cuda, case):
+    """Lists of one or a few groups: a single self pair, self pairs only, and one off-diagonal
+    pair listed both ways (a single group of two entries) -- E_K and gradients against the
+    oracle and the torch literal."""
+    k = 3
+    s = wl.make_small(12, k, n_atoms=2, seed=21)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    if case == "one_self_pair":
+        pi, pj = np.array([4]), np.array([4])
+    elif case == "self_pairs_only":
+        pi = pj = np.arange(s.M)
+    else:
+        pi, pj = np.array([2, 7]), np.array([7, 2])
+    pi, pj = pi.astype(np.int32), pj.astype(np.int32)
+    w = np.ones(len(pi))
+    basis, C = _basis(g, s), _cu(s.C, True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    E = g.df_exchange_energy_screened(basis, C, aux, torch.tensor(pi, device="cuda"),
+                                      torch.tensor(pj, device="cuda"), lam=1e-8,
+                                      valid=torch.tensor(w, device="cuda"))
+    Eo, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, w, 1e-8)
+    err = abs(E.item() - Eo) / abs(Eo)
+    print(f"[exchange] {case}: n={len(pi)} E_K {E.item():.15e} oracle {Eo:.15e} rel {err:.2e}")
+    assert err < REL_E
+    E.backward()
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*leaves, _t(la), _t(ac), _idx(pi), _idx(pj), _t(w), 1e-8)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"),
+                          (basis.quat, basis.log_scale, basis.centers, C), leaves):
+        e = rel_max(_np(a.grad), b.grad.numpy())
+        print(f"[exchange] {case}: d{name} rel-to-max {e:.2e}")
+        assert e < REL_G
+
+
 def _lr_tolerance(cond):
     """Relative bound on E_K[erf(omega r)/r] between two correct evaluations: the erf metric is
     ill-conditioned (cond(V + lam I) ~ 1e9 at lam = 1e-8), and E_K inherits ~cond x eps from
