@@ -590,11 +590,12 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 
 
 // Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | per node t: s_t, wh_t,
-// s_t^2, 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored centre-grouped: with G = N / M exponent scales (the
-// product aux is scale-major, P = s M + m, every scale of splat m at one centre), the record of P
-// sits at slot m G + s, so the scales sharing a centre are consecutive; otherwise (N not a
-// multiple of M) in aux order. "first" is 1 where the centre differs bitwise from the previous slot's (or at slot 0):
-// the reverse kernel recomputes the centre-dependent terms only there, whatever the aux holds.
+// s_t^2, 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored
+// centre-grouped: with G = N / M exponent scales (the product aux is scale-major, P = s M + m,
+// every scale of splat m at one centre), the record of P sits at slot m G + s, so the scales
+// sharing a centre are consecutive; otherwise (N not a multiple of M) in aux order. "first" is 1
+// where the centre differs bitwise from the previous slot's (or at slot 0): the reverse kernel
+// recomputes the centre-dependent terms only there, whatever the aux holds.
 // (aux_slot / aux_of_slot: common.h)
 
 __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
@@ -2491,12 +2492,14 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
                                                              sp.per_slab, w.acc,
                                                              profile_work_counter(kProfGammaBwd),
-                                                             nullptr, 0, nullptr, nullptr, nullptr, nullptr);
+                                                             nullptr, 0, nullptr, nullptr,
+                                                             nullptr, nullptr);
         profile_end(kProfGammaBwd, s);
         GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPref3c, w.pair_order.perm, pi,
-                                                           pj, weight, w.A6, centers, w.Nrm,
-                                                           w.rec_sorted, w.acc, J, w.contrib);
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPref3c,
+                                                           w.pair_order.perm, pi, pj, weight,
+                                                           w.A6, centers, w.Nrm, w.rec_sorted,
+                                                           w.acc, J, w.contrib);
         GSDFT_HIP(hipGetLastError());
     }
     k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
