@@ -734,41 +734,47 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     const int64_t p0 = blockIdx.y * per_slab;
     const int64_t p1 = min(N, p0 + per_slab);
     uint32_t nodes = 0;
-    // kLaneU: the lane's summed cotangents of the next records, fetched four records at a time
-    // (two 16-byte loads per row when the rows and the slab start are 16-byte aligned) and
-    // shifted down one record per step; each sum adds the rows in order, as one record at a time
-    double ub[4] = {0.0, 0.0, 0.0, 0.0};
+    // kLaneU: the lane's summed cotangents of the next kUb records, fetched kUb records at a time
+    // (16-byte loads, half a cache line per row, when the rows and the slab start are 16-byte
+    // aligned) and shifted down one record per step; each sum adds the rows in order, as one
+    // record at a time would. kUb = 4 (a quarter line per refill) was 2.5% slower; 16 (a whole
+    // line) cost a wave per SIMD and was 8% slower.
+    constexpr int kUb = 8;
+    double ub[kUb];
+#pragma unroll
+    for (int j = 0; j < kUb; ++j) ub[j] = 0.0;
     const bool uvec = kLaneU && (ldu % 2 == 0) && (p0 % 2 == 0) &&
                       (reinterpret_cast<uintptr_t>(ut) % 16 == 0);
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
         double u = x[3];
         if constexpr (kLaneU) {
-            if (((p - p0) & 3) == 0) {                 // wave-uniform
-                ub[0] = ub[1] = ub[2] = ub[3] = 0.0;
-                if (uvec && p + 4 <= p1) {
+            if (((p - p0) % kUb) == 0) {                 // wave-uniform
+#pragma unroll
+                for (int j = 0; j < kUb; ++j) ub[j] = 0.0;
+                if (uvec && p + kUb <= p1) {
                     for (int e = 0; e < utn; ++e) {
                         const double2* row = reinterpret_cast<const double2*>(
                             ut + (ut0 + e) * ldu + p);
-                        const double2 v0 = row[0], v1 = row[1];
-                        ub[0] += v0.x;
-                        ub[1] += v0.y;
-                        ub[2] += v1.x;
-                        ub[3] += v1.y;
+#pragma unroll
+                        for (int j = 0; j < kUb / 2; ++j) {
+                            const double2 v = row[j];
+                            ub[2 * j] += v.x;
+                            ub[2 * j + 1] += v.y;
+                        }
                     }
                 } else {
                     for (int e = 0; e < utn; ++e) {
                         const double* row = ut + (ut0 + e) * ldu;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
+                        for (int j = 0; j < kUb; ++j)
                             if (p + j < p1) ub[j] += row[p + j];
                     }
                 }
             }
             u *= ub[0];
-            ub[0] = ub[1];
-            ub[1] = ub[2];
-            ub[2] = ub[3];
+#pragma unroll
+            for (int j = 0; j + 1 < kUb; ++j) ub[j] = ub[j + 1];
         }
         if (p == p0 || new_centre(x)) {          // wave-uniform
             flush();
