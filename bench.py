@@ -661,6 +661,15 @@ def run_exchange(args) -> int:
             ("triangular solves (rocBLAS dtrsm)", trsm_ms, 2 * trsm, "mfma")]
     dom = max(fams, key=lambda f: f[1])
     dom_tf = dom[2] / (dom[1] * 1e-3)
+    # HBM bytes per launch (one aux chunk) of the dominant kernel, from the counter runs
+    traffic = None
+    tkey = {"three-centre reverse": "k_gamma_bwd_lane_u",
+            "three-centre block": "k_exch_block_pairs"}.get(dom[0].split(" (")[0])
+    tfile = ROOT / "profiles" / "exchange_traffic.json"
+    if tkey and tfile.exists():
+        rec = json.loads(tfile.read_text()).get(s.name, {}).get(tkey)
+        if rec:
+            traffic = rec["fetch_bytes"] + rec["write_bytes"]
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -713,7 +722,7 @@ def run_exchange(args) -> int:
                    "eps": s.eps, "parallelism": "single GPU"},
         "roofline": {"bound": dom[3], "kernel": dom[0], "achieved": dom_tf / 1e12,
                      "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom_tf / PEAK_FP64,
-                     "traffic": None, "flops_per_step": dom[2], "kernel_ms_per_step": dom[1],
+                     "traffic": traffic, "flops_per_step": dom[2], "kernel_ms_per_step": dom[1],
                      "note": "per step, summed over the chunk launches; algorithmic flops: "
                              "N n x 419 (block), N n x 780 (reverse), 4 N n k (Y = T C and "
                              "Tbar), 6 N M k^2 (GEMMs), 2 N^2 K2 (solves); FP64 peak 78.6 "
@@ -722,7 +731,9 @@ def run_exchange(args) -> int:
                              "unordered splat pair (half of them on a symmetric list) and once "
                              "per node the screen keeps, so the algorithmic fraction credits "
                              "both as done and can pass 1; reverse_nodes_evaluated_frac is "
-                             "the executed share of N n x 20 nodes"},
+                             "the executed share of N n x 20 nodes; traffic is the dominant "
+                             "kernel's HBM bytes per launch (one aux chunk) from the counter "
+                             "runs in profiles/"},
         "kernels": {"trsm_ms_per_step": trsm_ms, "trsm_tflops": trsm_tf / 1e12,
                     "gemm_ms_per_step": gemm_ms, "gemm_tflops": gemm_tf / 1e12,
                     "block_ms_per_step": blk_ms, "reverse_ms_per_step": rev_ms,
