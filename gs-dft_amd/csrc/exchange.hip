@@ -325,8 +325,7 @@ __global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int
         auto load_idx = [&](int64_t rb) {
             if (lane < 4) idx = col[clampr(rb + wave + 4 * lane)];
         };
-        auto load_c = [&](int64_t rb) {
-            (void)rb;
+        auto load_c = [&]() {                  // the tile whose columns idx holds
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t c = __builtin_amdgcn_readlane(idx, j);
@@ -344,7 +343,7 @@ __global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int
             }
         };
         load_idx(r0);
-        load_c(r0);
+        load_c();
         load_idx(r0 + kSdPairs);
         int64_t orow = inv[perm[clampr(r0 + c16)]];    // Tbar row of this lane's pair
         int32_t pnext = perm[clampr(r0 + kSdPairs + c16)];      // its pair in the next tile
@@ -355,7 +354,7 @@ __global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int
             // the next tiles' loads run unconditionally (clamped, so past the last tile they read
             // the row's last pair and go unused): no branch splits the loop body, and every index
             // a load needs arrived an iteration earlier
-            load_c(rb + kSdPairs);
+            load_c();
             load_idx(rb + 2 * kSdPairs);
             const int32_t pn2 = perm[clampr(rb + 2 * kSdPairs + c16)];
             v4d acc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
