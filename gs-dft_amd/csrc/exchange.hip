@@ -113,10 +113,10 @@ __global__ __launch_bounds__(256) void k_exch_spmm(int64_t W, int64_t k, int64_t
     // Stage at CSR position rs: wave w loads pairs w + 4 j (j < kSpPairs / 4) into registers. The
     // pairs' indices come one stage earlier from one vector load (lane j: perm, lane kPw + j: col;
     // vector rather than scalar loads, whose counter the LDS reads of the MFMAs share) and are
-    // broadcast with readlane. Every load reads an in-range address (positions past the row clamped to its
-    // last one, columns past W to W - 1, C columns past the block to its last); the values that
-    // stand for nothing are zeroed when the stage is written to LDS, so the loads stay in flight
-    // through the current stage's MFMAs.
+    // broadcast with readlane. Every load reads an in-range address (positions past the row
+    // clamped to its last one, columns past W to W - 1, C columns past the block to its last);
+    // the values that stand for nothing are zeroed when the stage is written to LDS, so the
+    // loads stay in flight through the current stage's MFMAs.
     constexpr int kPw = kSpPairs / 4;                           // pairs per wave and stage
     double sa[kPw][2], sc[kPw][2];
     int64_t staged = 0;                                         // position of the loaded stage
@@ -284,15 +284,16 @@ constexpr int kSdPairs = 16;
 __host__ __device__ constexpr int sd_ld_c(int ns) { return 4 * ns + (36 - (4 * ns) % 32) % 32; }
 
 template <int NS>
-__global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int64_t kp, int64_t ldt,
-                                                    int64_t oc_begin, int64_t oc_end, int first,
-                                                    const int32_t* __restrict__ ptr,
-                                                    const int32_t* __restrict__ perm,
-                                                    const int32_t* __restrict__ col,
-                                                    const int32_t* __restrict__ inv,
-                                                    const double* __restrict__ Ybar,
-                                                    const double* __restrict__ Cp,
-                                                    double* __restrict__ Tbar) {
+__global__ __launch_bounds__(256, 3) void k_exch_sddmm(int64_t W, int64_t k, int64_t kp,
+                                                     int64_t ldt, int64_t oc_begin,
+                                                     int64_t oc_end, int first,
+                                                     const int32_t* __restrict__ ptr,
+                                                     const int32_t* __restrict__ perm,
+                                                     const int32_t* __restrict__ col,
+                                                     const int32_t* __restrict__ inv,
+                                                     const double* __restrict__ Ybar,
+                                                     const double* __restrict__ Cp,
+                                                     double* __restrict__ Tbar) {
     constexpr int kW = 4 * NS;                  // orbitals per pass
     constexpr int kLd = sd_ld_c(NS);
     __shared__ double Cs[2][kSdPairs][kLd];
@@ -533,12 +534,23 @@ int launch_spmm(int64_t M, int64_t W, int64_t k, int64_t ldb, const int32_t* ptr
     if (tail > 0) {
         dim3 grid((unsigned)M, nblk(W, 4 * kMfAux), 1);
         const int64_t ob = full * kMfOrb;
+        // the remainder pass: 16 * tail orbitals
         switch (tail) {
-        case 1: k_exch_spmm<1><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
-        case 2: k_exch_spmm<2><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
-        case 3: k_exch_spmm<3><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
-        case 4: k_exch_spmm<4><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
-        default: k_exch_spmm<5><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y); break;
+        case 1:
+            k_exch_spmm<1><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y);
+            break;
+        case 2:
+            k_exch_spmm<2><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y);
+            break;
+        case 3:
+            k_exch_spmm<3><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y);
+            break;
+        case 4:
+            k_exch_spmm<4><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y);
+            break;
+        default:
+            k_exch_spmm<5><<<grid, 256, 0, s>>>(W, k, kp, ldb, ob, ptr, perm, col, Bt, Cp, Y);
+            break;
         }
     }
     profile_end(kProfExchSparse, s);
@@ -698,9 +710,11 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
             Ypc = sym ? nullptr : w.Yps + M * q0 * k;
         } else {
             GSDFT_TRY(exch_tc_block(M, N, q0, W, aux_centers, n, Pc, w.Bt, w.tc, s));
-            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, w.Y, s));
+            GSDFT_TRY(launch_spmm(M, W, k, Pc, row_ptr, w.row_grp, w.row_col, w.Bt, w.Cp, w.Y,
+                                  s));
             if (!sym)
-                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp, w.Yp, s));
+                GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp,
+                                      w.Yp, s));
         }
         profile_begin(kProfExchGemm, s);
         // dC += Y_P Dbar_P^T (+ Y'_P Dbar_P; the same term again on a symmetric list)

@@ -30,7 +30,8 @@ extern "C" {
 #define GSDFT_ERR_HIP 4          /* HIP runtime error                                           */
 #define GSDFT_ERR_LIB 5          /* rocBLAS / hipCUB error                                      */
 #define GSDFT_ERR_WORKSPACE 6    /* workspace too small; the query names the size               */
-#define GSDFT_ERR_FALLBACK 7     /* spatial screening: the list overflows its pad (use the dense build) */
+#define GSDFT_ERR_FALLBACK 7     /* spatial screening: the list overflows its pad (use the dense
+                                    build) */
 
 int gsdft_abi_version(void);
 const char* gsdft_last_error(void);
@@ -293,16 +294,16 @@ int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const
 /* Kernel timing with HIP events on the launch stream (no reference counterpart). Ids:
  * 0 three-centre forward, 1 three-centre reverse, 2 screening, 3 metric, 4 Cholesky, 5 solve,
  * 6 nuclear attraction per pair (values, splat moments and, with nuclear gradients, each pair
- * block's forces on the nuclei), 7 nuclear attraction per nucleus (the fixed-order force sums), 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and
- * gradient moments), 10 exchange three-centre block, 11 exchange three-centre reverse, 12
- * exchange triangular solves (rocBLAS), 13 exchange GEMMs (rocBLAS), 14 exchange pair-sparse
- * products (Y = T C and the sampled Tbar). gsdft_profile_read
- * synchronises the recorded events and returns the summed milliseconds and the launch count since
- * the last reset. gsdft_profile_read_work returns the
+ * block's forces on the nuclei), 7 nuclear attraction per nucleus (the fixed-order force sums),
+ * 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and gradient moments),
+ * 10 exchange three-centre block, 11 exchange three-centre reverse, 12 exchange triangular
+ * solves (rocBLAS), 13 exchange GEMMs (rocBLAS), 14 exchange pair-sparse products (Y = T C and
+ * the sampled Tbar). gsdft_profile_read synchronises the recorded events and returns the summed
+ * milliseconds and the launch count since the last reset. gsdft_profile_read_work returns the
  * work units the kernels executed while profiling was on (ids 0, 1, 6-11: quadrature nodes
  * evaluated, summed over live lanes, so at most 20 x (aux functions, nuclei or pairs) x pairs
- * per launch; other ids: 0). Profiling allocates a few bytes of
- * device memory on the device current when it is first enabled. */
+ * per launch; other ids: 0). Profiling allocates a few bytes of device memory on the device
+ * current when it is first enabled. */
 int gsdft_profile_enable(int on);
 int gsdft_profile_read(int id, double* total_ms, int64_t* launches, int reset);
 int gsdft_profile_read_work(int id, uint64_t* units, int reset);
