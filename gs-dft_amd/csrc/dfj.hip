@@ -2120,64 +2120,103 @@ constexpr int kPackedTri = kPanelRows * (kPanelRows + 1) / 2;
 __global__ void k_info_reset(int64_t* __restrict__ info) { *info = 0; }
 
 // Unblocked upper Cholesky of one ib x ib diagonal block (ib <= 128; column-major, leading
-// dimension N, A(r, c) at A[c N + r] for r <= c), in place, staged in LDS (As[c][r] = A(r, c)).
-// Step j subtracts A(j, r) A(j, c) / A(j, j) from A(r, c) for j < r <= c (one barrier per step);
-// the rows are scaled at the end: U(j, j) = sqrt(A(j, j)), U(j, c) = A(j, c) / U(j, j). A pivot that
-// is not positive records base + j + 1 in *info unless an earlier minor has failed (the factor is
-// then meaningless, as with any failed factorisation).
+// dimension N, A(r, c) at A[c N + r] for r <= c), in place. Step j subtracts A(j, r) A(j, c) / A(j, j)
+// from A(r, c) for j < r <= c; the rows are scaled at the end: U(j, j) = sqrt(A(j, j)),
+// U(j, c) = A(j, c) / U(j, j). A pivot that is not positive records base + j + 1 in *info unless an
+// earlier minor has failed (the factor is then meaningless, as with any failed factorisation).
+// Thread t holds column c = t % 128 in registers: during block J of eight steps, v[i] is row
+// rg + 8 (J + i) of the row group rg = t / 128 (wave-uniform); at the end of the block v[0] is
+// final, goes to LDS, and the registers shift down. Step j reads row j from LDS, where the threads
+// holding it published it at the end of step j - 1 (it is final then), in one of two buffers, so
+// each step takes one barrier. The published row keeps A(j, c) at (c % 8) 16 + c / 8, so a
+// thread's 16 rows are 16 consecutive entries: all are read at once, unconditionally, and the
+// registers past the last row take updates that are never stored (rows past 127 read the padding).
+// Every FMA of a stored entry is the one the right-looking order applies, in the same order, so
+// the factor does not depend on the thread layout. Steps past ib run on the zero padding: they
+// touch only columns >= ib, which are never stored or read. The block is staged through LDS so the
+// global loads and stores stay coalesced.
 __global__ __launch_bounds__(kPotfThreads) void k_potf2(int64_t N, double* __restrict__ A, int ib,
                                                         int64_t base,
                                                         int64_t* __restrict__ info) {
+    constexpr int kLoads = kPanelRows * kPanelRows / kPotfThreads;  // rows per thread (16)
+    constexpr int kGroups = kPotfThreads / kPanelRows;              // row groups (8)
+    static_assert(kLoads * kGroups == kPanelRows, "one register per row of the thread's group");
+    constexpr int kRowPad = kPanelRows + kLoads;
     __shared__ double As[kPanelRows][kPanelRows + 1];
+    __shared__ double rowj[2][kRowPad];
     __shared__ double sq[kPanelRows];
-    __shared__ int bad;
-    constexpr int kLoads = kPanelRows * kPanelRows / kPotfThreads;
     const int t = threadIdx.x;
+    {
+        double w[kLoads];
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) {
+            const int e = t + q * kPotfThreads, c = e >> 7, r = e & (kPanelRows - 1);
+            w[q] = (c < ib && r <= c) ? A[c * N + r] : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) {
+            const int e = t + q * kPotfThreads;
+            As[e >> 7][e & (kPanelRows - 1)] = w[q];
+        }
+    }
+    if (t < 2 * kLoads) rowj[t / kLoads][kPanelRows + t % kLoads] = 0.0;
+    __syncthreads();
+    const int c = t & (kPanelRows - 1);
+    const int pc = (c % kGroups) * kLoads + c / kGroups;          // c's place in a published row
+    const int rg = __builtin_amdgcn_readfirstlane(t >> 7);
     double v[kLoads];
 #pragma unroll
-    for (int q = 0; q < kLoads; ++q) {
-        const int e = t + q * kPotfThreads, c = e >> 7, r = e & (kPanelRows - 1);
-        v[q] = (c < ib && r <= c) ? A[c * N + r] : 0.0;
-    }
-#pragma unroll
-    for (int q = 0; q < kLoads; ++q) {
-        const int e = t + q * kPotfThreads;
-        As[e >> 7][e & (kPanelRows - 1)] = v[q];
-    }
-    if (t == 0) bad = 0;
+    for (int i = 0; i < kLoads; ++i) v[i] = As[c][rg + kGroups * i];
+    if (t < kPanelRows) rowj[0][pc] = As[c][0];
     __syncthreads();
-    const int cc = t & (kPanelRows - 1), rg = t >> 7;      // column, row group (8 groups)
-    for (int j = 0; j < ib; ++j) {
-        const double piv = As[j][j];
-        if (t == 0 && !(piv > 0.0) && bad == 0) bad = j + 1;
-        if (cc > j && cc < ib) {
-            const double uc = As[cc][j] / piv;
-            for (int r = j + 1 + rg; r <= cc; r += kPotfThreads / kPanelRows)
-                As[cc][r] = __builtin_fma(-As[r][j], uc, As[cc][r]);
+    int bad = 0;                                  // thread 0: first failing step + 1
+    for (int j = 0; j < kPanelRows; ++j) {
+        const int J = j / kGroups, jj = j % kGroups;
+        const double* __restrict__ rw = rowj[j & 1];
+        const double piv = rw[jj * kLoads + J];
+        if (t == 0 && j < ib && !(piv > 0.0) && bad == 0) bad = j + 1;
+        if (c > j) {
+            const double uc = rw[pc] / piv;
+            const double* __restrict__ rr = rw + rg * kLoads + J;   // rows rg + 8 (J + i)
+            double a[kLoads];
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) a[i] = rr[i];
+            if (rg > jj) v[0] = __builtin_fma(-a[0], uc, v[0]);    // rows j < r only
+#pragma unroll
+            for (int i = 1; i < kLoads; ++i) v[i] = __builtin_fma(-a[i], uc, v[i]);
         }
+        if (jj == kGroups - 1) {                  // row rg + 8 J is final
+            As[c][rg + kGroups * J] = v[0];
+#pragma unroll
+            for (int i = 0; i + 1 < kLoads; ++i) v[i] = v[i + 1];
+            v[kLoads - 1] = 0.0;
+        }
+        // publish row j + 1 (in v[0] of row group (j + 1) % 8)
+        if (j + 1 < kPanelRows && rg == (j + 1) % kGroups) rowj[(j + 1) & 1][pc] = v[0];
         __syncthreads();
     }
     if (t < ib) sq[t] = sqrt(As[t][t]);
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kLoads; ++q) {
-        const int e = t + q * kPotfThreads, c = e >> 7, r = e & (kPanelRows - 1);
-        if (c < ib && r <= c) A[c * N + r] = r == c ? sq[r] : As[c][r] / sq[r];
+        const int e = t + q * kPotfThreads, cc = e >> 7, r = e & (kPanelRows - 1);
+        if (cc < ib && r <= cc) A[cc * N + r] = r == cc ? sq[r] : As[cc][r] / sq[r];
     }
     if (t == 0 && bad != 0 && *info == 0) *info = base + bad;
 }
-
-constexpr int kSubstCols = 16;      // panel columns per wave of the panel solve
 
 // Offset of row c of a 128 x 128 upper triangle packed by rows (row c holds columns c..127).
 __device__ __forceinline__ int tri_row(int c) { return c * kPanelRows - c * (c - 1) / 2; }
 
 // X <- U^-T X for one diagonal block: U is ib x ib upper (column-major, leading dimension N; U(c, r)
 // at U[r N + c]), X is ib x T (column-major, leading dimension N). U's upper triangle is staged in
-// LDS packed by rows (zero past ib). Each wave solves 16 columns of X by column-oriented
-// substitution: lane l holds rows l and l + 64 of the 16 columns in registers; at step c the owner
-// lane's x_c = acc * (1 / U(c, c)) is broadcast with readlane and every row r > c takes
-// -U(c, r) x_c. Rows past ib carry zeros and a zero reciprocal, so all 128 steps run.
+// LDS packed by rows (zero past ib). Each wave solves NC columns of X by column-oriented
+// substitution (NC = 16 for wide panels, fewer for narrow ones, whose launches are
+// latency-bound and need the waves): lane l holds rows l and l + 64 of the NC columns in
+// registers; at step c the owner lane's x_c = acc * (1 / U(c, c)) is broadcast with readlane and
+// every row r > c takes -U(c, r) x_c. Rows past ib carry zeros and a zero reciprocal, so all 128
+// steps run.
+template <int NC>
 __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __restrict__ U,
                                                      int ib, double* __restrict__ X, int64_t T) {
     __shared__ double Us[kPackedTri];
@@ -2189,11 +2228,11 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
         if (l <= r) Us[tri_row(l) + r - l] = r < ib ? ur[l] : 0.0;
         if (l + 64 <= r) Us[tri_row(l + 64) + r - l - 64] = r < ib ? ur[l + 64] : 0.0;
     }
-    const int64_t jw = (int64_t)blockIdx.x * (4 * kSubstCols) + wv * kSubstCols;
+    const int64_t jw = (int64_t)blockIdx.x * (4 * NC) + wv * NC;
     const bool h0 = l < ib, h1 = l + 64 < ib;
-    double acc0[kSubstCols], acc1[kSubstCols];
+    double acc0[NC], acc1[NC];
 #pragma unroll
-    for (int k = 0; k < kSubstCols; ++k) {
+    for (int k = 0; k < NC; ++k) {
         const bool live = jw + k < T;
         const double* col = X + (jw + k) * N;
         acc0[k] = live && h0 ? col[l] : 0.0;
@@ -2207,7 +2246,7 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
         const double u0 = l > c ? Us[tri_row(c) + l - c] : 0.0;
         const double u1 = Us[tri_row(c) + l + 64 - c];
 #pragma unroll
-        for (int k = 0; k < kSubstCols; ++k) {
+        for (int k = 0; k < NC; ++k) {
             const double x = readlane_f64(acc0[k] * rd0, c);
             acc0[k] = __builtin_fma(-u0, x, acc0[k]);
             acc1[k] = __builtin_fma(-u1, x, acc1[k]);
@@ -2217,13 +2256,13 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
     for (int c = 64; c < kPanelRows; ++c) {
         const double u1 = l + 64 > c ? Us[tri_row(c) + l + 64 - c] : 0.0;
 #pragma unroll
-        for (int k = 0; k < kSubstCols; ++k) {
+        for (int k = 0; k < NC; ++k) {
             const double x = readlane_f64(acc1[k] * rd1, c - 64);
             acc1[k] = __builtin_fma(-u1, x, acc1[k]);
         }
     }
 #pragma unroll
-    for (int k = 0; k < kSubstCols; ++k) {
+    for (int k = 0; k < NC; ++k) {
         if (jw + k >= T) continue;
         double* col = X + (jw + k) * N;
         if (h0) col[l] = acc0[k] * rd0;
@@ -2232,22 +2271,30 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
 }
 
 // P <- U^-T P for the kb x kb upper factor U at Akk and the kb x T panel P (both column-major,
-// leading dimension N), by blocked substitution: each 128-row block is solved by k_panel_subst and
-// applied to the rows below it by an FP64 MFMA product. Backward stable, unlike a solve through
+// leading dimension N), by recursive blocked substitution: the top h rows (h a multiple of 128,
+// about half) are solved, their part of every lower row is subtracted with one FP64 MFMA product
+// (K = h), and the bottom rows are solved; 128-row blocks are solved by k_panel_subst. The halving
+// keeps most of the product work at large K, so each element of P is read and written about
+// log2(kb / 128) times instead of once per 128-row block. Backward stable, unlike a solve through
 // explicit inverses of the diagonal blocks, whose error grows with their condition number.
 static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, double* P,
                        int64_t T) {
-    for (int64_t i0 = 0; i0 < kb; i0 += kPanelRows) {
-        const int ib = (int)std::min((int64_t)kPanelRows, kb - i0);
-        k_panel_subst<<<(unsigned)((T + 4 * kSubstCols - 1) / (4 * kSubstCols)), 256, 0, s>>>(
-            N, Akk + i0 * N + i0, ib, P + i0, T);
+    if (kb <= kPanelRows) {
+        // columns per wave: keep about two waves per SIMD in flight
+        if (T >= 32768)
+            k_panel_subst<16><<<(unsigned)((T + 63) / 64), 256, 0, s>>>(N, Akk, (int)kb, P, T);
+        else if (T >= 16384)
+            k_panel_subst<8><<<(unsigned)((T + 31) / 32), 256, 0, s>>>(N, Akk, (int)kb, P, T);
+        else
+            k_panel_subst<4><<<(unsigned)((T + 15) / 16), 256, 0, s>>>(N, Akk, (int)kb, P, T);
         GSDFT_HIP(hipGetLastError());
-        // P(i0 + ib + m, c) -= sum_r U(i0 + r, i0 + ib + m) P(i0 + r, c)
-        if (i0 + ib < kb)
-            GSDFT_TRY(launch_gemm_tn_sub(kb - i0 - ib, T, ib, Akk + (i0 + ib) * N + i0, N,
-                                         P + i0, N, P + i0 + ib, N, false, s));
+        return GSDFT_OK;
     }
-    return GSDFT_OK;
+    const int64_t h = (kb / kPanelRows + 1) / 2 * kPanelRows;
+    GSDFT_TRY(panel_solve(s, N, Akk, h, P, T));
+    // P(h + m, c) -= sum_{r < h} U(r, h + m) P(r, c)
+    GSDFT_TRY(launch_gemm_tn_sub(kb - h, T, h, Akk + h * N, N, P, N, P + h, N, false, s));
+    return panel_solve(s, N, Akk + h * N + h, kb - h, P + h, T);
 }
 
 // C (T x T at C, leading dimension N) -= P^T P for the kb x T panel P, on the tiles on or above
