@@ -2115,15 +2115,15 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
 
 constexpr int kPanelRows = 128;     // rows per diagonal block (inner factorisation, panel solve)
 constexpr int kPotfThreads = 1024;
-constexpr int kPackedTri = kPanelRows * (kPanelRows + 1) / 2;
 
 __global__ void k_info_reset(int64_t* __restrict__ info) { *info = 0; }
 
 // Unblocked upper Cholesky of one ib x ib diagonal block (ib <= 128; column-major, leading
-// dimension N, A(r, c) at A[c N + r] for r <= c), in place. Step j subtracts A(j, r) A(j, c) / A(j, j)
-// from A(r, c) for j < r <= c; the rows are scaled at the end: U(j, j) = sqrt(A(j, j)),
-// U(j, c) = A(j, c) / U(j, j). A pivot that is not positive records base + j + 1 in *info unless an
-// earlier minor has failed (the factor is then meaningless, as with any failed factorisation).
+// dimension N, A(r, c) at A[c N + r] for r <= c), in place. Step j subtracts
+// A(j, r) A(j, c) / A(j, j) from A(r, c) for j < r <= c; the rows are scaled at the end:
+// U(j, j) = sqrt(A(j, j)), U(j, c) = A(j, c) / U(j, j). A pivot that is not positive records
+// base + j + 1 in *info unless an earlier minor has failed (the factor is then meaningless, as
+// with any failed factorisation).
 // Thread t holds column c = t % 128 in registers: during block J of eight steps, v[i] is row
 // rg + 8 (J + i) of the row group rg = t / 128 (wave-uniform); at the end of the block v[0] is
 // final, goes to LDS, and the registers shift down. Step j reads row j from LDS, where the threads
@@ -2205,69 +2205,121 @@ __global__ __launch_bounds__(kPotfThreads) void k_potf2(int64_t N, double* __res
     if (t == 0 && bad != 0 && *info == 0) *info = base + bad;
 }
 
-// Offset of row c of a 128 x 128 upper triangle packed by rows (row c holds columns c..127).
-__device__ __forceinline__ int tri_row(int c) { return c * kPanelRows - c * (c - 1) / 2; }
+// X <- U^-T X for one diagonal block on the FP64 MFMA: U is ib x ib upper (column-major, leading
+// dimension N; U(c, r) at U[r N + c]), X is ib x T (column-major, leading dimension N). Each wave
+// holds 16 columns of X as eight 16 x 16 accumulator tiles, one per 16-row block
+// (v_mfma_f64_16x16x4f64 layout: lane l holds rows l / 16 + 4 r, r < 4, of column l % 16). Block
+// b is solved row by row on the VALU (x_i = acc * (1 / U(i, i)), broadcast from the lane group
+// holding row i to all four with two permlane swaps, every row i' > i of the block takes
+// -U(i, i') x_i), then every later block b' takes -U(b rows, b' columns)^T X_b in four MFMAs whose
+// B operand is the solved tile's register r as it stands (row 4 r + l / 16). The MFMA adds its
+// four products in order with a rounding each, so every entry gets the same FMAs in the same
+// order as a row-by-row substitution. The 28 strictly-upper 16 x 16 tiles of U (negated) and the
+// eight diagonal tiles (arranged so a lane reads its four rows' entries as one 32-byte run, zero
+// on and below the diagonal) are staged in LDS once per workgroup, with the reciprocals of the
+// diagonal. Rows past ib and columns past T are zero and not stored; every load reads an
+// in-range address.
+typedef double v4d_sub __attribute__((ext_vector_type(4)));
+constexpr int kSubTiles = 28;
+__host__ __device__ constexpr int sub_tile(int a, int b) { return b * (b - 1) / 2 + a; }
 
-// X <- U^-T X for one diagonal block: U is ib x ib upper (column-major, leading dimension N; U(c, r)
-// at U[r N + c]), X is ib x T (column-major, leading dimension N). U's upper triangle is staged in
-// LDS packed by rows (zero past ib). Each wave solves NC columns of X by column-oriented
-// substitution (NC = 16 for wide panels, fewer for narrow ones, whose launches are
-// latency-bound and need the waves): lane l holds rows l and l + 64 of the NC columns in
-// registers; at step c the owner lane's x_c = acc * (1 / U(c, c)) is broadcast with readlane and
-// every row r > c takes -U(c, r) x_c. Rows past ib carry zeros and a zero reciprocal, so all 128
-// steps run.
-template <int NC>
+// f(std::integral_constant<int, i>) for i = I, ..., N - 1.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// v broadcast from the 16-lane group g (compile-time) to all four groups of the wave.
+template <int g>
+__device__ __forceinline__ double group_bcast(double v) {
+    double lo = v, hi = v;
+    swap32(lo, hi);                 // lo: lanes 0-31 twice, hi: lanes 32-63 twice
+    double w = g < 2 ? lo : hi;
+    double e = w, o = w;
+    swap16(e, o);                   // e: rows 0 and 2 of each half twice, o: rows 1 and 3
+    return g % 2 == 0 ? e : o;
+}
+
 __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __restrict__ U,
                                                      int ib, double* __restrict__ X, int64_t T) {
-    __shared__ double Us[kPackedTri];
-    const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __shared__ double Ut[kSubTiles][16][16];    // Ut[(a, b)][k][c] = -U(16 a + k, 16 b + c)
+    __shared__ double Ud[8][16][16];            // Ud[b][i][4 g + r] = U(16 b + i, 16 b + g + 4 r)
+    __shared__ double rdg[kPanelRows];
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int r0 = 0; r0 < kPanelRows; r0 += 4) {
-        const int r = r0 + wv;
-        const double* ur = U + (int64_t)r * N;
-        if (l <= r) Us[tri_row(l) + r - l] = r < ib ? ur[l] : 0.0;
-        if (l + 64 <= r) Us[tri_row(l + 64) + r - l - 64] = r < ib ? ur[l + 64] : 0.0;
-    }
-    const int64_t jw = (int64_t)blockIdx.x * (4 * NC) + wv * NC;
-    const bool h0 = l < ib, h1 = l + 64 < ib;
-    double acc0[NC], acc1[NC];
+    for (int b = 1; b < 8; ++b)
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-        const bool live = jw + k < T;
-        const double* col = X + (jw + k) * N;
-        acc0[k] = live && h0 ? col[l] : 0.0;
-        acc1[k] = live && h1 ? col[l + 64] : 0.0;
+        for (int a = 0; a < b; ++a) {
+            const int k = t & 15, c = t >> 4, row = 16 * a + k, col = 16 * b + c;
+            const double v = U[(int64_t)min(col, ib - 1) * N + min(row, ib - 1)];
+            Ut[sub_tile(a, b)][k][c] = (row < ib && col < ib) ? -v : 0.0;
+        }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const int i = t >> 4, sl = t & 15, ip = (sl >> 2) + 4 * (sl & 3);
+        const int row = 16 * b + i, col = 16 * b + ip;
+        const double v = U[(int64_t)min(col, ib - 1) * N + min(row, ib - 1)];
+        Ud[b][i][sl] = (ip > i && row < ib && col < ib) ? v : 0.0;
     }
+    if (t < kPanelRows) rdg[t] = t < ib ? 1.0 / U[(int64_t)t * N + t] : 0.0;
+    const int l = t & 63, g = l >> 4;
+    const int64_t cc = (int64_t)blockIdx.x * 64 + (t >> 6) * 16 + (l & 15);
+    const bool live = cc < T;
+    // every load reads an in-range address (columns past T and rows past ib clamped to the
+    // last ones); the values that stand for nothing are zeroed
+    const double* __restrict__ xc = X + (live ? cc : T - 1) * N;
+    v4d_sub C[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * b + g + 4 * r;
+            const double v = xc[row < ib ? row : ib - 1];
+            C[b][r] = (live && row < ib) ? v : 0.0;
+        }
     __syncthreads();
-    const double rd0 = h0 ? 1.0 / Us[tri_row(l)] : 0.0;
-    const double rd1 = h1 ? 1.0 / Us[tri_row(l + 64)] : 0.0;
-#pragma unroll 2
-    for (int c = 0; c < 64; ++c) {
-        const double u0 = l > c ? Us[tri_row(c) + l - c] : 0.0;
-        const double u1 = Us[tri_row(c) + l + 64 - c];
 #pragma unroll
-        for (int k = 0; k < NC; ++k) {
-            const double x = readlane_f64(acc0[k] * rd0, c);
-            acc0[k] = __builtin_fma(-u0, x, acc0[k]);
-            acc1[k] = __builtin_fma(-u1, x, acc1[k]);
+    for (int b = 0; b < 8; ++b) {
+        // the block's reciprocals, lane j % 16 holding row j's (read with readlane), and each
+        // step's four U entries loaded one step ahead, so the row chain waits on no LDS read
+        const double rv = rdg[16 * b + (l & 15)];
+        double un[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) un[r] = Ud[b][0][4 * g + r];
+        auto step = [&](auto ic) {
+            constexpr int i = decltype(ic)::value, gi = i % 4, ri = i / 4;
+            double u[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) u[r] = un[r];
+            if constexpr (i + 1 < 16) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) un[r] = Ud[b][i + 1][4 * g + r];
+            }
+            const double x = C[b][ri] * readlane_f64(rv, i);
+            const double y = group_bcast<gi>(x);
+            if (g == gi) C[b][ri] = x;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) C[b][r] = __builtin_fma(-u[r], y, C[b][r]);
+        };
+        static_for<0, 16>(step);
+#pragma unroll
+        for (int b2 = b + 1; b2 < 8; ++b2)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                C[b2] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                    Ut[sub_tile(b, b2)][4 * kk + g][l & 15], C[b][kk], C[b2], 0, 0, 0);
+    }
+    if (!live) return;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * b + g + 4 * r;
+            if (row < ib) X[cc * N + row] = C[b][r];
         }
-    }
-#pragma unroll 2
-    for (int c = 64; c < kPanelRows; ++c) {
-        const double u1 = l + 64 > c ? Us[tri_row(c) + l + 64 - c] : 0.0;
-#pragma unroll
-        for (int k = 0; k < NC; ++k) {
-            const double x = readlane_f64(acc1[k] * rd1, c - 64);
-            acc1[k] = __builtin_fma(-u1, x, acc1[k]);
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < NC; ++k) {
-        if (jw + k >= T) continue;
-        double* col = X + (jw + k) * N;
-        if (h0) col[l] = acc0[k] * rd0;
-        if (h1) col[l + 64] = acc1[k] * rd1;
-    }
 }
 
 // P <- U^-T P for the kb x kb upper factor U at Akk and the kb x T panel P (both column-major,
@@ -2280,13 +2332,7 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
 static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, double* P,
                        int64_t T) {
     if (kb <= kPanelRows) {
-        // columns per wave: keep about two waves per SIMD in flight
-        if (T >= 32768)
-            k_panel_subst<16><<<(unsigned)((T + 63) / 64), 256, 0, s>>>(N, Akk, (int)kb, P, T);
-        else if (T >= 16384)
-            k_panel_subst<8><<<(unsigned)((T + 31) / 32), 256, 0, s>>>(N, Akk, (int)kb, P, T);
-        else
-            k_panel_subst<4><<<(unsigned)((T + 15) / 16), 256, 0, s>>>(N, Akk, (int)kb, P, T);
+        k_panel_subst<<<(unsigned)((T + 63) / 64), 256, 0, s>>>(N, Akk, (int)kb, P, T);
         GSDFT_HIP(hipGetLastError());
         return GSDFT_OK;
     }
