@@ -8,10 +8,10 @@
 // pair list (every live (i, k, w) has its (k, i, w)) each D_P is symmetric up to round-off and the
 // antisymmetric columns are dropped.
 //
-// The list's entries are grouped by unordered splat pair {i, k}: (i, k) and (k, i) share one
-// product Gaussian, so the three-centre passes run once per group (on a symmetric list half the
-// entries), the block's row of a group serves all its entries, and the reverse takes the sum of
-// their cotangents.
+// The list's entries are grouped by unordered splat pair {i, k} and weight: (i, k) and (k, i)
+// share one product Gaussian, so the three-centre passes run once per group (on a symmetric list
+// half the entries), the block's row of a group serves all its entries, and the reverse takes the
+// sum of their cotangents.
 // Forward, per chunk of W aux functions (centre-grouped slot order):
 //   Bt (groups x W)     the screened three-centre block (k_exch_block_pairs, dfj.hip)
 //   Y[i][l][o']         = sum over pairs a of row i of Bt[g_a][l] C[k_a][o']   (k_exch_spmm, FP64

@@ -89,10 +89,11 @@ int pair_order_layout(Arena& ar, int64_t n, PairOrderWs* w);
 // after them.
 int launch_pair_order(int64_t n, const double* rec, int rec_stride, const PairOrderWs& w,
                       hipStream_t s, const int64_t* n_live = nullptr);
-// order.hip: groups of list entries by unordered splat pair (live entries; each dead entry, q = 0,
-// alone), numbered in key order, through the sort buffers of po (sized for n). Fills ent_group
-// and ent_pos (per entry), grp_first (n_groups + 1) and grp_rep (per group) and the device count
-// *n_groups; head is n ints of scratch, scan_tmp pair_groups_scan_bytes(n) bytes.
+// order.hip: groups of list entries by unordered splat pair and weight (live entries with equal
+// weights q; each dead entry, q = 0, alone), numbered in key order, through the sort buffers of po
+// (sized for n). Fills ent_group and ent_pos (per entry), grp_first (n_groups + 1) and grp_rep
+// (per group) and the device count *n_groups; head is n ints of scratch, scan_tmp
+// pair_groups_scan_bytes(n) bytes.
 size_t pair_groups_scan_bytes(int64_t n);
 int launch_pair_groups(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
                        const double* q, const PairOrderWs& po, int32_t* head, char* scan_tmp,

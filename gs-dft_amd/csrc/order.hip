@@ -55,7 +55,8 @@ __global__ void k_pair_keys(int64_t n, const int64_t* __restrict__ n_live,
 }
 
 // Group key of list entry p: min(i, j) M + max(i, j) for a live entry (the two orders of a splat
-// pair, and repeats of either, share it), M^2 + p for a dead one (a group of its own).
+// pair, and repeats of either, share it), M^2 + p for a dead one (a group of its own). The sort
+// is stable, so the entries of one key stay in list order.
 __global__ void k_group_keys(int64_t n, int64_t M, const int32_t* __restrict__ pi,
                              const int32_t* __restrict__ pj, const double* __restrict__ q,
                              uint64_t* __restrict__ key, int32_t* __restrict__ idx) {
@@ -66,12 +67,19 @@ __global__ void k_group_keys(int64_t n, int64_t M, const int32_t* __restrict__ p
     idx[p] = (int32_t)p;
 }
 
-// head[s] = 1 where key order position s starts a group.
+// head[s] = 1 where key order position s starts a group: a new key, or, within a run of one
+// key, an entry whose weight differs bitwise from the previous entry's (the entries of a group
+// share one three-centre row, formed with its first entry's weight).
 __global__ void k_group_heads(int64_t n, const uint64_t* __restrict__ key,
+                              const int32_t* __restrict__ ent, const double* __restrict__ q,
                               int32_t* __restrict__ head) {
     const int64_t s = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (s >= n) return;
-    head[s] = (s == 0 || key[s] != key[s - 1]) ? 1 : 0;
+    bool start = s == 0 || key[s] != key[s - 1];
+    if (!start)
+        start = __builtin_bit_cast(uint64_t, q[ent[s]]) !=
+                __builtin_bit_cast(uint64_t, q[ent[s - 1]]);
+    head[s] = start ? 1 : 0;
 }
 
 // gid[s]: inclusive count of group starts up to s; ent[s]: the entry at key order position s.
@@ -120,7 +128,7 @@ int launch_pair_groups(int64_t M, int64_t n, const int32_t* pi, const int32_t* p
     const int bits = bit_length((uint64_t)(M * M + n));
     GSDFT_HIP(hipcub::DeviceRadixSort::SortPairs(po.sort_tmp, b, po.key_in, po.key_out,
                                                  po.idx_in, po.perm, (int)n, 0, bits, s));
-    k_group_heads<<<blocks, 256, 0, s>>>(n, po.key_out, head);
+    k_group_heads<<<blocks, 256, 0, s>>>(n, po.key_out, po.perm, q, head);
     GSDFT_HIP(hipGetLastError());
     // the group ids go where the unsorted keys were (no longer needed)
     int32_t* gid = reinterpret_cast<int32_t*>(po.key_in);

@@ -254,12 +254,21 @@ def coulomb_pairs(splats: Splat, C_occ, occ, aux: IsotropicSplat, pi, pj, lam: f
 # ------------------------------------------------------------------------------------ RI-K
 
 def _list_symmetric(M: int, pi: torch.Tensor, pj: torch.Tensor, w: torch.Tensor, n: int) -> bool:
-    """True when the live entries of the first ``n`` (weight 1) come in (i, j) / (j, i) pairs."""
+    """True when the live entries of the first ``n`` come in (i, j) / (j, i) pairs of equal weight
+    (the multiset of (i, j, w) equals that of (j, i, w)); then every D_P is symmetric."""
     if n == 0:
         return True
     live = w[:n] != 0
-    i, j = pi[:n][live].long(), pj[:n][live].long()
-    return bool(torch.equal(torch.sort(i * M + j).values, torch.sort(j * M + i).values))
+    i, j, wl = pi[:n][live].long(), pj[:n][live].long(), w[:n][live]
+
+    def by_key_then_weight(key):
+        o = torch.argsort(wl, stable=True)
+        o = o[torch.argsort(key[o], stable=True)]
+        return key[o], wl[o]
+
+    k1, w1 = by_key_then_weight(i * M + j)
+    k2, w2 = by_key_then_weight(j * M + i)
+    return bool(torch.equal(k1, k2) and torch.equal(w1, w2))
 
 
 class _ExchangeInputs:

@@ -258,8 +258,9 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
 
 /* Screened exact exchange through density fitting (RI-K): E_K = -Tr((V + lam I)^-1 M) with
  * M_PQ = sum_oo' D[P,o,o'] D[Q,o,o'] and D[P,o,o'] = sum over the first n listed pairs
- * a = (pi[a], pj[a]) of weight[a] C_io C_ko' (P|a) (weight null: all 1; the list is the ordered
- * one, weights 0/1). Replaces gs_dft/coulomb/ri.py:497-544 (df_exchange_energy_screened and
+ * a = (pi[a], pj[a]) of weight[a] C_io C_ko' (P|a) (weight null: all 1). The reference passes the
+ * ordered list with 0/1 weights and reads them as a mask (ri.py:509-520); other weights multiply
+ * their entries here, an integer weight w counting as the entry listed w times. Replaces gs_dft/coulomb/ri.py:497-544 (df_exchange_energy_screened and
  * _exchange_M_streamed_screened) as called from gs_dft/ks/terms.py:250-253 with the frozen
  * product aux (N functions: log_alpha, aux_centers) and chol = the row-major lower Cholesky factor
  * of V + lam I (gsdft_cholesky). C is the (M, k) occupied block (occupation 2 folded into the
@@ -274,11 +275,11 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
  * omega > 0 is the long-range exchange E_K[erf(omega r)/r] of range-separated hybrids
  * (gs_dft/ks/terms.py:258-264): the three-centre integrals then use the 12-node Gauss-Legendre rule
  * on [0, omega] (ri.py:231-235) and chol must factor the erf metric (gsdft_aux_metric with the
- * same omega). Entries of one unordered splat pair ((i, j) and (j, i), repeats included) share
- * their product Gaussian, so each (P|a) is formed once per such pair and serves all its entries
- * (the result equals the entry-by-entry sum to round-off). The call never waits on the host
- * (the stream's work is only queued). Writes energy (one device double); with non-null dquat also
- * dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
+ * same omega). Entries of one unordered splat pair with equal weights ((i, j) and (j, i), repeats
+ * included) share their product Gaussian, so each (P|a) is formed once per such pair and serves
+ * all its entries (the result equals the entry-by-entry sum to round-off). The call never waits
+ * on the host (the stream's work is only queued). Writes energy (one device double); with
+ * non-null dquat also dE_K/d(quat, log_scale, centers, C) (M x 4, 3, 3, k). */
 int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, int symmetric,
                                   int grads, int64_t aux_chunk, int recompute, size_t* bytes);
 int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const double* centers,

@@ -118,6 +118,54 @@ def test_exchange_repeated_entries(g, wl, orc, tr, cuda, aux_chunk):
         assert e < REL_G
 
 
+@pytest.mark.parametrize("aux_chunk", [0, 37])
+def test_exchange_integer_weights_through_the_library_call(g, wl, orc, tr, cuda, aux_chunk):
+    """gsdft_exchange with weights other than 0/1. The Python entry point, like the reference
+    (ri.py:509-520 reads valid as a mask), takes only 0/1; the C interface multiplies each entry by
+    its weight, and an entry of integer weight w equals the same entry listed w times. Weights of
+    1, 2 or 3 drawn independently for (i, k) and (k, i), plus repeats with other weights: the
+    entries of an unordered pair then need three-centre rows of their own (groups split by
+    weight) and the list is not symmetric (D_P has an antisymmetric part). E_K and gradients of
+    the library call against the oracle and the torch literal on the list with each entry
+    repeated w times."""
+    from gs_dft_amd import ri
+    k = 4
+    s = wl.make_small(30, k, n_atoms=3, seed=13)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    live = np.flatnonzero(w != 0)
+    pi, pj = pi[live], pj[live]
+    rng = np.random.default_rng(6)
+    rep = rng.choice(len(pi), size=len(pi) // 6, replace=False)    # repeats
+    pi2 = np.concatenate([pi, pi[rep]]).astype(np.int32)
+    pj2 = np.concatenate([pj, pj[rep]]).astype(np.int32)
+    w2 = rng.integers(1, 4, size=len(pi2)).astype(np.float64)
+    pie, pje = np.repeat(pi2, w2.astype(int)), np.repeat(pj2, w2.astype(int))
+    we = np.ones(len(pie))
+    print(f"[exchange] integer weights: n={len(pi2)} (+{len(rep)} repeats), expanded "
+          f"{len(pie)}, aux_chunk={aux_chunk}", flush=True)
+    basis, C = _basis(g, s, grad=False), _cu(s.C)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    pit, pjt = torch.tensor(pi2, device="cuda"), torch.tensor(pj2, device="cuda")
+    x = ri._ExchangeInputs(basis, C, aux, pit, pjt, torch.ones(len(pi2), device="cuda"),
+                           ri.aux_cholesky(aux, 1e-8), None, aux_chunk, False)
+    x.w = torch.tensor(w2, device="cuda")
+    x.symmetric = ri._list_symmetric(x.M, x.pi, x.pj, x.w, x.n)
+    assert not x.symmetric and x.n == len(pi2)
+    E, dq, dl, dc, dC = ri._exchange(x, True)
+    Eo, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pie, pje, we, 1e-8)
+    err = abs(E.item() - Eo) / abs(Eo)
+    print(f"[exchange] E_K {E.item():.15e} oracle {Eo:.15e} rel {err:.2e}")
+    assert err < REL_E
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*leaves, _t(la), _t(ac), _idx(pie), _idx(pje), _t(we), 1e-8)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"), (dq, dl, dc, dC), leaves):
+        e = rel_max(_np(a), b.grad.numpy())
+        print(f"[exchange] d{name} rel-to-max {e:.2e}")
+        assert e < REL_G
+
+
 @pytest.mark.parametrize("case", ["one_self_pair", "self_pairs_only", "one_pair_both_ways"])
 def test_exchange_tiny_lists(g, wl, orc, tr, cuda, case):
     """Lists of one or a few groups: a single self pair, self pairs only, and one off-diagonal

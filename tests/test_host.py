@@ -116,3 +116,24 @@ def test_pair_index_range_check(g):
         check_pair_indices(torch.tensor([-1, 0, 4], dtype=torch.int32), ok, 5, "t")
     with pytest.raises(ValueError, match="same length"):
         check_pair_indices(ok, ok[:2], 5, "t")
+
+
+def test_exchange_symmetry_check_compares_weights(g):
+    """The RI-K symmetric path drops the antisymmetric part of every D_P, which is exact only when
+    the live entries come in (i, j) / (j, i) pairs of equal weight: a list with the same pattern
+    but a different weight on one order, or an entry whose mirror is dead, takes the general path;
+    repeats count as a multiset."""
+    import torch
+    from gs_dft_amd.ri import _list_symmetric
+    pi = torch.tensor([0, 1, 2, 0, 3], dtype=torch.int32)
+    pj = torch.tensor([1, 0, 2, 3, 0], dtype=torch.int32)
+    w = torch.tensor([1.0, 1.0, 1.0, 0.5, 0.5], dtype=torch.float64)
+    assert _list_symmetric(4, pi, pj, w, 5)
+    assert not _list_symmetric(4, pi, pj, torch.tensor([1.0, 2.0, 1.0, 0.5, 0.5]), 5)
+    assert not _list_symmetric(4, pi, pj, torch.tensor([1.0, 1.0, 1.0, 0.5, 0.0]), 5)
+    assert _list_symmetric(4, pi, pj, torch.tensor([1.0, 1.0, 1.0, 0.0, 0.0]), 5)
+    pr = torch.tensor([0, 0, 1, 1], dtype=torch.int32)
+    pc = torch.tensor([1, 1, 0, 0], dtype=torch.int32)
+    assert _list_symmetric(2, pr, pc, torch.tensor([1.0, 2.0, 2.0, 1.0]), 4)
+    assert not _list_symmetric(2, pr, pc, torch.tensor([1.0, 2.0, 2.0, 2.0]), 4)
+    assert _list_symmetric(4, pi, pj, w, 0)
