@@ -260,8 +260,9 @@ int gsdft_grid_density_vjp(int64_t M, const double* quat, const double* log_scal
  * M_PQ = sum_oo' D[P,o,o'] D[Q,o,o'] and D[P,o,o'] = sum over the first n listed pairs
  * a = (pi[a], pj[a]) of weight[a] C_io C_ko' (P|a) (weight null: all 1). The reference passes the
  * ordered list with 0/1 weights and reads them as a mask (ri.py:509-520); other weights multiply
- * their entries here, an integer weight w counting as the entry listed w times. Replaces gs_dft/coulomb/ri.py:497-544 (df_exchange_energy_screened and
- * _exchange_M_streamed_screened) as called from gs_dft/ks/terms.py:250-253 with the frozen
+ * their entries here, an integer weight w counting as the entry listed w times. Replaces
+ * gs_dft/coulomb/ri.py:497-544 (df_exchange_energy_screened and _exchange_M_streamed_screened) as
+ * called from gs_dft/ks/terms.py:250-253 with the frozen
  * product aux (N functions: log_alpha, aux_centers) and chol = the row-major lower Cholesky factor
  * of V + lam I (gsdft_cholesky). C is the (M, k) occupied block (occupation 2 folded into the
  * prefactor, as in the reference). row_ptr/row_perm (and col_ptr/col_perm for gradients) are the
