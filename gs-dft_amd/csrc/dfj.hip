@@ -649,7 +649,9 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // since every per-record term is linear in u and q0, q1 are the centre's.
 // With kLaneU the cotangent of (P|a) is not separable: lane slot a holds the group g = uperm[a] of
 // list entries sharing one product Gaussian, and u = x[3] * sum over e in [uptr[g], uptr[g + 1])
-// of ut[e * ldu + p] (the exchange's dE/d(P|a) per entry, rows in key order), added in order.
+// of ut[e * ldu + p] (the exchange's dE/d(P|a) per entry, rows in key order), added in order; with
+// ugroup the group's entries share one cotangent row, ut[g * ldu + p], and u = x[3] * (that row
+// times the entry count uptr[g + 1] - uptr[g]).
 // With kAtomF the records are nuclei (point charges) and the pass also forms every nucleus' force
 // from the same node sums: per (nucleus p, pair a) the vector 2 KN_a q_a (f0 d + f1 Ah d + f2 Ah^2 d),
 // f0 = -I3 sum g s, f1 = -(I1 sum g s^2 + sum g s^3), f2 = sum g s^2 (dF/dR of
@@ -664,7 +666,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
     const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part,
     const int32_t* __restrict__ uperm, const int32_t* __restrict__ uptr,
-    const int64_t* __restrict__ n_live) {
+    const int64_t* __restrict__ n_live, int ugroup = 0) {
     // whole workgroups past the real slots leave at once (workgroup-uniform, before any barrier)
     if (n_live && (int64_t)blockIdx.x * blockDim.x >= *n_live) return;
     __shared__ double tab[256];
@@ -692,11 +694,18 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     const double cq2 = kAtomF && live ? 2.0 * r[13] * r[14] : 0.0;
     int64_t ut0 = 0;                     // kLaneU: the lane's cotangent rows [ut0, ut0 + utn)
     int utn = 0;
+    double uscale = 1.0;                 // kLaneU with ugroup: the group's entry count
     if constexpr (kLaneU) {
         if (live) {
             const int32_t g = uperm[a];
-            ut0 = uptr[g];
-            utn = uptr[g + 1] - uptr[g];
+            if (ugroup) {
+                ut0 = g;
+                utn = 1;
+                uscale = (double)(uptr[g + 1] - uptr[g]);
+            } else {
+                ut0 = uptr[g];
+                utn = uptr[g + 1] - uptr[g];
+            }
         }
     }
     int64_t chunk0 = blockIdx.y * per_slab;
@@ -772,7 +781,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
                     }
                 }
             }
-            u *= ub[0];
+            u *= ub[0] * uscale;
 #pragma unroll
             for (int j = 0; j + 1 < kUb; ++j) ub[j] = ub[j + 1];
         }
@@ -1975,8 +1984,8 @@ int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux
 }
 
 int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, int64_t n_est,
-                    const double* Tbar, int64_t ldt, bool first, const ExchTcWs& w,
-                    hipStream_t s) {
+                    const double* Tbar, int64_t ldt, bool group_rows, bool first,
+                    const ExchTcWs& w, hipStream_t s) {
     if (n <= 0 || W <= 0) return GSDFT_OK;
     const Split sp = bwd_split(W, std::max<int64_t>(1, std::min(n, n_est)));
     dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
@@ -1985,13 +1994,13 @@ int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, int64_t n_est,
         k_gamma_bwd<true, false, false, kLrNodes><<<grid, 256, 0, s>>>(
             n, w.rec_sorted, W, w.aux + kAuxRec * q0, sp.per_slab, w.part,
             profile_work_counter(kProfExchBwd), Tbar, ldt, nullptr, w.pair_order.perm,
-            w.grp_first, w.n_groups_dev);
+            w.grp_first, w.n_groups_dev, group_rows ? 1 : 0);
     else
         k_gamma_bwd<true><<<grid, 256, 0, s>>>(n, w.rec_sorted, W, w.aux + kAuxRec * q0,
                                                sp.per_slab, w.part,
                                                profile_work_counter(kProfExchBwd), Tbar, ldt,
                                                nullptr, w.pair_order.perm, w.grp_first,
-                                               w.n_groups_dev);
+                                               w.n_groups_dev, group_rows ? 1 : 0);
     profile_end(kProfExchBwd, s);
     GSDFT_HIP(hipGetLastError());
     k_acc_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, sp.slabs, w.part, w.acc, first ? 1 : 0);

@@ -434,6 +434,45 @@ __global__ void k_gather_i32(int64_t n, const int32_t* __restrict__ idx,
     if (r < n) out[r] = src[idx[r]];
 }
 
+// A symmetric list's pair groups as a CSR by lower splat, for its sampled cotangents: the groups
+// (key order) run by lower splat, then upper splat, the dead ones (q = 0) last. gcol[g] = the
+// upper splat of live group g (zero past them and in the kColPad entries past n), giota[g] = g.
+__global__ void k_group_cols(int64_t n, const int64_t* __restrict__ n_groups,
+                             const int32_t* __restrict__ rep, const int32_t* __restrict__ pi,
+                             const int32_t* __restrict__ pj, const double* __restrict__ q,
+                             int32_t* __restrict__ gcol, int32_t* __restrict__ giota) {
+    const int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (g >= n + kColPad) return;
+    int32_t c = 0;
+    if (g < *n_groups) {
+        const int32_t e = rep[g];
+        if (q[e] != 0.0) c = max(pi[e], pj[e]);
+    }
+    gcol[g] = c;
+    if (g < n) giota[g] = (int32_t)g;
+}
+
+// gptr[i], i <= M: the number of live groups whose lower splat is below i (a binary search over the
+// groups in key order, a dead group counting as row M).
+__global__ void k_group_ptr(int64_t M, const int64_t* __restrict__ n_groups,
+                            const int32_t* __restrict__ rep, const int32_t* __restrict__ pi,
+                            const int32_t* __restrict__ pj, const double* __restrict__ q,
+                            int32_t* __restrict__ gptr) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i > M) return;
+    int64_t lo = 0, hi = *n_groups;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        const int32_t e = rep[mid];
+        const int64_t row = q[e] != 0.0 ? min(pi[e], pj[e]) : M;
+        if (row < i)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    gptr[i] = (int32_t)lo;
+}
+
 __global__ void k_fill0(int64_t n, double* __restrict__ out) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i < n) out[i] = 0.0;
@@ -474,6 +513,7 @@ struct ExchWs {
     double *Dt, *Bt, *Y, *Yp, *Ys, *Yps, *Dfull, *Ebar, *part, *red;
     int32_t *row_col, *col_row;       // partner splat per CSR position (rows: pj, columns: pi)
     int32_t *row_grp, *col_grp;       // pair group (block row) per CSR position
+    int32_t *gptr, *gcol, *giota;     // symmetric list: the groups as a CSR by lower splat
     double* Cp;                       // C with rows padded to padded_cols(k) columns
 };
 
@@ -497,6 +537,10 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
     w->col_row = sym ? nullptr : ar.take<int32_t>(n + kColPad);
     w->row_grp = ar.take<int32_t>(n + 1);
     w->col_grp = sym ? nullptr : ar.take<int32_t>(n + 1);
+    const bool gcsr = sym && grads;
+    w->gptr = gcsr ? ar.take<int32_t>(M + 2) : nullptr;
+    w->gcol = gcsr ? ar.take<int32_t>(n + kColPad) : nullptr;
+    w->giota = gcsr ? ar.take<int32_t>(n + 1) : nullptr;
     return GSDFT_OK;
 }
 
@@ -657,6 +701,12 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, col_perm, pi, w.col_row);
         k_gather_i32<<<nblk(n, 256), 256, 0, s>>>(n, col_perm, w.tc.ent_group, w.col_grp);
         GSDFT_HIP(hipGetLastError());
+    } else if (grads) {
+        k_group_cols<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, w.tc.n_groups_dev, w.tc.grp_rep,
+                                                            pi, pj, w.tc.q, w.gcol, w.giota);
+        k_group_ptr<<<nblk(M + 1, 256), 256, 0, s>>>(M, w.tc.n_groups_dev, w.tc.grp_rep, pi, pj,
+                                                     w.tc.q, w.gptr);
+        GSDFT_HIP(hipGetLastError());
     }
     const int64_t G = (N % M == 0) ? N / M : 1;
     const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
@@ -724,11 +774,18 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         GSDFT_BLAS(rocblas_dgemm_64(h, T_, N_, W * k, M, k, &one, w.Dfull, k, C, k, &zero, w.Y,
                                     W * k));
         profile_end(kProfExchGemm, s);
-        // Tbar (slot-major, ld Pc) into the block's buffer
-        GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.ent_pos, w.Y, w.Cp,
-                               w.Bt,
-                               s));
-        GSDFT_TRY(exch_tc_reverse(N, q0, W, n, sym ? (n + 1) / 2 : n, w.Bt, Pc, q0 == 0, w.tc, s));
+        // Tbar (ld Pc) into the block's buffer: on a symmetric list Dbar_P is symmetric, so the
+        // entries of a group, (i, k) and (k, i) and their repeats, share (C Dbar_P C^T)[i][k]:
+        // one row per group, over the group CSR; otherwise one row per entry, at its key-order
+        // position
+        if (sym)
+            GSDFT_TRY(launch_sddmm(M, W, k, Pc, w.gptr, w.giota, w.gcol, w.giota, w.Y, w.Cp, w.Bt,
+                                   s));
+        else
+            GSDFT_TRY(launch_sddmm(M, W, k, Pc, row_ptr, row_perm, w.row_col, w.tc.ent_pos, w.Y,
+                                   w.Cp, w.Bt, s));
+        GSDFT_TRY(exch_tc_reverse(N, q0, W, n, sym ? (n + 1) / 2 : n, w.Bt, Pc, sym, q0 == 0,
+                                  w.tc, s));
     }
     GSDFT_TRY(exch_tc_finish(M, n, pi, pj, weight, quat, log_scale, centers, row_ptr,
                              row_perm, col_ptr, col_perm, dquat, dlog_scale, dcenters, w.tc, s));

@@ -140,10 +140,12 @@ int exch_tc_block(int64_t M, int64_t N, int64_t q0, int64_t W, const double* aux
                   int64_t n, int64_t ldb, double* Bt, const ExchTcWs& w, hipStream_t s);
 // Adds (first: sets) the reverse moments of the aux slots q0 .. q0 + W - 1 with the cotangent of
 // group g's (P|a_l): the sum, in key order, of Tbar[e * ldt + l] over its entries' key-order
-// positions e. n_est (at least n / 2) estimates the group count for the split of the aux slots.
+// positions e; with group_rows, Tbar[g * ldt + l] (the entries' common cotangent) times the
+// group's entry count. n_est (at least n / 2) estimates the group count for the split of the aux
+// slots.
 int exch_tc_reverse(int64_t N, int64_t q0, int64_t W, int64_t n, int64_t n_est,
-                    const double* Tbar, int64_t ldt, bool first, const ExchTcWs& w,
-                    hipStream_t s);
+                    const double* Tbar, int64_t ldt, bool group_rows, bool first,
+                    const ExchTcWs& w, hipStream_t s);
 // Moments -> per-group splat contributions (on the group's first entry, zero on the others) ->
 // dquat, dlog_scale, dcenters.
 int exch_tc_finish(int64_t M, int64_t n, const int32_t* pi, const int32_t* pj,
