@@ -25,7 +25,9 @@
 //                                            Bt[a][l] C[i_a][o] (= Y on a symmetric list)
 //   Ybar_P = C Dbar_P,   Tbar[a][l] = Ybar[i_a][l] . C[k_a]            (k_exch_sddmm, FP64 MFMA)
 //   and the three-centre reverse with the per-(P, group) cotangent, the sum of its entries' Tbar
-//   (dfj.hip), for the splat gradients. Every sum runs in a fixed order (no atomics; rocBLAS runs
+//   (dfj.hip), for the splat gradients. On a symmetric list Dbar_P is symmetric, so the entries
+//   of a group share Tbar = (C Dbar_P C^T)[i][k]: the sampled product runs once per group (over
+//   the groups as a CSR by lower splat) and the reverse takes that row times the entry count. Every sum runs in a fixed order (no atomics; rocBLAS runs
 //   with atomics off).
 #include <rocblas/rocblas.h>
 
