@@ -696,7 +696,9 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     int utn = 0;
     double uscale = 1.0;                 // kLaneU with ugroup: the group's entry count
     if constexpr (kLaneU) {
-        if (live) {
+        // a dead group (weight 0: coefficient 0) reads no cotangent row: its row may never have
+        // been written
+        if (live && r[12] != 0.0) {
             const int32_t g = uperm[a];
             if (ugroup) {
                 ut0 = g;

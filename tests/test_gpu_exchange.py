@@ -119,6 +119,45 @@ def test_exchange_repeated_entries(g, wl, orc, tr, cuda, aux_chunk):
 
 
 @pytest.mark.parametrize("aux_chunk", [0, 37])
+def test_exchange_symmetric_list_with_dead_pairs(g, wl, orc, tr, cuda, aux_chunk):
+    """A list that stays symmetric with some pairs dead in both orders (weight 0 for (i, k) and
+    (k, i)): the symmetric path, whose sampled product forms rows for the live groups only --
+    E_K and gradients against the oracle and the torch literal."""
+    from gs_dft_amd import ri
+    k = 4
+    s = wl.make_small(30, k, n_atoms=3, seed=17)
+    la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, s.scales)
+    pi, pj, w, _ = orc.neighbor_pairs(s.quat, s.log_scale, s.centers, 1e-7, None, False)
+    w = w.astype(np.float64)
+    rng = np.random.default_rng(8)
+    lo, hi = np.minimum(pi, pj), np.maximum(pi, pj)
+    kill = rng.uniform(size=(s.M, s.M)) < 0.2                      # per unordered pair
+    w[kill[lo, hi] & (pi != pj)] = 0.0
+    assert ri._list_symmetric(s.M, torch.as_tensor(pi), torch.as_tensor(pj), torch.as_tensor(w),
+                              len(pi))
+    print(f"[exchange] symmetric with dead pairs: n={len(pi)} dead={int((w == 0).sum())} "
+          f"aux_chunk={aux_chunk}", flush=True)
+    basis, C = _basis(g, s), _cu(s.C, True)
+    aux = g.IsotropicSplat(log_alpha=la, centers=ac)
+    E = g.df_exchange_energy_screened(basis, C, aux, torch.tensor(pi, device="cuda"),
+                                      torch.tensor(pj, device="cuda"), lam=1e-8,
+                                      valid=torch.tensor(w, device="cuda"), aux_chunk=aux_chunk)
+    Eo, _ = orc.exchange_energy(s.quat, s.log_scale, s.centers, s.C, la, ac, pi, pj, w, 1e-8)
+    err = abs(E.item() - Eo) / abs(Eo)
+    print(f"[exchange] E_K {E.item():.15e} oracle {Eo:.15e} rel {err:.2e}")
+    assert err < REL_E
+    E.backward()
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(s.C, True)]
+    Et = tr.screened_exchange_energy(*leaves, _t(la), _t(ac), _idx(pi), _idx(pj), _t(w), 1e-8)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers", "C"),
+                          (basis.quat, basis.log_scale, basis.centers, C), leaves):
+        e = rel_max(_np(a.grad), b.grad.numpy())
+        print(f"[exchange] d{name} rel-to-max {e:.2e}")
+        assert e < REL_G
+
+
+@pytest.mark.parametrize("aux_chunk", [0, 37])
 def test_exchange_integer_weights_through_the_library_call(g, wl, orc, tr, cuda, aux_chunk):
     """gsdft_exchange with weights other than 0/1. The Python entry point, like the reference
     (ri.py:509-520 reads valid as a mask), takes only 0/1; the C interface multiplies each entry by
