@@ -2141,7 +2141,8 @@ __global__ void k_info_reset(int64_t* __restrict__ info) { *info = 0; }
 // holding it published it at the end of step j - 1 (it is final then), in one of two buffers, so
 // each step takes one barrier. The published row keeps A(j, c) at (c % 8) 16 + c / 8, so a
 // thread's 16 rows are 16 consecutive entries: all are read at once, unconditionally, and the
-// registers past the last row take updates that are never stored (rows past 127 read the padding).
+// registers past the thread's last row take updates that are never stored (their reads land on
+// the next row group's entries or on the zero padding past the row).
 // Every FMA of a stored entry is the one the right-looking order applies, in the same order, so
 // the factor does not depend on the thread layout. Steps past ib run on the zero padding: they
 // touch only columns >= ib, which are never stored or read. The block is staged through LDS so the
