@@ -662,7 +662,7 @@ def run_exchange(args) -> int:
     dom = max(fams, key=lambda f: f[1])
     dom_tf = dom[2] / (dom[1] * 1e-3)
     # HBM bytes per launch (one aux chunk) of the dominant kernel, from the counter runs
-    traffic = None
+    traffic, counters = None, None
     tkey = {"three-centre reverse": "k_gamma_bwd_lane_u",
             "three-centre block": "k_exch_block_pairs"}.get(dom[0].split(" (")[0])
     tfile = ROOT / "profiles" / "exchange_traffic.json"
@@ -670,6 +670,7 @@ def run_exchange(args) -> int:
         rec = json.loads(tfile.read_text()).get(s.name, {}).get(tkey)
         if rec:
             traffic = rec["fetch_bytes"] + rec["write_bytes"]
+            counters = rec.get("fp64_counters")      # executed FP64 flops on hardware counters
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -723,6 +724,7 @@ def run_exchange(args) -> int:
         "roofline": {"bound": dom[3], "kernel": dom[0], "achieved": dom_tf / 1e12,
                      "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom_tf / PEAK_FP64,
                      "traffic": traffic, "flops_per_step": dom[2], "kernel_ms_per_step": dom[1],
+                     "frac_basis": "algorithmic", "fp64_counters": counters,
                      "note": "per step, summed over the chunk launches; algorithmic flops: "
                              "N n x 419 (block), N n x 780 (reverse), 4 N n k (Y = T C and "
                              "Tbar), 6 N M k^2 (GEMMs), 2 N^2 K2 (solves); FP64 peak 78.6 "
@@ -732,8 +734,8 @@ def run_exchange(args) -> int:
                              "per node the screen keeps, so the algorithmic fraction credits "
                              "both as done and can pass 1; reverse_nodes_evaluated_frac is "
                              "the executed share of N n x 20 nodes; traffic is the dominant "
-                             "kernel's HBM bytes per launch (one aux chunk) from the counter "
-                             "runs in profiles/"},
+                             "kernel's HBM bytes per launch (one aux chunk) and fp64_counters "
+                             "its executed FP64 flops, from the counter runs in profiles/"},
         "kernels": {"trsm_ms_per_step": trsm_ms, "trsm_tflops": trsm_tf / 1e12,
                     "gemm_ms_per_step": gemm_ms, "gemm_tflops": gemm_tf / 1e12,
                     "block_ms_per_step": blk_ms, "reverse_ms_per_step": rev_ms,
