@@ -69,6 +69,11 @@ def main() -> int:
     ap.add_argument("--eps", type=float, default=None,
                     help="screening threshold (default: the configuration's, 1e-7); the C20H42 "
                          "configuration is also quoted at 1e-5 and 1e-9")
+    ap.add_argument("--pad-from-eps", type=float, default=None,
+                    help="DF-J term: size the frozen pad (ceil(2 n0 / G) G) from the pair count "
+                         "at this threshold instead of --eps, as a trainer does with its first "
+                         "list; with a smaller --eps the list then stands for one grown within "
+                         "that pad")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle baseline sample (0 disables it)")
     ap.add_argument("--cpu-sample-frac", type=float, default=0.0,
@@ -142,7 +147,8 @@ def main() -> int:
     basis0 = g.Splat(quat=quat, log_scale=ls, centers=cen)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    n0 = g.count_significant(basis0, s.eps, s.unique)
+    n0 = g.count_significant(basis0, s.eps if args.pad_from_eps is None else args.pad_from_eps,
+                             s.unique)
     pad_to = g.train_pad_to(ks.screen, n0)
     t_count = time.perf_counter() - t0
     t0 = time.perf_counter()
@@ -203,9 +209,11 @@ def main() -> int:
         f"{bwd_exec_tf / 1e12:.2f} TFLOP/s, {100 * bwd_node_frac:.1f}% of nodes), "
         f"solves {solve_ms / max(args.steps, 1):.2f} ms")
     if bwd_ms >= fwd_ms:
-        dom = ("reverse", "k_gamma_bwd", bwd_ms, FLOPS_BWD, bwd_tf, bwd_exec_tf, bwd_node_frac)
+        dom = ("reverse", "k_gamma_bwd", bwd_ms, FLOPS_BWD, bwd_tf, bwd_exec_tf, bwd_node_frac,
+               BWD_PER_INTEGRAL, BWD_PER_NODE)
     else:
-        dom = ("forward", "k_gamma_fwd", fwd_ms, FLOPS_FWD, fwd_tf, fwd_exec_tf, fwd_node_frac)
+        dom = ("forward", "k_gamma_fwd", fwd_ms, FLOPS_FWD, fwd_tf, fwd_exec_tf, fwd_node_frac,
+               FWD_PER_INTEGRAL, FWD_PER_NODE)
     traffic = None
     tfile = ROOT / "profiles" / "three_centre_traffic.json"
     if tfile.exists():
@@ -277,28 +285,36 @@ def main() -> int:
         "config": {"workload": f"{s.name}: screened DF-J fwd+bwd, M={s.M} splats, "
                                f"N_aux={N}, k={s.k}, eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "N_aux": N, "k": s.k, "n_pairs": n,
-                   "pad_to": pad_to, "eps": s.eps, "parallelism": "single GPU"},
+                   "pad_to": pad_to, "eps": s.eps, "parallelism": "single GPU",
+                   **({} if args.pad_from_eps is None else
+                      {"pad_from_eps": args.pad_from_eps, "n0_at_pad_eps": n0,
+                       "n_pairs_over_n0": n / n0})},
         "roofline": {"bound": "valu", "kernel": f"three-centre {dom[0]} ({dom[1]})",
-                     "achieved": dom[4] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
-                     "frac": dom[4] / PEAK_FP64, "frac_basis": "algorithmic",
+                     "achieved": dom[5] / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": dom[5] / PEAK_FP64, "frac_basis": "evaluated nodes",
                      "traffic": traffic,
-                     "flops_per_integral": dom[3], "integrals_per_launch": integrals,
-                     "kernel_ms": dom[2],
-                     "executed_achieved": dom[5] / 1e12, "executed_frac": dom[5] / PEAK_FP64,
-                     "nodes_evaluated_frac": dom[6],
+                     "flops_per_integral": dom[7], "flops_per_evaluated_node": dom[8],
+                     "integrals_per_launch": integrals,
+                     "evaluated_nodes_per_launch": dom[6] * NODES * integrals,
+                     "kernel_ms": dom[2], "nodes_evaluated_frac": dom[6],
+                     "algorithmic_achieved": dom[4] / 1e12,
+                     "algorithmic_frac": dom[4] / PEAK_FP64,
+                     "algorithmic_flops_per_integral": dom[3],
                      "fp64_counters": counter_record(s.name, dom[1]),
                      "note": "FP64 compute bound on the vector ALUs (VALU; MI355X FP64 vector "
-                             "peak 78.6 TFLOP/s, no MFMA: the work is elementwise). frac is "
-                             "algorithmic (the per-integral figure at all 20 nodes): it credits "
-                             "the nodes the screen skips as done, so it can exceed 1 once the "
-                             "screen skips more than the kernel loses to the peak; executed_* "
-                             "count only the nodes evaluated; fp64_counters holds the hardware "
+                             "peak 78.6 TFLOP/s, no MFMA: the work is elementwise). achieved "
+                             "counts the work the kernel has to do: flops_per_integral for "
+                             "every (P, a) plus flops_per_evaluated_node for each node the "
+                             "e^-36 screen keeps (the kernel's own node counter); "
+                             "algorithmic_* credit all 20 nodes of every integral, skipped ones "
+                             "included, and so can pass 1; fp64_counters holds the hardware "
                              "FP64 VALU instruction rate of the same kernel at this workload "
                              "from the rocprofv3 counter runs in profiles/"},
         "kernels": {"three_centre_fwd_ms": fwd_ms, "three_centre_bwd_ms": bwd_ms,
-                    "fwd_frac_fp64": fwd_tf / PEAK_FP64, "bwd_frac_fp64": bwd_tf / PEAK_FP64,
-                    "fwd_executed_frac_fp64": fwd_exec_tf / PEAK_FP64,
-                    "bwd_executed_frac_fp64": bwd_exec_tf / PEAK_FP64,
+                    "fwd_frac_fp64": fwd_exec_tf / PEAK_FP64,
+                    "bwd_frac_fp64": bwd_exec_tf / PEAK_FP64,
+                    "fwd_algorithmic_frac_fp64": fwd_tf / PEAK_FP64,
+                    "bwd_algorithmic_frac_fp64": bwd_tf / PEAK_FP64,
                     "fwd_nodes_evaluated_frac": fwd_node_frac,
                     "bwd_nodes_evaluated_frac": bwd_node_frac,
                     "fwd_integrals_per_s": integrals / (fwd_ms * 1e-3),
@@ -376,11 +392,14 @@ def run_nuclear(args) -> int:
     pair_ms /= max(pair_k, 1)
     atom_ms /= max(atom_k, 1)
     pair_tf = integrals * FLOPS_NUC_PAIR / (pair_ms * 1e-3)
+    nuc_per_integral = FLOPS_NUC_PAIR - NODES * BWD_PER_NODE
+    pair_exec_tf = (integrals * nuc_per_integral + pair_nodes * BWD_PER_NODE) / (pair_ms * 1e-3)
     log(f"E_ext={E.item():.12e} step {wall * 1e3:.2f} ms; pair pass with nuclear forces "
-        f"{pair_ms:.2f} ms ({pair_tf / 1e12:.2f} TFLOP/s, {pair_nodes / (NODES * integrals):.3f} "
-        f"of nodes), force sums over pair blocks {atom_ms:.2f} ms")
+        f"{pair_ms:.2f} ms ({pair_exec_tf / 1e12:.2f} TFLOP/s on the evaluated nodes, "
+        f"{pair_tf / 1e12:.2f} algorithmic, {pair_nodes / (NODES * integrals):.3f} of nodes), "
+        f"force sums over pair blocks {atom_ms:.2f} ms")
     dom = ("pair pass with nuclear forces (k_gamma_bwd<false, true> over point-charge records)",
-           pair_ms, FLOPS_NUC_PAIR, pair_tf)
+           pair_ms, FLOPS_NUC_PAIR, pair_tf, pair_exec_tf, nuc_per_integral)
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -418,13 +437,18 @@ def run_nuclear(args) -> int:
                                f"{A} nuclei, k={s.k}, eps={s.eps}, unique pairs",
                    "system": args.system, "M": s.M, "n_atoms": A, "k": s.k, "n_pairs": n,
                    "eps": s.eps, "parallelism": "single GPU"},
-        "roofline": {"bound": "valu", "kernel": dom[0], "achieved": dom[3] / 1e12,
-                     "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom[3] / PEAK_FP64,
-                     "frac_basis": "algorithmic",
-                     "traffic": None, "flops_per_integral": dom[2],
+        "roofline": {"bound": "valu", "kernel": dom[0], "achieved": dom[4] / 1e12,
+                     "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom[4] / PEAK_FP64,
+                     "frac_basis": "evaluated nodes",
+                     "traffic": None, "flops_per_integral": dom[5],
+                     "flops_per_evaluated_node": BWD_PER_NODE,
                      "integrals_per_launch": integrals, "kernel_ms": dom[1],
-                     "note": "FP64 vector (VALU) bound; algorithmic: every integral credited "
-                             "with all 20 nodes, including the nodes the screen skips"},
+                     "algorithmic_achieved": dom[3] / 1e12, "algorithmic_frac": dom[3] / PEAK_FP64,
+                     "algorithmic_flops_per_integral": dom[2],
+                     "note": "FP64 vector (VALU) bound; achieved counts flops_per_integral for "
+                             "every (nucleus, pair) plus flops_per_evaluated_node for each node "
+                             "the e^-36 screen keeps; algorithmic_* credit all 20 nodes of every "
+                             "integral, skipped ones included"},
         "kernels": {"pair_pass_ms": pair_ms, "force_sums_ms": atom_ms,
                     "pair_nodes_evaluated_frac": pair_nodes / (NODES * integrals)},
         "cpu_baseline": cpu,
@@ -506,6 +530,10 @@ def run_exact(args) -> int:
     fwd_ms /= max(fwd_k, 1)
     bwd_tf = sym_integrals * FLOPS_ERI_BWD / (bwd_ms * 1e-3)
     fwd_tf = sym_integrals * FLOPS_ERI_FWD / (fwd_ms * 1e-3)
+    bwd_exec_tf = (sym_integrals * ERI_BWD_PER_INTEGRAL + bwd_nodes * ERI_BWD_PER_NODE) / (
+        bwd_ms * 1e-3)
+    fwd_exec_tf = (sym_integrals * ERI_FWD_PER_INTEGRAL + fwd_nodes * ERI_FWD_PER_NODE) / (
+        fwd_ms * 1e-3)
     log(f"E_J={E.item():.12e} (energy only {E0.item():.12e}) step {wall * 1e3:.1f} ms, energy "
         f"only {wall_e * 1e3:.1f} ms; reverse kernel {bwd_ms:.1f} ms ({bwd_tf / 1e12:.2f} "
         f"TFLOP/s, {bwd_nodes / (NODES * sym_integrals):.3f} of nodes), forward kernel "
@@ -549,17 +577,22 @@ def run_exact(args) -> int:
                    "system": args.system, "M": s.M, "k": s.k, "n_pairs": n, "eps": s.eps,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "valu", "kernel": "exact pair-pair reverse (k_eri_bwd_sym, all bands)",
-                     "achieved": bwd_tf / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
-                     "frac": bwd_tf / PEAK_FP64, "frac_basis": "algorithmic", "traffic": None,
-                     "flops_per_integral": FLOPS_ERI_BWD, "integrals_per_launch": sym_integrals,
-                     "kernel_ms": bwd_ms,
-                     "note": "FP64 vector (VALU) bound; algorithmic: every integral credited "
-                             "with all 20 nodes, over the n(n+1)/2 unordered pair-pairs each "
-                             "pass evaluates ((a|b) = (b|a)); "
-                             "kernel_ms spans every band launch and its reductions"},
+                     "achieved": bwd_exec_tf / 1e12, "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s",
+                     "frac": bwd_exec_tf / PEAK_FP64, "frac_basis": "evaluated nodes",
+                     "traffic": None, "flops_per_integral": ERI_BWD_PER_INTEGRAL,
+                     "flops_per_evaluated_node": ERI_BWD_PER_NODE,
+                     "integrals_per_launch": sym_integrals, "kernel_ms": bwd_ms,
+                     "algorithmic_achieved": bwd_tf / 1e12, "algorithmic_frac": bwd_tf / PEAK_FP64,
+                     "algorithmic_flops_per_integral": FLOPS_ERI_BWD,
+                     "note": "FP64 vector (VALU) bound, over the n(n+1)/2 unordered pair-pairs "
+                             "each pass evaluates ((a|b) = (b|a)); achieved counts "
+                             "flops_per_integral per pair-pair plus flops_per_evaluated_node "
+                             "for each node the e^-36 screen keeps; algorithmic_* credit all 20 "
+                             "nodes; kernel_ms spans every band launch and its reductions"},
         "kernels": {"reverse_ms": bwd_ms, "forward_ms": fwd_ms,
                     "energy_only_ms": wall_e * 1e3,
-                    "forward_frac_fp64": fwd_tf / PEAK_FP64,
+                    "forward_frac_fp64": fwd_exec_tf / PEAK_FP64,
+                    "forward_algorithmic_frac_fp64": fwd_tf / PEAK_FP64,
                     "forward_pair_pairs": sym_integrals,
                     "reverse_nodes_evaluated_frac": bwd_nodes / (NODES * sym_integrals),
                     "forward_nodes_evaluated_frac": fwd_nodes / (NODES * sym_integrals)},
@@ -631,8 +664,13 @@ def run_exchange(args) -> int:
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
     prof = {kid: _lib.profile_read(kid, reset=True) for kid in ids}
-    bwd_nodes = _lib.profile_read_work(_lib.PROF_EXCH_BWD, reset=True)
+    bwd_nodes = _lib.profile_read_work(_lib.PROF_EXCH_BWD, reset=True) / args.steps
+    blk_nodes = _lib.profile_read_work(_lib.PROF_EXCH_BLOCK, reset=True) / args.steps
     _lib.profile_enable(False)
+    # the three-centre passes run once per unordered splat pair (the list is symmetric)
+    groups = int(((pi <= pj) & (w != 0)).sum().item())
+    blk_exec = float(groups) * N * FWD_PER_INTEGRAL + blk_nodes * FWD_PER_NODE
+    rev_exec = float(groups) * N * BWD_PER_INTEGRAL + bwd_nodes * BWD_PER_NODE
     per_step = {kid: prof[kid][0] / args.steps for kid in ids}
     blk_ms, rev_ms = per_step[_lib.PROF_EXCH_BLOCK], per_step[_lib.PROF_EXCH_BWD]
     trsm_ms, gemm_ms = per_step[_lib.PROF_EXCH_TRSM], per_step[_lib.PROF_EXCH_GEMM]
@@ -652,15 +690,21 @@ def run_exchange(args) -> int:
         f"{sparse_ms:.1f} ms")
     # the dominant kernel family of the step and its algorithmic flops per step (work that a
     # recompute repeats is not counted again)
-    fams = [("three-centre block (k_exch_block)", blk_ms, integrals * FLOPS_FWD, "valu"),
-            ("three-centre reverse (k_gamma_bwd, per-(P,a) cotangent)", rev_ms,
+    # (name, ms per step, work the kernels do per step, algorithmic work per step, bound): the
+    # three-centre passes do one integral per (group, aux) and the nodes the screen keeps, the
+    # algorithmic figure counts every ordered entry at all 20 nodes, as the reference evaluates
+    fams = [("three-centre block (k_exch_block)", blk_ms, blk_exec, integrals * FLOPS_FWD,
+             "valu"),
+            ("three-centre reverse (k_gamma_bwd, per-(P,a) cotangent)", rev_ms, rev_exec,
              integrals * FLOPS_BWD, "valu"),
             ("pair-sparse products (k_exch_spmm, k_exch_sddmm; FP64 MFMA)", sparse_ms, sparse,
+             sparse, "mfma"),
+            ("FP64 GEMMs (rocBLAS dgemm)", gemm_ms, gemm_fwd + gemm_bwd, gemm_fwd + gemm_bwd,
              "mfma"),
-            ("FP64 GEMMs (rocBLAS dgemm)", gemm_ms, gemm_fwd + gemm_bwd, "mfma"),
-            ("triangular solves (rocBLAS dtrsm)", trsm_ms, 2 * trsm, "mfma")]
+            ("triangular solves (rocBLAS dtrsm)", trsm_ms, 2 * trsm, 2 * trsm, "mfma")]
     dom = max(fams, key=lambda f: f[1])
     dom_tf = dom[2] / (dom[1] * 1e-3)
+    dom_alg_tf = dom[3] / (dom[1] * 1e-3)
     # HBM bytes per launch (one aux chunk) of the dominant kernel, from the counter runs
     traffic, counters = None, None
     tkey = {"three-centre reverse": "k_gamma_bwd_lane_u",
@@ -721,26 +765,31 @@ def run_exchange(args) -> int:
                                f"N_aux={N}, eps={s.eps}, ordered pairs",
                    "system": args.system, "M": M, "k": k, "N_aux": N, "n_pairs": n,
                    "eps": s.eps, "parallelism": "single GPU"},
-        "roofline": {"bound": dom[3], "kernel": dom[0], "achieved": dom_tf / 1e12,
+        "roofline": {"bound": dom[4], "kernel": dom[0], "achieved": dom_tf / 1e12,
                      "peak": PEAK_FP64 / 1e12, "unit": "TFLOP/s", "frac": dom_tf / PEAK_FP64,
                      "traffic": traffic, "flops_per_step": dom[2], "kernel_ms_per_step": dom[1],
-                     "frac_basis": "algorithmic", "fp64_counters": counters,
-                     "note": "per step, summed over the chunk launches; algorithmic flops: "
-                             "N n x 419 (block), N n x 780 (reverse), 4 N n k (Y = T C and "
-                             "Tbar), 6 N M k^2 (GEMMs), 2 N^2 K2 (solves); FP64 peak 78.6 "
-                             "(vector and matrix). n counts the ordered list entries, as the "
-                             "reference evaluates them; the three-centre passes run once per "
-                             "unordered splat pair (half of them on a symmetric list) and once "
-                             "per node the screen keeps, so the algorithmic fraction credits "
-                             "both as done and can pass 1; reverse_nodes_evaluated_frac is "
-                             "the executed share of N n x 20 nodes; traffic is the dominant "
-                             "kernel's HBM bytes per launch (one aux chunk) and fp64_counters "
-                             "its executed FP64 flops, from the counter runs in profiles/"},
+                     "frac_basis": "evaluated nodes, one integral per unordered splat pair",
+                     "algorithmic_achieved": dom_alg_tf / 1e12,
+                     "algorithmic_frac": dom_alg_tf / PEAK_FP64,
+                     "algorithmic_flops_per_step": dom[3], "pair_groups": groups,
+                     "fp64_counters": counters,
+                     "note": "per step, summed over the chunk launches; FP64 peak 78.6 (vector "
+                             "and matrix). Three-centre passes: achieved counts, per unordered "
+                             "splat pair (pair_groups) and aux function, the per-integral "
+                             "prologue (39 block, 40 reverse) plus 19 (block) or 37 (reverse) "
+                             "flops per node the e^-36 screen keeps; algorithmic_* count every "
+                             "ordered entry at all 20 nodes (N n x 419 block, N n x 780 "
+                             "reverse), as the reference evaluates them, and so can pass 1. "
+                             "Other families: 4 N n k (Y = T C and Tbar), 6 N M k^2 (GEMMs), "
+                             "2 N^2 K2 (solves). traffic is the dominant kernel's HBM bytes per "
+                             "launch (one aux chunk) and fp64_counters its executed FP64 "
+                             "flops, from the counter runs in profiles/"},
         "kernels": {"trsm_ms_per_step": trsm_ms, "trsm_tflops": trsm_tf / 1e12,
                     "gemm_ms_per_step": gemm_ms, "gemm_tflops": gemm_tf / 1e12,
                     "block_ms_per_step": blk_ms, "reverse_ms_per_step": rev_ms,
                     "sparse_ms_per_step": sparse_ms,
-                    "reverse_nodes_evaluated_frac": bwd_nodes / args.steps / (NODES * integrals),
+                    "reverse_nodes_evaluated_frac": bwd_nodes / (NODES * float(groups) * N),
+                    "block_nodes_evaluated_frac": blk_nodes / (NODES * float(groups) * N),
                     "energy_only_ms": wall_e * 1e3},
         "cpu_baseline": cpu,
         "E_K": E.item(),

@@ -7,7 +7,8 @@ exact screened Coulomb, nuclear attraction, density on the XC grid): the ``df()`
 """
 from .basis import IsotropicSplat, Splat, init_product_aux
 from .energy import SplatDFJ, SplatModel, SplatState, refresh, train_pad_to
-from .exact import screened_coulomb_J, screened_coulomb_energy
+from .exact import (full_coulomb_J, full_coulomb_energy, make_pairs, screened_coulomb_J,
+                    screened_coulomb_energy)
 from .grid import chunked_density, chunked_density_and_grad, chunked_density_grad_tau
 from .ri import (aux_cholesky, aux_metric, coulomb_pairs, df_coulomb_energy_screened,
                  df_coulomb_gamma_screened, df_coulomb_solve, df_exchange_energy_screened,
@@ -16,19 +17,20 @@ from .screening import (PairIndex, build_pair_index, count_significant, density_
                         live_length, neighbor_pairs, pair_weight, screened_external_energy,
                         screened_nuclear_pairs, screened_overlap_pairs)
 from .terms import (SCREEN_PAD, CoulombTerm, DFSpec, ExactSpec, Pairlist, ScreenedExactCoulomb,
-                    ScreenedProductDFCoulomb, df, exact, hf_coeff, pairlist)
+                    ScreenedProductDFCoulomb, StreamedExactCoulomb, df, exact, hf_coeff, pairlist)
 
 __all__ = [
     "Splat", "IsotropicSplat", "init_product_aux",
     "SplatDFJ", "SplatModel", "SplatState", "refresh", "train_pad_to",
     "aux_metric", "aux_cholesky", "shift_diag", "df_coulomb_gamma_screened", "df_coulomb_solve",
     "df_coulomb_energy_screened", "coulomb_pairs", "df_exchange_energy_screened",
-    "screened_coulomb_energy", "screened_coulomb_J",
+    "screened_coulomb_energy", "screened_coulomb_J", "full_coulomb_energy", "full_coulomb_J",
+    "make_pairs",
     "chunked_density", "chunked_density_and_grad", "chunked_density_grad_tau",
     "neighbor_pairs", "count_significant", "pair_weight", "screened_overlap_pairs",
     "density_pairs", "screened_nuclear_pairs", "screened_external_energy",
     "PairIndex", "build_pair_index", "live_length",
     "SCREEN_PAD", "CoulombTerm", "DFSpec", "ExactSpec", "Pairlist", "ScreenedProductDFCoulomb",
-    "ScreenedExactCoulomb",
+    "ScreenedExactCoulomb", "StreamedExactCoulomb",
     "df", "exact", "pairlist", "hf_coeff",
 ]

@@ -52,6 +52,7 @@ SIGNATURES = {
     "gsdft_metric_workspace_size": [_i64, _psz],
     "gsdft_aux_metric": [_i64, _vp, _vp, _dbl, _dbl, _vp, _vp, _sz, _vp],
     "gsdft_cholesky": [_i64, _vp, _vp, _sz, _vp],
+    "gsdft_aux_cholesky": [_i64, _vp, _vp, _dbl, _dbl, _vp, _vp, _sz, _vp],
     "gsdft_cho_solve": [_i64, _vp, _vp, _vp, _vp, _vp],
     "gsdft_gamma_workspace_size": [_i64, _i64, _i64, _i64, _psz],
     "gsdft_gamma": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
@@ -72,6 +73,8 @@ SIGNATURES = {
     "gsdft_exact_coulomb_workspace_size": [_i64, _i64, _i64, _int, _psz],
     "gsdft_exact_coulomb": [_i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "gsdft_exact_coulomb_density": [_i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _vp,
+                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_exchange_workspace_size": [_i64, _i64, _i64, _i64, _int, _int, _i64, _int, _psz],
     "gsdft_exchange": [_i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                        _vp, _vp, _vp, _vp, _int, _i64, _int, _dbl, _vp, _vp, _vp, _vp, _vp, _vp,

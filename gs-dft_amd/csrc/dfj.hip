@@ -173,7 +173,10 @@ __device__ __forceinline__ double boys0(double T) {
 // gs_dft/coulomb/ri.py:63-76 + shift_diag: F0 = boys0(rho R^2) for 1/r, or, for the long-range
 // kernel erf(omega r)/r (omega > 0), sqrt(z) boys0(z rho R^2) with z = omega^2 / (omega^2 + rho).
 // One thread per element; a block covers 4 rows x 64 columns so each wave writes 64 consecutive
-// doubles of one row.
+// doubles of one row. kLower forms only the lower triangle (q <= p) and writes zeros above it,
+// so a factorisation that follows clears only its diagonal tiles (k_zero_diag_tiles) instead of
+// the whole upper triangle.
+template <bool kLower>
 __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restrict__ beta,
                                                 const double* __restrict__ kn,
                                                 const double* __restrict__ R, double lam,
@@ -181,6 +184,10 @@ __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restr
     const int64_t q = blockIdx.x * 64 + (threadIdx.x & 63);
     const int64_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (p >= N || q >= N) return;
+    if (kLower && q > p) {
+        V[p * N + q] = 0.0;
+        return;
+    }
     const double g1 = beta[p], g2 = beta[q];
     const double gab = g1 * g2;
     const double gsum = g1 + g2;
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
     const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part,
     const int32_t* __restrict__ uperm, const int32_t* __restrict__ uptr,
-    const int64_t* __restrict__ n_live, int ugroup = 0) {
+    const int64_t* __restrict__ n_live, int ugroup = 0, int64_t slab0 = 0, int acc_first = -1) {
     // whole workgroups past the real slots leave at once (workgroup-uniform, before any barrier)
     if (n_live && (int64_t)blockIdx.x * blockDim.x >= *n_live) return;
     __shared__ double tab[256];
@@ -710,7 +717,8 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             }
         }
     }
-    int64_t chunk0 = blockIdx.y * per_slab;
+    const int64_t slab = slab0 + blockIdx.y;       // aux slab of this workgroup
+    int64_t chunk0 = slab * per_slab;
     double F = 0, dP0 = 0, dP1 = 0, dP2 = 0, gs1 = 0, gs2 = 0, gs3 = 0;      // node sums
     auto flush = [&]() {
         if constexpr (kFold) {           // the node sums span the centre's records, u folded in
@@ -742,7 +750,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         Sb[5] = __builtin_fma(e2y, d[2], Sb[5]);
         C0 = 0; C1 = 0; C2 = 0;
     };
-    const int64_t p0 = blockIdx.y * per_slab;
+    const int64_t p0 = slab * per_slab;
     const int64_t p1 = min(N, p0 + per_slab);
     uint32_t nodes = 0;
     // kLaneU: the lane's summed cotangents of the next kUb records, fetched kUb records at a time
@@ -878,6 +886,14 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     const double v[kAcc] = {jt, T1, T2, T3, Vc[0], Vc[1], Vc[2], Va[0], Va[1], Va[2],
                             Vb[0], Vb[1], Vb[2], Sa[0], Sa[1], Sa[2], Sa[3], Sa[4], Sa[5],
                             Sb[0], Sb[1], Sb[2], Sb[3], Sb[4], Sb[5]};
+    if (acc_first >= 0 && blockIdx.y == 0) {
+        // the launch's first slab adds its moments to the running sums of the slabs before it
+        // (acc_first: none yet, start from 0), in slab order like a sum over every slab
+#pragma unroll
+        for (int c = 0; c < kAcc; ++c)
+            o[(int64_t)c * n] = (acc_first ? 0.0 : o[(int64_t)c * n]) + v[c];
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < kAcc; ++c) o[(int64_t)c * n] = v[c];
 }
@@ -1154,7 +1170,7 @@ __global__ void k_atom_rec(int64_t n_atoms, const double* __restrict__ coords,
 //   s d.adj(I + sT).d = s (p0 + s (p1 + s p2)),     p0 = |d|^2, p1 = J1 p0 - d.T d, p2 = d.adj T.d,
 // so (a|b) = h_a h_b 2 pi^2.5 sum_t w_t E^(-1/2) e^(-z), z = s (p0 + s p1 + s^2 p2) / E, with
 // h = KN det(A)^(-1/2) per pair -- the node of the three-centre kernels with s_t = t^2.
-// Pair record (slot order): A^-1 (6) | P (3) | h | Pw = w sum_o occ_o C_io C_jo | pad.
+// Pair record (slot order): A^-1 (6) | P (3) | h | Pw (= w sum_o occ_o C_io C_jo, or w P_ij) | w.
 constexpr int kEriRec = 12;
 constexpr double kPrefEri = kTwoPi25;                 // (2/sqrt(pi)) pi^3 = 2 pi^2.5
 
@@ -1162,7 +1178,7 @@ __global__ void k_eri_rec(int64_t n, const int32_t* __restrict__ perm,
                           const int32_t* __restrict__ pi, const int32_t* __restrict__ pj,
                           const double* __restrict__ A6, const double* __restrict__ mu,
                           const double* __restrict__ Nrm, const double* __restrict__ q,
-                          double* __restrict__ rec) {
+                          const double* __restrict__ weight, double* __restrict__ rec) {
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (slot >= n) return;
     const int64_t a = perm[slot];
@@ -1182,7 +1198,7 @@ __global__ void k_eri_rec(int64_t n, const int32_t* __restrict__ perm,
     r[6] = P[0]; r[7] = P[1]; r[8] = P[2];
     r[9] = KN / sqrt(det);
     r[10] = q[a];
-    r[11] = 0.0;
+    r[11] = weight ? weight[a] : 1.0;
 }
 
 // The centre-dependent scalars of one pair-pair from T (six slots) and d.
@@ -1535,7 +1551,7 @@ __global__ void k_eri_finish(int64_t n, int64_t slabs, const int32_t* __restrict
     const double* r = rec + kEriRec * slot;
     double acc = 0.0;
     for (int64_t k = 0; k < slabs; ++k) acc += partial[k * n + slot];
-    J[perm[slot]] = (r[10] == 0.0) ? 0.0 : r[9] * kPrefEri * acc;
+    J[perm[slot]] = (r[11] == 0.0) ? 0.0 : r[9] * kPrefEri * acc;     // 0 on dead entries
 }
 
 // Per slot: J and the pair's gradient from the reverse moments. E = 1/2 sum_ab Pw_a Pw_b (a|b), so
@@ -1553,7 +1569,7 @@ __global__ void k_eri_finalize(int64_t n, int64_t slabs, const int32_t* __restri
     const int64_t a = perm[slot];
     const double* r = rec + kEriRec * slot;
     const double h = r[9], Pw = r[10];
-    if (Pw == 0.0) {
+    if (r[11] == 0.0) {                 // a dead (zero-weight) entry
         J[a] = 0.0;
         for (int c = 0; c < 20; ++c) contrib[(int64_t)c * n + a] = 0.0;
         return;
@@ -1694,6 +1710,16 @@ __global__ void k_acc_fold(int64_t n, int64_t slabs, const double* __restrict__ 
     acc[t] = v;
 }
 
+// buf[0][c][slot] += buf[1][c][slot] + ... + buf[slabs - 1][c][slot], in slab order (the running
+// moment sums of the DF-J reverse and the later slabs of one launch, stride kAcc n per slab).
+__global__ void k_slab_fold(int64_t n, int64_t slabs, double* __restrict__ buf) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= n * kAcc) return;
+    double v = buf[t];
+    for (int64_t k = 1; k < slabs; ++k) v += buf[k * kAcc * n + t];
+    buf[t] = v;
+}
+
 // inv[perm[slot]] = slot.
 __global__ void k_inv_perm(int64_t n, const int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
     const int64_t slot = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -1722,25 +1748,33 @@ Split bwd_split(int64_t N, int64_t n) {
 // The DF-J reverse: besides enough slabs to fill the device (bwd_split), the aux records are cut
 // into slabs of at most kL2Records records (2.9 MB) so that the workgroups running together walk
 // one slab, which then stays in the XCD's 4 MB L2 instead of coming from the MALL once per
-// workgroup, as long as the slabs' partial moments (kAcc x n doubles each) fit in kSlabBudget.
-// At globule700 (80,000 records, 11.2 M pairs) that is 20 slabs and 44.6 GB of partial moments:
-// the reverse takes 8.49 instead of 9.05 s. The result depends on the split only through the
-// order in which the slabs' moments are added (fixed for given N and n).
+// workgroup: at globule700 (80,000 records, 11.2 M pairs) 20 slabs, and the reverse takes 8.49
+// instead of 9.05 s. The result depends on the split only through the order in which the slabs'
+// moments are added (fixed for given N and n).
 constexpr int64_t kL2Records = 4096;
-constexpr double kSlabBudget = 48.0 * (1ull << 30);
+constexpr double kSlabBudget = 5.0 * (1ull << 30);
 
 Split bwd_split_records(int64_t N, int64_t n) {
     Split sp = bwd_split(N, n);
     const int64_t want = (N + kL2Records - 1) / kL2Records;
     if (N <= 0 || sp.slabs >= want) return sp;
-    const double per_slab_bytes = 8.0 * kAcc * (double)(n > 0 ? n : 1);
-    int64_t slabs = want;
-    const int64_t cap = (int64_t)(kSlabBudget / per_slab_bytes);
-    if (slabs > cap) slabs = cap;
-    if (slabs > 65535) slabs = 65535;
-    if (slabs <= sp.slabs || slabs < 1) return sp;
+    int64_t slabs = want > 65535 ? 65535 : want;
     const int64_t per = (N + slabs - 1) / slabs;
     return Split{(N + per - 1) / per, per};
+}
+
+// Slabs per launch of the DF-J reverse: every slab in one launch while their partial moments
+// (kAcc n doubles each) fit in kSlabBudget, else launches of `per_launch` slabs one after the
+// other, each adding its slabs' moments to running sums (the first slab in the kernel, the rest by
+// k_slab_fold), so the moment storage is per_launch slabs whatever the slab count: 4.5 GB at
+// 11.2 M pairs (2 slabs a launch), 4.1 GB at 20.6 M (1). The sums run in slab order either way,
+// so the result does not depend on the launch grouping.
+int64_t bwd_slabs_per_launch(int64_t N, int64_t n) {
+    const Split sp = bwd_split_records(N, n);
+    const double per_slab_bytes = 8.0 * kAcc * (double)(n > 0 ? n : 1);
+    int64_t r = (int64_t)(kSlabBudget / per_slab_bytes);
+    if (r < 1) r = 1;
+    return r < sp.slabs ? r : sp.slabs;
 }
 
 struct GammaWs {
@@ -1755,19 +1789,22 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
     w->beta = ar.take<double>(N + 1);
     w->kn = ar.take<double>(N + 1);
     w->q = ar.take<double>(n + 1);
-    w->rec = ar.take<double>(kRec * n + kRec);
-    w->partial = w->aux = w->acc = w->contrib = w->rec_sorted = nullptr;
+    w->partial = w->aux = w->acc = w->contrib = w->rec_sorted = w->rec = nullptr;
     if (!reverse) {
+        w->rec = ar.take<double>(kRec * n + kRec);
         const int64_t groups = n > 0 ? (n + kFwdPairs - 1) / kFwdPairs : 1;
         w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
         w->rec_sorted = ar.take<double>(kRec * n + kRec);
         GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
         w->partial = ar.take<double>(groups * N + 1);
     } else {
-        // at least as many slabs as bwd_split's, which the nuclear pass launches with
-        const Split sp = bwd_split_records(N, n);
+        // at least as many slabs as bwd_split's, which the nuclear pass launches with; the
+        // unsorted pair records are dead once gathered into slot order, before any moment is
+        // written, so they occupy the start of the moment storage
+        const int64_t slabs = std::max(bwd_split(N, n).slabs, bwd_slabs_per_launch(N, n));
         w->aux = ar.take<double>(kAuxRec * N + kAuxRec);
-        w->acc = ar.take<double>(sp.slabs * kAcc * n + 1);
+        w->acc = ar.take<double>(std::max(slabs * kAcc * n + 1, kRec * n + kRec));
+        w->rec = w->acc;
         w->rec_sorted = ar.take<double>(kRec * n + kRec);
         GSDFT_TRY(pair_order_layout(ar, n, &w->pair_order));
         w->contrib = ar.take<double>(20 * n + 1);
@@ -2118,7 +2155,7 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
     profile_begin(kProfMetric, s);
-    k_metric<<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, V);
+    k_metric<false><<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, V);
     profile_end(kProfMetric, s);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -2428,6 +2465,51 @@ extern "C" int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t work
     return GSDFT_OK;
 }
 
+// Zeroes the strict upper triangle (row-major) of the 128 x 128 diagonal tiles: the only
+// entries above the diagonal that the factorisation writes (the sub-diagonal half of its
+// column-major diagonal tiles, formed by the updates and never read), when the metric was formed
+// with zeros above the diagonal.
+__global__ void k_zero_diag_tiles(int64_t N, double* __restrict__ V) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t p = t / kPanelRows;
+    if (p >= N) return;
+    const int64_t q = (p / kPanelRows) * kPanelRows + t % kPanelRows;
+    if (q > p && q < N) V[p * N + q] = 0.0;
+}
+
+extern "C" int gsdft_aux_cholesky(int64_t N, const double* log_alpha, const double* aux_centers,
+                                  double lam, double omega, double* L, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    if (N <= 0 || !log_alpha || !aux_centers || !L)
+        return fail(GSDFT_ERR_ARG, "gsdft_aux_cholesky: bad arguments");
+    if (!(omega >= 0.0) || std::isinf(omega))
+        return fail(GSDFT_ERR_ARG, "gsdft_aux_cholesky: omega must be finite and >= 0");
+    if ((N + 3) / 4 > 65535) return fail(GSDFT_ERR_ARG, "gsdft_aux_cholesky: N too large");
+    hipStream_t s = (hipStream_t)stream;
+    Arena ar{(char*)workspace, workspace_bytes, 0};
+    double* bk = ar.take<double>(2 * N + 2);
+    int64_t* info = ar.take<int64_t>(2);
+    if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_aux_cholesky: workspace too small");
+    k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
+    profile_begin(kProfMetric, s);
+    k_metric<true><<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, L);
+    profile_end(kProfMetric, s);
+    GSDFT_HIP(hipGetLastError());
+    {
+        ProfileScope prof(kProfCholesky, s);
+        GSDFT_TRY(cholesky_blocked(s, N, L, info));
+    }
+    k_zero_diag_tiles<<<blocks_for(N * kPanelRows, 256), 256, 0, s>>>(N, L);
+    GSDFT_HIP(hipGetLastError());
+    int64_t h_info = 0;
+    GSDFT_TRY(read_back(&h_info, info, sizeof(int64_t), s, "gsdft_aux_cholesky: status"));
+    if (h_info != 0)
+        return fail(GSDFT_ERR_NOT_PD, "Cholesky: leading minor %lld of V + lam I is not positive "
+                    "definite", (long long)h_info);
+    return GSDFT_OK;
+}
+
 extern "C" int gsdft_cho_solve(int64_t N, const double* L, const double* gamma, double* d,
                                double* energy, void* stream) {
     if (N <= 0 || !L || !gamma || !d) return fail(GSDFT_ERR_ARG, "gsdft_cho_solve: bad arguments");
@@ -2598,16 +2680,23 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
         k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
                                                                 w.rec_sorted);
         const Split sp = bwd_split_records(N, n);
-        dim3 grid((unsigned)((n + 255) / 256), (unsigned)sp.slabs);
+        const int64_t per_launch = bwd_slabs_per_launch(N, n);
         profile_begin(kProfGammaBwd, s);
-        k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux,
-                                                             sp.per_slab, w.acc,
-                                                             profile_work_counter(kProfGammaBwd),
-                                                             nullptr, 0, nullptr, nullptr,
-                                                             nullptr, nullptr);
+        for (int64_t sl = 0; sl < sp.slabs; sl += per_launch) {
+            const int64_t r = std::min(per_launch, sp.slabs - sl);
+            dim3 grid((unsigned)((n + 255) / 256), (unsigned)r);
+            k_gamma_bwd<false, false, true><<<grid, 256, 0, s>>>(
+                n, w.rec_sorted, N, w.aux, sp.per_slab, w.acc,
+                profile_work_counter(kProfGammaBwd), nullptr, 0, nullptr, nullptr, nullptr,
+                nullptr, 0, sl, sl == 0 ? 1 : 0);
+            GSDFT_HIP(hipGetLastError());
+            if (r > 1) {
+                k_slab_fold<<<blocks_for(n * kAcc, 256), 256, 0, s>>>(n, r, w.acc);
+                GSDFT_HIP(hipGetLastError());
+            }
+        }
         profile_end(kProfGammaBwd, s);
-        GSDFT_HIP(hipGetLastError());
-        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, sp.slabs, kPref3c,
+        k_pair_finalize<<<blocks_for(n, 256), 256, 0, s>>>(n, n, 1, kPref3c,
                                                            w.pair_order.perm, pi, pj, weight,
                                                            w.A6, centers, w.Nrm, w.rec_sorted,
                                                            w.acc, J, w.contrib);
@@ -2889,53 +2978,89 @@ extern "C" int gsdft_exact_coulomb_workspace_size(int64_t M, int64_t k, int64_t 
     return GSDFT_OK;
 }
 
-extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
-                                   const double* centers, int64_t k, const double* C,
-                                   const double* occ, int64_t n, const int32_t* pi,
-                                   const int32_t* pj, const double* weight,
-                                   const int32_t* row_ptr, const int32_t* row_perm,
-                                   const int32_t* col_ptr, const int32_t* col_perm,
-                                   double* energy, double* J, double* dquat, double* dlog_scale,
-                                   double* dcenters, double* dC, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-    const bool grads = dquat || dlog_scale || dcenters || dC;
-    if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy ||
-        (n > 0 && (!pi || !pj || !weight || !J)))
-        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: bad arguments");
-    if (grads && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
-                  (n > 0 && (!row_perm || !col_perm))))
-        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: the gradients come together (dquat, "
-                    "dlog_scale, dcenters, dC) and need the pair index");
-    if (n > INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the int32 range");
-    hipStream_t s = (hipStream_t)stream;
+namespace gsdft {
+namespace {
+
+// Pw_a = w_a P[i_a][j_a] for a row-major (M, M) density matrix P.
+__global__ void k_pair_gather_density(int64_t n, int64_t M, const int32_t* __restrict__ pi,
+                                      const int32_t* __restrict__ pj,
+                                      const double* __restrict__ weight,
+                                      const double* __restrict__ P, double* __restrict__ q) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    q[a] = weight[a] * P[(int64_t)pi[a] * M + pj[a]];
+}
+
+// dP (M, M, zeroed beforehand) = the Coulomb matrix on the listed entries: dP[i_a][j_a] = J_a
+// and, with sym, dP[j_a][i_a] = J_a too (gs_dft/coulomb/stream.py:127-134); dead entries are
+// skipped. The live entries name distinct pairs, so no two threads write one element.
+__global__ void k_scatter_density_grad(int64_t n, int64_t M, const int32_t* __restrict__ pi,
+                                       const int32_t* __restrict__ pj,
+                                       const double* __restrict__ weight,
+                                       const double* __restrict__ J, int sym,
+                                       double* __restrict__ dP) {
+    const int64_t a = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (a >= n || weight[a] == 0.0) return;
+    const int64_t i = pi[a], j = pj[a];
+    dP[i * M + j] = J[a];
+    if (sym && i != j) dP[j * M + i] = J[a];
+}
+
+// The density source of the exact Coulomb: occupied orbitals (Pw_a = w_a sum_o occ_o C_io C_jo,
+// gradient dC) or a density matrix (Pw_a = w_a P_ij, gradient dP).
+struct ExactDensity {
+    int64_t k;
+    const double *C, *occ, *P;
+    int sym;
+    double *dC, *dP;
+};
+
+int exact_run(int64_t M, const double* quat, const double* log_scale, const double* centers,
+              const ExactDensity& den, int64_t n, const int32_t* pi, const int32_t* pj,
+              const double* weight, const int32_t* row_ptr, const int32_t* row_perm,
+              const int32_t* col_ptr, const int32_t* col_perm, double* energy, double* J,
+              double* dquat, double* dlog_scale, double* dcenters, bool grads, void* workspace,
+              size_t workspace_bytes, hipStream_t s, const char* name) {
+    if (n > INT32_MAX) return fail(GSDFT_ERR_ARG, "%s: n exceeds the int32 range", name);
     Arena ar{(char*)workspace, workspace_bytes, 0};
     EriWs w;
     GSDFT_TRY(layout_eri(ar, M, n, grads, &w));
     if (!w.partial || (grads && !w.contrib))
-        return fail(GSDFT_ERR_WORKSPACE, "gsdft_exact_coulomb: workspace too small");
+        return fail(GSDFT_ERR_WORKSPACE, "%s: workspace too small", name);
+    if (den.dP) {
+        k_fill<<<blocks_for(M * M, 256), 256, 0, s>>>(M * M, 0.0, den.dP);
+        GSDFT_HIP(hipGetLastError());
+    }
     if (n == 0) {
         k_fill<<<1, 256, 0, s>>>(1, 0.0, energy);
         if (grads) {
             k_fill<<<blocks_for(4 * M, 256), 256, 0, s>>>(4 * M, 0.0, dquat);
             k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dlog_scale);
             k_fill<<<blocks_for(3 * M, 256), 256, 0, s>>>(3 * M, 0.0, dcenters);
-            k_fill<<<blocks_for(M * k, 256), 256, 0, s>>>(M * k, 0.0, dC);
+            if (den.dC)
+                k_fill<<<blocks_for(M * den.k, 256), 256, 0, s>>>(M * den.k, 0.0, den.dC);
         }
         GSDFT_HIP(hipGetLastError());
         return GSDFT_OK;
     }
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
-    GSDFT_TRY(launch_pair_density(n, pi, pj, weight, k, C, occ, w.q, s));
+    if (den.P) {
+        k_pair_gather_density<<<blocks_for(n, 256), 256, 0, s>>>(n, M, pi, pj, weight, den.P,
+                                                                 w.q);
+        GSDFT_HIP(hipGetLastError());
+    } else {
+        GSDFT_TRY(launch_pair_density(n, pi, pj, weight, den.k, den.C, den.occ, w.q, s));
+    }
     k_pair_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, pi, pj, w.A6, centers, w.Nrm, w.q, w.rec3);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec3, kRec, w.order, s));
     k_eri_rec<<<blocks_for(n, 256), 256, 0, s>>>(n, w.order.perm, pi, pj, w.A6, centers, w.Nrm,
-                                                 w.q, w.rec);
+                                                 w.q, weight, w.rec);
     GSDFT_HIP(hipGetLastError());
     if (!grads) {
         // bands of bra slots, each against the kets from its own start on
         if ((n + kEriSymSlab - 1) / kEriSymSlab > 65535)
-            return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the supported %lld pairs",
+            return fail(GSDFT_ERR_ARG, "%s: n exceeds the supported %lld pairs", name,
                         (long long)65535 * kEriSymSlab);
         k_fill<<<blocks_for(n, 256), 256, 0, s>>>(n, 0.0, w.jacc);
         profile_begin(kProfEriFwd, s);
@@ -2953,7 +3078,7 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
         k_eri_finish<<<blocks_for(n, 256), 256, 0, s>>>(n, 1, w.order.perm, w.rec, w.jacc, J);
     } else {
         if ((n + kEriSymSlabB - 1) / kEriSymSlabB > 65535)
-            return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: n exceeds the supported %lld pairs",
+            return fail(GSDFT_ERR_ARG, "%s: n exceeds the supported %lld pairs", name,
                         (long long)65535 * kEriSymSlabB);
         k_fill<<<blocks_for(kEriAcc * n, 256), 256, 0, s>>>(kEriAcc * n, 0.0, w.jacc);
         profile_begin(kProfEriBwd, s);
@@ -2977,15 +3102,70 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
     GSDFT_HIP(hipGetLastError());
     // E_J = 1/2 sum_a Pw_a J_a (gs_dft/coulomb/stream.py:319-320), fixed summation order
     GSDFT_TRY(launch_scaled_dot(n, w.q, J, 0.5, energy, w.dot_part, s));
+    if (den.dP) {
+        k_scatter_density_grad<<<blocks_for(n, 256), 256, 0, s>>>(n, M, pi, pj, weight, J,
+                                                                  den.sym, den.dP);
+        GSDFT_HIP(hipGetLastError());
+    }
     if (grads) {
         k_splat_grad<<<blocks_for(M * 64, 256), 256, 0, s>>>(M, n, row_ptr, row_perm, col_ptr,
                                                              col_perm, w.contrib, quat,
                                                              log_scale, dquat, dlog_scale,
                                                              dcenters);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(launch_dC(M, k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J, weight, C, occ,
-                            dC, s));
+        if (den.dC)
+            GSDFT_TRY(launch_dC(M, den.k, row_ptr, row_perm, col_ptr, col_perm, pi, pj, J,
+                                weight, den.C, den.occ, den.dC, s));
     }
     return GSDFT_OK;
+}
+
+}  // namespace
+}  // namespace gsdft
+
+extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
+                                   const double* centers, int64_t k, const double* C,
+                                   const double* occ, int64_t n, const int32_t* pi,
+                                   const int32_t* pj, const double* weight,
+                                   const int32_t* row_ptr, const int32_t* row_perm,
+                                   const int32_t* col_ptr, const int32_t* col_perm,
+                                   double* energy, double* J, double* dquat, double* dlog_scale,
+                                   double* dcenters, double* dC, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    const bool grads = dquat || dlog_scale || dcenters || dC;
+    if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy ||
+        (n > 0 && (!pi || !pj || !weight || !J)))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: bad arguments");
+    if (grads && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
+                  (n > 0 && (!row_perm || !col_perm))))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: the gradients come together (dquat, "
+                    "dlog_scale, dcenters, dC) and need the pair index");
+    const ExactDensity den{k, C, occ, nullptr, 0, dC, nullptr};
+    return exact_run(M, quat, log_scale, centers, den, n, pi, pj, weight, row_ptr, row_perm,
+                     col_ptr, col_perm, energy, J, dquat, dlog_scale, dcenters, grads, workspace,
+                     workspace_bytes, (hipStream_t)stream, "gsdft_exact_coulomb");
+}
+
+extern "C" int gsdft_exact_coulomb_density(int64_t M, const double* quat,
+                                           const double* log_scale, const double* centers,
+                                           const double* P, int64_t n, const int32_t* pi,
+                                           const int32_t* pj, const double* weight, int sym,
+                                           const int32_t* row_ptr, const int32_t* row_perm,
+                                           const int32_t* col_ptr, const int32_t* col_perm,
+                                           double* energy, double* J, double* dquat,
+                                           double* dlog_scale, double* dcenters, double* dP,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    const bool grads = dquat || dlog_scale || dcenters;
+    if (M <= 0 || n < 0 || !P || !energy || (n > 0 && (!pi || !pj || !weight || !J)))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb_density: bad arguments");
+    if (grads && (!dquat || !dlog_scale || !dcenters || !row_ptr || !col_ptr ||
+                  (n > 0 && (!row_perm || !col_perm))))
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb_density: the splat gradients come "
+                    "together (dquat, dlog_scale, dcenters) and need the pair index");
+    const ExactDensity den{0, nullptr, nullptr, P, sym, nullptr, dP};
+    return exact_run(M, quat, log_scale, centers, den, n, pi, pj, weight, row_ptr, row_perm,
+                     col_ptr, col_perm, energy, J, dquat, dlog_scale, dcenters, grads, workspace,
+                     workspace_bytes, (hipStream_t)stream, "gsdft_exact_coulomb_density");
 }
 

@@ -69,18 +69,18 @@ class SplatDFJ:
         if mesh is not None:
             raise NotImplementedError("mesh= shards the step across GPUs; this library runs the "
                                       "DF-J path on one GPU")
-        if screen is None:
-            raise NotImplementedError("the DF-J path here is the screened one: pass "
-                                      "screen=pairlist(...) (eps=-1.0 keeps every pair)")
         from .terms import hf_coeff
         spec = DFSpec() if coulomb is None else coulomb
+        if screen is None and not isinstance(spec, ExactSpec):
+            raise NotImplementedError("the DF-J path here is the screened one: pass "
+                                      "screen=pairlist(...) (eps=-1.0 keeps every pair)")
         self.screen = screen
-        self.coulomb = _make_coulomb(spec, screened=True,
+        self.coulomb = _make_coulomb(spec, screened=screen is not None,
                                      a_x=hf_coeff(xc) if xc is not None else 0.0,
                                      a_x_lr=float(getattr(xc, "hf_coeff_lr", 0.0) or 0.0),
                                      omega=float(getattr(xc, "omega", 0.0) or 0.0),
-                                     skip_pad=bool(screen.skip_pad))
-        if screen.unique and self.coulomb.hf_coeff != 0.0:
+                                     skip_pad=bool(screen is not None and screen.skip_pad))
+        if screen is not None and screen.unique and self.coulomb.hf_coeff != 0.0:
             raise ValueError("pairlist(unique=True) is PBE-class only: the screened RI-K "
                              "contraction is not symmetric in the pair index")
         self.mesh = None

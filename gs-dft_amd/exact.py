@@ -109,3 +109,104 @@ def screened_coulomb_J(splats, C_orth, occ, pi, pj, valid=None,
     J = torch.zeros(x["pi"].shape[0], dtype=torch.float64, device=x["dev"])
     J[:x["n"]] = x["J"]
     return J
+
+
+# ------------------------------------------------------------------ density-matrix form
+
+def make_pairs(M: int, unique: bool = True, device=None):
+    """(i, j, w) over basis-function pairs (gs_dft/coulomb/stream.py:47-60): unique=True the
+    M(M+1)/2 pairs i <= j in row-major order with w = 2 - delta_ij, unique=False all M^2 ordered
+    pairs with w = 1. int32 indices and float64 weights on ``device``."""
+    dev = _lib.device() if device is None else device
+    if unique:
+        ij = torch.triu_indices(M, M, device=dev)
+        i, j = ij[0].to(torch.int32), ij[1].to(torch.int32)
+        w = torch.where(i == j, 1.0, 2.0).to(torch.float64)
+    else:
+        r = torch.arange(M, dtype=torch.int32, device=dev)
+        i, j = r.repeat_interleave(M), r.repeat(M)
+        w = torch.ones(M * M, dtype=torch.float64, device=dev)
+    return i.contiguous(), j.contiguous(), w
+
+
+class _ExactDensityFn(torch.autograd.Function):
+    """One library pass over the list of ``x`` with the pair densities read from P: the energy
+    and, with gradients requested, dE/d(quat, log_scale, centers) and dE/dP = the Coulomb matrix
+    (the reference's custom VJP, gs_dft/coulomb/stream.py:159-183), scaled in the backward by
+    the incoming cotangent."""
+
+    @staticmethod
+    def forward(ctx, quat, log_scale, centers, P, x):
+        M, n, dev = x["M"], x["n"], x["dev"]
+        grads = any(ctx.needs_input_grad[:3])
+        E = torch.empty((), dtype=torch.float64, device=dev)
+        J = torch.empty(max(n, 1), dtype=torch.float64, device=dev)
+        outs = [None] * 3
+        csr = (None, None, None, None)
+        if grads:
+            outs = [torch.empty((M, 4), dtype=torch.float64, device=dev),
+                    torch.empty((M, 3), dtype=torch.float64, device=dev),
+                    torch.empty((M, 3), dtype=torch.float64, device=dev)]
+            idx = build_pair_index(M, x["pi"], x["pj"], x["w"])
+            csr = (idx.row_ptr, idx.row_perm, idx.col_ptr, idx.col_perm)
+        dP = None
+        if ctx.needs_input_grad[3] or x.get("want_J_matrix"):
+            dP = torch.empty((M, M), dtype=torch.float64, device=dev)
+        outs.append(dP)
+        L = _lib.lib()
+        ws = _lib.workspace(_lib.size_query(L.gsdft_exact_coulomb_workspace_size, M, 1, n,
+                                            int(grads)), dev)
+        q, l, c, Pd = (t.detach().contiguous() for t in (quat, log_scale, centers, P))
+        _lib.check(L.gsdft_exact_coulomb_density(
+            M, _lib.ptr(q), _lib.ptr(l), _lib.ptr(c), _lib.ptr(Pd), n, _lib.ptr(x["pi"]),
+            _lib.ptr(x["pj"]), _lib.ptr(x["w"]), int(x["unique"]), *(_lib.ptr(t) for t in csr),
+            _lib.ptr(E), _lib.ptr(J), *(_lib.ptr(t) for t in outs), _lib.ptr(ws), ws.numel(),
+            _lib.stream()), "full_coulomb_energy")
+        ctx.grads = outs
+        x["J"] = J[:n]
+        x["J_matrix"] = dP
+        return E
+
+    @staticmethod
+    def backward(ctx, gE):
+        return tuple(None if g is None else g * gE for g in ctx.grads) + (None,)
+
+
+def _density_inputs(splats, P, unique):
+    if not _has_splat_interface(splats):
+        raise NotImplementedError(f"full_coulomb_energy: {type(splats).__name__} is not a Splat")
+    dev = _lib.device()
+    M = splats.n_basis
+    Pt = P if isinstance(P, torch.Tensor) else _lib.f64(P, dev)
+    if Pt.device != dev or Pt.dtype != torch.float64:
+        Pt = Pt.to(device=dev, dtype=torch.float64)
+    if Pt.dim() != 2 or tuple(Pt.shape) != (M, M):
+        raise ValueError(f"P must be (M, M) with M = {M}, got {tuple(Pt.shape)}")
+    pi, pj, w = make_pairs(M, unique, dev)
+    x = {"M": M, "n": int(pi.shape[0]), "dev": dev, "pi": pi, "pj": pj, "w": w,
+         "unique": bool(unique)}
+    return Pt, x
+
+
+def full_coulomb_energy(splats, P, bra_chunk: int = 64, unique: bool = True) -> torch.Tensor:
+    """Exact E_J = 1/2 sum_pqrs (pq|rs) P_pq P_rs over every basis-function pair
+    (gs_dft/coulomb/stream.py:284-287 through coulomb_energy_fused :145-187), differentiable
+    w.r.t. the splat leaves and the density matrix P (M, M); the gradient w.r.t. P is the Coulomb
+    matrix J (symmetric fill on the unique list), as the reference's custom VJP defines it. Only
+    the upper triangle of P is read when ``unique``. O(M^4) work: the evaluation-size path.
+    ``bra_chunk`` only shaped the reference's XLA stream and does not change the value."""
+    del bra_chunk
+    Pt, x = _density_inputs(splats, P, unique)
+    return _ExactDensityFn.apply(splats.quat, splats.log_scale, splats.centers, Pt, x)
+
+
+def full_coulomb_J(splats, P, bra_chunk: int = 128, unique: bool = True) -> torch.Tensor:
+    """The Hartree matrix J_pq = sum_rs (pq|rs) P_rs (M, M) (gs_dft/coulomb/stream.py:189-195,
+    coulomb_J_fused); values only."""
+    del bra_chunk
+    Pt, x = _density_inputs(splats, P, unique)
+    x["want_J_matrix"] = True
+    with torch.no_grad():
+        _ExactDensityFn.apply(splats.quat.detach(), splats.log_scale.detach(),
+                              splats.centers.detach(), Pt.detach(), x)
+    return x["J_matrix"]

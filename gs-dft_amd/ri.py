@@ -51,15 +51,20 @@ def shift_diag(V: torch.Tensor, lam: float) -> torch.Tensor:
 
 
 def aux_cholesky(aux: IsotropicSplat, lam: float, omega=None) -> torch.Tensor:
-    """Lower Cholesky factor of V + lam I (gs_dft/coulomb/ri.py:253-264), V the metric of the
-    kernel ``omega`` selects, factored in place in the metric's own buffer."""
-    V = aux_metric(aux, omega, lam=lam)
-    N = V.shape[0]
+    """Lower Cholesky factor of V + lam I (gs_dft/coulomb/ri.py:259-264), V the metric of the
+    kernel ``omega`` selects: its lower triangle formed in the factor's own buffer and factored
+    in place."""
+    w = _omega(omega)
+    N = aux.n_basis
+    dev = aux.log_alpha.device
+    L = torch.empty((N, N), dtype=torch.float64, device=dev)
     Lb = _lib.lib()
-    ws = _lib.workspace(_lib.size_query(Lb.gsdft_metric_workspace_size, N), V.device)
-    _lib.check(Lb.gsdft_cholesky(N, _lib.ptr(V), _lib.ptr(ws), ws.numel(), _lib.stream()),
+    ws = _lib.workspace(_lib.size_query(Lb.gsdft_metric_workspace_size, N), dev)
+    _lib.check(Lb.gsdft_aux_cholesky(N, _lib.ptr(aux.log_alpha), _lib.ptr(aux.centers),
+                                     float(lam), w, _lib.ptr(L), _lib.ptr(ws), ws.numel(),
+                                     _lib.stream()),
                "aux_cholesky")
-    return V
+    return L
 
 
 # ------------------------------------------------------------------------------------ helpers

@@ -2,9 +2,10 @@
 
 ``df()``, ``exact()`` and ``pairlist()`` build the same frozen spec values as the reference
 (terms.py:58-139) and ``_make_coulomb`` resolves ``df()`` + ``screen=pairlist(...)`` to
-``ScreenedProductDFCoulomb`` and ``exact()`` + ``screen=pairlist(...)`` to
-``ScreenedExactCoulomb``, whose ``energy`` has the reference signature
-``energy(basis, C_orth, P, occ, state) -> (E_J, E_K)`` (terms.py:146-169,193-205,236-256).
+``ScreenedProductDFCoulomb``, ``exact()`` + ``screen=pairlist(...)`` to
+``ScreenedExactCoulomb`` and ``exact()`` without a screen to ``StreamedExactCoulomb``, whose
+``energy`` has the reference signature
+``energy(basis, C_orth, P, occ, state) -> (E_J, E_K)`` (terms.py:146-169,180-205,236-256).
 """
 from __future__ import annotations
 
@@ -20,8 +21,9 @@ from . import ri as _cdf
 @dataclass(frozen=True)
 class ExactSpec:
     """Exact streamed-ERI Coulomb backend (gs_dft/ks/terms.py:48-55). With a pair screen it
-    resolves to ``ScreenedExactCoulomb``; the dense (unscreened) exact strategy is not part of
-    this library. ``chunk=None`` is the strategy default (128 screened)."""
+    resolves to ``ScreenedExactCoulomb``, without one to ``StreamedExactCoulomb`` (every basis
+    pair, the density matrix P). ``chunk=None`` is the strategy default (128 screened, 64
+    streamed)."""
 
     chunk: int | None = None
 
@@ -145,6 +147,25 @@ class ScreenedExactCoulomb(CoulombTerm):
         return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
 
 
+@dataclass(frozen=True)
+class StreamedExactCoulomb(CoulombTerm):
+    """Exact E_J over every basis pair from the density matrix P (gs_dft/ks/terms.py:180-191:
+    full_coulomb_energy, the path ``evaluate()`` reports, gs_dft/ks/train.py:554); pure
+    functionals only here (the reference's hybrid branch builds the dense M^4 ERI tensor for
+    E_K, which this library does not form). With P None it is formed from C_orth and occ as the
+    reference's SplatKS does (gs_dft/ks/energy.py:335)."""
+
+    hf_coeff: float = 0.0
+    chunk: int = 64
+
+    def energy(self, basis, C_orth, P, occ, state):
+        if P is None:
+            occ_t = torch.as_tensor(occ, dtype=torch.float64, device=C_orth.device)
+            P = (C_orth * occ_t) @ C_orth.T
+        e_j = _cs.full_coulomb_energy(basis, P, bra_chunk=self.chunk)
+        return e_j, torch.zeros((), dtype=torch.float64, device=e_j.device)
+
+
 def hf_coeff(xc) -> float:
     """Exact-exchange fraction a_x of a functional (gs_dft/ks/terms.py:267-270)."""
     a = getattr(xc, "exact_exchange_fraction", None)
@@ -154,7 +175,8 @@ def hf_coeff(xc) -> float:
 def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
                   omega: float = 0.0, skip_pad: bool = False) -> CoulombTerm:
     """Resolve a spec into its term (gs_dft/ks/terms.py:273-301). The screened strategies
-    (DF-J and exact) are implemented here; the others raise with the reason."""
+    (DF-J and exact) and the streamed exact one are implemented here; the others raise with the
+    reason."""
     if isinstance(spec, DFSpec):
         if not screened:
             raise NotImplementedError("dense (unscreened) DF is not part of this library; pass "
@@ -167,9 +189,12 @@ def _make_coulomb(spec, screened: bool, a_x: float = 0.0, a_x_lr: float = 0.0,
             raise ValueError("coulomb=exact() has no range-separated exchange path; a functional "
                              f"with hf_coeff_lr={a_x_lr} needs coulomb=df()")
         if not screened:
-            raise NotImplementedError("the dense exact Coulomb (StreamedExactCoulomb) is not part "
-                                      "of this library; pass screen=pairlist(eps=-1.0) for the "
-                                      "full pair list")
+            if a_x != 0.0:
+                raise NotImplementedError(
+                    "StreamedExactCoulomb's exact exchange needs the dense M^4 ERI tensor "
+                    "(gs_dft/ks/terms.py:187-189), which this library does not form; use "
+                    "coulomb=df() (screened RI-K) for hybrids")
+            return StreamedExactCoulomb(hf_coeff=0.0, chunk=64 if spec.chunk is None else spec.chunk)
         if a_x != 0.0:
             raise ValueError("screened exact Coulomb has no exact-exchange path; use a pure "
                              "functional or coulomb=df() (screened RI-K) for hybrids.")

@@ -115,7 +115,7 @@ int gsdft_product_aux_pairs(int64_t M, const double* quat, const double* log_sca
                             int n_scales, double* log_alpha, double* aux_centers,
                             void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace for gsdft_aux_metric and gsdft_cholesky. */
+/* Workspace for gsdft_aux_metric, gsdft_cholesky and gsdft_aux_cholesky. */
 int gsdft_metric_workspace_size(int64_t N, size_t* bytes);
 
 /* V_PQ = (P|Q) with lam added to the diagonal: the 1/r kernel for omega = 0, the long-range
@@ -127,9 +127,16 @@ int gsdft_aux_metric(int64_t N, const double* log_alpha, const double* aux_cente
                      void* stream);
 
 /* In-place lower Cholesky of V (row-major), strict upper triangle zeroed. Synchronises the stream
- * to read the factorisation status. Replaces _chol_donated / aux_cholesky,
- * gs_dft/coulomb/ri.py:253-264. */
+ * to read the factorisation status. Replaces _chol_donated, gs_dft/coulomb/ri.py:253-256. */
 int gsdft_cholesky(int64_t N, double* V, void* workspace, size_t workspace_bytes, void* stream);
+
+/* L (N,N, row-major) = the lower Cholesky factor of V + lam I, V the metric gsdft_aux_metric forms
+ * for the same arguments, strict upper triangle zero. Only the lower triangle of V is formed, in L's
+ * own buffer, and factored in place. Synchronises the stream to read the factorisation status.
+ * Replaces aux_cholesky, gs_dft/coulomb/ri.py:259-264. */
+int gsdft_aux_cholesky(int64_t N, const double* log_alpha, const double* aux_centers, double lam,
+                       double omega, double* L, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* d = (L L^T)^-1 gamma and, when energy is non-null, *energy = 0.5 gamma.d (device scalar).
  * Replaces df_coulomb_solve's cho_solve branch, gs_dft/coulomb/ri.py:472-479. */
@@ -167,9 +174,11 @@ int gsdft_gamma_noalloc(int64_t M, const double* quat, const double* log_scale,
  * pair index of the same n entries. Replaces JAX's reverse pass through
  * gs_dft/coulomb/ri.py:436-469, :190-222, gs_dft/coulomb/stream.py:203-215 and
  * gs_dft/basis/spectral.py:33-40,72-82 (gs_dft/ks/train.py:367-373 holds the aux constant).
- * The workspace holds 200 bytes per pair for each slab of at most 4096 aux functions the pass is
- * cut into (up to 48 GiB in all: 44.6 GB for 11.2 M pairs and 80,000 aux functions), so that each
- * slab's records stay in one XCD's L2 while the workgroups running together walk it. */
+ * The pass is cut into slabs of at most 4096 aux functions, so that each slab's records stay in
+ * one XCD's L2 while the workgroups running together walk it; the workspace holds 200 bytes per
+ * pair for the slabs of one launch (all of them while that fits in 5 GiB, else as many as fit and
+ * at least one, the launches adding their moments to running sums): 4.5 GB for 11.2 M pairs and
+ * 80,000 aux functions, 4.1 GB for 20.6 M. */
 int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, int64_t n, size_t* bytes);
 int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_scale,
                     const double* centers, int64_t k, const double* C, const double* occ,
@@ -231,6 +240,24 @@ int gsdft_exact_coulomb(int64_t M, const double* quat, const double* log_scale,
                         const int32_t* col_perm, double* energy, double* J, double* dquat,
                         double* dlog_scale, double* dcenters, double* dC, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/* gsdft_exact_coulomb with the pair densities read from a density matrix: Pw_a = w_a P[i_a][j_a]
+ * for P (M,M) row-major. Optional, each on its own: the splat gradients (dquat, dlog_scale,
+ * dcenters together, with the pair index; grads = 1 in the workspace query) and dP (M,M) = dE/dP
+ * = the Coulomb matrix on the listed entries, dP[i_a][j_a] = J_a and, for sym != 0 (a unique
+ * list), dP[j_a][i_a] = J_a as well, zero elsewhere; the live entries must name distinct pairs.
+ * Same workspace query as gsdft_exact_coulomb (k unused).
+ * Replaces full_coulomb_energy / coulomb_energy_fused and its custom VJP,
+ * gs_dft/coulomb/stream.py:127-187,284-287 (StreamedExactCoulomb, gs_dft/ks/terms.py:180-191),
+ * over the list make_pairs builds (stream.py:47-60). */
+int gsdft_exact_coulomb_density(int64_t M, const double* quat, const double* log_scale,
+                                const double* centers, const double* P, int64_t n,
+                                const int32_t* pi, const int32_t* pj, const double* weight,
+                                int sym, const int32_t* row_ptr, const int32_t* row_perm,
+                                const int32_t* col_ptr, const int32_t* col_perm, double* energy,
+                                double* J, double* dquat, double* dlog_scale, double* dcenters,
+                                double* dP, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /* Density on a grid for the exchange-correlation term, streamed over chunks of `chunk` points
  * (<= 65535): rho (G) and, for mode >= 1, grad (G,3), and for mode 2 tau (G), of the orbitals

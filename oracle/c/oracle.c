@@ -513,6 +513,28 @@ void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, d
     free(KN);
 }
 
+/* Rows rows[0..nrows) of the same metric: V (nrows, N), lam added where the row meets the
+ * diagonal. */
+void orc_aux_metric_rows(int64_t N, const double* log_alpha, const double* centers, double lam,
+                         double omega, int64_t nrows, const int64_t* rows, double* V) {
+    double* beta = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
+    double* KN = (double*)malloc(sizeof(double) * (N > 0 ? N : 1));
+    for (int64_t p = 0; p < N; ++p) {          /* gs_dft/basis/isotropic.py:30-39 */
+        beta[p] = exp(log_alpha[p]);
+        KN[p] = pow(2.0 * beta[p] / M_PI, 0.75);
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < nrows; ++r) {
+        const int64_t p = rows[r];
+        for (int64_t q = 0; q < N; ++q)
+            V[r * N + q] = metric_one(beta[p], centers + 3 * p, KN[p], beta[q], centers + 3 * q,
+                                      KN[q], omega);
+        if (lam != 0.0) V[r * N + p] += lam;   /* ri.py:243-250 */
+    }
+    free(beta);
+    free(KN);
+}
+
 /* ---------------------------------------------------------------- Cholesky + solve */
 
 int orc_cholesky(int64_t N, double* V) {

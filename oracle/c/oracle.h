@@ -82,6 +82,10 @@ void orc_product_aux_pairs(int64_t M, const double* quat, const double* log_scal
 void orc_aux_metric(int64_t N, const double* log_alpha, const double* centers, double lam,
                     double omega, double* V);
 
+/* Rows `rows` (nrows of them) of the metric orc_aux_metric forms: V (nrows, N). */
+void orc_aux_metric_rows(int64_t N, const double* log_alpha, const double* centers, double lam,
+                         double omega, int64_t nrows, const int64_t* rows, double* V);
+
 /* Boys F0 used by the metric: 0.5*sqrt(pi/T)*erf(sqrt(T)), series below 1e-12. */
 double orc_boys0(double T);
 

@@ -243,6 +243,20 @@ def aux_metric(log_alpha, centers, lam=0.0, omega=0.0):
     return V
 
 
+def aux_metric_rows(log_alpha, centers, rows, lam=0.0, omega=0.0):
+    """Rows ``rows`` of aux_metric's V (len(rows), N), without forming the rest."""
+    la, cen = _f64(log_alpha), _f64(centers)
+    N = la.shape[0]
+    r = np.ascontiguousarray(rows, dtype=np.int64)
+    if r.size and (r.min() < 0 or r.max() >= N):
+        raise IndexError("aux_metric_rows: row index out of range")
+    V = np.empty((r.shape[0], N))
+    lib().orc_aux_metric_rows(_i64(N), _d(la), _d(cen), ctypes.c_double(lam),
+                              ctypes.c_double(omega), _i64(r.shape[0]),
+                              r.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), _d(V))
+    return V
+
+
 def cholesky(V):
     L = np.array(V, dtype=np.float64, copy=True, order="C")
     rc = lib().orc_cholesky(_i64(L.shape[0]), _d(L))

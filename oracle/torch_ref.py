@@ -301,6 +301,24 @@ def screened_coulomb_energy(quat, log_scale, centers, C, occ, pi, pj, valid):
     return 0.5 * torch.sum((block @ Pw) * Pw)
 
 
+def make_pairs(M, unique=True):
+    """gs_dft/coulomb/stream.py:47-60"""
+    if not unique:
+        i = torch.arange(M).repeat_interleave(M)
+        j = torch.arange(M).repeat(M)
+        return i, j, torch.ones(M * M, dtype=torch.float64)
+    i, j = torch.triu_indices(M, M)
+    return i, j, torch.where(i == j, 1.0, 2.0).to(torch.float64)
+
+
+def full_coulomb_energy(quat, log_scale, centers, P, unique=True):
+    """gs_dft/coulomb/stream.py:145-151,284-287 (coulomb_energy_fused's value; one bra chunk)."""
+    pi, pj, w = make_pairs(P.shape[0], unique)
+    Pw = P[pi, pj] * w
+    block = full_eri_block_schur(quat, log_scale, centers, pi, pj, pi, pj)
+    return 0.5 * torch.sum((block @ Pw) * Pw)
+
+
 def full_eval_block(A, centers, norm, pts):
     """gs_dft/screening/grid.py:52-70: splat values g (n, M) and gradients dg (n, M, 3) at pts."""
     dx = pts[:, None, 0] - centers[None, :, 0]

@@ -190,3 +190,96 @@ def test_exact_water8_energy_paths_and_sampled_J(g, wl, orc, cuda):
     err = float(np.max(np.abs(J[sel] - Jref) / np.abs(Jref)))
     print(f"[eri] water8 sampled J max elementwise rel {err:.2e}")
     assert err < 1e-12
+
+
+@pytest.mark.parametrize("unique", [True, False])
+def test_full_coulomb_energy_with_a_general_density_matrix(g, wl, orc, tr, cuda, unique):
+    """full_coulomb_energy(splats, P) (gs_dft/coulomb/stream.py:284-287) over every basis pair
+    (make_pairs, stream.py:47-60) with a density matrix that is not C occ C^T: a random indefinite
+    symmetric P on the unique list, a random non-symmetric one on the ordered list. E_J and the
+    Coulomb matrix against the oracle's Schur-form block; the splat gradients against autograd of
+    the torch literal form; dE/dP against the reference's custom VJP, the Coulomb matrix J with
+    the symmetric fill on the unique list (stream.py:127-134,159-167), which on the unique list is
+    the symmetrised autograd gradient (G + G^T) / 2."""
+    s = _small(wl, SMALL[0])
+    M = s.M
+    rng = np.random.default_rng(11 + int(unique))
+    X = rng.normal(size=(M, M))
+    P = 0.5 * (X + X.T) if unique else X
+    if unique:
+        pi, pj = np.triu_indices(M)
+        w = np.where(pi == pj, 1.0, 2.0)
+    else:
+        pi, pj = np.repeat(np.arange(M), M), np.tile(np.arange(M), M)
+        w = np.ones(M * M)
+    print(f"[full-eri] M={M} unique={unique} n={len(pi)}", flush=True)
+    B = orc.eri_block(s.quat, s.log_scale, s.centers, pi, pj, pi, pj)
+    Pw = w * P[pi, pj]
+    Jv = B @ Pw
+    E_ref = 0.5 * float(Pw @ Jv)
+    Jm_ref = np.zeros((M, M))
+    Jm_ref[pi, pj] = Jv
+    if unique:
+        Jm_ref[pj, pi] = Jv
+    basis = g.Splat(quat=_cu(s.quat, True), log_scale=_cu(s.log_scale, True),
+                    centers=_cu(s.centers, True))
+    Pd = _cu(P, True)
+    E = g.full_coulomb_energy(basis, Pd, unique=unique)
+    E.backward()
+    rel = abs(E.item() - E_ref) / abs(E_ref)
+    print(f"[full-eri] E gpu {E.item():.15e} oracle {E_ref:.15e} rel {rel:.2e}", flush=True)
+    assert rel < REL_E
+    errP = rel_max(_np(Pd.grad), Jm_ref)
+    Jm = _np(g.full_coulomb_J(basis, Pd.detach(), unique=unique))
+    errJ = rel_max(Jm, Jm_ref)
+    print(f"[full-eri] dE/dP rel-to-max {errP:.2e}, full_coulomb_J {errJ:.2e}", flush=True)
+    assert errP < REL_E and errJ < REL_E
+    assert rel_max(Jm, _np(Pd.grad)) < 1e-13     # the forward and reverse kernels' J
+    leaves = [_t(s.quat, True), _t(s.log_scale, True), _t(s.centers, True), _t(P, True)]
+    Et = tr.full_coulomb_energy(*leaves, unique=unique)
+    Et.backward()
+    for name, a, b in zip(("quat", "log_scale", "centers"),
+                          (basis.quat.grad, basis.log_scale.grad, basis.centers.grad), leaves):
+        err = rel_max(_np(a), b.grad.numpy())
+        print(f"[full-eri] d{name} rel-to-max {err:.2e}", flush=True)
+        assert err < REL_G
+    Gt = leaves[3].grad.numpy()
+    if unique:
+        Gt = 0.5 * (Gt + Gt.T)
+    assert rel_max(_np(Pd.grad), Gt) < REL_G
+
+
+def test_streamed_exact_term_equals_the_screened_full_list(g, wl, cuda):
+    """coulomb=exact() without a screen resolves to StreamedExactCoulomb (gs_dft/ks/terms.py:
+    180-191,299-300) and reads P = C diag(occ) C^T (gs_dft/ks/energy.py:335); with every pair kept
+    (eps < 0) the screened exact term computes the same energy from the same C (the reference's
+    full-list-equals-dense relation, tests/unit/test_coulomb_df.py:107), and the gradients with
+    respect to C agree. A hybrid functional on the streamed path is refused."""
+    s = wl.make_system(1)
+    mk = lambda a: _cu(a, True)
+    b1 = g.Splat(quat=mk(s.quat), log_scale=mk(s.log_scale), centers=mk(s.centers))
+    b2 = g.Splat(quat=mk(s.quat), log_scale=mk(s.log_scale), centers=mk(s.centers))
+    C1, C2 = mk(s.C), mk(s.C)
+    occ = _cu(s.occ)
+    ks1 = g.SplatDFJ(coulomb=g.exact())
+    assert isinstance(ks1.coulomb, g.StreamedExactCoulomb)
+    E1 = ks1(g.SplatModel(basis=b1, C=C1, occupations=occ), g.refresh(ks1, b1))
+    ks2 = g.SplatDFJ(coulomb=g.exact(), screen=g.pairlist(-1.0, unique=True))
+    E2 = ks2(g.SplatModel(basis=b2, C=C2, occupations=occ), g.refresh(ks2, b2))
+    rel = abs(E1.item() - E2.item()) / abs(E2.item())
+    print(f"[full-eri] CO2 M={s.M}: streamed {E1.item():.15e} screened full list "
+          f"{E2.item():.15e} rel {rel:.2e}", flush=True)
+    assert rel < 1e-12
+    E1.backward()
+    E2.backward()
+    for name, a, b in (("C", C1, C2), ("centers", b1.centers, b2.centers),
+                       ("quat", b1.quat, b2.quat)):
+        err = rel_max(_np(a.grad), _np(b.grad))
+        print(f"[full-eri] d{name} streamed vs screened rel-to-max {err:.2e}", flush=True)
+        assert err < 1e-11
+
+    class Hybrid:
+        exact_exchange_fraction = 0.25
+
+    with pytest.raises(NotImplementedError, match="M\\^4 ERI tensor"):
+        g.SplatDFJ(coulomb=g.exact(), xc=Hybrid())

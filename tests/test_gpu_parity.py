@@ -226,6 +226,26 @@ def test_cholesky_and_solve(g, wl, orc, cuda):
     assert abs(E - En) < 1e-10 * abs(En)
 
 
+@pytest.mark.parametrize("system,omega", [(1, 0.0), (2, 0.0), (2, 0.4)])
+def test_aux_cholesky_equals_metric_then_factor(g, wl, cuda, system, omega):
+    """gsdft_aux_cholesky forms only the metric's lower triangle (zeros above it) in the factor's
+    buffer and factors it in place; the factorisation reads only that triangle, so the factor is
+    bit-identical to gsdft_aux_metric's full V factored by gsdft_cholesky (1/r and erf kernels)."""
+    from gs_dft_amd import _lib, ri as _ri
+    s = wl.make_system(system)
+    aux = g.init_product_aux(_splat(g, s), scales=s.scales)
+    N = aux.n_basis
+    print(f"[aux_cholesky] system={system} N={N} omega={omega}", flush=True)
+    lam = 1e-8 if omega == 0.0 else 1e-2
+    L = g.aux_cholesky(aux, lam, omega or None)
+    V = _ri.aux_metric(aux, omega or None, lam=lam)
+    Lb = _lib.lib()
+    ws = _lib.workspace(_lib.size_query(Lb.gsdft_metric_workspace_size, N), V.device)
+    _lib.check(Lb.gsdft_cholesky(N, _lib.ptr(V), _lib.ptr(ws), ws.numel(), _lib.stream()), "chol")
+    assert torch.equal(L, V)
+    assert not torch.any(torch.triu(L, 1))
+
+
 @pytest.mark.parametrize("N", [1, 100, 1000, 1024, 2500, 3137, 4500])
 def test_blocked_cholesky_matches_lapack(g, cuda, N):
     """The blocked factorisation (2048-row panels, 128-row substitution blocks, FP64 MFMA

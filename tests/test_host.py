@@ -20,9 +20,9 @@ def test_pairlist_defaults(g):
 
 def test_make_coulomb_resolves_the_screened_strategies(g):
     """gs_dft/ks/terms.py:273-301: df() and exact() with a screen resolve to their screened terms
-    (exact() with the reference's default chunk 128), df() with a hybrid carries its a_x and a
-    range-separated one its a_x_lr and omega; the dense strategies and hybrids on the exact path
-    raise."""
+    (exact() with the reference's default chunk 128), exact() without one to
+    StreamedExactCoulomb (default chunk 64), df() with a hybrid carries its a_x and a
+    range-separated one its a_x_lr and omega; dense DF and hybrids on the exact paths raise."""
     from gs_dft_amd.terms import _make_coulomb
     t = _make_coulomb(g.df(lam=1e-6), screened=True, skip_pad=True)
     assert isinstance(t, g.ScreenedProductDFCoulomb) and t.lam == 1e-6 and t.skip_pad
@@ -31,8 +31,16 @@ def test_make_coulomb_resolves_the_screened_strategies(g):
     assert _make_coulomb(g.exact(chunk=32), screened=True).chunk == 32
     with pytest.raises(NotImplementedError):
         _make_coulomb(g.df(), screened=False)
+    st = _make_coulomb(g.exact(), screened=False)
+    assert isinstance(st, g.StreamedExactCoulomb) and st.chunk == 64 and st.hf_coeff == 0.0
+    assert _make_coulomb(g.exact(chunk=16), screened=False).chunk == 16
+    with pytest.raises(NotImplementedError, match="M\\^4 ERI tensor"):
+        _make_coulomb(g.exact(), screened=False, a_x=0.25)
+    with pytest.raises(ValueError):
+        _make_coulomb(g.exact(), screened=False, a_x_lr=0.5)
+    assert isinstance(g.SplatDFJ(coulomb=g.exact()).coulomb, g.StreamedExactCoulomb)
     with pytest.raises(NotImplementedError):
-        _make_coulomb(g.exact(), screened=False)
+        g.SplatDFJ(coulomb=g.df())
     with pytest.raises(ValueError):
         _make_coulomb(g.exact(), screened=True, a_x=0.25)
     with pytest.raises(ValueError):

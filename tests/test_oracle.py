@@ -293,6 +293,21 @@ def test_metric_textbook_closed_form_and_limits(orc):
     assert abs(orc.boys0(0.0) - 1.0) < 1e-16 and abs(orc.boys0(1e-13) - (1 - 1e-13 / 3)) < 1e-16
 
 
+@pytest.mark.parametrize("lam,omega", [(0.0, 0.0), (1e-8, 0.0), (1e-2, 0.7)])
+def test_metric_rows_are_the_metric_rows(orc, lam, omega):
+    """aux_metric_rows (the full-size tests' sampled rows) gives exactly the rows of aux_metric,
+    the shift on the diagonal included; an out-of-range row is refused."""
+    rng = np.random.default_rng(15)
+    N = 57
+    la = rng.uniform(-2.5, 2.0, N)
+    cen = rng.normal(0, 2.0, (N, 3))
+    V = orc.aux_metric(la, cen, lam, omega)
+    rows = np.array([0, 3, 3, 56, 20])
+    assert np.array_equal(orc.aux_metric_rows(la, cen, rows, lam, omega), V[rows])
+    with pytest.raises(IndexError):
+        orc.aux_metric_rows(la, cen, [N], lam, omega)
+
+
 def test_cholesky_and_solve_match_lapack(orc, wl):
     s = wl.make_small(40, 3, seed=14)
     la, ac = orc.product_aux(s.quat, s.log_scale, s.centers, (0.5, 1.0, 2.0, 4.0))
