@@ -75,6 +75,8 @@ SIGNATURES = {
                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "gsdft_exact_coulomb_density": [_i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _vp,
                                     _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "gsdft_dgemm": [_int, _int, _i64, _i64, _i64, _dbl, _vp, _i64, _vp, _i64, _dbl, _vp, _i64,
+                    _vp],
     "gsdft_exchange_workspace_size": [_i64, _i64, _i64, _i64, _int, _int, _i64, _int, _psz],
     "gsdft_exchange": [_i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                        _vp, _vp, _vp, _vp, _int, _i64, _int, _dbl, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -1,7 +1,7 @@
 """Compile libgsdft.so for gfx950 in-tree (``gs-dft_amd/lib/libgsdft.so``).
 
-The library is plain hipcc output linked against rocBLAS; the translation units are
-compiled in parallel and linked into one shared object. FP contraction is off so every fused
+The library is plain hipcc output with no library dependency beyond the HIP runtime; the
+translation units are compiled in parallel and linked into one shared object. FP contraction is off so every fused
 multiply-add in the kernels is an explicit ``fma``; packed-FP32 instruction selection is disabled.
 """
 from __future__ import annotations
@@ -66,7 +66,7 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> pathlib.Path
     tmp = LIB.with_suffix(".so.tmp")
     link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
             *[str(obj_dir / (pathlib.Path(s).stem + ".o")) for s in SOURCES],
-            f"-L{ROCM / 'lib'}", "-lrocblas", f"-Wl,-rpath,{ROCM / 'lib'}"]
+            f"-Wl,-rpath,{ROCM / 'lib'}"]
     r = subprocess.run(link, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

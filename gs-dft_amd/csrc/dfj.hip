@@ -23,7 +23,6 @@
 //               cotangent moments per slab in registers; the slabs' moments are added in slab
 //               order, and per-pair results are mapped to per-splat gradients by wave-per-splat
 //               segmented sums over the CSR pair index.
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
@@ -479,24 +478,39 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                      Pz = live ? r[11] : kFarAway;
         const double coef = live ? r[12] : 0.0;
         double q0d = 0, q1 = 0, X0 = 0, rr = 0, cf = coef;
+        // Each record's centre, new-centre flag and node-0 constants are read one record ahead
+        // (the first record's here), so their scalar loads overlap a node loop instead of
+        // stalling the record's start.
+        const double* __restrict__ xf = aux + kAuxRec * q0;
+        double c_x = xf[0], c_y = xf[1], c_z = xf[2];
+        double c_s = xf[rec_s(0)], c_wh = xf[rec_wh(0)], c_is = xf[rec_is(0)];
+        uint64_t c_new = 1;                          // the flag's bits, tested when used
         for (int j = 0; j < nrec; ++j) {
             const double* __restrict__ x = aux + kAuxRec * (q0 + j);
-            if (j == 0 || new_centre(x)) {           // wave-uniform
-                const double dx = x[0] - Px, dy = x[1] - Py, dz = x[2] - Pz;
-                const double ax = xx * dx + xy * dy + xz * dz;
-                const double ay = xy * dx + yy * dy + yz * dz;
-                const double az = xz * dx + yz * dy + zz * dz;
-                q0d = dx * dx + dy * dy + dz * dz;
-                q1 = dx * ax + dy * ay + dz * az;
-                const double q2 = ax * ax + ay * ay + az * az;
+            const double Rx = c_x, Ry = c_y, Rz = c_z;
+            double n_s = c_s, n_wh = c_wh, n_is = c_is;
+            const bool fresh = c_new != 0;
+            if (j + 1 < nrec) {                      // wave-uniform
+                const double* __restrict__ xn = x + kAuxRec;
+                c_x = xn[0]; c_y = xn[1]; c_z = xn[2];
+                c_s = xn[rec_s(0)]; c_wh = xn[rec_wh(0)]; c_is = xn[rec_is(0)];
+                c_new = __builtin_bit_cast(uint64_t, xn[5]);
+            }
+            if (fresh) {                             // wave-uniform
+                const double dx = Rx - Px, dy = Ry - Py, dz = Rz - Pz;
+                const double ax = __builtin_fma(xx, dx, __builtin_fma(xy, dy, xz * dz));
+                const double ay = __builtin_fma(xy, dx, __builtin_fma(yy, dy, yz * dz));
+                const double az = __builtin_fma(xz, dx, __builtin_fma(yz, dy, zz * dz));
+                q0d = __builtin_fma(dx, dx, __builtin_fma(dy, dy, dz * dz));
+                q1 = __builtin_fma(dx, ax, __builtin_fma(dy, ay, dz * az));
+                const double q2 = __builtin_fma(ax, ax, __builtin_fma(ay, ay, az * az));
                 X0 = I3 * q0d;
-                rr = I1 * q1 - q2;
+                rr = __builtin_fma(I1, q1, -q2);
                 cf = (q0d == q0d) ? coef : q0d;      // a NaN centre propagates
             }
             double F = 0.0;
             // each node's constants are read one node ahead, so their scalar load overlaps the
             // previous node's arithmetic
-            double n_s = x[rec_s(0)], n_wh = x[rec_wh(0)], n_is = x[rec_is(0)];
             auto node = [&](auto tc) {
                 constexpr int t = decltype(tc)::value;
                 const double st = n_s, wh = n_wh, is = n_is;
@@ -764,9 +778,28 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
     for (int j = 0; j < kUb; ++j) ub[j] = 0.0;
     const bool uvec = kLaneU && (ldu % 2 == 0) && (p0 % 2 == 0) &&
                       (reinterpret_cast<uintptr_t>(ut) % 16 == 0);
+    // Each record's centre, u, new-centre flag and node-0 constants are read one record ahead
+    // (the first record's here), so their scalar loads overlap a node loop instead of stalling the
+    // record's start.
+    double c_x = 0, c_y = 0, c_z = 0, c_u = 0, c_s = 0, c_wh = 0, c_s2 = 0, c_is = 0;
+    uint64_t c_new = 1;                                  // the flag's bits, tested when used
+    if (p0 < p1) {
+        const double* __restrict__ xf = aux + kAuxRec * p0;
+        c_x = xf[0]; c_y = xf[1]; c_z = xf[2]; c_u = xf[3];
+        c_s = xf[rec_s(0)]; c_wh = xf[rec_wh(0)]; c_s2 = xf[rec_s2(0)]; c_is = xf[rec_is(0)];
+    }
     for (int64_t p = p0; p < p1; ++p) {
         const double* __restrict__ x = aux + kAuxRec * p;
-        double u = x[3];
+        const double Rx = c_x, Ry = c_y, Rz = c_z;
+        double u = c_u;
+        double n_s = c_s, n_wh = c_wh, n_s2 = c_s2, n_is = c_is;
+        const bool fresh = c_new != 0;
+        if (p + 1 < p1) {                                // wave-uniform
+            const double* __restrict__ xn = x + kAuxRec;
+            c_x = xn[0]; c_y = xn[1]; c_z = xn[2]; c_u = xn[3];
+            c_s = xn[rec_s(0)]; c_wh = xn[rec_wh(0)]; c_s2 = xn[rec_s2(0)]; c_is = xn[rec_is(0)];
+            c_new = __builtin_bit_cast(uint64_t, xn[5]);
+        }
         if constexpr (kLaneU) {
             if (((p - p0) % kUb) == 0) {                 // wave-uniform
 #pragma unroll
@@ -795,25 +828,25 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
 #pragma unroll
             for (int j = 0; j + 1 < kUb; ++j) ub[j] = ub[j + 1];
         }
-        if (p == p0 || new_centre(x)) {          // wave-uniform
+        if (fresh) {                                     // wave-uniform
             flush();
             const int l = threadIdx.x;
             const double xx = geo[0][l], yy = geo[1][l], zz = geo[2][l], xy = geo[3][l],
                          xz = geo[4][l], yz = geo[5][l];
-            d[0] = x[0] - geo[6][l]; d[1] = x[1] - geo[7][l]; d[2] = x[2] - geo[8][l];
-            const double ax = xx * d[0] + xy * d[1] + xz * d[2];
-            const double ay = xy * d[0] + yy * d[1] + yz * d[2];
-            const double az = xz * d[0] + yz * d[1] + zz * d[2];
-            q0 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
-            q1 = d[0] * ax + d[1] * ay + d[2] * az;
-            const double q2 = ax * ax + ay * ay + az * az;
+            d[0] = Rx - geo[6][l]; d[1] = Ry - geo[7][l]; d[2] = Rz - geo[8][l];
+            const double ax = __builtin_fma(xx, d[0], __builtin_fma(xy, d[1], xz * d[2]));
+            const double ay = __builtin_fma(xy, d[0], __builtin_fma(yy, d[1], yz * d[2]));
+            const double az = __builtin_fma(xz, d[0], __builtin_fma(yz, d[1], zz * d[2]));
+            q0 = __builtin_fma(d[0], d[0], __builtin_fma(d[1], d[1], d[2] * d[2]));
+            q1 = __builtin_fma(d[0], ax, __builtin_fma(d[1], ay, d[2] * az));
+            const double q2 = __builtin_fma(ax, ax, __builtin_fma(ay, ay, az * az));
             X0 = I3 * q0;
-            rr = I1 * q1 - q2;
+            rr = __builtin_fma(I1, q1, -q2);
             if constexpr (kAtomF) {
                 ad[0] = ax; ad[1] = ay; ad[2] = az;
-                a2d[0] = xx * ax + xy * ay + xz * az;
-                a2d[1] = xy * ax + yy * ay + yz * az;
-                a2d[2] = xz * ax + yz * ay + zz * az;
+                a2d[0] = __builtin_fma(xx, ax, __builtin_fma(xy, ay, xz * az));
+                a2d[1] = __builtin_fma(xy, ax, __builtin_fma(yy, ay, yz * az));
+                a2d[2] = __builtin_fma(xz, ax, __builtin_fma(yz, ay, zz * az));
             }
         }
         if constexpr (!kFold) {
@@ -821,7 +854,6 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
         }
         // each node's constants are read one node ahead, so their scalar load overlaps the
         // previous node's arithmetic
-        double n_s = x[rec_s(0)], n_wh = x[rec_wh(0)], n_s2 = x[rec_s2(0)], n_is = x[rec_is(0)];
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
             const double st = n_s, wh = n_wh, s2 = n_s2, is = n_is;
@@ -1872,27 +1904,6 @@ int gamma_prologue(int64_t M, const double* quat, const double* log_scale, const
 
 }  // namespace
 
-namespace {
-std::mutex g_blas_mu;
-std::vector<rocblas_handle> g_blas;
-}  // namespace
-
-// rocBLAS handle per device, bound to stream s.
-int blas_handle(hipStream_t s, rocblas_handle* out) {
-    int dev = 0;
-    GSDFT_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_blas_mu);
-    if ((int)g_blas.size() <= dev) g_blas.resize(dev + 1, nullptr);
-    if (!g_blas[dev]) {
-        if (rocblas_create_handle(&g_blas[dev]) != rocblas_status_success)
-            return fail(GSDFT_ERR_LIB, "rocblas_create_handle failed");
-    }
-    if (rocblas_set_stream(g_blas[dev], s) != rocblas_status_success)
-        return fail(GSDFT_ERR_LIB, "rocblas_set_stream failed");
-    *out = g_blas[dev];
-    return GSDFT_OK;
-}
-
 
 // ------------------------------------------------------------------ exchange: three-centre passes
 
@@ -2255,7 +2266,7 @@ __global__ __launch_bounds__(kPotfThreads) void k_potf2(int64_t N, double* __res
 }
 
 // X <- U^-T X for one diagonal block on the FP64 MFMA: U is ib x ib upper (column-major, leading
-// dimension N; U(c, r) at U[r N + c]), X is ib x T (column-major, leading dimension N). Each wave
+// dimension N; U(c, r) at U[r N + c]), X is ib x T (column-major, leading dimension ldx). Each wave
 // holds 16 columns of X as eight 16 x 16 accumulator tiles, one per 16-row block
 // (v_mfma_f64_16x16x4f64 layout: lane l holds rows l / 16 + 4 r, r < 4, of column l % 16). Block
 // b is solved row by row on the VALU (x_i = acc * (1 / U(i, i)), broadcast from the lane group
@@ -2268,6 +2279,10 @@ __global__ __launch_bounds__(kPotfThreads) void k_potf2(int64_t N, double* __res
 // on and below the diagonal) are staged in LDS once per workgroup, with the reciprocals of the
 // diagonal. Rows past ib and columns past T are zero and not stored; every load reads an
 // in-range address.
+// kBack solves U X = P instead (X <- U^-1 X): the blocks and their rows from the last, row i
+// subtracting U(i', i) x_i from the rows i' < i and block b subtracting U(b' rows, b columns) X_b
+// from the blocks b' < b. kRowRHS takes the right-hand sides as the columns of a row-major block:
+// X(r, c) at X[r ldx + c] (the solves of X U = B and X U^T = B for a column-major X).
 typedef double v4d_sub __attribute__((ext_vector_type(4)));
 constexpr int kSubTiles = 28;
 __host__ __device__ constexpr int sub_tile(int a, int b) { return b * (b - 1) / 2 + a; }
@@ -2292,26 +2307,32 @@ __device__ __forceinline__ double group_bcast(double v) {
     return g % 2 == 0 ? e : o;
 }
 
+template <bool kBack, bool kRowRHS>
 __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __restrict__ U,
-                                                     int ib, double* __restrict__ X, int64_t T) {
-    __shared__ double Ut[kSubTiles][16][16];    // Ut[(a, b)][k][c] = -U(16 a + k, 16 b + c)
-    __shared__ double Ud[8][16][16];            // Ud[b][i][4 g + r] = U(16 b + i, 16 b + g + 4 r)
+                                                     int ib, double* __restrict__ X, int64_t T,
+                                                     int64_t ldx) {
+    // Ut[(a, b)][k][c] = -U(16 a + k, 16 b + c) (kBack: -U(16 a + c, 16 b + k)), a < b;
+    // Ud[b][i][4 g + r] = U(16 b + i, 16 b + g + 4 r) for g + 4 r > i
+    // (kBack: U(16 b + g + 4 r, 16 b + i) for g + 4 r < i)
+    __shared__ double Ut[kSubTiles][16][16];
+    __shared__ double Ud[8][16][16];
     __shared__ double rdg[kPanelRows];
     const int t = threadIdx.x;
 #pragma unroll
     for (int b = 1; b < 8; ++b)
 #pragma unroll
         for (int a = 0; a < b; ++a) {
-            const int k = t & 15, c = t >> 4, row = 16 * a + k, col = 16 * b + c;
+            const int k = t & 15, c = t >> 4;
+            const int row = kBack ? 16 * a + c : 16 * a + k, col = kBack ? 16 * b + k : 16 * b + c;
             const double v = U[(int64_t)min(col, ib - 1) * N + min(row, ib - 1)];
             Ut[sub_tile(a, b)][k][c] = (row < ib && col < ib) ? -v : 0.0;
         }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
         const int i = t >> 4, sl = t & 15, ip = (sl >> 2) + 4 * (sl & 3);
-        const int row = 16 * b + i, col = 16 * b + ip;
+        const int row = kBack ? 16 * b + ip : 16 * b + i, col = kBack ? 16 * b + i : 16 * b + ip;
         const double v = U[(int64_t)min(col, ib - 1) * N + min(row, ib - 1)];
-        Ud[b][i][sl] = (ip > i && row < ib && col < ib) ? v : 0.0;
+        Ud[b][i][sl] = ((kBack ? ip < i : ip > i) && row < ib && col < ib) ? v : 0.0;
     }
     if (t < kPanelRows) rdg[t] = t < ib ? 1.0 / U[(int64_t)t * N + t] : 0.0;
     const int l = t & 63, g = l >> 4;
@@ -2319,33 +2340,36 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
     const bool live = cc < T;
     // every load reads an in-range address (columns past T and rows past ib clamped to the
     // last ones); the values that stand for nothing are zeroed
-    const double* __restrict__ xc = X + (live ? cc : T - 1) * N;
+    const int64_t ccl = live ? cc : T - 1;
+    auto at = [&](int row) -> int64_t { return kRowRHS ? row * ldx + ccl : ccl * ldx + row; };
     v4d_sub C[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 16 * b + g + 4 * r;
-            const double v = xc[row < ib ? row : ib - 1];
+            const double v = X[at(row < ib ? row : ib - 1)];
             C[b][r] = (live && row < ib) ? v : 0.0;
         }
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int bb = 0; bb < 8; ++bb) {
+        const int b = kBack ? 7 - bb : bb;
         // the block's reciprocals, lane j % 16 holding row j's (read with readlane), and each
         // step's four U entries loaded one step ahead, so the row chain waits on no LDS read
         const double rv = rdg[16 * b + (l & 15)];
         double un[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) un[r] = Ud[b][0][4 * g + r];
+        for (int r = 0; r < 4; ++r) un[r] = Ud[b][kBack ? 15 : 0][4 * g + r];
         auto step = [&](auto ic) {
-            constexpr int i = decltype(ic)::value, gi = i % 4, ri = i / 4;
+            constexpr int i = kBack ? 15 - decltype(ic)::value : decltype(ic)::value;
+            constexpr int gi = i % 4, ri = i / 4;
             double u[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) u[r] = un[r];
-            if constexpr (i + 1 < 16) {
+            if constexpr (kBack ? i > 0 : i + 1 < 16) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) un[r] = Ud[b][i + 1][4 * g + r];
+                for (int r = 0; r < 4; ++r) un[r] = Ud[b][kBack ? i - 1 : i + 1][4 * g + r];
             }
             const double x = C[b][ri] * readlane_f64(rv, i);
             const double y = group_bcast<gi>(x);
@@ -2355,11 +2379,14 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
         };
         static_for<0, 16>(step);
 #pragma unroll
-        for (int b2 = b + 1; b2 < 8; ++b2)
+        for (int b2 = 0; b2 < 8; ++b2) {
+            if (kBack ? b2 >= b : b2 <= b) continue;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
                 C[b2] = __builtin_amdgcn_mfma_f64_16x16x4f64(
-                    Ut[sub_tile(b, b2)][4 * kk + g][l & 15], C[b][kk], C[b2], 0, 0, 0);
+                    Ut[kBack ? sub_tile(b2, b) : sub_tile(b, b2)][4 * kk + g][l & 15], C[b][kk],
+                    C[b2], 0, 0, 0);
+        }
     }
     if (!live) return;
 #pragma unroll
@@ -2367,7 +2394,7 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 16 * b + g + 4 * r;
-            if (row < ib) X[cc * N + row] = C[b][r];
+            if (row < ib) X[at(row)] = C[b][r];
         }
 }
 
@@ -2381,7 +2408,8 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
 static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, double* P,
                        int64_t T) {
     if (kb <= kPanelRows) {
-        k_panel_subst<<<(unsigned)((T + 63) / 64), 256, 0, s>>>(N, Akk, (int)kb, P, T);
+        k_panel_subst<false, false><<<(unsigned)((T + 63) / 64), 256, 0, s>>>(N, Akk, (int)kb, P,
+                                                                             T, N);
         GSDFT_HIP(hipGetLastError());
         return GSDFT_OK;
     }
@@ -2391,6 +2419,43 @@ static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, 
     GSDFT_TRY(launch_gemm_tn_sub(kb - h, T, h, Akk + h * N, N, P, N, P + h, N, false, s));
     return panel_solve(s, N, Akk + h * N + h, kb - h, P + h, T);
 }
+
+namespace gsdft {
+
+// X (m x n, column-major, leading dimension ldx) <- X U^-1, the solution of X U = B, or, with
+// trans, X <- X U^-T, the solution of X U^T = B, for the n x n upper U (column-major, leading
+// dimension ldu): the same recursive halving as panel_solve with the right-hand sides as X's rows
+// (k_panel_subst with kRowRHS; kBack for U^T) and the coupling products on the general FP64 MFMA
+// product. Each row of X is solved by substitution in the order a row-by-row solve takes.
+int trsm_right_upper(hipStream_t s, bool trans, int64_t n, const double* U, int64_t ldu,
+                     double* X, int64_t m, int64_t ldx) {
+    if (n <= 0 || m <= 0) return GSDFT_OK;
+    if (n <= kPanelRows) {
+        const unsigned blocks = (unsigned)((m + 63) / 64);
+        if (trans)
+            k_panel_subst<true, true><<<blocks, 256, 0, s>>>(ldu, U, (int)n, X, m, ldx);
+        else
+            k_panel_subst<false, true><<<blocks, 256, 0, s>>>(ldu, U, (int)n, X, m, ldx);
+        GSDFT_HIP(hipGetLastError());
+        return GSDFT_OK;
+    }
+    const int64_t h = (n / kPanelRows + 1) / 2 * kPanelRows;
+    const double* U01 = U + h * ldu;                 // rows [0, h), columns [h, n)
+    const double* U11 = U + h * ldu + h;
+    if (!trans) {
+        GSDFT_TRY(trsm_right_upper(s, false, h, U, ldu, X, m, ldx));
+        // X(:, h:n) -= X(:, 0:h) U(0:h, h:n)
+        GSDFT_TRY(gemm_cm('N', 'N', m, n - h, h, -1.0, X, ldx, U01, ldu, 1.0, X + h * ldx, ldx,
+                          s));
+        return trsm_right_upper(s, false, n - h, U11, ldu, X + h * ldx, m, ldx);
+    }
+    GSDFT_TRY(trsm_right_upper(s, true, n - h, U11, ldu, X + h * ldx, m, ldx));
+    // X(:, 0:h) -= X(:, h:n) U(0:h, h:n)^T
+    GSDFT_TRY(gemm_cm('N', 'T', m, h, n - h, -1.0, X + h * ldx, ldx, U01, ldu, 1.0, X, ldx, s));
+    return trsm_right_upper(s, true, h, U, ldu, X, m, ldx);
+}
+
+}  // namespace gsdft
 
 // C (T x T at C, leading dimension N) -= P^T P for the kb x T panel P, on the tiles on or above
 // the diagonal (the sub-diagonal half of the diagonal tiles is formed too and never read).

@@ -18,7 +18,8 @@
 //                         MFMA over the row's block columns and gathered C rows)
 //   D_P = C^T Y_P       one FP64 GEMM per chunk: k x (W k) x M
 //   Dt[:, P]            packed columns of D_P                                    (k_exch_pack)
-// then Wt = Dt L^-T (rocBLAS trsm over the packed-column right-hand sides) and E_K = -sum Wt^2.
+// then Wt = Dt L^-T (blocked substitution over the packed-column right-hand sides,
+// trsm_right_upper) and E_K = -sum Wt^2.
 // Reverse with seed dE_K = 1: Dbar_t = -2 Wt L^-1 (trsm), then per chunk Dbar_P (k_exch_unpack),
 // with the forward's Y (and Y') kept in the workspace when they fit, else recomputed,
 //   dC    += Y_P Dbar_P^T + Y'_P Dbar_P      Y'[m][l][o] = sum over pairs a of column m of
@@ -27,10 +28,9 @@
 //   and the three-centre reverse with the per-(P, group) cotangent, the sum of its entries' Tbar
 //   (dfj.hip), for the splat gradients. On a symmetric list Dbar_P is symmetric, so the entries
 //   of a group share Tbar = (C Dbar_P C^T)[i][k]: the sampled product runs once per group (over
-//   the groups as a CSR by lower splat) and the reverse takes that row times the entry count. Every sum runs in a fixed order (no atomics; rocBLAS runs
-//   with atomics off).
-#include <rocblas/rocblas.h>
-
+//   the groups as a CSR by lower splat) and the reverse takes that row times the entry count.
+//   Every sum runs in a fixed order (no atomics); the dense products and the triangular solves
+//   are the library's own FP64 MFMA kernels (gemm.hip, trsm_right_upper).
 #include <algorithm>
 
 #include <cmath>
@@ -44,12 +44,11 @@ namespace {
 
 inline unsigned nblk(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
-#define GSDFT_BLAS(call)                                                                   \
-    do {                                                                                   \
-        rocblas_status st_ = (call);                                                       \
-        if (st_ != rocblas_status_success)                                                 \
-            return fail(GSDFT_ERR_LIB, "%s failed (rocBLAS status %d)", #call, (int)st_);  \
-    } while (0)
+// x <- alpha x over n doubles.
+__global__ void k_scale(int64_t n, double alpha, double* __restrict__ x) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i < n) x[i] *= alpha;
+}
 
 constexpr double kRsqrt2 = 0.70710678118654752440;
 constexpr int kRedBlocks = 1024;
@@ -221,10 +220,18 @@ __global__ void k_csr_partner(int64_t n, const int32_t* __restrict__ perm,
     else if (r < n + kColPad) col[r] = 0;
 }
 
-// Packed columns of D_P (P the aux of slot q0 + l): Dfull[o + k (l k + o')] = D_P[o][o'];
-// Dt[j + K2 P] with j = o'(o'+1)/2 + o for the symmetric part (o <= o') and
+// The leading dimension of the packed columns: K2 rounded up to even, so that every column starts
+// 16-byte aligned (the triangular solves stage them by DMA); the padding row stays zero.
+inline int64_t packed_ld(int64_t K2) { return K2 + (K2 & 1); }
+
+// The leading dimension of the per-chunk D_P blocks: k rounded up to even (16-byte aligned
+// columns for the DMA path of the products that read them).
+__host__ __device__ inline int64_t dblock_ld(int64_t k) { return k + (k & 1); }
+
+// Packed columns of D_P (P the aux of slot q0 + l): Dfull[o + kd (l k + o')] = D_P[o][o'];
+// Dt[j + ldd P] with j = o'(o'+1)/2 + o for the symmetric part (o <= o') and
 // k(k+1)/2 + o'(o'-1)/2 + o for the antisymmetric part (o < o', only when !sym).
-__global__ void k_exch_pack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q0, int64_t N,
+__global__ void k_exch_pack(int64_t W, int64_t k, int64_t ldd, int sym, int64_t q0, int64_t N,
                             int64_t G, const double* __restrict__ Dfull, double* __restrict__ Dt) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     const int64_t kk = k * k;
@@ -233,9 +240,10 @@ __global__ void k_exch_pack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q
     const int64_t op = rem / k, o = rem - op * k;
     if (o > op) return;
     const int64_t P = aux_of_slot(q0 + l, N, G);
-    const double* Dl = Dfull + l * kk;
-    double* col = Dt + K2 * P;
-    const double d1 = Dl[o + k * op], d2 = Dl[op + k * o];
+    const int64_t kd = dblock_ld(k);
+    const double* Dl = Dfull + l * k * kd;
+    double* col = Dt + ldd * P;
+    const double d1 = Dl[o + kd * op], d2 = Dl[op + kd * o];
     const int64_t js = op * (op + 1) / 2 + o;
     if (o == op) {
         col[js] = d1;
@@ -245,9 +253,9 @@ __global__ void k_exch_pack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q
     }
 }
 
-// Reverse of k_exch_pack: Dbar[o + k (l k + o')] = dE/dD_P[o][o'] and, for a non-null E, its
-// block transpose E[o' + k (l k + o)].
-__global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t q0, int64_t N,
+// Reverse of k_exch_pack: Dbar[o + kd (l k + o')] = dE/dD_P[o][o'] and, for a non-null E, its
+// block transpose E[o' + kd (l k + o)].
+__global__ void k_exch_unpack(int64_t W, int64_t k, int64_t ldd, int sym, int64_t q0, int64_t N,
                               int64_t G, const double* __restrict__ Dbt, double* __restrict__ Dbar,
                               double* __restrict__ E) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -256,7 +264,7 @@ __global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t
     const int64_t l = t / kk, rem = t - l * kk;
     const int64_t op = rem / k, o = rem - op * k;
     const int64_t P = aux_of_slot(q0 + l, N, G);
-    const double* col = Dbt + K2 * P;
+    const double* col = Dbt + ldd * P;
     const int64_t lo = o < op ? o : op, hi = o < op ? op : o;
     double v = col[hi * (hi + 1) / 2 + lo];
     if (o != op) {
@@ -266,8 +274,9 @@ __global__ void k_exch_unpack(int64_t W, int64_t k, int64_t K2, int sym, int64_t
             v += (o < op) ? a : -a;
         }
     }
-    Dbar[o + k * (l * k + op)] = v;
-    if (E) E[op + k * (l * k + o)] = v;
+    const int64_t kd = dblock_ld(k);
+    Dbar[o + kd * (l * k + op)] = v;
+    if (E) E[op + kd * (l * k + o)] = v;
 }
 
 // Tbar[inv[a] * ldt + l] = sum_o Ybar[i][l][o] C[k_a][o] for the pairs a of row i and l < W
@@ -524,14 +533,14 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
     GSDFT_TRY(exch_tc_layout(ar, M, N, n, Pc, grads, &w->tc));
     const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
     const bool store = exch_store(M, k, N, sym, grads, recompute);
-    w->Dt = ar.take<double>(K2 * N + 1);
+    w->Dt = ar.take<double>(packed_ld(K2) * N + 1);
     w->Bt = ar.take<double>(n * Pc + 1);
     w->Y = ar.take<double>(M * Pc * k + 1);
     w->Yp = (grads && !sym && !store) ? ar.take<double>(M * Pc * k + 1) : nullptr;
     w->Ys = store ? ar.take<double>(M * N * k + 1) : nullptr;
     w->Yps = (store && !sym) ? ar.take<double>(M * N * k + 1) : nullptr;
-    w->Dfull = ar.take<double>(k * k * Pc + 1);
-    w->Ebar = (grads && !sym) ? ar.take<double>(k * k * Pc + 1) : nullptr;
+    w->Dfull = ar.take<double>(dblock_ld(k) * k * Pc + 1);
+    w->Ebar = (grads && !sym) ? ar.take<double>(dblock_ld(k) * k * Pc + 1) : nullptr;
     w->part = grads ? ar.take<double>(kSplitMax * k * M + 1) : nullptr;
     w->red = ar.take<double>(kRedBlocks);
     w->Cp = ar.take<double>(M * padded_cols(k) + 1);
@@ -546,21 +555,18 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
     return GSDFT_OK;
 }
 
-// dC^T (k x M, column-major = row-major dC) += alpha Dbar (k x W k) Y^T-view (W k x M, ld W k),
-// as S K-slices of Ws = W / S aux functions (the remainder joins the last slice) into part, then
-// summed in slice order.
-int dc_gemm(rocblas_handle h, int64_t k, int64_t M, int64_t W, double alpha, const double* Dbar,
-            const double* Y, double* part, double* dC, hipStream_t s) {
-    const int64_t S = dc_slices(k, M, W), Ws = W / S, Wk = W * k;
-    const double one = 1.0, zero = 0.0;
-    const auto N_ = rocblas_operation_none;
-    GSDFT_BLAS(rocblas_dgemm_strided_batched_64(h, N_, N_, k, M, Ws * k, &alpha, Dbar, k,
-                                                k * Ws * k, Y, Wk, Ws * k, &zero, part, k, k * M,
-                                                S));
+// dC^T (k x M, column-major = row-major dC) += alpha Dbar (k x W k, leading dimension
+// dblock_ld(k)) Y^T-view (W k x M, ld W k), as S K-slices of Ws = W / S aux functions (the
+// remainder joins the last slice) into part, then summed in slice order.
+int dc_gemm(int64_t k, int64_t M, int64_t W, double alpha, const double* Dbar, const double* Y,
+            double* part, double* dC, hipStream_t s) {
+    const int64_t S = dc_slices(k, M, W), Ws = W / S, Wk = W * k, kd = dblock_ld(k);
+    GSDFT_TRY(launch_gemm(k, M, Ws * k, alpha, Dbar, kd, false, kd * Ws * k, Y, Wk, true, Ws * k,
+                          0.0, part, k, k * M, S, s));
     const int64_t rem = W - S * Ws;
     if (rem > 0)
-        GSDFT_BLAS(rocblas_dgemm_64(h, N_, N_, k, M, rem * k, &alpha, Dbar + k * (S * Ws * k), k,
-                                    Y + S * Ws * k, Wk, &one, part + (S - 1) * k * M, k));
+        GSDFT_TRY(gemm_cm('N', 'N', k, M, rem * k, alpha, Dbar + kd * (S * Ws * k), kd,
+                          Y + S * Ws * k, Wk, 1.0, part + (S - 1) * k * M, k, s));
     k_sum_slices<<<nblk(k * M, 256), 256, 0, s>>>(k * M, S, part, dC);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -693,8 +699,6 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         }
         return GSDFT_OK;
     }
-    rocblas_handle h;
-    GSDFT_TRY(blas_handle(s, &h));
     k_csr_partner<<<nblk(n + kColPad, 256), 256, 0, s>>>(n, row_perm, pj, w.row_col);
     k_gather_i32<<<nblk(n, 256), 256, 0, s>>>(n, row_perm, w.tc.ent_group, w.row_grp);
     k_pad_cols<<<nblk(M * padded_cols(k), 256), 256, 0, s>>>(M, k, padded_cols(k), C, w.Cp);
@@ -711,11 +715,10 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         GSDFT_HIP(hipGetLastError());
     }
     const int64_t G = (N % M == 0) ? N / M : 1;
-    const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
-    const double one = 1.0, zero = 0.0, mtwo = -2.0;
-    const auto N_ = rocblas_operation_none, T_ = rocblas_operation_transpose;
-
+    const int64_t K2 = sym ? k * (k + 1) / 2 : k * k, ldd = packed_ld(K2);
     const bool store = exch_store(M, k, N, sym, grads, recompute != 0);
+    k_fill0<<<nblk(ldd * N, 256), 256, 0, s>>>(ldd * N, w.Dt);
+    GSDFT_HIP(hipGetLastError());
     for (int64_t q0 = 0; q0 < N; q0 += Pc) {
         const int64_t W = std::min(Pc, N - q0);
         double* Yc = store ? w.Ys + M * q0 * k : w.Y;
@@ -725,19 +728,18 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
             GSDFT_TRY(launch_spmm(M, W, k, Pc, col_ptr, w.col_grp, w.col_row, w.Bt, w.Cp,
                                   w.Yps + M * q0 * k, s));
         profile_begin(kProfExchGemm, s);
-        GSDFT_BLAS(rocblas_dgemm_64(h, N_, T_, k, W * k, M, &one, C, k, Yc, W * k, &zero,
-                                    w.Dfull, k));
+        GSDFT_TRY(gemm_cm('N', 'T', k, W * k, M, 1.0, w.Cp, padded_cols(k), Yc, W * k, 0.0,
+                          w.Dfull, dblock_ld(k), s));
         profile_end(kProfExchGemm, s);
-        k_exch_pack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, K2, sym ? 1 : 0, q0, N, G, w.Dfull,
+        k_exch_pack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, ldd, sym ? 1 : 0, q0, N, G, w.Dfull,
                                                          w.Dt);
         GSDFT_HIP(hipGetLastError());
     }
     // Wt = Dt L^-T: chol is the row-major lower factor, i.e. the column-major upper L^T.
     profile_begin(kProfExchTrsm, s);
-    GSDFT_BLAS(rocblas_dtrsm_64(h, rocblas_side_right, rocblas_fill_upper, N_,
-                                rocblas_diagonal_non_unit, K2, N, &one, chol, N, w.Dt, K2));
+    GSDFT_TRY(trsm_right_upper(s, false, N, chol, N, w.Dt, K2, ldd));
     profile_end(kProfExchTrsm, s);
-    k_sumsq_part<<<kRedBlocks, 256, 0, s>>>(K2 * N, w.Dt, w.red);
+    k_sumsq_part<<<kRedBlocks, 256, 0, s>>>(ldd * N, w.Dt, w.red);
     GSDFT_HIP(hipGetLastError());
     k_sum_scaled<<<1, 1024, 0, s>>>(kRedBlocks, w.red, -1.0, energy);
     GSDFT_HIP(hipGetLastError());
@@ -745,14 +747,16 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
 
     // Dbar_t = -2 Wt L^-1
     profile_begin(kProfExchTrsm, s);
-    GSDFT_BLAS(rocblas_dtrsm_64(h, rocblas_side_right, rocblas_fill_upper, T_,
-                                rocblas_diagonal_non_unit, K2, N, &mtwo, chol, N, w.Dt, K2));
+    // (the scaling by -2 is exact, so it may come before the solve)
+    k_scale<<<nblk(ldd * N, 256), 256, 0, s>>>(ldd * N, -2.0, w.Dt);
+    GSDFT_HIP(hipGetLastError());
+    GSDFT_TRY(trsm_right_upper(s, true, N, chol, N, w.Dt, K2, ldd));
     profile_end(kProfExchTrsm, s);
     k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
     GSDFT_HIP(hipGetLastError());
     for (int64_t q0 = 0; q0 < N; q0 += Pc) {
         const int64_t W = std::min(Pc, N - q0);
-        k_exch_unpack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, K2, sym ? 1 : 0, q0, N, G, w.Dt,
+        k_exch_unpack<<<nblk(W * k * k, 256), 256, 0, s>>>(W, k, ldd, sym ? 1 : 0, q0, N, G, w.Dt,
                                                            w.Dfull, w.Ebar);
         GSDFT_HIP(hipGetLastError());
         const double* Yc = w.Y;
@@ -770,11 +774,11 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         }
         profile_begin(kProfExchGemm, s);
         // dC += Y_P Dbar_P^T (+ Y'_P Dbar_P; the same term again on a symmetric list)
-        GSDFT_TRY(dc_gemm(h, k, M, W, sym ? 2.0 : 1.0, w.Dfull, Yc, w.part, dC, s));
-        if (!sym) GSDFT_TRY(dc_gemm(h, k, M, W, 1.0, w.Ebar, Ypc, w.part, dC, s));
+        GSDFT_TRY(dc_gemm(k, M, W, sym ? 2.0 : 1.0, w.Dfull, Yc, w.part, dC, s));
+        if (!sym) GSDFT_TRY(dc_gemm(k, M, W, 1.0, w.Ebar, Ypc, w.part, dC, s));
         // Ybar (Wk x M column-major, i.e. [i][l][o']) = Dbar^T C^T-view, into Y's buffer
-        GSDFT_BLAS(rocblas_dgemm_64(h, T_, N_, W * k, M, k, &one, w.Dfull, k, C, k, &zero, w.Y,
-                                    W * k));
+        GSDFT_TRY(gemm_cm('T', 'N', W * k, M, k, 1.0, w.Dfull, dblock_ld(k), w.Cp,
+                          padded_cols(k), 0.0, w.Y, W * k, s));
         profile_end(kProfExchGemm, s);
         // Tbar (ld Pc) into the block's buffer: on a symmetric list Dbar_P is symmetric, so the
         // entries of a group, (i, k) and (k, i) and their repeats, share (C Dbar_P C^T)[i][k]:

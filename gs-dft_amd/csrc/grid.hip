@@ -3,7 +3,7 @@
 //
 // Per chunk of Gc grid points (rows):
 //   g_rm = N_m exp(-dr.A_m dr), dg_rm = -2 A_m dr g_rm      (k_grid_basis, VALU, one lane per (r,m))
-//   psi = g C, dpsi_d = dg_d C                              (FP64 GEMMs, rocBLAS / Tensile MFMA)
+//   psi = g C, dpsi_d = dg_d C                              (FP64 MFMA products, gemm.hip)
 //   rho_r = sum_o occ_o psi_ro^2
 //   grad rho_r = 2 sum_m phi_rm dg_rm, phi = (psi occ) C^T   (grid.py:104-107; the tau variant
 //                uses 2 sum_o occ_o psi_ro dpsi_ro as grid.py:132 does)
@@ -16,10 +16,9 @@
 //   reverse. No atomics; the result does not depend on the chunk size beyond round-off of the
 //   row order inside the GEMMs.
 //
-// Storage: row-major (Gc, M) basis blocks (the column-major (M, Gc) view rocBLAS reads), row-major
-// (Gc, k) orbital blocks; g and the three dg blocks are consecutive, as are psi and the dpsi.
-#include <rocblas/rocblas.h>
-
+// Storage: row-major (Gc, M) basis blocks (the column-major (M, Gc) view the products read),
+// row-major (Gc, k) orbital blocks; g and the three dg blocks are consecutive, as are psi and the
+// dpsi.
 #include "common.h"
 #include "internal.h"
 
@@ -28,13 +27,6 @@ namespace gsdft {
 namespace {
 
 inline unsigned nblk(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
-
-#define GSDFT_BLAS(call)                                                                   \
-    do {                                                                                   \
-        rocblas_status st_ = (call);                                                       \
-        if (st_ != rocblas_status_success)                                                 \
-            return fail(GSDFT_ERR_LIB, "%s failed (rocBLAS status %d)", #call, (int)st_);  \
-    } while (0)
 
 // One lane per (row r, splat m): grid (ceil(M/256), Gc).
 __global__ __launch_bounds__(256) void k_grid_basis(int64_t M, int64_t Gc,
@@ -268,13 +260,10 @@ int check_grid_args(int64_t M, int64_t k, int64_t G, int64_t chunk, int mode) {
 }
 
 // psi (and dpsi) for rows [0, Gc) of the chunk: [psi; dpsi] (nb Gc x k) = [g; dg] (nb Gc x M) C.
-int grid_orbitals(rocblas_handle h, int64_t M, int64_t k, int64_t Gc, int nb, const double* C,
-                  const double* gb, double* pb) {
-    const double one = 1.0, zero = 0.0;
+int grid_orbitals(int64_t M, int64_t k, int64_t Gc, int nb, const double* C, const double* gb,
+                  double* pb, hipStream_t s) {
     // column-major: pb (k x nb Gc) = C^T-view (k x M) * gb (M x nb Gc)
-    GSDFT_BLAS(rocblas_dgemm_64(h, rocblas_operation_none, rocblas_operation_none, k, nb * Gc, M,
-                                &one, C, k, gb, M, &zero, pb, k));
-    return GSDFT_OK;
+    return gemm_cm('N', 'N', k, nb * Gc, M, 1.0, C, k, gb, M, 0.0, pb, k, s);
 }
 
 }  // namespace
@@ -310,17 +299,14 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
     GSDFT_TRY(layout_grid(ar, M, k, chunk, mode, false, &w));
     if (!w.pb || (mode == 1 && !w.phi))
         return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density: workspace too small");
-    rocblas_handle h;
-    GSDFT_TRY(blas_handle(s, &h));
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
-    const double one = 1.0, zero = 0.0;
     for (int64_t r0 = 0; r0 < G; r0 += chunk) {
         const int64_t Gc = G - r0 < chunk ? G - r0 : chunk;
         double* dg = mode >= 1 ? w.gb + Gc * M : nullptr;
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(h, M, k, Gc, mode == 2 ? 4 : 1, C, w.gb, w.pb));
+        GSDFT_TRY(grid_orbitals(M, k, Gc, mode == 2 ? 4 : 1, C, w.gb, w.pb, s));
         k_grid_rho<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, w.pb, occ, rho + r0);
         GSDFT_HIP(hipGetLastError());
         if (mode == 1) {
@@ -328,8 +314,7 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
             double* pocc = w.pb + Gc * k;
             k_grid_scale_occ<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, w.pb, occ, pocc);
             GSDFT_HIP(hipGetLastError());
-            GSDFT_BLAS(rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none,
-                                        M, Gc, k, &one, C, k, pocc, k, &zero, w.phi, M));
+            GSDFT_TRY(gemm_cm('T', 'N', M, Gc, k, 1.0, C, k, pocc, k, 0.0, w.phi, M, s));
             k_grid_grad_phi<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, M, w.phi, dg, grad + 3 * r0);
         } else if (mode == 2) {
             k_grid_grad_tau<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, w.pb, occ, grad + 3 * r0,
@@ -361,28 +346,23 @@ extern "C" int gsdft_grid_density_vjp(int64_t M, const double* quat, const doubl
     k_grid_fill<<<nblk(slabs * 10 * M, 256), 256, 0, s>>>(slabs * 10 * M, 0.0, w.partial);
     k_grid_fill<<<nblk(M * k, 256), 256, 0, s>>>(M * k, 0.0, dC);
     GSDFT_HIP(hipGetLastError());
-    rocblas_handle h;
-    GSDFT_TRY(blas_handle(s, &h));
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
-    const double one = 1.0, zero = 0.0;
     for (int64_t r0 = 0; r0 < G; r0 += chunk) {
         const int64_t Gc = G - r0 < chunk ? G - r0 : chunk;
         double* dg = mode >= 1 ? w.gb + Gc * M : nullptr;
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(h, M, k, Gc, nb, C, w.gb, w.pb));
+        GSDFT_TRY(grid_orbitals(M, k, Gc, nb, C, w.gb, w.pb, s));
         k_grid_pbar<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, mode, w.pb, occ,
                                                       v_rho ? v_rho + r0 : nullptr,
                                                       v_grad ? v_grad + 3 * r0 : nullptr,
                                                       v_tau ? v_tau + r0 : nullptr, w.pbar);
         GSDFT_HIP(hipGetLastError());
         // dC (column-major k x M) += pbar (k x nb Gc) [g; dg]^T (nb Gc x M)
-        GSDFT_BLAS(rocblas_dgemm_64(h, rocblas_operation_none, rocblas_operation_transpose, k, M,
-                                    nb * Gc, &one, w.pbar, k, w.gb, M, &one, dC, k));
+        GSDFT_TRY(gemm_cm('N', 'T', k, M, nb * Gc, 1.0, w.pbar, k, w.gb, M, 1.0, dC, k, s));
         // [gbar; dgbar] (column-major M x nb Gc) = C (M x k) pbar (k x nb Gc)
-        GSDFT_BLAS(rocblas_dgemm_64(h, rocblas_operation_transpose, rocblas_operation_none, M,
-                                    nb * Gc, k, &one, C, k, w.pbar, k, &zero, w.gbar, M));
+        GSDFT_TRY(gemm_cm('T', 'N', M, nb * Gc, k, 1.0, C, k, w.pbar, k, 0.0, w.gbar, M, s));
         const int64_t cslabs = (Gc + kRowsPerSlab - 1) / kRowsPerSlab;
         k_grid_basis_bwd<<<dim3(nblk(M, 256), (unsigned)cslabs), 256, 0, s>>>(
             M, Gc, kRowsPerSlab, points + 3 * r0, w.A6, centers, w.Nrm, w.gb, w.gbar, mode,

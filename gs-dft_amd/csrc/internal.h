@@ -73,6 +73,26 @@ int launch_gemm_tn_sub(int64_t Mr, int64_t Nc, int64_t K, const double* A, int64
                        const double* B, int64_t ldb, double* C, int64_t ldc, bool upper,
                        hipStream_t s);
 
+// gemm.hip: C = alpha op(A) op(B) + beta C over Mr x Nc (C column-major, leading dimension ldc;
+// beta = 0 does not read C), op(A)(m, k) at A[m lda + k] when a_kc (k-contiguous), else at
+// A[k lda + m]; op(B)(k, n) at B[n ldb + k] when b_kc, else at B[k ldb + n]; `batch` products
+// with the operands `stride_*` doubles apart. FP64 MFMA tiles of 128 x 128.
+int launch_gemm(int64_t Mr, int64_t Nc, int64_t K, double alpha, const double* A, int64_t lda,
+                bool a_kc, int64_t stride_a, const double* B, int64_t ldb, bool b_kc,
+                int64_t stride_b, double beta, double* C, int64_t ldc, int64_t stride_c,
+                int64_t batch, hipStream_t s);
+
+// The same as a column-major BLAS dgemm: C (m x n) = alpha op(A) op(B) + beta C, op = 'N' or 'T'.
+int gemm_cm(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+            const double* A, int64_t lda, const double* B, int64_t ldb, double beta, double* C,
+            int64_t ldc, hipStream_t s);
+
+// dfj.hip: X (m x n, column-major, leading dimension ldx) <- X U^-1 (X U = B) or, with trans,
+// X U^-T (X U^T = B), for the n x n upper U (column-major, leading dimension ldu), by blocked
+// substitution with FP64 MFMA products between the blocks.
+int trsm_right_upper(hipStream_t s, bool trans, int64_t n, const double* U, int64_t ldu,
+                     double* X, int64_t m, int64_t ldx);
+
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
 
@@ -99,9 +119,6 @@ int launch_pair_groups(int64_t M, int64_t n, const int32_t* pi, const int32_t* p
                        const double* q, const PairOrderWs& po, int32_t* head, char* scan_tmp,
                        size_t scan_bytes, int32_t* ent_group, int32_t* ent_pos,
                        int32_t* grp_first, int32_t* grp_rep, int64_t* n_groups, hipStream_t s);
-
-// dfj.hip: the library's rocBLAS handle for the current device, bound to stream s.
-int blas_handle(hipStream_t s, struct _rocblas_handle** out);
 
 // dfj.hip: the three-centre passes of the screened exchange. Charts, aux quantities and pair
 // records (q_a = w_a) in list order. The entries of the list are grouped by their unordered splat

@@ -259,6 +259,15 @@ int gsdft_exact_coulomb_density(int64_t M, const double* quat, const double* log
                                 double* dP, void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* C (m x n, column-major, leading dimension ldc) = alpha op(A) op(B) + beta C in FP64 on the MFMA
+ * units, op(X) = X for a zero trans flag and X^T otherwise, A and B column-major as in BLAS dgemm;
+ * beta = 0 does not read C. No counterpart in the reference: the library's own dense product,
+ * which the grid density and the exchange run on, exported so that it can be checked and timed
+ * on its own. */
+int gsdft_dgemm(int transa, int transb, int64_t m, int64_t n, int64_t k, double alpha,
+                const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                double* C, int64_t ldc, void* stream);
+
 /* Density on a grid for the exchange-correlation term, streamed over chunks of `chunk` points
  * (<= 65535): rho (G) and, for mode >= 1, grad (G,3), and for mode 2 tau (G), of the orbitals
  * C (M,k) with occupations occ at points (G,3). mode 0 replaces chunked_density, 1
