@@ -214,8 +214,7 @@ __device__ __forceinline__ void gemm_tile_dma(int64_t m0, int64_t n0, int64_t K,
                                               const double* __restrict__ A, int64_t lda,
                                               const double* __restrict__ B, int64_t ldb,
                                               double* __restrict__ C, int64_t ldc,
-                                              double* __restrict__ lds, double alpha,
-                                              double beta) {
+                                              double* __restrict__ lds) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const int l16 = lane & 15, l4 = lane >> 4;
@@ -293,8 +292,7 @@ __device__ __forceinline__ void gemm_tile_dma(int64_t m0, int64_t n0, int64_t K,
             const int64_t n = n0 + wn * 64 + 16 * i + l4 + 4 * r;
             double* col = C + n * ldc;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                epilogue(col + m0 + wm * 64 + 16 * j + l16, acc[i][j][r], alpha, beta);
+            for (int j = 0; j < 4; ++j) col[m0 + wm * 64 + 16 * j + l16] -= acc[i][j][r];
         }
 }
 
@@ -496,7 +494,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_tn_sub(int64_t Mr, int64_t
     C += blockIdx.y * bt.sc;
     if constexpr (kMode == kDma) {
         __shared__ __align__(16) double lds[2 * 2 * kTile * kStepK];
-        gemm_tile_dma(tm * kTile, tn * kTile, K, A, lda, B, ldb, C, ldc, lds, bt.alpha, bt.beta);
+        // the factorisation's own path: C -= A^T B
+        gemm_tile_dma(tm * kTile, tn * kTile, K, A, lda, B, ldb, C, ldc, lds);
     } else if constexpr (kMode == kDmaGen) {
         __shared__ __align__(16) double lds[2 * 2 * kOpMax];
         gemm_tile_dma_gen<kAK, kBK>(tm * kTile, tn * kTile, Mr, Nc, K, A, lda, B, ldb, C, ldc,

@@ -28,7 +28,7 @@ extern "C" {
 #define GSDFT_ERR_OVERFLOW 2     /* significant pairs exceed twice the pad (pairs.py:157-161)   */
 #define GSDFT_ERR_NOT_PD 3       /* Cholesky met a non-positive pivot                           */
 #define GSDFT_ERR_HIP 4          /* HIP runtime error                                           */
-#define GSDFT_ERR_LIB 5          /* rocBLAS / hipCUB error                                      */
+#define GSDFT_ERR_LIB 5          /* hipCUB error                                                */
 #define GSDFT_ERR_WORKSPACE 6    /* workspace too small; the query names the size               */
 #define GSDFT_ERR_FALLBACK 7     /* spatial screening: the list overflows its pad (use the dense
                                     build) */
@@ -335,7 +335,7 @@ int gsdft_exchange(int64_t M, const double* quat, const double* log_scale, const
  * block's forces on the nuclei), 7 nuclear attraction per nucleus (the fixed-order force sums),
  * 8 exact pair-pair Coulomb (values), 9 exact pair-pair Coulomb (values and gradient moments),
  * 10 exchange three-centre block, 11 exchange three-centre reverse, 12 exchange triangular
- * solves (rocBLAS), 13 exchange GEMMs (rocBLAS), 14 exchange pair-sparse products (Y = T C and
+ * solves (blocked, FP64 MFMA), 13 exchange GEMMs (FP64 MFMA), 14 exchange pair-sparse products (Y = T C and
  * the sampled Tbar). gsdft_profile_read synchronises the recorded events and returns the summed
  * milliseconds and the launch count since the last reset. gsdft_profile_read_work returns the
  * work units the kernels executed while profiling was on (ids 0, 1, 6-11: quadrature nodes
