@@ -114,6 +114,46 @@ __device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __rest
     return __builtin_bit_cast(double, w) * p;
 }
 
+// The same with a node weight folded in: 24 wh e^-z for wh = 2^n w', where the caller passes
+// z' = z - ln w' (|ln w'| <= ln2/2, so z' rounds as finely as z) and S = 1.5 * 2^52 + 256 n. The
+// shift S puts k + 256 n in the low word of sh, so the high-word add scales the result by 2^n
+// exactly, while sh - S is still k itself for the reduction. With n >= kFoldMinExp the cap
+// kFoldCapZ keeps m + n >= -1022 (the result normal). c256 is -256/ln2 (kNegC256) held in a
+// vector register by the caller (vgpr_const), so that the fma forming sh reads one scalar operand
+// (S) rather than two, which would cost a register move per call.
+constexpr int kFoldMinExp = -60;
+constexpr double kFoldCapZ = 666.7;     // 708.3 - 60 ln 2, rounded down
+constexpr double kNegC256 = -0x1.71547652b82fep+8;
+__device__ __forceinline__ double vgpr_const(double c) {
+    asm volatile("" : "+v"(c));
+    return c;
+}
+__device__ __forceinline__ double exp_neg_tab_x24_w(double z, double S, double c256,
+                                                    const double* __restrict__ lead) {
+    z = __builtin_fmin(z, kFoldCapZ);
+    const double sh = __builtin_fma(z, c256, S);
+    const double kf = sh - S;
+    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
+    const double r = __builtin_fma(-kf, 0x1.62e42fefa39efp-9, -z);
+    double p = r + 4.0;
+    p = __builtin_fma(p, r, 12.0);
+    p = __builtin_fma(p, r, 24.0);
+    p = __builtin_fma(p, r, 24.0);
+    struct Words { uint32_t lo, hi; };
+    Words w = __builtin_bit_cast(Words, lead[k & 255]);
+    asm("v_lshl_add_u32 %0, %1, 12, %2" : "=v"(w.hi) : "v"(k), "v"(w.hi));
+    return __builtin_bit_cast(double, w) * p;
+}
+
+// Host/device split of a positive node weight for exp_neg_tab_x24_w: wh = 2^n w' with n the
+// nearest integer to log2 wh (at least kFoldMinExp); returns -ln w' and sets S.
+__host__ __device__ inline double fold_weight(double wh, double* S) {
+    int n = (int)rint(log2(wh));
+    n = n < kFoldMinExp ? kFoldMinExp : n;
+    *S = 0x1.8p52 + 256.0 * n;
+    return -log(ldexp(wh, -n));
+}
+
 // One quadrature node in scaled form: with P = Pn(s)/s > 0 (Pn the node's determinant
 // polynomial) and Q = Qn(s), so that the exponent is z = Q/P = s Qn/Pn without the product s Qn,
 // returns y0 ~ P^(-1/2), ip = 1/P, zh = z - 1/2 and arg = zh - eps/2, so that

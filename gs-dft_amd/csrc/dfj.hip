@@ -414,6 +414,19 @@ __device__ __forceinline__ void put_node_consts(double* o, int t, double s, doub
     o[rec_is(t)] = 1.0 / s;
 }
 
+// The forward's records (k_gamma_fwd_pairs) hold the weight split for exp_neg_tab_x24_w in the
+// same four slots: s_t, -ln w'_t, S_t, 1/s_t with wh_t = 2^n w'_t (fold_weight).
+__host__ __device__ constexpr int rec_lw(int t) { return 8 + 4 * t + 1; }
+__host__ __device__ constexpr int rec_S(int t) { return 8 + 4 * t + 2; }
+
+__device__ __forceinline__ void put_fwd_node_consts(double* o, int t, double s, double wp) {
+    double S;
+    o[rec_s(t)] = s;
+    o[rec_lw(t)] = fold_weight(wp / sqrt(s) * (kExpMinusHalf / 24.0), &S);
+    o[rec_S(t)] = S;
+    o[rec_is(t)] = 1.0 / s;
+}
+
 // body(std::integral_constant<int, t>) for t = 0, 1, ..., kN - 1 until it returns true: a fully
 // unrolled node loop with early exits (node tables stay in registers). Returns the number of
 // nodes evaluated (wave-uniform).
@@ -466,6 +479,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
     const int64_t a_begin = g * kFwdPairs;
     const int64_t a_end = min(n, a_begin + kFwdPairs);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const double c256 = vgpr_const(kNegC256);
     uint64_t lane_nodes = 0;                 // profiling: node evaluations over live lanes
     for (int64_t a0 = a_begin + 64 * wave; a0 < a_end; a0 += 256) {      // wave-uniform
         const int64_t a = a0 + lane;
@@ -483,17 +497,19 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
         // stalling the record's start.
         const double* __restrict__ xf = aux + kAuxRec * q0;
         double c_x = xf[0], c_y = xf[1], c_z = xf[2];
-        double c_s = xf[rec_s(0)], c_wh = xf[rec_wh(0)], c_is = xf[rec_is(0)];
+        double c_s = xf[rec_s(0)], c_lw = xf[rec_lw(0)], c_S = xf[rec_S(0)],
+               c_is = xf[rec_is(0)];
         uint64_t c_new = 1;                          // the flag's bits, tested when used
         for (int j = 0; j < nrec; ++j) {
             const double* __restrict__ x = aux + kAuxRec * (q0 + j);
             const double Rx = c_x, Ry = c_y, Rz = c_z;
-            double n_s = c_s, n_wh = c_wh, n_is = c_is;
+            double n_s = c_s, n_lw = c_lw, n_S = c_S, n_is = c_is;
             const bool fresh = c_new != 0;
             if (j + 1 < nrec) {                      // wave-uniform
                 const double* __restrict__ xn = x + kAuxRec;
                 c_x = xn[0]; c_y = xn[1]; c_z = xn[2];
-                c_s = xn[rec_s(0)]; c_wh = xn[rec_wh(0)]; c_is = xn[rec_is(0)];
+                c_s = xn[rec_s(0)]; c_lw = xn[rec_lw(0)]; c_S = xn[rec_S(0)];
+                c_is = xn[rec_is(0)];
                 c_new = __builtin_bit_cast(uint64_t, xn[5]);
             }
             if (fresh) {                             // wave-uniform
@@ -511,21 +527,31 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
             double F = 0.0;
             // each node's constants are read one node ahead, so their scalar load overlaps the
             // previous node's arithmetic
+            // The node weight rides in the exponent (exp_neg_tab_x24_w): with y0 ~ Pr^(-1/2),
+            // h = y0^2 and 1 + eps = 2 - Pr h, the term is y0 e^-(a (1 + eps) - ln w') 2^n for
+            // a = Qn h - 1/2 (node_arg_h's argument, formed as one fma with ln w'), so no
+            // multiply by the weight is left. The screen tests a, which differs from
+            // a (1 + eps) by less than 4e-6 where it matters.
             auto node = [&](auto tc) {
                 constexpr int t = decltype(tc)::value;
-                const double st = n_s, wh = n_wh, is = n_is;
+                const double st = n_s, lw = n_lw, S = n_S, is = n_is;
                 if constexpr (t + 1 < kNodes) {
                     n_s = x[rec_s(t + 1)];
-                    n_wh = x[rec_wh(t + 1)];
+                    n_lw = x[rec_lw(t + 1)];
+                    n_S = x[rec_S(t + 1)];
                     n_is = x[rec_is(t + 1)];
                 }
                 const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
                 const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
-                const NodeArgH v = node_arg_h(Pr, Qn);
-                F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+                const double y0 = __builtin_amdgcn_rsq(Pr);
+                const double h = y0 * y0;
+                const double e1 = __builtin_fma(-Pr, h, 2.0);
+                const double a = __builtin_fma(Qn, h, -0.5);
+                F = __builtin_fma(y0, exp_neg_tab_x24_w(__builtin_fma(a, e1, lw), S, c256, tab), F);
                 // keep the next node's loads ahead of the early exit (not sunk past it)
-                if constexpr (t + 1 < kNodes) asm volatile("" ::"s"(n_s), "s"(n_wh), "s"(n_is));
-                return screen_after(t) && wave_all_beyond_h(v.arg);
+                if constexpr (t + 1 < kNodes)
+                    asm volatile("" ::"s"(n_s), "s"(n_lw), "s"(n_S), "s"(n_is));
+                return screen_after(t) && wave_all_beyond_h(a);
             };
             lane_nodes += lanes * node_loop<0>(node);
             acc[j][threadIdx.x] = __builtin_fma(F, cf, acc[j][threadIdx.x]);
@@ -611,13 +637,16 @@ __device__ __forceinline__ double wave_sum3(const double v[3], int* comp) {
 
 
 // Aux record: R (3) | u = dgamma_P * scale * KN_P | b | first | pad (2) | per node t: s_t, wh_t,
-// s_t^2, 1/s_t (put_node_consts; with `fold` the weights carry u). Records are stored
+// s_t^2, 1/s_t (put_node_consts; with fold == kAuxFoldU the weights carry u; with
+// fold == kAuxForward the forward's split weights instead, put_fwd_node_consts). Records are stored
 // centre-grouped: with G = N / M exponent scales (the product aux is scale-major, P = s M + m,
 // every scale of splat m at one centre), the record of P sits at slot m G + s, so the scales
 // sharing a centre are consecutive; otherwise (N not a multiple of M) in aux order. "first" is 1
 // where the centre differs bitwise from the previous slot's (or at slot 0): the reverse kernel
 // recomputes the centre-dependent terms only there, whatever the aux holds.
 // (aux_slot / aux_of_slot: common.h)
+
+enum AuxFold { kAuxPlain = 0, kAuxFoldU = 1, kAuxForward = 2 };
 
 __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ beta,
                                const double* __restrict__ kn, const double* __restrict__ R,
@@ -645,8 +674,10 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
     }
     o[4] = b; o[5] = first ? 1.0 : 0.0; o[6] = 0.0; o[7] = 0.0;
     for (int t = 0; t < kNodes; ++t) {
-        if (t < tb.n) {
-            put_node_consts(o, t, s[t], wp[t], fold ? u : 1.0);
+        if (t < tb.n && fold == kAuxForward) {
+            put_fwd_node_consts(o, t, s[t], wp[t]);
+        } else if (t < tb.n) {
+            put_node_consts(o, t, s[t], wp[t], fold == kAuxFoldU ? u : 1.0);
         } else {            // slots past the table: never read by a kernel of tb.n nodes
             o[rec_s(t)] = 0.0;
             o[rec_wh(t)] = 0.0;
@@ -1979,7 +2010,7 @@ int exch_tc_prologue(int64_t M, const double* quat, const double* log_scale,
     GSDFT_HIP(hipGetLastError());
     const int64_t G = (N % M == 0) ? N / M : 1;
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, 0, w.table, w.aux);
+                                                      nullptr, kAuxPlain, w.table, w.aux);
     GSDFT_HIP(hipGetLastError());
     // one record per group (its first entry's), then the groups' slot order: the group count
     // stays on the device, the first n_groups_dev slots are the groups and the rest idle
@@ -2635,7 +2666,8 @@ int gamma_run(int64_t M, const double* quat, const double* log_scale, const doub
                              weight, w, s));
     const int64_t G = (N % M == 0) ? N / M : 1;          // scales per centre of a product aux
     k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers, nullptr,
-                                                      nullptr, 0, coulomb_table(), w.aux);
+                                                      nullptr, kAuxForward, coulomb_table(),
+                                                      w.aux);
     GSDFT_HIP(hipGetLastError());
     GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
     k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
@@ -2739,7 +2771,8 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     if (n > 0) {
         const int64_t G = (N % M == 0) ? N / M : 1;      // scales per centre of a product aux
         k_aux_bwd_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, G, w.beta, w.kn, aux_centers,
-                                                          dgamma, dgamma_scale, 1, coulomb_table(),
+                                                          dgamma, dgamma_scale, kAuxFoldU,
+                                                          coulomb_table(),
                                                           w.aux);
         GSDFT_TRY(launch_pair_order(n, w.rec, kRec, w.pair_order, s));
         k_rec_gather<<<blocks_for(n * kRec, 256), 256, 0, s>>>(n, w.pair_order.perm, w.rec,
