@@ -171,27 +171,12 @@ __device__ __forceinline__ double boys0(double T) {
 
 // gs_dft/coulomb/ri.py:63-76 + shift_diag: F0 = boys0(rho R^2) for 1/r, or, for the long-range
 // kernel erf(omega r)/r (omega > 0), sqrt(z) boys0(z rho R^2) with z = omega^2 / (omega^2 + rho).
-// One thread per element; a block covers 4 rows x 64 columns so each wave writes 64 consecutive
-// doubles of one row. kLower forms only the lower triangle (q <= p) and writes zeros above it,
-// so a factorisation that follows clears only its diagonal tiles (k_zero_diag_tiles) instead of
-// the whole upper triangle.
-template <bool kLower>
-__global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restrict__ beta,
-                                                const double* __restrict__ kn,
-                                                const double* __restrict__ R, double lam,
-                                                double omega, double* __restrict__ V) {
-    const int64_t q = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int64_t p = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (p >= N || q >= N) return;
-    if (kLower && q > p) {
-        V[p * N + q] = 0.0;
-        return;
-    }
-    const double g1 = beta[p], g2 = beta[q];
+__device__ __forceinline__ double metric_entry(double g1, double k1, double x1, double y1,
+                                               double z1, double g2, double k2, double x2,
+                                               double y2, double z2, double omega) {
     const double gab = g1 * g2;
     const double gsum = g1 + g2;
-    const double dx = R[3 * p] - R[3 * q], dy = R[3 * p + 1] - R[3 * q + 1],
-                 dz = R[3 * p + 2] - R[3 * q + 2];
+    const double dx = x1 - x2, dy = y1 - y2, dz = z1 - z2;
     const double PQ2 = dx * dx + dy * dy + dz * dz;
     const double rho = gab / gsum;
     const double T = rho * PQ2;
@@ -203,9 +188,46 @@ __global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restr
         F0 = boys0(T);
     }
     const double coul = kTwoPi25 / (gab * sqrt(gsum)) * F0;
-    double v = (kn[p] * kn[q]) * coul;
-    if (p == q) v += lam;
-    V[p * N + q] = v;
+    return (k1 * k2) * coul;
+}
+
+// One workgroup per 64 x 64 tile: lane l of wave w holds column q = 64 bx + l (its aux function
+// read once into registers) and forms rows 64 by + w + 4 i, i < 16, whose aux data is
+// wave-uniform; each row's 64 values are one contiguous 512-byte store per wave. kLower forms
+// only the lower triangle (q <= p) and writes zeros above it -- tiles wholly above the diagonal
+// only store zeros -- so a factorisation that follows clears only its diagonal tiles
+// (k_zero_diag_tiles) instead of the whole upper triangle.
+constexpr int kMetricRows = 16;
+template <bool kLower>
+__global__ __launch_bounds__(256) void k_metric(int64_t N, const double* __restrict__ beta,
+                                                const double* __restrict__ kn,
+                                                const double* __restrict__ R, double lam,
+                                                double omega, double* __restrict__ V) {
+    const int64_t q = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+    const int64_t p0 = (int64_t)blockIdx.y * (4 * kMetricRows) + (threadIdx.x >> 6);
+    if (q >= N) return;
+    if (kLower && (int64_t)blockIdx.x * 64 > (int64_t)blockIdx.y * (4 * kMetricRows) +
+                                                 4 * kMetricRows - 1) {     // workgroup-uniform
+#pragma unroll 4
+        for (int i = 0; i < kMetricRows; ++i) {
+            const int64_t p = p0 + 4 * i;
+            if (p < N) V[p * N + q] = 0.0;
+        }
+        return;
+    }
+    const double g2 = beta[q], k2 = kn[q], x2 = R[3 * q], y2 = R[3 * q + 1], z2 = R[3 * q + 2];
+    for (int i = 0; i < kMetricRows; ++i) {
+        const int64_t p = p0 + 4 * i;                                      // wave-uniform
+        if (p >= N) break;
+        if (kLower && q > p) {
+            V[p * N + q] = 0.0;
+            continue;
+        }
+        double v = metric_entry(beta[p], kn[p], R[3 * p], R[3 * p + 1], R[3 * p + 2], g2, k2, x2,
+                                y2, z2, omega);
+        if (p == q) v += lam;
+        V[p * N + q] = v;
+    }
 }
 
 __global__ void k_fill(int64_t n, double v, double* __restrict__ out) {
@@ -2195,7 +2217,7 @@ extern "C" int gsdft_aux_metric(int64_t N, const double* log_alpha, const double
     double* bk = ar.take<double>(2 * N + 2);
     if (!bk) return fail(GSDFT_ERR_WORKSPACE, "gsdft_aux_metric: workspace too small");
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
-    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 4 * kMetricRows - 1) / (4 * kMetricRows)));
     profile_begin(kProfMetric, s);
     k_metric<false><<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, V);
     profile_end(kProfMetric, s);
@@ -2587,7 +2609,7 @@ extern "C" int gsdft_aux_cholesky(int64_t N, const double* log_alpha, const doub
     int64_t* info = ar.take<int64_t>(2);
     if (!info) return fail(GSDFT_ERR_WORKSPACE, "gsdft_aux_cholesky: workspace too small");
     k_aux_prep<<<blocks_for(N, 256), 256, 0, s>>>(N, log_alpha, bk, bk + N);
-    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4));
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)((N + 4 * kMetricRows - 1) / (4 * kMetricRows)));
     profile_begin(kProfMetric, s);
     k_metric<true><<<grid, 256, 0, s>>>(N, bk, bk + N, aux_centers, lam, omega, L);
     profile_end(kProfMetric, s);
