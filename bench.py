@@ -59,6 +59,11 @@ def counter_record(workload: str, kernel: str):
     return json.loads(f.read_text()).get(workload, {}).get(kernel)
 
 
+def _with_command(out: dict) -> dict:
+    """The JSON line with the command line that produced it."""
+    return {**out, "command": "python bench.py " + " ".join(sys.argv[1:])}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -331,7 +336,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "E_J": E.item(),
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0
 
 
@@ -459,7 +464,7 @@ def run_nuclear(args) -> int:
         "cpu_baseline": cpu,
         "E_ext": E.item(),
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0
 
 
@@ -604,7 +609,7 @@ def run_exact(args) -> int:
         "cpu_baseline": cpu,
         "E_J": E.item(),
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0
 
 
@@ -799,7 +804,7 @@ def run_exchange(args) -> int:
         "cpu_baseline": cpu,
         "E_K": E.item(),
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0
 
 
@@ -901,7 +906,7 @@ def run_grid(args) -> int:
         "kernels": {"forward_only_ms": wall_f * 1e3},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0
 
 
@@ -962,7 +967,7 @@ def run_screen(args) -> int:
         "dense": res["dense"], "spatial": res["spatial"], "identical_lists": bool(same),
         "speedup": res["dense"]["gpu_ms"] / max(res["spatial"]["gpu_ms"], 1e-9),
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_with_command(out)), flush=True)
     return 0 if same else 1
 
 

@@ -48,6 +48,9 @@ struct TileSet {
 // its triangle. Workgroups dispatched together then cover a few rows of one band and share both
 // operand panels (in L2 and the MALL) instead of walking a whole column of A panels.
 constexpr int64_t kBand = 16;
+// gemm_cm_split: products with fewer than kSplitTiles output tiles split K into up to
+// kSplitMaxSlices slices of at least kSplitMinK, for about 2 kSplitTiles workgroups.
+constexpr int64_t kSplitTiles = 256, kSplitMaxSlices = 32, kSplitMinK = 256;
 
 __host__ __device__ inline void upper_tile_of(int64_t b, int64_t T, int64_t* tm, int64_t* tn) {
     // full bands before band c hold sum_{c' < c} (kBand^2 c' + kBand (kBand + 1) / 2) tiles
@@ -628,6 +631,51 @@ int gemm_cm(char transa, char transb, int64_t m, int64_t n, int64_t k, double al
             int64_t ldc, hipStream_t s) {
     return launch_gemm(m, n, k, alpha, A, lda, transa == 'T', 0, B, ldb, transb == 'N', 0, beta,
                        C, ldc, 0, 1, s);
+}
+
+namespace {
+
+// C(i, j) = beta C(i, j) + sum over the S slices, in slice order, of part[q m n + j m + i]
+// (beta = 0 does not read C).
+__global__ void k_add_slices(int64_t m, int64_t n, int64_t S, const double* __restrict__ part,
+                             double beta, double* __restrict__ C, int64_t ldc) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= m * n) return;
+    double v = 0.0;
+    for (int64_t q = 0; q < S; ++q) v += part[q * m * n + e];
+    double* c = C + (e / m) * ldc + e % m;
+    *c = beta == 0.0 ? v : __builtin_fma(beta, *c, v);
+}
+
+}  // namespace
+
+int64_t gemm_split_slices(int64_t m, int64_t n, int64_t k) {
+    const int64_t tiles = ((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);
+    if (tiles >= kSplitTiles) return 1;
+    int64_t S = (2 * kSplitTiles + tiles - 1) / tiles;
+    S = S < kSplitMaxSlices ? S : kSplitMaxSlices;
+    S = S < k / kSplitMinK ? S : k / kSplitMinK;
+    return S < 1 ? 1 : S;
+}
+
+int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+                  const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                  double* C, int64_t ldc, double* part, int64_t part_doubles, hipStream_t s) {
+    int64_t S = part && m > 0 && n > 0 ? gemm_split_slices(m, n, k) : 1;
+    if (S > 1 && S * m * n > part_doubles) S = part_doubles / (m * n);
+    if (S <= 1 || m <= 0 || n <= 0)
+        return gemm_cm(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    const bool a_kc = transa == 'T', b_kc = transb == 'N';
+    const int64_t Ks = (k / S) / kStepK * kStepK;            // even slice offsets keep the DMA path
+    const int64_t sa = a_kc ? Ks : Ks * lda, sb = b_kc ? Ks : Ks * ldb;
+    GSDFT_TRY(launch_gemm(m, n, Ks, alpha, A, lda, a_kc, sa, B, ldb, b_kc, sb, 0.0, part, m, m * n,
+                          S, s));
+    if (k > S * Ks)                                          // the remainder, into the last slice
+        GSDFT_TRY(gemm_cm(transa, transb, m, n, k - S * Ks, alpha, A + S * sa, lda, B + S * sb,
+                          ldb, 1.0, part + (S - 1) * m * n, m, s));
+    k_add_slices<<<(unsigned)((m * n + 255) / 256), 256, 0, s>>>(m, n, S, part, beta, C, ldc);
+    GSDFT_HIP(hipGetLastError());
+    return GSDFT_OK;
 }
 
 }  // namespace gsdft

@@ -235,6 +235,8 @@ constexpr int64_t kRowsPerSlab = 64;
 
 struct GridWs {
     double *A6, *Nrm, *gb, *pb, *phi, *gbar, *pbar, *partial;
+    double* part;             // K slices of the products with few output tiles (gemm_cm_split)
+    int64_t part_doubles;
 };
 
 int layout_grid(Arena& ar, int64_t M, int64_t k, int64_t chunk, int mode, bool reverse,
@@ -249,6 +251,13 @@ int layout_grid(Arena& ar, int64_t M, int64_t k, int64_t chunk, int mode, bool r
     w->pbar = reverse ? ar.take<double>(nb * chunk * k + 1) : nullptr;
     const int64_t slabs = (chunk + kRowsPerSlab - 1) / kRowsPerSlab;
     w->partial = reverse ? ar.take<double>(slabs * 10 * M + 1) : nullptr;
+    // room for the slices of the orbital product (k x nb chunk over K = M) and, in the reverse,
+    // of dC (k x M over K = nb chunk) at the chunk's full size; smaller chunks split into at most
+    // as many blocks of their own size as fit
+    const int64_t orb = gemm_split_slices(k, nb * chunk, M) * k * nb * chunk;
+    const int64_t dc = reverse ? gemm_split_slices(k, M, nb * chunk) * k * M : 0;
+    w->part_doubles = std::max<int64_t>(orb > k * nb * chunk ? orb : 0, dc > k * M ? dc : 0);
+    w->part = w->part_doubles > 0 ? ar.take<double>(w->part_doubles) : nullptr;
     return GSDFT_OK;
 }
 
@@ -261,9 +270,10 @@ int check_grid_args(int64_t M, int64_t k, int64_t G, int64_t chunk, int mode) {
 
 // psi (and dpsi) for rows [0, Gc) of the chunk: [psi; dpsi] (nb Gc x k) = [g; dg] (nb Gc x M) C.
 int grid_orbitals(int64_t M, int64_t k, int64_t Gc, int nb, const double* C, const double* gb,
-                  double* pb, hipStream_t s) {
+                  double* pb, const GridWs& w, hipStream_t s) {
     // column-major: pb (k x nb Gc) = C^T-view (k x M) * gb (M x nb Gc)
-    return gemm_cm('N', 'N', k, nb * Gc, M, 1.0, C, k, gb, M, 0.0, pb, k, s);
+    return gemm_cm_split('N', 'N', k, nb * Gc, M, 1.0, C, k, gb, M, 0.0, pb, k, w.part,
+                         w.part_doubles, s);
 }
 
 }  // namespace
@@ -306,7 +316,7 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(M, k, Gc, mode == 2 ? 4 : 1, C, w.gb, w.pb, s));
+        GSDFT_TRY(grid_orbitals(M, k, Gc, mode == 2 ? 4 : 1, C, w.gb, w.pb, w, s));
         k_grid_rho<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, w.pb, occ, rho + r0);
         GSDFT_HIP(hipGetLastError());
         if (mode == 1) {
@@ -353,14 +363,15 @@ extern "C" int gsdft_grid_density_vjp(int64_t M, const double* quat, const doubl
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(M, k, Gc, nb, C, w.gb, w.pb, s));
+        GSDFT_TRY(grid_orbitals(M, k, Gc, nb, C, w.gb, w.pb, w, s));
         k_grid_pbar<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, mode, w.pb, occ,
                                                       v_rho ? v_rho + r0 : nullptr,
                                                       v_grad ? v_grad + 3 * r0 : nullptr,
                                                       v_tau ? v_tau + r0 : nullptr, w.pbar);
         GSDFT_HIP(hipGetLastError());
         // dC (column-major k x M) += pbar (k x nb Gc) [g; dg]^T (nb Gc x M)
-        GSDFT_TRY(gemm_cm('N', 'T', k, M, nb * Gc, 1.0, w.pbar, k, w.gb, M, 1.0, dC, k, s));
+        GSDFT_TRY(gemm_cm_split('N', 'T', k, M, nb * Gc, 1.0, w.pbar, k, w.gb, M, 1.0, dC, k,
+                                w.part, w.part_doubles, s));
         // [gbar; dgbar] (column-major M x nb Gc) = C (M x k) pbar (k x nb Gc)
         GSDFT_TRY(gemm_cm('T', 'N', M, nb * Gc, k, 1.0, C, k, w.pbar, k, 0.0, w.gbar, M, s));
         const int64_t cslabs = (Gc + kRowsPerSlab - 1) / kRowsPerSlab;

@@ -87,6 +87,15 @@ int gemm_cm(char transa, char transb, int64_t m, int64_t n, int64_t k, double al
             const double* A, int64_t lda, const double* B, int64_t ldb, double beta, double* C,
             int64_t ldc, hipStream_t s);
 
+// gemm_cm with K split over S = gemm_split_slices(m, n, k) slices when the m x n output has too
+// few tiles to fill the GPU (fewer when part, part_doubles long, holds fewer m x n blocks): the
+// slices' products go to part (column-major m x n each) and are added in slice order,
+// C = alpha op(A) op(B) + beta C; with S = 1 it is gemm_cm.
+int64_t gemm_split_slices(int64_t m, int64_t n, int64_t k);
+int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+                  const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                  double* C, int64_t ldc, double* part, int64_t part_doubles, hipStream_t s);
+
 // dfj.hip: X (m x n, column-major, leading dimension ldx) <- X U^-1 (X U = B) or, with trans,
 // X U^-T (X U^T = B), for the n x n upper U (column-major, leading dimension ldu), by blocked
 // substitution with FP64 MFMA products between the blocks.
