@@ -307,7 +307,7 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GridWs w;
     GSDFT_TRY(layout_grid(ar, M, k, chunk, mode, false, &w));
-    if (!w.pb || (mode == 1 && !w.phi))
+    if (!w.pb || (mode == 1 && !w.phi) || (w.part_doubles > 0 && !w.part))
         return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density: workspace too small");
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
     for (int64_t r0 = 0; r0 < G; r0 += chunk) {
@@ -350,7 +350,8 @@ extern "C" int gsdft_grid_density_vjp(int64_t M, const double* quat, const doubl
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GridWs w;
     GSDFT_TRY(layout_grid(ar, M, k, chunk, mode, true, &w));
-    if (!w.partial) return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density_vjp: workspace too small");
+    if (!w.partial || (w.part_doubles > 0 && !w.part))
+        return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density_vjp: workspace too small");
     const int nb = mode >= 1 ? 4 : 1;
     const int64_t slabs = (chunk + kRowsPerSlab - 1) / kRowsPerSlab;
     k_grid_fill<<<nblk(slabs * 10 * M, 256), 256, 0, s>>>(slabs * 10 * M, 0.0, w.partial);
