@@ -1406,6 +1406,7 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
     const int64_t kb0 = A0 + (int64_t)blockIdx.y * kEriSymSlab;
     const int64_t kb1 = min(n, kb0 + kEriSymSlab);
     const int64_t amin = A0 + (int64_t)blockIdx.x * 256 + wv * 64;
+    const double c256 = vgpr_const(kNegC256);
     double acc = 0.0;
     uint32_t nodes = 0;
     auto ket = [&](int64_t b, auto maskc) {
@@ -1420,18 +1421,28 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
         double adjT[6], Td[3];
         const EriGeom G = eri_geom(T, d, adjT, Td);
         double F = 0.0;
+        // the node weight rides in the exponent as in the DF-J forward (exp_neg_tab_x24_w); the
+        // split of the compile-time weight folds to constants
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
             constexpr double st = quad_t(t) * quad_t(t), is = 1.0 / st;
             constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / 24.0);
+            double S;
+            double lw = fold_weight(wh, &S);
+            // materialised in scalar registers at each node (not held in vector registers
+            // across the ket loop)
+            asm volatile("" : "+s"(lw), "+s"(S));
             const double Er = __builtin_fma(st, __builtin_fma(st, G.J3, G.J2), G.J1) + is;
             const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
-            const NodeArgH v = node_arg_h(Er, num);
-            F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            const double y0 = __builtin_amdgcn_rsq(Er);
+            const double h = y0 * y0;
+            const double e1 = __builtin_fma(-Er, h, 2.0);
+            const double za = __builtin_fma(num, h, -0.5);
+            F = __builtin_fma(y0, exp_neg_tab_x24_w(__builtin_fma(za, e1, lw), S, c256, tab), F);
             if constexpr (kMask)
-                return screen_after(t) && wave_all_beyond_h(off ? kFarAway : v.arg);
+                return screen_after(t) && wave_all_beyond_h(off ? kFarAway : za);
             else
-                return screen_after(t) && wave_all_beyond_h(v.arg);
+                return screen_after(t) && wave_all_beyond_h(za);
         };
         nodes += node_loop<0>(node);
         F = (G.p0 == G.p0) ? F : G.p0;                 // a NaN centre propagates
