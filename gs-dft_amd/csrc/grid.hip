@@ -17,8 +17,10 @@
 //   row order inside the GEMMs.
 //
 // Storage: row-major (Gc, M) basis blocks (the column-major (M, Gc) view the products read),
-// row-major (Gc, k) orbital blocks; g and the three dg blocks are consecutive, as are psi and the
-// dpsi.
+// row-major (Gc, k) orbital blocks with rows ldk = k + (k & 1) doubles apart; g and the three dg
+// blocks are consecutive, as are psi and the dpsi. The even row length keeps every operand of the
+// products 16-byte aligned row by row, which their LDS-DMA path needs; for odd k the products read
+// C from a copy with rows of ldk (the last column zero).
 #include "common.h"
 #include "internal.h"
 
@@ -54,8 +56,17 @@ __global__ __launch_bounds__(256) void k_grid_basis(int64_t M, int64_t Gc,
     }
 }
 
+// Cp[m ldk + o] = C[m k + o] for o < k, 0 for k <= o < ldk.
+__global__ void k_grid_pad_cols(int64_t M, int64_t k, int64_t ldk, const double* __restrict__ C,
+                                double* __restrict__ Cp) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= M * ldk) return;
+    const int64_t m = i / ldk, o = i % ldk;
+    Cp[i] = o < k ? C[m * k + o] : 0.0;
+}
+
 // rho_r = sum_o occ_o psi_ro^2, one wave per row.
-__global__ __launch_bounds__(256) void k_grid_rho(int64_t Gc, int64_t k,
+__global__ __launch_bounds__(256) void k_grid_rho(int64_t Gc, int64_t k, int64_t ldk,
                                                   const double* __restrict__ psi,
                                                   const double* __restrict__ occ,
                                                   double* __restrict__ rho) {
@@ -64,19 +75,21 @@ __global__ __launch_bounds__(256) void k_grid_rho(int64_t Gc, int64_t k,
     if (r >= Gc) return;
     double s = 0.0;
     for (int64_t o = lane; o < k; o += 64) {
-        const double p = psi[r * k + o];
+        const double p = psi[r * ldk + o];
         s = __builtin_fma(occ[o] * p, p, s);
     }
     s = wave_sum(s);
     if (lane == 0) rho[r] = s;
 }
 
-// out = psi * occ (column scaling of the (Gc, k) block).
-__global__ void k_grid_scale_occ(int64_t Gc, int64_t k, const double* __restrict__ psi,
-                                 const double* __restrict__ occ, double* __restrict__ out) {
+// out = psi * occ (column scaling of the (Gc, k) block, rows ldk apart).
+__global__ void k_grid_scale_occ(int64_t Gc, int64_t k, int64_t ldk,
+                                 const double* __restrict__ psi, const double* __restrict__ occ,
+                                 double* __restrict__ out) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= Gc * k) return;
-    out[i] = psi[i] * occ[i % k];
+    const int64_t e = (i / k) * ldk + i % k;
+    out[e] = psi[e] * occ[i % k];
 }
 
 // grad_rd = 2 sum_m phi_rm dg_d,rm, one wave per row (grid.py:104-107).
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(256) void k_grid_grad_phi(int64_t Gc, int64_t M,
 }
 
 // grad_rd = 2 sum_o occ_o psi_ro dpsi_d,ro and tau_r = 1/2 sum_o occ_o |dpsi_ro|^2 (grid.py:128-134).
-__global__ __launch_bounds__(256) void k_grid_grad_tau(int64_t Gc, int64_t k,
+__global__ __launch_bounds__(256) void k_grid_grad_tau(int64_t Gc, int64_t k, int64_t ldk,
                                                        const double* __restrict__ psi,
                                                        const double* __restrict__ occ,
                                                        double* __restrict__ grad,
@@ -111,12 +124,12 @@ __global__ __launch_bounds__(256) void k_grid_grad_tau(int64_t Gc, int64_t k,
     const int64_t r = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
     if (r >= Gc) return;
-    const double* dpsi = psi + Gc * k;
+    const double* dpsi = psi + Gc * ldk;
     double s0 = 0.0, s1 = 0.0, s2 = 0.0, t = 0.0;
     for (int64_t o = lane; o < k; o += 64) {
-        const double op = occ[o] * psi[r * k + o];
-        const double d0 = dpsi[r * k + o], d1 = dpsi[(Gc + r) * k + o],
-                     d2 = dpsi[(2 * Gc + r) * k + o];
+        const double op = occ[o] * psi[r * ldk + o];
+        const double d0 = dpsi[r * ldk + o], d1 = dpsi[(Gc + r) * ldk + o],
+                     d2 = dpsi[(2 * Gc + r) * ldk + o];
         s0 = __builtin_fma(op, d0, s0);
         s1 = __builtin_fma(op, d1, s1);
         s2 = __builtin_fma(op, d2, s2);
@@ -132,29 +145,30 @@ __global__ __launch_bounds__(256) void k_grid_grad_tau(int64_t Gc, int64_t k,
 }
 
 // Pbar = 2 v_rho occ psi + 2 occ sum_d v_grad,d dpsi_d; Pbar_d = 2 occ v_grad,d psi
-// + v_tau occ dpsi_d. One lane per (r, o); psi and dpsi consecutive (Gc, k) blocks, likewise pbar.
-__global__ void k_grid_pbar(int64_t Gc, int64_t k, int mode, const double* __restrict__ psi,
-                            const double* __restrict__ occ, const double* __restrict__ v_rho,
-                            const double* __restrict__ v_grad, const double* __restrict__ v_tau,
-                            double* __restrict__ pbar) {
+// + v_tau occ dpsi_d. One lane per (r, o); psi and dpsi consecutive (Gc, k) blocks with rows ldk
+// apart, likewise pbar.
+__global__ void k_grid_pbar(int64_t Gc, int64_t k, int64_t ldk, int mode,
+                            const double* __restrict__ psi, const double* __restrict__ occ,
+                            const double* __restrict__ v_rho, const double* __restrict__ v_grad,
+                            const double* __restrict__ v_tau, double* __restrict__ pbar) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i >= Gc * k) return;
-    const int64_t r = i / k, o = i % k;
-    const double oc = occ[o], p = psi[i];
+    const int64_t r = i / k, o = i % k, e = r * ldk + o;
+    const double oc = occ[o], p = psi[e];
     double pb = 2.0 * (v_rho ? v_rho[r] : 0.0) * oc * p;
     if (mode >= 1) {
-        const double* dpsi = psi + Gc * k;
+        const double* dpsi = psi + Gc * ldk;
         const double vg[3] = {v_grad ? v_grad[3 * r] : 0.0, v_grad ? v_grad[3 * r + 1] : 0.0,
                               v_grad ? v_grad[3 * r + 2] : 0.0};
         const double vt = (mode == 2 && v_tau) ? v_tau[r] : 0.0;
 #pragma unroll
         for (int d = 0; d < 3; ++d) {
-            const double dp = dpsi[d * Gc * k + i];
+            const double dp = dpsi[d * Gc * ldk + e];
             pb = __builtin_fma(2.0 * oc * vg[d], dp, pb);
-            pbar[(1 + d) * Gc * k + i] = __builtin_fma(2.0 * oc * vg[d], p, vt * oc * dp);
+            pbar[(1 + d) * Gc * ldk + e] = __builtin_fma(2.0 * oc * vg[d], p, vt * oc * dp);
         }
     }
-    pbar[i] = pb;
+    pbar[e] = pb;
 }
 
 // Basis reverse for splat m over the rows [r0, r1) of the chunk, added to partial[slab][c][m]:
@@ -233,8 +247,12 @@ __global__ void k_grid_fill(int64_t n, double v, double* __restrict__ out) {
 
 constexpr int64_t kRowsPerSlab = 64;
 
+// Row length of the orbital blocks (even: every row of the products' operands 16-byte aligned).
+inline int64_t grid_ldk(int64_t k) { return k + (k & 1); }
+
 struct GridWs {
     double *A6, *Nrm, *gb, *pb, *phi, *gbar, *pbar, *partial;
+    double* Cp;               // C with rows of grid_ldk(k) (odd k only)
     double* part;             // K slices of the products with few output tiles (gemm_cm_split)
     int64_t part_doubles;
 };
@@ -242,13 +260,15 @@ struct GridWs {
 int layout_grid(Arena& ar, int64_t M, int64_t k, int64_t chunk, int mode, bool reverse,
                 GridWs* w) {
     const int nb = mode >= 1 ? 4 : 1;
+    const int64_t ldk = grid_ldk(k);
     w->A6 = ar.take<double>(6 * M + 1);
     w->Nrm = ar.take<double>(M + 1);
     w->gb = ar.take<double>(nb * chunk * M + 1);
-    w->pb = ar.take<double>(nb * chunk * k + 1);
+    w->pb = ar.take<double>(nb * chunk * ldk + 1);
     w->phi = (!reverse && mode == 1) ? ar.take<double>(chunk * M + 1) : nullptr;
     w->gbar = reverse ? ar.take<double>(nb * chunk * M + 1) : nullptr;
-    w->pbar = reverse ? ar.take<double>(nb * chunk * k + 1) : nullptr;
+    w->pbar = reverse ? ar.take<double>(nb * chunk * ldk + 1) : nullptr;
+    w->Cp = ldk != k ? ar.take<double>(M * ldk + 1) : nullptr;
     const int64_t slabs = (chunk + kRowsPerSlab - 1) / kRowsPerSlab;
     w->partial = reverse ? ar.take<double>(slabs * 10 * M + 1) : nullptr;
     // room for the slices of the orbital product (k x nb chunk over K = M) and, in the reverse,
@@ -261,6 +281,20 @@ int layout_grid(Arena& ar, int64_t M, int64_t k, int64_t chunk, int mode, bool r
     return GSDFT_OK;
 }
 
+// C as the products read it: rows of grid_ldk(k) (a padded copy for odd k).
+int grid_c(int64_t M, int64_t k, const double* C, const GridWs& w, hipStream_t s,
+           const double** Cuse) {
+    const int64_t ldk = grid_ldk(k);
+    if (ldk == k) {
+        *Cuse = C;
+        return GSDFT_OK;
+    }
+    k_grid_pad_cols<<<nblk(M * ldk, 256), 256, 0, s>>>(M, k, ldk, C, w.Cp);
+    GSDFT_HIP(hipGetLastError());
+    *Cuse = w.Cp;
+    return GSDFT_OK;
+}
+
 int check_grid_args(int64_t M, int64_t k, int64_t G, int64_t chunk, int mode) {
     if (M <= 0 || k <= 0 || G < 0 || chunk <= 0 || chunk > 65535 || mode < 0 || mode > 2)
         return fail(GSDFT_ERR_ARG, "grid density: need M, k > 0, G >= 0, 0 < chunk <= 65535 and "
@@ -268,11 +302,13 @@ int check_grid_args(int64_t M, int64_t k, int64_t G, int64_t chunk, int mode) {
     return GSDFT_OK;
 }
 
-// psi (and dpsi) for rows [0, Gc) of the chunk: [psi; dpsi] (nb Gc x k) = [g; dg] (nb Gc x M) C.
-int grid_orbitals(int64_t M, int64_t k, int64_t Gc, int nb, const double* C, const double* gb,
+// psi (and dpsi) for rows [0, Gc) of the chunk: [psi; dpsi] (nb Gc x k) = [g; dg] (nb Gc x M) C,
+// C (from grid_c) and the result with rows of grid_ldk(k).
+int grid_orbitals(int64_t M, int64_t k, int64_t Gc, int nb, const double* Cuse, const double* gb,
                   double* pb, const GridWs& w, hipStream_t s) {
-    // column-major: pb (k x nb Gc) = C^T-view (k x M) * gb (M x nb Gc)
-    return gemm_cm_split('N', 'N', k, nb * Gc, M, 1.0, C, k, gb, M, 0.0, pb, k, w.part,
+    const int64_t ldk = grid_ldk(k);
+    // column-major: pb (k x nb Gc, leading dimension ldk) = C^T-view (k x M) * gb (M x nb Gc)
+    return gemm_cm_split('N', 'N', k, nb * Gc, M, 1.0, Cuse, ldk, gb, M, 0.0, pb, ldk, w.part,
                          w.part_doubles, s);
 }
 
@@ -307,8 +343,12 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GridWs w;
     GSDFT_TRY(layout_grid(ar, M, k, chunk, mode, false, &w));
-    if (!w.pb || (mode == 1 && !w.phi) || (w.part_doubles > 0 && !w.part))
+    if (!w.pb || (mode == 1 && !w.phi) || (w.part_doubles > 0 && !w.part) ||
+        (grid_ldk(k) != k && !w.Cp))
         return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density: workspace too small");
+    const int64_t ldk = grid_ldk(k);
+    const double* Cuse = nullptr;
+    GSDFT_TRY(grid_c(M, k, C, w, s, &Cuse));
     GSDFT_TRY(launch_chart(M, quat, log_scale, w.A6, w.Nrm, s));
     for (int64_t r0 = 0; r0 < G; r0 += chunk) {
         const int64_t Gc = G - r0 < chunk ? G - r0 : chunk;
@@ -316,19 +356,20 @@ extern "C" int gsdft_grid_density(int64_t M, const double* quat, const double* l
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(M, k, Gc, mode == 2 ? 4 : 1, C, w.gb, w.pb, w, s));
-        k_grid_rho<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, w.pb, occ, rho + r0);
+        GSDFT_TRY(grid_orbitals(M, k, Gc, mode == 2 ? 4 : 1, Cuse, w.gb, w.pb, w, s));
+        k_grid_rho<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, ldk, w.pb, occ, rho + r0);
         GSDFT_HIP(hipGetLastError());
         if (mode == 1) {
-            // phi (column-major M x Gc) = C (M x k) (psi occ)^T; the scaled psi goes to pb + Gc k
-            double* pocc = w.pb + Gc * k;
-            k_grid_scale_occ<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, w.pb, occ, pocc);
+            // phi (column-major M x Gc) = C (M x k) (psi occ)^T; the scaled psi goes to
+            // pb + Gc ldk
+            double* pocc = w.pb + Gc * ldk;
+            k_grid_scale_occ<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, ldk, w.pb, occ, pocc);
             GSDFT_HIP(hipGetLastError());
-            GSDFT_TRY(gemm_cm('T', 'N', M, Gc, k, 1.0, C, k, pocc, k, 0.0, w.phi, M, s));
+            GSDFT_TRY(gemm_cm('T', 'N', M, Gc, k, 1.0, Cuse, ldk, pocc, ldk, 0.0, w.phi, M, s));
             k_grid_grad_phi<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, M, w.phi, dg, grad + 3 * r0);
         } else if (mode == 2) {
-            k_grid_grad_tau<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, w.pb, occ, grad + 3 * r0,
-                                                               tau + r0);
+            k_grid_grad_tau<<<nblk(Gc * 64, 256), 256, 0, s>>>(Gc, k, ldk, w.pb, occ,
+                                                               grad + 3 * r0, tau + r0);
         }
         GSDFT_HIP(hipGetLastError());
     }
@@ -350,8 +391,11 @@ extern "C" int gsdft_grid_density_vjp(int64_t M, const double* quat, const doubl
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GridWs w;
     GSDFT_TRY(layout_grid(ar, M, k, chunk, mode, true, &w));
-    if (!w.partial || (w.part_doubles > 0 && !w.part))
+    if (!w.partial || (w.part_doubles > 0 && !w.part) || (grid_ldk(k) != k && !w.Cp))
         return fail(GSDFT_ERR_WORKSPACE, "gsdft_grid_density_vjp: workspace too small");
+    const int64_t ldk = grid_ldk(k);
+    const double* Cuse = nullptr;
+    GSDFT_TRY(grid_c(M, k, C, w, s, &Cuse));
     const int nb = mode >= 1 ? 4 : 1;
     const int64_t slabs = (chunk + kRowsPerSlab - 1) / kRowsPerSlab;
     k_grid_fill<<<nblk(slabs * 10 * M, 256), 256, 0, s>>>(slabs * 10 * M, 0.0, w.partial);
@@ -364,17 +408,18 @@ extern "C" int gsdft_grid_density_vjp(int64_t M, const double* quat, const doubl
         k_grid_basis<<<dim3(nblk(M, 256), (unsigned)Gc), 256, 0, s>>>(M, Gc, points + 3 * r0, w.A6,
                                                                       centers, w.Nrm, w.gb, dg);
         GSDFT_HIP(hipGetLastError());
-        GSDFT_TRY(grid_orbitals(M, k, Gc, nb, C, w.gb, w.pb, w, s));
-        k_grid_pbar<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, mode, w.pb, occ,
+        GSDFT_TRY(grid_orbitals(M, k, Gc, nb, Cuse, w.gb, w.pb, w, s));
+        k_grid_pbar<<<nblk(Gc * k, 256), 256, 0, s>>>(Gc, k, ldk, mode, w.pb, occ,
                                                       v_rho ? v_rho + r0 : nullptr,
                                                       v_grad ? v_grad + 3 * r0 : nullptr,
                                                       v_tau ? v_tau + r0 : nullptr, w.pbar);
         GSDFT_HIP(hipGetLastError());
         // dC (column-major k x M) += pbar (k x nb Gc) [g; dg]^T (nb Gc x M)
-        GSDFT_TRY(gemm_cm_split('N', 'T', k, M, nb * Gc, 1.0, w.pbar, k, w.gb, M, 1.0, dC, k,
+        GSDFT_TRY(gemm_cm_split('N', 'T', k, M, nb * Gc, 1.0, w.pbar, ldk, w.gb, M, 1.0, dC, k,
                                 w.part, w.part_doubles, s));
         // [gbar; dgbar] (column-major M x nb Gc) = C (M x k) pbar (k x nb Gc)
-        GSDFT_TRY(gemm_cm('T', 'N', M, nb * Gc, k, 1.0, C, k, w.pbar, k, 0.0, w.gbar, M, s));
+        GSDFT_TRY(gemm_cm('T', 'N', M, nb * Gc, k, 1.0, Cuse, ldk, w.pbar, ldk, 0.0, w.gbar, M,
+                          s));
         const int64_t cslabs = (Gc + kRowsPerSlab - 1) / kRowsPerSlab;
         k_grid_basis_bwd<<<dim3(nblk(M, 256), (unsigned)cslabs), 256, 0, s>>>(
             M, Gc, kRowsPerSlab, points + 3 * r0, w.A6, centers, w.Nrm, w.gb, w.gbar, mode,
