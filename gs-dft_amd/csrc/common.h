@@ -78,12 +78,15 @@ __device__ __forceinline__ double exp_fast(double x) {
     return __builtin_ldexp(p, (int)kf);
 }
 
-// 24 e^-z for the quadrature node loops, z >= -1 (Tang's table-driven method): z is reduced as
-// -z = (256 m + j) ln2/256 + r with |r| <= ln2/512, e^r comes from its degree-4 Taylor polynomial
-// (truncation < 4e-17 relative) scaled by 24, 24 e^r = (((r + 4) r + 12) r + 24) r + 24, whose
-// coefficients are exact and whose first step adds an inline constant (no coefficient has to sit
-// in a vector register; the node weights carry the 1/24), and 2^(j/256) from a 256-entry table in
-// LDS. z is capped at 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308
+// K e^-z for the quadrature node loops, z >= -1 (Tang's table-driven method): z is reduced as
+// -z = (256 m + j) ln2/256 + r with |r| <= ln2/512, K e^r comes from the monic cubic
+// p(r) = ((r + a2) r + a1) r + a0 (exp_cubic; K = kExpPolyK ~ 6, the node weights carry the 1/K),
+// and 2^(j/256) from a 256-entry table in LDS. The cubic is the minimax fit of the relative error
+// on |r| <= ln2/512 (Remez; equioscillating at 1.75e-14, evaluated in doubles within 2.0e-14 and
+// unbiased, mean 4e-16): one instruction fewer than the degree-4 Taylor polynomial, whose
+// 4e-17 truncation the node sums do not need (their tolerance is 1e-10 relative). Each step adds
+// one scalar operand, so no coefficient has to sit in a vector register.
+// z is capped at 708.3, so the result never leaves the normal range (e^-708.3 ~ 2.5e-308
 // stands in for the smaller values, whose contribution to any node sum is far below round-off). A
 // NaN z is lost here; callers check their inputs for NaN once per integral instead of per node.
 // The integer k = 256 m + j = round(-z 256/ln2) is formed by adding 1.5 * 2^52 in the same fma:
@@ -96,17 +99,27 @@ __device__ __forceinline__ double exp_fast(double x) {
 // taken off its high word (exp2_frac_lead), so adding k << 12 = (m << 20) + (j << 12) leaves
 // 2^(j/256) with m added to its exponent field -- exact while the result stays normal, which the
 // cap ensures (m >= -1022 and 2^(j/256) >= 1).
-__device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __restrict__ lead) {
+constexpr double kExpPolyK = 0x1.8000024e61c28p+2;     // 6.0000005498359669...
+constexpr double kExpA2 = 0x1.800006265a012p+1;
+constexpr double kExpA1 = 0x1.8000024e61d2cp+2;
+constexpr double kExpA0 = 0x1.8000024e61bb2p+2;
+// The coefficients are passed through scalar registers at every call: held in vector registers
+// (where the compiler otherwise hoists them), each fma would become a register move plus an fmac.
+__device__ __forceinline__ double exp_cubic(double r) {
+    double a2 = kExpA2, a1 = kExpA1, a0 = kExpA0;
+    asm volatile("" : "+s"(a2), "+s"(a1), "+s"(a0));
+    double p = r + a2;
+    p = __builtin_fma(p, r, a1);
+    return __builtin_fma(p, r, a0);
+}
+__device__ __forceinline__ double exp_neg_tab_k(double z, const double* __restrict__ lead) {
     constexpr double kShift = 0x1.8p52;
     z = __builtin_fmin(z, 708.3);
     const double sh = __builtin_fma(z, -0x1.71547652b82fep+8, kShift);  // -z * 256/ln2 + shift
     const double kf = sh - kShift;
     const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
     const double r = __builtin_fma(-kf, 0x1.62e42fefa39efp-9, -z);      // ln2 / 256
-    double p = r + 4.0;
-    p = __builtin_fma(p, r, 12.0);
-    p = __builtin_fma(p, r, 24.0);
-    p = __builtin_fma(p, r, 24.0);
+    const double p = exp_cubic(r);
     struct Words { uint32_t lo, hi; };
     Words w = __builtin_bit_cast(Words, lead[k & 255]);
     // a 32-bit add on the high word (written out: the compiler otherwise forms a 64-bit add)
@@ -114,7 +127,7 @@ __device__ __forceinline__ double exp_neg_tab_x24(double z, const double* __rest
     return __builtin_bit_cast(double, w) * p;
 }
 
-// The same with a node weight folded in: 24 wh e^-z for wh = 2^n w', where the caller passes
+// The same with a node weight folded in: K wh e^-z for wh = 2^n w', where the caller passes
 // z' = z - ln w' (|ln w'| <= ln2/2, so z' rounds as finely as z) and S = 1.5 * 2^52 + 256 n. The
 // shift S puts k + 256 n in the low word of sh, so the high-word add scales the result by 2^n
 // exactly, while sh - S is still k itself for the reduction. With n >= kFoldMinExp the cap
@@ -128,24 +141,21 @@ __device__ __forceinline__ double vgpr_const(double c) {
     asm volatile("" : "+v"(c));
     return c;
 }
-__device__ __forceinline__ double exp_neg_tab_x24_w(double z, double S, double c256,
-                                                    const double* __restrict__ lead) {
+__device__ __forceinline__ double exp_neg_tab_k_w(double z, double S, double c256,
+                                                  const double* __restrict__ lead) {
     z = __builtin_fmin(z, kFoldCapZ);
     const double sh = __builtin_fma(z, c256, S);
     const double kf = sh - S;
     const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
     const double r = __builtin_fma(-kf, 0x1.62e42fefa39efp-9, -z);
-    double p = r + 4.0;
-    p = __builtin_fma(p, r, 12.0);
-    p = __builtin_fma(p, r, 24.0);
-    p = __builtin_fma(p, r, 24.0);
+    const double p = exp_cubic(r);
     struct Words { uint32_t lo, hi; };
     Words w = __builtin_bit_cast(Words, lead[k & 255]);
     asm("v_lshl_add_u32 %0, %1, 12, %2" : "=v"(w.hi) : "v"(k), "v"(w.hi));
     return __builtin_bit_cast(double, w) * p;
 }
 
-// Host/device split of a positive node weight for exp_neg_tab_x24_w: wh = 2^n w' with n the
+// Host/device split of a positive node weight for exp_neg_tab_k_w: wh = 2^n w' with n the
 // nearest integer to log2 wh (at least kFoldMinExp); returns -ln w' and sets S.
 __host__ __device__ inline double fold_weight(double wh, double* S) {
     int n = (int)rint(log2(wh));
@@ -270,7 +280,7 @@ __host__ __device__ constexpr double exp2_frac(int j) {
     return t[j];
 }
 
-// exp2_frac(j) with j << 12 taken off its high word (the table of exp_neg_tab_x24).
+// exp2_frac(j) with j << 12 taken off its high word (the table of exp_neg_tab_k).
 __host__ __device__ inline double exp2_frac_lead(int j) {
     return __builtin_bit_cast(double, __builtin_bit_cast(uint64_t, exp2_frac(j)) -
                                           ((uint64_t)j << 44));

@@ -416,8 +416,8 @@ __device__ __forceinline__ bool new_centre(const double* __restrict__ x) {
     return __builtin_bit_cast(uint64_t, x[5]) != 0;
 }
 
-// Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / 24, s_t^2
-// and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_x24 of the three-centre passes;
+// Node constants of one aux record (layout below): s_t, wh_t = wp_t s_t^(-1/2) e^(-1/2) / K, s_t^2
+// and 1/s_t, for the scaled node form (node_val_h) and exp_neg_tab_k of the three-centre passes;
 // `scale` multiplies the weight (the record's u, for the reverse pass that folds it in). Stored
 // node-major from offset 8 (node t at 8 + 4 t): the four values a node reads are one 32-byte run,
 // a single scalar load, and two nodes share a cache line.
@@ -431,12 +431,12 @@ __host__ __device__ constexpr int rec_is(int t) { return 8 + 4 * t + 3; }
 __device__ __forceinline__ void put_node_consts(double* o, int t, double s, double wp,
                                                 double scale = 1.0) {
     o[rec_s(t)] = s;
-    o[rec_wh(t)] = wp / sqrt(s) * (kExpMinusHalf / 24.0) * scale;
+    o[rec_wh(t)] = wp / sqrt(s) * (kExpMinusHalf / kExpPolyK) * scale;
     o[rec_s2(t)] = s * s;
     o[rec_is(t)] = 1.0 / s;
 }
 
-// The forward's records (k_gamma_fwd_pairs) hold the weight split for exp_neg_tab_x24_w in the
+// The forward's records (k_gamma_fwd_pairs) hold the weight split for exp_neg_tab_k_w in the
 // same four slots: s_t, -ln w'_t, S_t, 1/s_t with wh_t = 2^n w'_t (fold_weight).
 __host__ __device__ constexpr int rec_lw(int t) { return 8 + 4 * t + 1; }
 __host__ __device__ constexpr int rec_S(int t) { return 8 + 4 * t + 2; }
@@ -444,7 +444,7 @@ __host__ __device__ constexpr int rec_S(int t) { return 8 + 4 * t + 2; }
 __device__ __forceinline__ void put_fwd_node_consts(double* o, int t, double s, double wp) {
     double S;
     o[rec_s(t)] = s;
-    o[rec_lw(t)] = fold_weight(wp / sqrt(s) * (kExpMinusHalf / 24.0), &S);
+    o[rec_lw(t)] = fold_weight(wp / sqrt(s) * (kExpMinusHalf / kExpPolyK), &S);
     o[rec_S(t)] = S;
     o[rec_is(t)] = 1.0 / s;
 }
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
             double F = 0.0;
             // each node's constants are read one node ahead, so their scalar load overlaps the
             // previous node's arithmetic
-            // The node weight rides in the exponent (exp_neg_tab_x24_w): with y0 ~ Pr^(-1/2),
+            // The node weight rides in the exponent (exp_neg_tab_k_w): with y0 ~ Pr^(-1/2),
             // h = y0^2 and 1 + eps = 2 - Pr h, the term is y0 e^-(a (1 + eps) - ln w') 2^n for
             // a = Qn h - 1/2 (node_arg_h's argument, formed as one fma with ln w'), so no
             // multiply by the weight is left. The screen tests a, which differs from
@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
                 const double h = y0 * y0;
                 const double e1 = __builtin_fma(-Pr, h, 2.0);
                 const double a = __builtin_fma(Qn, h, -0.5);
-                F = __builtin_fma(y0, exp_neg_tab_x24_w(__builtin_fma(a, e1, lw), S, c256, tab), F);
+                F = __builtin_fma(y0, exp_neg_tab_k_w(__builtin_fma(a, e1, lw), S, c256, tab), F);
                 // keep the next node's loads ahead of the early exit (not sunk past it)
                 if constexpr (t + 1 < kNodes)
                     asm volatile("" ::"s"(n_s), "s"(n_lw), "s"(n_S), "s"(n_is));
@@ -919,7 +919,7 @@ __global__ __launch_bounds__(256) void k_gamma_bwd(
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeValH v = node_val_h(Pr, Qn);
-            const double f = (wh * v.y0) * exp_neg_tab_x24(v.arg, tab);
+            const double f = (wh * v.y0) * exp_neg_tab_k(v.arg, tab);
             F += f;
             const double G = f * v.ip;                  // g s
             const double Gh = G * v.zh;                 // s df/dPn
@@ -1421,12 +1421,12 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
         double adjT[6], Td[3];
         const EriGeom G = eri_geom(T, d, adjT, Td);
         double F = 0.0;
-        // the node weight rides in the exponent as in the DF-J forward (exp_neg_tab_x24_w); the
+        // the node weight rides in the exponent as in the DF-J forward (exp_neg_tab_k_w); the
         // split of the compile-time weight folds to constants
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
             constexpr double st = quad_t(t) * quad_t(t), is = 1.0 / st;
-            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / 24.0);
+            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / kExpPolyK);
             double S;
             double lw = fold_weight(wh, &S);
             // materialised in scalar registers at each node (not held in vector registers
@@ -1438,7 +1438,7 @@ __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __
             const double h = y0 * y0;
             const double e1 = __builtin_fma(-Er, h, 2.0);
             const double za = __builtin_fma(num, h, -0.5);
-            F = __builtin_fma(y0, exp_neg_tab_x24_w(__builtin_fma(za, e1, lw), S, c256, tab), F);
+            F = __builtin_fma(y0, exp_neg_tab_k_w(__builtin_fma(za, e1, lw), S, c256, tab), F);
             if constexpr (kMask)
                 return screen_after(t) && wave_all_beyond_h(off ? kFarAway : za);
             else
@@ -1537,11 +1537,11 @@ __global__ __launch_bounds__(256) void k_eri_bwd_sym(int64_t n, const double* __
         auto node = [&](auto tc) {
             constexpr int t = decltype(tc)::value;
             constexpr double st = quad_t(t) * quad_t(t), is = 1.0 / st;
-            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / 24.0);
+            constexpr double wh = quad_w(t) / quad_t(t) * (kExpMinusHalf / kExpPolyK);
             const double Er = __builtin_fma(st, __builtin_fma(st, G.J3, G.J2), G.J1) + is;
             const double num = __builtin_fma(st, __builtin_fma(st, G.p2, G.p1), G.p0);
             const NodeValH v = node_val_h(Er, num);
-            const double f = (wh * v.y0) * exp_neg_tab_x24(v.arg, tab);
+            const double f = (wh * v.y0) * exp_neg_tab_k(v.arg, tab);
             F += f;
             const double gs = f * v.ip;                 // g s, g = f / Es
             const double ghs = gs * v.zh;               // gh s, gh = g (z - 1/2)
@@ -1774,7 +1774,7 @@ __global__ __launch_bounds__(256) void k_exch_block_pairs(int64_t n,
             const double Pr = __builtin_fma(is, I3, __builtin_fma(st, I1 + st, I2));
             const double Qn = __builtin_fma(st, __builtin_fma(st, q1, rr), X0);
             const NodeArgH v = node_arg_h(Pr, Qn);
-            F = __builtin_fma(wh * v.y0, exp_neg_tab_x24(v.arg, tab), F);
+            F = __builtin_fma(wh * v.y0, exp_neg_tab_k(v.arg, tab), F);
             // keep the next node's loads ahead of the early exit (not sunk past it)
             if constexpr (t + 1 < kN) asm volatile("" ::"s"(n_s), "s"(n_wh), "s"(n_is));
             return screen_after<kN>(t) && wave_all_beyond_h(v.arg);
