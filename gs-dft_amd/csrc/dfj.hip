@@ -479,8 +479,12 @@ __device__ __forceinline__ void count_work(unsigned long long* work, bool live, 
 // are formed once per centre and shared by its exponent scales, and the wave's node screen acts on
 // 64 pairs in precision band + Morton order. Each lane keeps its running sums of coef_a F(P, a) for
 // the block's records in LDS; at the end the 256 lane sums of each record are added in lane order
-// and scaled by KN_P (the record's u): partial[g * N + slot].
-constexpr int kFwdRecs = 16;
+// and scaled by KN_P (the record's u): partial[g * N + slot]. Twelve records per block keep the
+// LDS at 26 KB, so six workgroups (six waves per SIMD, within the kernel's 60 registers) share a
+// CU; 16 records (34 KB, four waves per SIMD) were 1.9% slower and 8 or 10 records 0.9% and 1.6%.
+// The sums do not depend on the block size: each lane adds its pairs to a record's sum in the
+// same order, and the lanes are added in lane order.
+constexpr int kFwdRecs = 12;
 constexpr int64_t kFwdPairs = 8192;
 
 __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
