@@ -1386,7 +1386,9 @@ __device__ __forceinline__ double wave_sum_x(double v) {
 // kept per wave in LDS and written per workgroup (the four waves added in order) to
 // ket_part[x][b - A0] for the whole slab (zeros where a wave had no ket). Lanes with a > b (only
 // near the diagonal) contribute nothing and do not hold the wave in the node loop.
-constexpr int kEriSymSlab = 1024;        // kets per workgroup
+// 768 kets per workgroup: the per-wave ket sums then take 24 KB of LDS, so the kernel runs the
+// five waves per SIMD its registers allow (1024 kets, 32 KB: four, 1.9% slower).
+constexpr int kEriSymSlab = 768;
 
 __global__ __launch_bounds__(256) void k_eri_fwd_sym(int64_t n, const double* __restrict__ rec,
                                                      int64_t A0, int64_t H,
@@ -1494,7 +1496,9 @@ constexpr int kEriAcc = 10;
 // and the ket's moments c_a (F, gT, -gd) (T is symmetric in a and b, d changes sign) are summed over
 // the wave (wave_sum10) and written per wave to ket_part[(4 x + wave) * 10 + c][b - A0] for every
 // ket of the workgroup's slab (zeros where the wave had no ket).
-constexpr int kEriSymSlabB = 1024;       // kets per workgroup (reverse)
+// kets per workgroup of the reverse: the forward's, so that both passes sum the bra partials of
+// a band over the same slabs and their E_J agree bit for bit
+constexpr int kEriSymSlabB = kEriSymSlab;
 
 __global__ __launch_bounds__(256) void k_eri_bwd_sym(int64_t n, const double* __restrict__ rec,
                                                      int64_t A0, int64_t H,
