@@ -738,8 +738,11 @@ __global__ void k_aux_bwd_prep(int64_t N, int64_t G, const double* __restrict__ 
 // later).
 constexpr int kAtomChunk = 64;
 
+// The nuclear-force form (kAtomF) is held to four waves per SIMD (128 registers, a 20-byte spill
+// outside the node loop): 1.6% faster than the three its 134 registers allowed. The other forms
+// keep their allocation (for kLaneU four waves cost a 32-byte spill and 2.6%).
 template <bool kLaneU, bool kAtomF = false, bool kFold = false, int kN = kNodes>
-__global__ __launch_bounds__(256) void k_gamma_bwd(
+__global__ __launch_bounds__(256, kAtomF ? 4 : 1) void k_gamma_bwd(
     int64_t n, const double* __restrict__ rec, int64_t N, const double* __restrict__ aux,
     int64_t per_slab, double* __restrict__ partial, unsigned long long* __restrict__ work,
     const double* __restrict__ ut, int64_t ldu, double* __restrict__ atom_part,
