@@ -42,6 +42,8 @@ constexpr int kAuxRec = 88;   // doubles per aux record of the reverse pass
 constexpr int kAcc = 25;      // cotangent moments per pair
 
 inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+// Blocks in the y or z dimension of a grid (the x dimension is bounded by its 2^32 - 1 work-items).
+constexpr int64_t kMaxGridY = 65535;
 
 // ------------------------------------------------------------------ aux
 
@@ -320,7 +322,7 @@ __device__ __forceinline__ int64_t xcd_block(int64_t nb) {
 }
 
 // q_a = w_a sum_o occ_o C_io C_jo (gs_dft/coulomb/ri.py:456; w_a = 1 for a null weight); G lanes
-// per pair.
+// per pair, the grid striding over the pairs (G n work-items can pass a grid dimension's 2^32 - 1).
 template <int G>
 __global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* __restrict__ pi,
                                                       const int32_t* __restrict__ pj,
@@ -328,15 +330,17 @@ __global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* 
                                                       const double* __restrict__ C,
                                                       const double* __restrict__ occ,
                                                       double* __restrict__ q) {
-    const int64_t a = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / G;
     const int l = threadIdx.x % G;
-    const bool live = a < n;
-    const int64_t i = live ? pi[a] : 0, j = live ? pj[a] : 0;
-    double s = 0.0;
-    if (live)
+    const int64_t stride = (int64_t)gridDim.x * (blockDim.x / G);
+    // the G lanes of a pair share a, so a group is wholly in or out of the loop and the butterfly
+    // (lane offsets below G) reads only lanes of its own group
+    for (int64_t a = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / G; a < n; a += stride) {
+        const int64_t i = pi[a], j = pj[a];
+        double s = 0.0;
         for (int64_t o = l; o < k; o += G) s += (occ[o] * C[i * k + o]) * C[j * k + o];
-    for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (live && l == 0) q[a] = (weight ? weight[a] : 1.0) * s;
+        for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (l == 0) q[a] = (weight ? weight[a] : 1.0) * s;
+    }
 }
 
 // Pair record: I1 I2 I3 | Ah (6) | Pa (3) | coef = KN q pref | KN | q | pad.
@@ -472,10 +476,11 @@ __device__ __forceinline__ void count_work(unsigned long long* work, bool live, 
 // ------------------------------------------------------------------ forward
 
 // Forward with one lane per pair slot (the reverse's slot order) and the aux records of the reverse
-// (centre-grouped, wave-uniform): block g nrb + s (nrb = ceil(N / kFwdRecs)) sums the pair slots
-// [g kFwdPairs, (g + 1) kFwdPairs) against the kFwdRecs aux slots from s kFwdRecs on. The record
-// blocks run fastest, so the workgroups dispatched together share their pair slots (read once
-// into L2) and differ only in their aux records. The centre-dependent terms (d, Ah d, q0..q2)
+// (centre-grouped, wave-uniform): block (s, g) of the 2-D grid (ceil(N / kFwdRecs), pair groups)
+// sums the pair slots [g kFwdPairs, (g + 1) kFwdPairs) against the kFwdRecs aux slots from
+// s kFwdRecs on. The record blocks (x) run fastest, so the workgroups dispatched together share
+// their pair slots (read once into L2) and differ only in their aux records. (One dimension of a
+// grid holds at most 2^32 - 1 work-items: a 1-D grid of both would pass that at 20 M pairs.) The centre-dependent terms (d, Ah d, q0..q2)
 // are formed once per centre and shared by its exponent scales, and the wave's node screen acts on
 // 64 pairs in precision band + Morton order. Each lane keeps its running sums of coef_a F(P, a) for
 // the block's records in LDS; at the end the 256 lane sums of each record are added in lane order
@@ -499,8 +504,7 @@ __global__ __launch_bounds__(256) void k_gamma_fwd_pairs(int64_t n,
 #pragma unroll
     for (int j = 0; j < kFwdRecs; ++j) acc[j][threadIdx.x] = 0.0;
     __syncthreads();
-    const int64_t nrb = (N + kFwdRecs - 1) / kFwdRecs;
-    const int64_t q0 = ((int64_t)blockIdx.x % nrb) * kFwdRecs, g = (int64_t)blockIdx.x / nrb;
+    const int64_t q0 = (int64_t)blockIdx.x * kFwdRecs, g = blockIdx.y;
     const int nrec = (int)min((int64_t)kFwdRecs, N - q0);
     const int64_t a_begin = g * kFwdPairs;
     const int64_t a_end = min(n, a_begin + kFwdPairs);
@@ -1922,14 +1926,18 @@ int layout_gamma(Arena& ar, int64_t M, int64_t N, int64_t n, bool reverse, Gamma
 int launch_pair_density(int64_t n, const int32_t* pi, const int32_t* pj, const double* weight,
                         int64_t k, const double* C, const double* occ, double* q, hipStream_t s) {
     if (n <= 0) return GSDFT_OK;
+    // one pass while G n work-items fit a grid dimension, else the grid strides over the pairs
+    auto grid = [n](int G) {
+        return (unsigned)std::min<int64_t>((n * G + 255) / 256, (int64_t)(UINT32_MAX / 256));
+    };
     if (k <= 8) {
-        k_pair_density<8><<<blocks_for(n * 8, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        k_pair_density<8><<<grid(8), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     } else if (k <= 16) {
-        k_pair_density<16><<<blocks_for(n * 16, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        k_pair_density<16><<<grid(16), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     } else if (k <= 32) {
-        k_pair_density<32><<<blocks_for(n * 32, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        k_pair_density<32><<<grid(32), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     } else {
-        k_pair_density<64><<<blocks_for(n * 64, 256), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        k_pair_density<64><<<grid(64), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     }
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
@@ -2198,6 +2206,7 @@ extern "C" int gsdft_product_aux_pairs(int64_t M, const double* quat, const doub
         (n > 0 && (!pi || !pj || !log_alpha || !aux_centers)))
         return fail(GSDFT_ERR_ARG, "gsdft_product_aux_pairs: need M > 0, n >= 0, at least one "
                     "scale and every array");
+    GSDFT_TRY(check_pairs(n, "gsdft_product_aux_pairs"));
     if (n == 0) return GSDFT_OK;
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
@@ -2670,6 +2679,7 @@ extern "C" int gsdft_gamma_workspace_size(int64_t M, int64_t k, int64_t N, int64
                                           size_t* bytes) {
     (void)k;
     if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_workspace_size: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gamma_workspace_size"));
     Arena ar{nullptr, 0, 0};
     GammaWs w;
     GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
@@ -2681,6 +2691,7 @@ extern "C" int gsdft_gamma_vjp_workspace_size(int64_t M, int64_t k, int64_t N, i
                                               size_t* bytes) {
     (void)k;
     if (M < 0 || N < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "gamma_vjp_workspace_size: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gamma_vjp_workspace_size"));
     Arena ar{nullptr, 0, 0};
     GammaWs w;
     GSDFT_TRY(layout_gamma(ar, M, N, n, true, &w));
@@ -2718,9 +2729,11 @@ int gamma_run(int64_t M, const double* quat, const double* log_scale, const doub
                                                             w.rec_sorted);
     GSDFT_HIP(hipGetLastError());
     const int64_t groups = (n + kFwdPairs - 1) / kFwdPairs;
-    const int64_t blocks = groups * ((N + kFwdRecs - 1) / kFwdRecs);
-    if (blocks > INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_gamma: n x N_aux too large");
-    const dim3 grid((unsigned)blocks);
+    const int64_t nrb = (N + kFwdRecs - 1) / kFwdRecs;
+    if (nrb * 256 > (int64_t)UINT32_MAX || groups > kMaxGridY)
+        return fail(GSDFT_ERR_ARG, "gsdft_gamma: N_aux = %lld or n = %lld too large for one launch",
+                    (long long)N, (long long)n);
+    const dim3 grid((unsigned)nrb, (unsigned)groups);
     if (profile) profile_begin(kProfGammaFwd, s);
     k_gamma_fwd_pairs<<<grid, 256, 0, s>>>(n, w.rec_sorted, N, w.aux, w.partial,
                                            profile ? profile_work_counter(kProfGammaFwd)
@@ -2766,6 +2779,7 @@ extern "C" int gsdft_gamma(int64_t M, const double* quat, const double* log_scal
                            double* gamma, void* workspace, size_t workspace_bytes, void* stream) {
     if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
         return fail(GSDFT_ERR_ARG, "gsdft_gamma: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_gamma"));
     return gamma_run(M, quat, log_scale, centers, k, C, occ, N, log_alpha, aux_centers, n, pi, pj,
                      weight, gamma, workspace, workspace_bytes, (hipStream_t)stream, true);
 }
@@ -2778,6 +2792,7 @@ extern "C" int gsdft_gamma_noalloc(int64_t M, const double* quat, const double* 
                                    void* stream) {
     if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !gamma)
         return fail(GSDFT_ERR_ARG, "gsdft_gamma_noalloc: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_gamma_noalloc"));
     Arena ar{nullptr, 0, 0};
     GammaWs w;
     GSDFT_TRY(layout_gamma(ar, M, N, n, false, &w));
@@ -2805,6 +2820,7 @@ extern "C" int gsdft_gamma_vjp(int64_t M, const double* quat, const double* log_
     if (M <= 0 || N <= 0 || n < 0 || k <= 0 || !dgamma || !dquat || !dlog_scale || !dcenters ||
         !dC || !row_ptr || !col_ptr || (n > 0 && (!J || !row_perm || !col_perm)))
         return fail(GSDFT_ERR_ARG, "gsdft_gamma_vjp: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_gamma_vjp"));
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
     GammaWs w;
@@ -2953,6 +2969,7 @@ extern "C" int gsdft_external_workspace_size(int64_t M, int64_t k, int64_t n, in
     (void)k;
     if (M < 0 || n < 0 || n_atoms < 0 || !bytes)
         return fail(GSDFT_ERR_ARG, "external_workspace_size: bad arguments");
+    GSDFT_TRY(check_pairs(n, "external_workspace_size"));
     Arena ar{nullptr, 0, 0};
     ExternalWs w;
     GSDFT_TRY(layout_external(ar, M, n, n_atoms, &w));
@@ -2967,6 +2984,7 @@ extern "C" int gsdft_nuclear_pairs(int64_t M, const double* quat, const double* 
                                    size_t workspace_bytes, void* stream) {
     if (M <= 0 || n < 0 || (n > 0 && (!pi || !pj || !V)))
         return fail(GSDFT_ERR_ARG, "gsdft_nuclear_pairs: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_nuclear_pairs"));
     GSDFT_TRY(check_atoms(n_atoms, atom_coords, atom_charges));
     if (n == 0) return GSDFT_OK;
     hipStream_t s = (hipStream_t)stream;
@@ -2989,6 +3007,7 @@ extern "C" int gsdft_external_energy(
     const bool splat_grad = dquat || dlog_scale || dcenters || dC;
     if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy || (n > 0 && (!pi || !pj || !weight || !V)))
         return fail(GSDFT_ERR_ARG, "gsdft_external_energy: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_external_energy"));
     if (splat_grad && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
                        (n > 0 && (!row_perm || !col_perm))))
         return fail(GSDFT_ERR_ARG, "gsdft_external_energy: the splat gradients come together "
@@ -3043,6 +3062,7 @@ extern "C" int gsdft_density_pairs(int64_t n, const int32_t* pi, const int32_t* 
                                    void* stream) {
     if (n < 0 || k <= 0 || (n > 0 && (!pi || !pj || !C || !occ || !out)))
         return fail(GSDFT_ERR_ARG, "gsdft_density_pairs: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_density_pairs"));
     return launch_pair_density(n, pi, pj, nullptr, k, C, occ, out, (hipStream_t)stream);
 }
 
@@ -3113,6 +3133,7 @@ extern "C" int gsdft_exact_coulomb_workspace_size(int64_t M, int64_t k, int64_t 
     (void)k;
     if (M < 0 || n < 0 || !bytes)
         return fail(GSDFT_ERR_ARG, "exact_coulomb_workspace_size: bad arguments");
+    GSDFT_TRY(check_pairs(n, "exact_coulomb_workspace_size"));
     Arena ar{nullptr, 0, 0};
     EriWs w;
     GSDFT_TRY(layout_eri(ar, M, n, grads != 0, &w));
@@ -3278,6 +3299,7 @@ extern "C" int gsdft_exact_coulomb(int64_t M, const double* quat, const double* 
     if (M <= 0 || n < 0 || k <= 0 || !C || !occ || !energy ||
         (n > 0 && (!pi || !pj || !weight || !J)))
         return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_exact_coulomb"));
     if (grads && (!dquat || !dlog_scale || !dcenters || !dC || !row_ptr || !col_ptr ||
                   (n > 0 && (!row_perm || !col_perm))))
         return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb: the gradients come together (dquat, "
@@ -3301,6 +3323,10 @@ extern "C" int gsdft_exact_coulomb_density(int64_t M, const double* quat,
     const bool grads = dquat || dlog_scale || dcenters;
     if (M <= 0 || n < 0 || !P || !energy || (n > 0 && (!pi || !pj || !weight || !J)))
         return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb_density: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_exact_coulomb_density"));
+    if (M * M > (int64_t)UINT32_MAX - 255)             // dE/dP is M x M, cleared by one launch
+        return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb_density: M = %lld too large for a dense "
+                    "M x M dE/dP", (long long)M);
     if (grads && (!dquat || !dlog_scale || !dcenters || !row_ptr || !col_ptr ||
                   (n > 0 && (!row_perm || !col_perm))))
         return fail(GSDFT_ERR_ARG, "gsdft_exact_coulomb_density: the splat gradients come "

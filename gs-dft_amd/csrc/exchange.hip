@@ -650,6 +650,7 @@ extern "C" int gsdft_exchange_workspace_size(int64_t M, int64_t k, int64_t N, in
                                              int recompute, size_t* bytes) {
     if (M <= 0 || k <= 0 || N <= 0 || n < 0 || aux_chunk < 0 || !bytes)
         return fail(GSDFT_ERR_ARG, "exchange_workspace_size: bad arguments");
+    GSDFT_TRY(check_pairs(n, "exchange_workspace_size"));
     const bool sym = symmetric != 0, gr = grads != 0;
     const int64_t Pc = exch_chunk(M, k, N, n, sym, gr, aux_chunk);
     Arena ar{nullptr, 0, 0};
@@ -675,6 +676,7 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
         (n > 0 && (!pi || !pj || !row_perm)) ||
         (grads && (!dlog_scale || !dcenters || !dC || !col_ptr || (n > 0 && !col_perm))))
         return fail(GSDFT_ERR_ARG, "gsdft_exchange: bad arguments");
+    GSDFT_TRY(check_pairs(n, "gsdft_exchange"));
     if (!(omega >= 0.0) || std::isinf(omega))
         return fail(GSDFT_ERR_ARG, "gsdft_exchange: omega must be finite and >= 0");
     hipStream_t s = (hipStream_t)stream;

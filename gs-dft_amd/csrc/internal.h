@@ -26,6 +26,17 @@ int hip_fail(hipError_t e, const char* what);
         if (rc_ != GSDFT_OK) return rc_;                                  \
     } while (0)
 
+// One dimension of a grid holds at most 2^32 - 1 work-items. The one-dimensional launches over a
+// pair list take at most 25 work-items per pair (the reverse's moments), so every entry point that
+// takes a list accepts at most kMaxPairs pairs and reports larger ones rather than launching a
+// grid whose size would wrap.
+constexpr int64_t kMaxPairs = 160000000;
+inline int check_pairs(int64_t n, const char* who) {
+    return n > kMaxPairs ? fail(GSDFT_ERR_ARG, "%s: n = %lld pairs, more than the %lld one call takes",
+                                who, (long long)n, (long long)kMaxPairs)
+                         : GSDFT_OK;
+}
+
 // Bump allocator over a caller-provided workspace (256-byte aligned slices).
 struct Arena {
     char* base;

@@ -646,6 +646,7 @@ extern "C" int gsdft_overlap_pairs(int64_t M, const double* quat, const double* 
                                    const int32_t* pj, double* S, void* workspace,
                                    size_t workspace_bytes, void* stream) {
     if (M <= 0 || n < 0) return fail(GSDFT_ERR_ARG, "gsdft_overlap_pairs: bad sizes");
+    GSDFT_TRY(check_pairs(n, "gsdft_overlap_pairs"));
     if (n == 0) return GSDFT_OK;
     hipStream_t s = (hipStream_t)stream;
     Arena ar{(char*)workspace, workspace_bytes, 0};
@@ -741,6 +742,7 @@ extern "C" int gsdft_pair_index_workspace_size(int64_t M, int64_t n, size_t* byt
     if (M < 0 || n < 0 || !bytes) return fail(GSDFT_ERR_ARG, "pair_index_workspace_size: bad arguments");
     if (n >= INT32_MAX)
         return fail(GSDFT_ERR_ARG, "pair_index_workspace_size: n exceeds the int32 range");
+    GSDFT_TRY(check_pairs(n, "pair_index_workspace_size"));
     size_t sb = 0;
     if (hipcub::DeviceRadixSort::SortPairs(nullptr, sb, (const int32_t*)nullptr,
                                            (int32_t*)nullptr, (const int32_t*)nullptr,
@@ -761,6 +763,7 @@ extern "C" int gsdft_pair_index(int64_t M, int64_t n, const int32_t* pi, const i
     if (M <= 0 || n < 0 || !row_ptr || !col_ptr)
         return fail(GSDFT_ERR_ARG, "gsdft_pair_index: bad arguments");
     if (n >= INT32_MAX) return fail(GSDFT_ERR_ARG, "gsdft_pair_index: n exceeds the int32 range");
+    GSDFT_TRY(check_pairs(n, "gsdft_pair_index"));
     hipStream_t s = (hipStream_t)stream;
     size_t sb = 0;
     if (hipcub::DeviceRadixSort::SortPairs(nullptr, sb, (const int32_t*)nullptr,

@@ -78,6 +78,27 @@ def test_workspace_queries_accept_empty_inputs(built):
                 assert rc in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)
 
 
+def test_size_queries_refuse_lists_past_one_launch(built):
+    """A one-dimensional grid holds at most 2^32 - 1 work-items and the launches over a pair list
+    take up to 25 per pair, so every entry point that takes a list refuses more than 160 M pairs
+    with an argument error (the size queries included, which need no GPU) instead of launching a
+    grid whose size would wrap; 160 M itself is accepted by the queries."""
+    lib = built.lib()
+    out = ctypes.c_size_t(0)
+    limit = 160_000_000
+    queries = (lambda n: lib.gsdft_gamma_workspace_size(4, 1, 4, n, ctypes.byref(out)),
+               lambda n: lib.gsdft_gamma_vjp_workspace_size(4, 1, 4, n, ctypes.byref(out)),
+               lambda n: lib.gsdft_external_workspace_size(4, 1, n, 10, ctypes.byref(out)))
+    for query in queries:
+        assert query(limit + 1) == built.GSDFT_ERR_ARG
+        assert b"pairs, more than the 160000000" in lib.gsdft_last_error()
+        assert query(limit) in (built.GSDFT_OK, built.GSDFT_ERR_LIB, built.GSDFT_ERR_HIP)
+    assert lib.gsdft_exact_coulomb_workspace_size(4, 1, limit + 1, 1,
+                                                  ctypes.byref(out)) == built.GSDFT_ERR_ARG
+    assert lib.gsdft_exchange_workspace_size(4, 2, 8, limit + 1, 1, 1, 0, 0,
+                                             ctypes.byref(out)) == built.GSDFT_ERR_ARG
+
+
 def test_pair_index_refuses_counts_past_int32(built):
     """The pair index sorts with 32-bit counts: a pair count past the int32 range is refused with
     an argument error before any library call, by the size query and by the builder itself."""

@@ -256,3 +256,39 @@ def test_energy_gamma_and_gradient_rows_full_size(g, wl, orc, cuda, system, eps)
         assert eta < 1e-12
     del V
     torch.cuda.empty_cache()
+
+
+# ----------------------------------------------------------------------------- launch geometry
+
+def test_forward_grid_past_one_grid_dimension(g, wl, cuda):
+    """The forward's workgroups (pair groups x aux record blocks) outnumber what one grid dimension
+    holds (2^32 - 1 work-items) on the 700-atom globule's list grown to 1.86 n0 (eps 5e-12:
+    20.7 M pairs against 80000 aux functions, as a trainer's pad allows). gamma is linear in the
+    list, so gamma of the whole list must equal gamma of its two halves added (each half within
+    one grid dimension even as a one-dimensional grid), to the round-off of the regrouped sums."""
+    from gs_dft_amd import ri as _ri
+    eps = 5e-12
+    s = wl.make_system(5, eps=eps)
+    basis = _splat(g, s)
+    pi, pj, w = g.neighbor_pairs(basis, eps, unique=True)
+    aux = g.init_product_aux(basis, scales=s.scales)
+    C = torch.tensor(s.C, device="cuda")
+    x = _ri._Inputs(basis, C, s.occ, aux, pi, pj, w, None)
+    n, N = x.n_live, aux.n_basis
+    groups, rec_blocks = (n + 8191) // 8192, (N + 11) // 12
+    print(f"[grid] n={n} N_aux={N}: {groups} pair groups x {rec_blocks} record blocks x 256 = "
+          f"{groups * rec_blocks * 256:.3e} work-items", flush=True)
+    assert groups * rec_blocks * 256 > 2 ** 32
+    gam = _ri._gamma_forward(x)
+    h = n // 2
+    halves = [_ri._Inputs(basis, C, s.occ, aux, pi[a:b], pj[a:b], w[a:b], None)
+              for a, b in ((0, h), (h, n))]
+    assert all(((hx.n_live + 8191) // 8192) * rec_blocks * 256 < 2 ** 32 for hx in halves)
+    gsum = _ri._gamma_forward(halves[0]) + _ri._gamma_forward(halves[1])
+    torch.cuda.synchronize()
+    err = float(((gam - gsum).abs() / gam.abs()).max())
+    print(f"[grid] gamma of the whole list vs its halves added: max elementwise rel {err:.2e}",
+          flush=True)
+    assert err < 1e-12
+    del gam, gsum, x, halves
+    torch.cuda.empty_cache()
