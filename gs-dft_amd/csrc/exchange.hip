@@ -532,6 +532,9 @@ int layout_exchange(Arena& ar, int64_t M, int64_t k, int64_t N, int64_t n, bool 
                     bool recompute, int64_t Pc, ExchWs* w) {
     GSDFT_TRY(exch_tc_layout(ar, M, N, n, Pc, grads, &w->tc));
     const int64_t K2 = sym ? k * (k + 1) / 2 : k * k;
+    GSDFT_TRY(check_items(packed_ld(K2) * N, "exchange", "the packed columns (K2 x N_aux)"));
+    GSDFT_TRY(check_items(M * padded_cols(k), "exchange", "the padded orbitals (M x k)"));
+    GSDFT_TRY(check_items(Pc * k * k, "exchange", "an aux chunk's D blocks (W x k x k)"));
     const bool store = exch_store(M, k, N, sym, grads, recompute);
     w->Dt = ar.take<double>(packed_ld(K2) * N + 1);
     w->Bt = ar.take<double>(n * Pc + 1);

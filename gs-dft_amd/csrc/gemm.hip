@@ -13,6 +13,8 @@
 // while the current step's 64 MFMAs per wave run. The wave forms the transposed tile
 // D(n, m) = sum_k B(k, n) A(k, m), so that the 16 lanes of an MFMA output row hold 16 consecutive
 // m of one column of C and the read-modify-write of C goes in 128-byte segments.
+#include <algorithm>
+
 #include "common.h"
 #include "internal.h"
 
@@ -555,12 +557,14 @@ int launch_all_tiles(int64_t Mr, int64_t Nc, int64_t K, const double* A, int64_t
 }
 
 // C = beta C (beta = 0 writes zeros) over an Mr x Nc column-major block of each batch.
+// (the grid strides over the Mr Nc elements: they can pass one grid dimension's 2^32 - 1)
 __global__ void k_scale_c(int64_t Mr, int64_t Nc, double beta, double* __restrict__ C,
                           int64_t ldc, int64_t sc) {
-    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (e >= Mr * Nc) return;
-    double* c = C + blockIdx.y * sc + (e / Mr) * ldc + e % Mr;
-    *c = beta == 0.0 ? 0.0 : beta * *c;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < Mr * Nc;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        double* c = C + blockIdx.y * sc + (e / Mr) * ldc + e % Mr;
+        *c = beta == 0.0 ? 0.0 : beta * *c;
+    }
 }
 
 }  // namespace
@@ -574,8 +578,9 @@ int launch_gemm(int64_t Mr, int64_t Nc, int64_t K, double alpha, const double* A
     if (K <= 0) {                              // C = beta C: a product over no terms
         if (beta == 1.0) return GSDFT_OK;
         if (batch > 65535) return fail(GSDFT_ERR_ARG, "gemm: too many batches");
-        k_scale_c<<<dim3((unsigned)((Mr * Nc + 255) / 256), (unsigned)batch), 256, 0, s>>>(
-            Mr, Nc, beta, C, ldc, stride_c);
+        const int64_t blocks = std::min<int64_t>((Mr * Nc + 255) / 256, UINT32_MAX / 256);
+        k_scale_c<<<dim3((unsigned)blocks, (unsigned)batch), 256, 0, s>>>(Mr, Nc, beta, C, ldc,
+                                                                         stride_c);
         GSDFT_HIP(hipGetLastError());
         return GSDFT_OK;
     }

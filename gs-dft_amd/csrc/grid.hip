@@ -299,6 +299,10 @@ int check_grid_args(int64_t M, int64_t k, int64_t G, int64_t chunk, int mode) {
     if (M <= 0 || k <= 0 || G < 0 || chunk <= 0 || chunk > 65535 || mode < 0 || mode > 2)
         return fail(GSDFT_ERR_ARG, "grid density: need M, k > 0, G >= 0, 0 < chunk <= 65535 and "
                     "mode 0 (rho), 1 (rho, grad) or 2 (rho, grad, tau)");
+    GSDFT_TRY(check_items(M * (k + 1), "grid density", "the orbitals (M x k)"));
+    GSDFT_TRY(check_items(chunk * (k + 1), "grid density", "a chunk's orbital values"));
+    GSDFT_TRY(check_items(((chunk + kRowsPerSlab - 1) / kRowsPerSlab) * 10 * M, "grid density",
+                          "the reverse's per-slab moments"));
     return GSDFT_OK;
 }
 

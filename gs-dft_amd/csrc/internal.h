@@ -31,6 +31,15 @@ int hip_fail(hipError_t e, const char* what);
 // takes a list accepts at most kMaxPairs pairs and reports larger ones rather than launching a
 // grid whose size would wrap.
 constexpr int64_t kMaxPairs = 160000000;
+// Element-wise launches over a dense array use one work-item per element: the arrays they cover
+// must stay within one grid dimension.
+constexpr int64_t kMaxLaunchItems = (int64_t)UINT32_MAX - 255;
+inline int check_items(int64_t items, const char* who, const char* what) {
+    return items > kMaxLaunchItems
+               ? fail(GSDFT_ERR_ARG, "%s: %s has %lld elements, more than one launch covers (%lld)",
+                      who, what, (long long)items, (long long)kMaxLaunchItems)
+               : GSDFT_OK;
+}
 inline int check_pairs(int64_t n, const char* who) {
     return n > kMaxPairs ? fail(GSDFT_ERR_ARG, "%s: n = %lld pairs, more than the %lld one call takes",
                                 who, (long long)n, (long long)kMaxPairs)

@@ -82,7 +82,8 @@ def test_size_queries_refuse_lists_past_one_launch(built):
     """A one-dimensional grid holds at most 2^32 - 1 work-items and the launches over a pair list
     take up to 25 per pair, so every entry point that takes a list refuses more than 160 M pairs
     with an argument error (the size queries included, which need no GPU) instead of launching a
-    grid whose size would wrap; 160 M itself is accepted by the queries."""
+    grid whose size would wrap; 160 M itself is accepted by the queries. Dense arrays that one
+    element-wise launch covers are held to the same bound."""
     lib = built.lib()
     out = ctypes.c_size_t(0)
     limit = 160_000_000
@@ -97,6 +98,14 @@ def test_size_queries_refuse_lists_past_one_launch(built):
                                                   ctypes.byref(out)) == built.GSDFT_ERR_ARG
     assert lib.gsdft_exchange_workspace_size(4, 2, 8, limit + 1, 1, 1, 0, 0,
                                              ctypes.byref(out)) == built.GSDFT_ERR_ARG
+    # dense arrays covered by one element-wise launch: RI-K's packed columns (K2 x N_aux, here
+    # 45150 x 100000 at k = 300) and the grid density's orbitals (M x k)
+    assert lib.gsdft_exchange_workspace_size(2000, 300, 100000, 1000, 1, 1, 0, 0,
+                                             ctypes.byref(out)) == built.GSDFT_ERR_ARG
+    assert b"packed columns" in lib.gsdft_last_error()
+    assert lib.gsdft_grid_density_workspace_size(3_000_000, 1500, 1024, 1, 1,
+                                                 ctypes.byref(out)) == built.GSDFT_ERR_ARG
+    assert b"orbitals" in lib.gsdft_last_error()
 
 
 def test_pair_index_refuses_counts_past_int32(built):
