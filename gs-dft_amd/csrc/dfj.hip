@@ -2507,13 +2507,28 @@ static int panel_solve(hipStream_t s, int64_t N, const double* Akk, int64_t kb, 
 
 namespace gsdft {
 
+// K-slices for a coupling product of trsm_right_upper (output m x w, K = h): the deep levels of
+// the halving have outputs of a few dozen 128 x 128 tiles (26 for RI-K's 3321 right-hand sides
+// at K = 128), which leave most CUs idle. The count doubles until the tiles times the slices
+// reach one workgroup per CU, each slice a multiple of 16 long and all of them within
+// part_doubles.
+static int64_t trsm_slices(int64_t m, int64_t w, int64_t h, int64_t part_doubles) {
+    const int64_t tiles = ((m + 127) / 128) * ((w + 127) / 128);
+    int64_t S = 1;
+    while (S < 32 && S * tiles < 256 && (h / 16) % (2 * S) == 0 && h % 16 == 0 &&
+           2 * S * m * w <= part_doubles)
+        S *= 2;
+    return S;
+}
+
 // X (m x n, column-major, leading dimension ldx) <- X U^-1, the solution of X U = B, or, with
 // trans, X <- X U^-T, the solution of X U^T = B, for the n x n upper U (column-major, leading
 // dimension ldu): the same recursive halving as panel_solve with the right-hand sides as X's rows
 // (k_panel_subst with kRowRHS; kBack for U^T) and the coupling products on the general FP64 MFMA
-// product. Each row of X is solved by substitution in the order a row-by-row solve takes.
+// product, split over K (trsm_slices, summed in slice order) when `part` has room. Each row of X
+// is solved by substitution in the order a row-by-row solve takes.
 int trsm_right_upper(hipStream_t s, bool trans, int64_t n, const double* U, int64_t ldu,
-                     double* X, int64_t m, int64_t ldx) {
+                     double* X, int64_t m, int64_t ldx, double* part, int64_t part_doubles) {
     if (n <= 0 || m <= 0) return GSDFT_OK;
     if (n <= kPanelRows) {
         const unsigned blocks = (unsigned)((m + 63) / 64);
@@ -2528,16 +2543,19 @@ int trsm_right_upper(hipStream_t s, bool trans, int64_t n, const double* U, int6
     const double* U01 = U + h * ldu;                 // rows [0, h), columns [h, n)
     const double* U11 = U + h * ldu + h;
     if (!trans) {
-        GSDFT_TRY(trsm_right_upper(s, false, h, U, ldu, X, m, ldx));
+        GSDFT_TRY(trsm_right_upper(s, false, h, U, ldu, X, m, ldx, part, part_doubles));
         // X(:, h:n) -= X(:, 0:h) U(0:h, h:n)
-        GSDFT_TRY(gemm_cm('N', 'N', m, n - h, h, -1.0, X, ldx, U01, ldu, 1.0, X + h * ldx, ldx,
-                          s));
-        return trsm_right_upper(s, false, n - h, U11, ldu, X + h * ldx, m, ldx);
+        GSDFT_TRY(gemm_cm_slices('N', 'N', m, n - h, h, -1.0, X, ldx, U01, ldu, 1.0, X + h * ldx,
+                                 ldx, trsm_slices(m, n - h, h, part_doubles), part, s));
+        return trsm_right_upper(s, false, n - h, U11, ldu, X + h * ldx, m, ldx, part,
+                                part_doubles);
     }
-    GSDFT_TRY(trsm_right_upper(s, true, n - h, U11, ldu, X + h * ldx, m, ldx));
+    GSDFT_TRY(trsm_right_upper(s, true, n - h, U11, ldu, X + h * ldx, m, ldx, part,
+                               part_doubles));
     // X(:, 0:h) -= X(:, h:n) U(0:h, h:n)^T
-    GSDFT_TRY(gemm_cm('N', 'T', m, h, n - h, -1.0, X + h * ldx, ldx, U01, ldu, 1.0, X, ldx, s));
-    return trsm_right_upper(s, true, h, U, ldu, X, m, ldx);
+    GSDFT_TRY(gemm_cm_slices('N', 'T', m, h, n - h, -1.0, X + h * ldx, ldx, U01, ldu, 1.0, X, ldx,
+                             trsm_slices(m, h, n - h, part_doubles), part, s));
+    return trsm_right_upper(s, true, h, U, ldu, X, m, ldx, part, part_doubles);
 }
 
 }  // namespace gsdft

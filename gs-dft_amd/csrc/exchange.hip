@@ -742,7 +742,8 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     }
     // Wt = Dt L^-T: chol is the row-major lower factor, i.e. the column-major upper L^T.
     profile_begin(kProfExchTrsm, s);
-    GSDFT_TRY(trsm_right_upper(s, false, N, chol, N, w.Dt, K2, ldd));
+    // (the block buffer is idle until the reverse pass: it holds the solve's K-slices)
+    GSDFT_TRY(trsm_right_upper(s, false, N, chol, N, w.Dt, K2, ldd, w.Bt, n * Pc));
     profile_end(kProfExchTrsm, s);
     k_sumsq_part<<<kRedBlocks, 256, 0, s>>>(ldd * N, w.Dt, w.red);
     GSDFT_HIP(hipGetLastError());
@@ -755,7 +756,7 @@ extern "C" int gsdft_exchange(int64_t M, const double* quat, const double* log_s
     // (the scaling by -2 is exact, so it may come before the solve)
     k_scale<<<nblk(ldd * N, 256), 256, 0, s>>>(ldd * N, -2.0, w.Dt);
     GSDFT_HIP(hipGetLastError());
-    GSDFT_TRY(trsm_right_upper(s, true, N, chol, N, w.Dt, K2, ldd));
+    GSDFT_TRY(trsm_right_upper(s, true, N, chol, N, w.Dt, K2, ldd, w.Bt, n * Pc));
     profile_end(kProfExchTrsm, s);
     k_fill0<<<nblk(M * k, 256), 256, 0, s>>>(M * k, dC);
     GSDFT_HIP(hipGetLastError());

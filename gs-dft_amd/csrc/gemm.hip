@@ -663,12 +663,10 @@ int64_t gemm_split_slices(int64_t m, int64_t n, int64_t k) {
     return S < 1 ? 1 : S;
 }
 
-int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
-                  const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
-                  double* C, int64_t ldc, double* part, int64_t part_doubles, hipStream_t s) {
-    int64_t S = part && m > 0 && n > 0 ? gemm_split_slices(m, n, k) : 1;
-    if (S > 1 && S * m * n > part_doubles) S = part_doubles / (m * n);
-    if (S <= 1 || m <= 0 || n <= 0)
+int gemm_cm_slices(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+                   const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                   double* C, int64_t ldc, int64_t S, double* part, hipStream_t s) {
+    if (S <= 1 || !part || m <= 0 || n <= 0 || k < S * kStepK)
         return gemm_cm(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, s);
     const bool a_kc = transa == 'T', b_kc = transb == 'N';
     const int64_t Ks = (k / S) / kStepK * kStepK;            // even slice offsets keep the DMA path
@@ -681,6 +679,15 @@ int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, dou
     k_add_slices<<<(unsigned)((m * n + 255) / 256), 256, 0, s>>>(m, n, S, part, beta, C, ldc);
     GSDFT_HIP(hipGetLastError());
     return GSDFT_OK;
+}
+
+int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+                  const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                  double* C, int64_t ldc, double* part, int64_t part_doubles, hipStream_t s) {
+    int64_t S = part && m > 0 && n > 0 ? gemm_split_slices(m, n, k) : 1;
+    if (S > 1 && S * m * n > part_doubles) S = part_doubles / (m * n);
+    return gemm_cm_slices(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, S, part,
+                          s);
 }
 
 }  // namespace gsdft

@@ -115,12 +115,19 @@ int64_t gemm_split_slices(int64_t m, int64_t n, int64_t k);
 int gemm_cm_split(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
                   const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
                   double* C, int64_t ldc, double* part, int64_t part_doubles, hipStream_t s);
+// The same with the caller's slice count S (part holds S m x n blocks; slices of (k / S) rounded
+// down to a multiple of 16, the remainder joining the last one); gemm_cm when S <= 1 or k < 16 S.
+int gemm_cm_slices(char transa, char transb, int64_t m, int64_t n, int64_t k, double alpha,
+                   const double* A, int64_t lda, const double* B, int64_t ldb, double beta,
+                   double* C, int64_t ldc, int64_t S, double* part, hipStream_t s);
 
 // dfj.hip: X (m x n, column-major, leading dimension ldx) <- X U^-1 (X U = B) or, with trans,
 // X U^-T (X U^T = B), for the n x n upper U (column-major, leading dimension ldu), by blocked
-// substitution with FP64 MFMA products between the blocks.
+// substitution with FP64 MFMA products between the blocks; `part` (part_doubles long, may be
+// null) holds the K-slices of the products whose output has too few tiles to fill the GPU.
 int trsm_right_upper(hipStream_t s, bool trans, int64_t n, const double* U, int64_t ldu,
-                     double* X, int64_t m, int64_t ldx);
+                     double* X, int64_t m, int64_t ldx, double* part = nullptr,
+                     int64_t part_doubles = 0);
 
 // solve.hip: forward then backward substitution with the row-major lower factor, in place.
 int launch_trsv_pair(int64_t N, const double* L, double* x, hipStream_t s);
