@@ -2403,6 +2403,26 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
     __shared__ double Ud[8][16][16];
     __shared__ double rdg[kPanelRows];
     const int t = threadIdx.x;
+    const int l = t & 63, g = l >> 4;
+    const int64_t cc = (int64_t)blockIdx.x * 64 + (t >> 6) * 16 + (l & 15);
+    const bool live = cc < T;
+    // every load reads an in-range address (columns past T and rows past ib clamped to the
+    // last ones); the values that stand for nothing are zeroed. The right-hand sides and the
+    // diagonal are loaded first and pinned (empty asm) before they are masked: left to itself the
+    // compiler moves each right-hand-side load into a branch on its mask and waits on it there,
+    // one memory round trip per value (32 in a row).
+    const int64_t ccl = live ? cc : T - 1;
+    auto at = [&](int row) -> int64_t { return kRowRHS ? row * ldx + ccl : ccl * ldx + row; };
+    double xv[8][4];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * b + g + 4 * r;
+            xv[b][r] = X[at(row < ib ? row : ib - 1)];
+        }
+    const int td = t < ib ? t : ib - 1;
+    double dg = U[(int64_t)td * N + td];
 #pragma unroll
     for (int b = 1; b < 8; ++b)
 #pragma unroll
@@ -2419,22 +2439,16 @@ __global__ __launch_bounds__(256) void k_panel_subst(int64_t N, const double* __
         const double v = U[(int64_t)min(col, ib - 1) * N + min(row, ib - 1)];
         Ud[b][i][sl] = ((kBack ? ip < i : ip > i) && row < ib && col < ib) ? v : 0.0;
     }
-    if (t < kPanelRows) rdg[t] = t < ib ? 1.0 / U[(int64_t)t * N + t] : 0.0;
-    const int l = t & 63, g = l >> 4;
-    const int64_t cc = (int64_t)blockIdx.x * 64 + (t >> 6) * 16 + (l & 15);
-    const bool live = cc < T;
-    // every load reads an in-range address (columns past T and rows past ib clamped to the
-    // last ones); the values that stand for nothing are zeroed
-    const int64_t ccl = live ? cc : T - 1;
-    auto at = [&](int row) -> int64_t { return kRowRHS ? row * ldx + ccl : ccl * ldx + row; };
+    asm volatile("" : "+v"(dg));
+    if (t < kPanelRows) rdg[t] = t < ib ? 1.0 / dg : 0.0;
     v4d_sub C[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 16 * b + g + 4 * r;
-            const double v = X[at(row < ib ? row : ib - 1)];
-            C[b][r] = (live && row < ib) ? v : 0.0;
+            asm volatile("" : "+v"(xv[b][r]));
+            C[b][r] = (live && row < ib) ? xv[b][r] : 0.0;
         }
     __syncthreads();
 #pragma unroll
