@@ -211,13 +211,18 @@ __global__ __launch_bounds__(kThreads) void k_trsv_fwd_step(int64_t N, const dou
     for (int64_t i0 = j1 + kNb + (int64_t)(blockIdx.x - 1) * kNb; i0 < N;
          i0 += (int64_t)(gridDim.x - 1) * kNb) {
         const int64_t ia = i0 + rsub, ib = ia + 64;
+        // the rows' x is read ahead of the rows and pinned after them, so that the compiler
+        // keeps every load of the pass in one memory round trip rather than issuing these behind
+        // the wait for the rows
+        double xa = x[ia < N ? ia : N - 1], xb = x[ib < N ? ib : N - 1];
         double2 va[4], vb[4];
         load_row(ia < N, ia, va);
         load_row(ib < N, ib, vb);
+        asm volatile("" : "+v"(xa), "+v"(xb));
         const double pa = dot_row(va), pb = dot_row(vb);
         if (sub == 0) {
-            if (ia < N) x[ia] -= pa;
-            if (ib < N) x[ib] -= pb;
+            if (ia < N) x[ia] = xa - pa;
+            if (ib < N) x[ib] = xb - pb;
         }
     }
 }
@@ -246,13 +251,13 @@ __global__ __launch_bounds__(kThreads) void k_trsv_bwd_step(int64_t N, const dou
         double tri[kTriLoads];
         load_triangle(N, L, jm, kNb, tri);
         double xv = 0.0, dg0 = 1.0, dg1 = 1.0;
+        if (t < 64) {               // ahead of the store of d below, which waits on its load
+            dg0 = L[(jm + t) * N + jm + t];
+            dg1 = L[(jm + 64 + t) * N + jm + 64 + t];
+        }
         if (t < kNb) {
             xv = x[jm + t];
             ds[t] = t < nb ? x[j0 + t] : 0.0;
-        }
-        if (t < 64) {
-            dg0 = L[(jm + t) * N + jm + t];
-            dg1 = L[(jm + 64 + t) * N + jm + 64 + t];
         }
         store_triangle(tri, Ls);
         __syncthreads();
