@@ -343,6 +343,54 @@ __global__ __launch_bounds__(256) void k_pair_density(int64_t n, const int32_t* 
     }
 }
 
+// The same for 64 lanes per pair (k > 32), one wave per run of kRun consecutive pairs: the lane's
+// occ_o C_io (o = lane + 64 t, kR values per lane, k <= 64 kR) stay in registers while i does not
+// change -- on a list sorted by i, for most of a splat's partners -- so a pair reads only C_j from
+// the cache hierarchy instead of C_i, C_j and occ. Each product and each lane's sum are formed in
+// the order of k_pair_density<64>, so q is bit-identical.
+constexpr int64_t kDensityRun = 16;
+template <int kR>
+__global__ __launch_bounds__(256) void k_pair_density_run(int64_t n,
+                                                          const int32_t* __restrict__ pi,
+                                                          const int32_t* __restrict__ pj,
+                                                          const double* __restrict__ weight,
+                                                          int64_t k,
+                                                          const double* __restrict__ C,
+                                                          const double* __restrict__ occ,
+                                                          double* __restrict__ q) {
+    const int lane = threadIdx.x & 63;
+    const int64_t a0 = ((blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6) * kDensityRun;
+    const int64_t a1 = min(n, a0 + kDensityRun);
+    double ci[kR];
+    int64_t cur = -1;
+    for (int64_t a = a0; a < a1; ++a) {                  // wave-uniform
+        const int64_t i = pi[a], j = pj[a];
+        // every load of a row is issued before any is used (addresses clamped in range; the
+        // values past k are never added), so a row costs one memory round trip
+        if (i != cur) {                                  // wave-uniform
+            double cv[kR], ov[kR];
+#pragma unroll
+            for (int t = 0; t < kR; ++t) {
+                const int64_t o = min((int64_t)(lane + 64 * t), k - 1);
+                cv[t] = C[i * k + o];
+                ov[t] = occ[o];
+            }
+#pragma unroll
+            for (int t = 0; t < kR; ++t) ci[t] = ov[t] * cv[t];
+            cur = i;
+        }
+        double cj[kR];
+#pragma unroll
+        for (int t = 0; t < kR; ++t) cj[t] = C[j * k + min((int64_t)(lane + 64 * t), k - 1)];
+        double s = 0.0;
+#pragma unroll
+        for (int t = 0; t < kR; ++t)
+            if (lane + 64 * t < k) s += ci[t] * cj[t];
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (lane == 0) q[a] = (weight ? weight[a] : 1.0) * s;
+    }
+}
+
 // Pair record: I1 I2 I3 | Ah (6) | Pa (3) | coef = KN q pref | KN | q | pad.
 __global__ void k_pair_rec(int64_t n, const int32_t* __restrict__ pi,
                            const int32_t* __restrict__ pj, const double* __restrict__ A6,
@@ -1939,6 +1987,18 @@ int launch_pair_density(int64_t n, const int32_t* pi, const int32_t* pj, const d
         k_pair_density<16><<<grid(16), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     } else if (k <= 32) {
         k_pair_density<32><<<grid(32), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+    } else if (k <= 64 * 32) {
+        // one wave per run of kDensityRun pairs (at most n / 16 waves: within one grid dimension
+        // for any list the entry points accept)
+        const unsigned blocks = (unsigned)(((n + kDensityRun - 1) / kDensityRun + 3) / 4);
+        if (k <= 64 * 8)
+            k_pair_density_run<8><<<blocks, 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        else if (k <= 64 * 16)
+            k_pair_density_run<16><<<blocks, 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        else if (k <= 64 * 24)
+            k_pair_density_run<24><<<blocks, 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
+        else
+            k_pair_density_run<32><<<blocks, 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     } else {
         k_pair_density<64><<<grid(64), 256, 0, s>>>(n, pi, pj, weight, k, C, occ, q);
     }
